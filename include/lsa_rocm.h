@@ -1,0 +1,159 @@
+/*
+ * lsa_rocm.h - C ABI of the MI355X (gfx950) select+read kernels for Latent Sparse
+ * Attention. One shared library, liblsa_rocm.so; every entry point:
+ *   - takes plain device pointers, sizes and a hipStream_t (as void*); the library
+ *     never allocates device memory: scratch comes in through `workspace`;
+ *   - launches asynchronously on that stream and never synchronizes;
+ *   - validates its arguments on the host first and returns LSA_OK (0) or a negative
+ *     LSA_ERR_* code, with a message from lsa_last_error() (thread-local).
+ * Layouts are dense row-major (the Python host layer makes tensors contiguous).
+ *
+ * Selection keys are the reference's packed int64 layout:
+ *   key = (ordered_bits(score) << 32) | (0x7FFFFFFF - column),  EMPTY = INT64_MIN.
+ * Scores are the canonical fp32 dot product: operands rounded to the scoring type
+ * (bf16 RNE or fp32), exact fp64 products, 16 in-order partial sums over contiguous
+ * D/16 slices, combined by the tree (p,p+8),(p,p+4),(p,p+2),(p,p+1), one fp32 rounding.
+ *
+ * Bucket tables: a contiguous stack of `n_tables` tables, each `rows` buckets. The
+ * table used by (query row r, group g) is r * row_tables + g * group_tables, so
+ * (0, 0) shares one table (the reference layout), (0, 1) is one table per kv-head
+ * (per-kv-head selection) and (G, 1) one per (sequence, kv-head).
+ */
+#ifndef LSA_ROCM_H
+#define LSA_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LSA_ABI_VERSION 1
+
+enum lsa_status {
+  LSA_OK = 0,
+  LSA_ERR_NULL = -1,      /* a required pointer is NULL */
+  LSA_ERR_SHAPE = -2,     /* sizes inconsistent or out of the supported range */
+  LSA_ERR_DTYPE = -3,     /* unsupported element type */
+  LSA_ERR_POW2 = -4,      /* a size that must be a power of two is not */
+  LSA_ERR_WORKSPACE = -5, /* workspace missing or too small */
+  LSA_ERR_LAUNCH = -6,    /* the HIP launch failed */
+  LSA_ERR_ALIGN = -7      /* a pointer is not aligned for vector access */
+};
+
+enum lsa_dtype { LSA_F32 = 0, LSA_BF16 = 1, LSA_F16 = 2 };
+enum lsa_score_mode { LSA_SCORE_BF16 = 0, LSA_SCORE_F32 = 1 };
+enum lsa_centroid_mode { LSA_CENTROID_MEAN = 0, LSA_CENTROID_NORMALIZED = 1 };
+
+int lsa_abi_version(void);
+const char* lsa_last_error(void);
+
+/* Visible bucket counts per (row, group) [R, G] int32 (reference pipeline.py:184-186
+ * visible_counts): without `ends`, (pos // cluster_block_size) * block_buckets clamped
+ * to rows; with `ends` [tables, rows] the buckets whose span ends at or before pos+1. */
+int lsa_visible_counts(const int32_t* positions, int64_t R, int32_t G, int32_t rows, int32_t cluster_block_size,
+                       int32_t block_buckets, const int32_t* ends, int64_t row_tables, int64_t group_tables,
+                       int32_t* counts, void* stream);
+
+/* Canonical scores [R, G, N] fp32 of queries [R, G, D] (dtype q_dtype) against the
+ * tables' centroids (bf16 for LSA_SCORE_BF16, fp32 for LSA_SCORE_F32). Replaces the
+ * reference's score GEMM, pipeline.py:217-232 _production_scores. */
+int lsa_score_rows(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D, const void* centroids,
+                   int32_t N, int64_t row_tables, int64_t group_tables, int score_mode, float* scores, void* stream);
+
+/* Whole-path listing: keys [R, N] int64, every column packed, EMPTY at or past
+ * counts[r] (reference pipeline.py:266-267, upstream TopK.listed whole path). */
+int lsa_pack_listing(const float* scores, const int32_t* counts, int64_t R, int32_t N, int64_t* keys, void* stream);
+
+/* best_first_keys (reference pipeline.py:189-214): out [R, k] the k greatest keys of
+ * each row of keys [R, W], descending; counts (nullable) masks slots >= counts[r]. */
+int lsa_topk_keys(const int64_t* keys, const int32_t* counts, int64_t R, int32_t W, int32_t k, int64_t* out,
+                  void* stream);
+
+/* select_topk_scores (reference select_fused.py:83-137): out [R, K2] int64 with
+ * K2 = next_pow2(min(top_p, N)), the best min(top_p, N) packed keys of the fp32 scores
+ * [R, N] (columns >= lengths[r] are EMPTY), descending, EMPTY tail. */
+int lsa_select_topk_scores(const float* scores, const int32_t* lengths, int64_t R, int32_t N, int32_t top_p,
+                           int64_t* out, void* stream);
+
+/* unpack_ids (upstream keys.unpack_ids, reference pipeline.py:268): ids [n] int32. */
+int lsa_unpack_ids(const int64_t* keys, int64_t n, int32_t* ids, void* stream);
+
+/* Rank-order expansion (upstream expand_in_order, reference select_fused.py:140-280
+ * expand_in_order_from_keys). picks [R, G, P]: int32 bucket ids (-1 none) when
+ * picks_are_keys == 0, int64 packed keys (EMPTY none) otherwise. members [tables, rows,
+ * cap]; positions [R] int32. Out: lists [R, G, top_k + window + sink] int32 (-1 padded)
+ * and lengths [R, G] int32. */
+int lsa_expand(const void* picks, int picks_are_keys, int64_t R, int32_t G, int32_t P, const int32_t* members,
+               int32_t rows, int32_t cap, int64_t row_tables, int64_t group_tables, const int32_t* positions,
+               int32_t window, int32_t sink, int32_t top_k, int32_t* lists, int32_t* lengths, void* stream);
+
+/* Fused flat select: score + top-k + expansion in one launch (reference pipeline.py:
+ * 274-316 flat_select, LSA_SELECT_IMPL=fused). queries [R, G, D]; tables as above
+ * (centroids bf16 or fp32 per score_mode, members, optional ends); positions [R]. The
+ * N columns of a (row, group) are split over `splits` workgroups whose sorted partial
+ * top-k lists the last one to arrive merges (splits == 1: counters and scratch unused).
+ * counters: R * G int32 that read zero at launch; every launch leaves them zero again.
+ * scratch: lsa_select_flat_scratch_bytes(), no initialisation. Out as lsa_expand. */
+size_t lsa_select_flat_scratch_bytes(int64_t R, int32_t G, int32_t top_p, int32_t N, int32_t splits);
+int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D, const void* centroids,
+                    const int32_t* members, const int32_t* ends, int32_t rows, int32_t cap, int64_t row_tables,
+                    int64_t group_tables, int score_mode, const int32_t* positions, int32_t cluster_block_size,
+                    int32_t block_buckets, int32_t top_p, int32_t window, int32_t sink, int32_t top_k,
+                    int32_t splits, int32_t* counters, void* scratch, size_t scratch_bytes, int32_t* lists,
+                    int32_t* lengths, void* stream);
+
+/* Two-level tree select (reference pipeline.py:319-337 tree_select, _tree.py:438-493
+ * _beam_pick_rows with one node level): the best `beam_width` of the n_nodes node
+ * centroids, then the best top_p of their children plus the uncovered visible buckets
+ * [covered, visible), then the flat expansion. node_centroids [tables, n_nodes, D],
+ * children [tables, n_nodes, node_size] int32 bucket ids. */
+int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D, const void* node_centroids,
+                    const int32_t* children, int32_t n_nodes, int32_t node_size, const void* centroids,
+                    const int32_t* members, const int32_t* ends, int32_t rows, int32_t cap, int64_t row_tables,
+                    int64_t group_tables, int score_mode, const int32_t* positions, int32_t cluster_block_size,
+                    int32_t block_buckets, int32_t covered, int32_t beam_width, int32_t top_p, int32_t window,
+                    int32_t sink, int32_t top_k, int32_t* lists, int32_t* lengths, void* stream);
+
+/* GQA-collapsed index queries (reference gates.py:50-59 make_index_space, per-kv-head
+ * form): out [B, T/chunk, Hkv, D] fp32 = fp32 mean of q [B, T, Hq, D] over each
+ * kv-head's query group and `chunk` consecutive tokens (tokens outer, heads inner). */
+int lsa_index_queries(const void* q, int q_dtype, int64_t B, int64_t T, int32_t Hq, int32_t Hkv, int32_t D,
+                      int32_t chunk, float* out, void* stream);
+
+/* Bucket centroids (reference pipeline.py:108-115, :396-403): for each of n_tables *
+ * rows buckets, the mean (or L2-normalized sum) of its member keys. keys: element
+ * (t, d) of table k lives at keys[k_off(k) + t * token_stride + d] with k_off(k) =
+ * (k / kv_heads) * batch_stride + (k % kv_heads) * D; member ids outside [0, tokens) are
+ * skipped. Out fp32 and bf16 [tables, rows, D]. */
+int lsa_bucket_centroids(const void* keys, int k_dtype, int64_t tokens, int64_t token_stride, int64_t batch_stride,
+                         int32_t kv_heads, int32_t D, const int32_t* members, int64_t n_tables, int32_t rows,
+                         int32_t cap, int centroid_mode, float* out_f32, uint16_t* out_bf16, void* stream);
+
+/* Sparse gather read (reference read_kernel_tiled.py:30-156 sparse_read_auto / tiled,
+ * read_kernel.py:26-120 v1): q [B, Tq, Hq, D], k/v [B, Tk, Hkv, D] (dtype), ids
+ * [B*Tq, W] shared by all heads (ids_per_head == 0) or [B*Tq, Hkv, W] per kv-head, and
+ * lengths likewise. Each (row, kv-head) list is split over `splits` workgroups whose
+ * online-softmax partials the last one to arrive combines. empty_nan: a row with no key
+ * gives NaN (v1 contract) instead of 0. Ids outside [0, Tk) are skipped.
+ * counters: B*Tq*Hkv int32 that read zero at launch, left zero (splits > 1 only);
+ * scratch: lsa_read_scratch_bytes(), no initialisation. */
+size_t lsa_read_scratch_bytes(int64_t rows, int32_t Hq, int32_t Hkv, int32_t D, int32_t splits);
+int lsa_read(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t Tq, int64_t Tk, int32_t Hq,
+             int32_t Hkv, int32_t D, const int32_t* ids, const int32_t* lengths, int32_t W, int ids_per_head,
+             float scale, int empty_nan, int32_t splits, int32_t* counters, void* scratch, size_t scratch_bytes,
+             void* out, void* stream);
+
+/* Chunked prefill read on MFMA (bf16): query row t of chunk c = t / chunk reads chunk
+ * c's per-kv-head list ids [B, C, Hkv, W] (first lengths[b, c, g] slots) plus the
+ * chunk's causal block [c*chunk, t]. q [B, T, Hq, D], k/v [B, Tk, Hkv, D], out like q. */
+int lsa_read_chunked(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t T, int64_t Tk,
+                     int32_t Hq, int32_t Hkv, int32_t D, const int32_t* ids, const int32_t* lengths, int32_t W,
+                     int32_t chunk, float scale, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LSA_ROCM_H */

@@ -1,0 +1,243 @@
+// Device building blocks shared by the select and read kernels (gfx950, wave64).
+//
+// Packed selection keys follow the reference layout (select_fused.py:71-77):
+//   key = (ordered_bits(score) << 32) | (0x7FFFFFFF - column),   EMPTY = INT64_MIN
+// Inside a workgroup keys are handled as u = key ^ 0x8000000000000000, an unsigned
+// value with the same order, so EMPTY is u == 0 and "best first" is "largest u first".
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define LSA_BLOCK 256
+#define LSA_WAVE 64
+#define LSA_WAVES (LSA_BLOCK / LSA_WAVE)
+
+namespace lsa {
+
+constexpr int64_t kEmpty = (int64_t)0x8000000000000000ull;
+constexpr uint64_t kSignBit = 0x8000000000000000ull;
+// Partial sums per canonical dot product (16 lanes, tree (p,p+8),(p,p+4),(p,p+2),(p,p+1)).
+constexpr int kScorePartials = 16;
+
+struct bf16_t { uint16_t bits; };
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// fp32 -> bf16, round to nearest even; NaN -> 0x7FC0 (torch's conversion).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return 0x7FC0;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+template <typename T> struct elem;
+template <> struct elem<float> {
+  static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void store(float* p, int64_t i, float x) { p[i] = x; }
+};
+template <> struct elem<bf16_t> {
+  static __device__ __forceinline__ float load(const bf16_t* p, int64_t i) { return bf16_to_f32(p[i].bits); }
+  static __device__ __forceinline__ void store(bf16_t* p, int64_t i, float x) { p[i].bits = f32_to_bf16(x); }
+};
+template <> struct elem<_Float16> {
+  static __device__ __forceinline__ float load(const _Float16* p, int64_t i) { return (float)p[i]; }
+  static __device__ __forceinline__ void store(_Float16* p, int64_t i, float x) { p[i] = (_Float16)x; }
+};
+
+// ---------------------------------------------------------------- packed keys
+
+__device__ __forceinline__ int32_t ordered_bits(float s) {
+  int32_t b = __float_as_int(s);
+  return b ^ ((b >> 31) & 0x7FFFFFFF);
+}
+
+__device__ __forceinline__ int64_t pack_key(float s, int32_t column) {
+  uint64_t hi = (uint64_t)(uint32_t)ordered_bits(s) << 32;
+  return (int64_t)(hi | (uint64_t)(uint32_t)(0x7FFFFFFF - column));
+}
+
+__device__ __forceinline__ uint64_t key_to_u(int64_t key) { return (uint64_t)key ^ kSignBit; }
+__device__ __forceinline__ int64_t u_to_key(uint64_t u) { return (int64_t)(u ^ kSignBit); }
+
+// Column of a key; -1 for EMPTY (upstream key_bucket / unpack_ids).
+__device__ __forceinline__ int32_t key_column(int64_t key) {
+  if (key == kEmpty) return -1;
+  return 0x7FFFFFFF - (int32_t)(uint32_t)((uint64_t)key & 0xFFFFFFFFull);
+}
+
+// ---------------------------------------------------------------- wave / block scans
+
+__device__ __forceinline__ int wave_inclusive_sum(int x) {
+  const int lane = threadIdx.x & (LSA_WAVE - 1);
+#pragma unroll
+  for (int d = 1; d < LSA_WAVE; d <<= 1) {
+    int y = __shfl_up(x, d, LSA_WAVE);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
+// Exclusive prefix sum over the 256 threads; *total receives the block sum.
+// `scratch` holds LSA_WAVES ints. Contains barriers: every thread must call it.
+__device__ __forceinline__ int block_exclusive_sum(int x, int* scratch, int* total) {
+  const int lane = threadIdx.x & (LSA_WAVE - 1);
+  const int wave = threadIdx.x / LSA_WAVE;
+  int inc = wave_inclusive_sum(x);
+  if (lane == LSA_WAVE - 1) scratch[wave] = inc;
+  __syncthreads();
+  int before = 0, sum = 0;
+#pragma unroll
+  for (int w = 0; w < LSA_WAVES; ++w) {
+    int v = scratch[w];
+    before += (w < wave) ? v : 0;
+    sum += v;
+  }
+  __syncthreads();
+  *total = sum;
+  return before + inc - x;
+}
+
+// ---------------------------------------------------------------- radix select
+
+// State of a top-k radix select, kept in LDS by the caller.
+struct RadixState {
+  uint64_t prefix;     // selected high digits
+  uint64_t mask;       // which bits of prefix are fixed
+  int need;            // how many keys equal to (prefix-range) are still needed
+  int done;            // 1: every key >= prefix is selected (early exit)
+  int hist[256];
+  int slot;            // collection cursor
+};
+
+// Finds the k-th largest of the n values produced by get(i) (u-ordered keys).
+// On return (after a barrier) the selected set is either
+//   done == 1: every value v >= prefix (its low digits are zero), exactly k of them;
+//   done == 0: every value > prefix plus `need` copies of prefix (ties).
+// 1 <= k <= n. Every thread of the block must call it.
+template <typename Get>
+__device__ void radix_select(Get get, int n, int k, RadixState* st) {
+  const int tid = threadIdx.x;
+  if (tid == 0) { st->prefix = 0; st->mask = 0; st->need = k; st->done = 0; }
+  for (int pass = 0; pass < 8; ++pass) {
+    const int shift = 56 - 8 * pass;
+    st->hist[tid] = 0;  // LSA_BLOCK == 256 bins
+    __syncthreads();
+    const uint64_t prefix = st->prefix, mask = st->mask;
+    for (int i = tid; i < n; i += LSA_BLOCK) {
+      uint64_t v = get(i);
+      if ((v & mask) == prefix) atomicAdd(&st->hist[(v >> shift) & 255], 1);
+    }
+    __syncthreads();
+    if (tid < LSA_WAVE) {
+      // lane l owns bins 255-4l .. 252-4l (descending); suffix counts from the top bin
+      int c0 = st->hist[255 - 4 * tid], c1 = st->hist[254 - 4 * tid];
+      int c2 = st->hist[253 - 4 * tid], c3 = st->hist[252 - 4 * tid];
+      int mine = c0 + c1 + c2 + c3;
+      int inc = wave_inclusive_sum(mine);
+      int above = inc - mine;  // count in bins above this lane's group
+      const int need = st->need;
+      if (above < need && need <= inc) {
+        int d = 255 - 4 * tid, cnt = c0;
+        if (above + c0 < need) { above += c0; d -= 1; cnt = c1;
+          if (above + c1 < need) { above += c1; d -= 1; cnt = c2;
+            if (above + c2 < need) { above += c2; d -= 1; cnt = c3; } } }
+        const int rest = need - above;
+        st->prefix = prefix | ((uint64_t)d << shift);
+        st->mask = mask | (0xFFull << shift);
+        st->need = rest;
+        st->done = (cnt == rest) ? 1 : 0;
+      }
+    }
+    __syncthreads();
+    if (st->done) break;
+  }
+}
+
+// Appends the selected values (see radix_select) to out[0..k) in arbitrary order.
+template <typename Get>
+__device__ void radix_collect(Get get, int n, int k, RadixState* st, uint64_t* out) {
+  const int tid = threadIdx.x;
+  if (tid == 0) st->slot = 0;
+  __syncthreads();
+  const uint64_t prefix = st->prefix;
+  const int done = st->done;
+  for (int i = tid; i < n; i += LSA_BLOCK) {
+    uint64_t v = get(i);
+    bool take = done ? (v >= prefix) : (v > prefix);
+    if (take) out[atomicAdd(&st->slot, 1)] = v;
+  }
+  __syncthreads();
+  if (!done) {
+    const int base = st->slot;  // == k - need
+    for (int i = base + tid; i < k; i += LSA_BLOCK) out[i] = prefix;
+  }
+  __syncthreads();
+}
+
+// Sorts a[0..n) descending in LDS; n is a power of two. Every thread must call it.
+__device__ void bitonic_sort_desc(uint64_t* a, int n) {
+  const int tid = threadIdx.x;
+  for (int size = 2; size <= n; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < n / 2; i += LSA_BLOCK) {
+        int lo = 2 * i - (i & (stride - 1));
+        int hi = lo + stride;
+        bool desc = ((lo & size) == 0);
+        uint64_t x = a[lo], y = a[hi];
+        if ((x < y) == desc) { a[lo] = y; a[hi] = x; }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Sorts 64 values held one per lane descending across the wave (lane 0 = largest).
+__device__ __forceinline__ uint64_t wave_sort64_desc(uint64_t v) {
+  const int lane = threadIdx.x & (LSA_WAVE - 1);
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      uint32_t lo32 = (uint32_t)v, hi32 = (uint32_t)(v >> 32);
+      uint32_t olo = __shfl_xor(lo32, stride, LSA_WAVE), ohi = __shfl_xor(hi32, stride, LSA_WAVE);
+      uint64_t o = ((uint64_t)ohi << 32) | olo;
+      bool desc = ((lane & size) == 0);
+      bool lower = ((lane & stride) == 0);
+      // in a descending block the lower lane keeps the max
+      bool keep_max = (lower == desc);
+      uint64_t mx = v > o ? v : o, mn = v > o ? o : v;
+      v = keep_max ? mx : mn;
+    }
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------- canonical score
+
+// One canonical dot product shared by 16 lanes: lane p (0..15 within its group) has
+// already summed dims [p*span, (p+1)*span) in order into `partial` (fp64).
+// Returns the fp32 score in every lane of the 16-lane group.
+__device__ __forceinline__ float score_tree16(double partial) {
+  partial += __shfl_xor(partial, 8, 16);
+  partial += __shfl_xor(partial, 4, 16);
+  partial += __shfl_xor(partial, 2, 16);
+  partial += __shfl_xor(partial, 1, 16);
+  return (float)partial;
+}
+
+// Scores one centroid row against a query slice held by the lane: q[j] are the lane's
+// span query values (already rounded to the scoring type), c points at the row.
+template <typename C>
+__device__ __forceinline__ double partial_dot(const float* q, const C* c, int span, int p) {
+  double acc = 0.0;
+  const C* base = c + (int64_t)p * span;
+#pragma unroll 4
+  for (int j = 0; j < span; ++j) acc = fma((double)q[j], (double)elem<C>::load(base, j), acc);
+  return acc;
+}
+
+}  // namespace lsa

@@ -1,0 +1,678 @@
+// Selection kernels for gfx950: canonical scoring, the whole-path listing, best-first
+// top-k, unpack, the rank-order expansion, the fused flat select (score + top-k +
+// expansion, split over workgroups for decode) and the two-level tree select.
+//
+// Reference behaviour restated: pipeline.py:184-316 (visible_counts, best_first_keys,
+// _production_scores, flat_select[_reference]), select_fused.py:52-280
+// (select_topk_scores, expand_in_order_from_keys), _tree.py:438-493 (_beam_pick_rows).
+#include "lsa_abi_common.h"
+#include "lsa_select_dev.h"
+
+using namespace lsa;
+
+namespace {
+
+constexpr int kMaxLdsKeys = 4096;  // u64 keys a workgroup holds in LDS (32 KiB)
+
+// ------------------------------------------------------------------ visible counts
+
+__global__ void visible_counts_kernel(const int32_t* positions, int64_t R, int G, int rows, int cluster_block,
+                                      int block_buckets, const int32_t* ends, int64_t row_tables,
+                                      int64_t group_tables, int32_t* counts) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= R * G) return;
+  const int64_t r = i / G, g = i % G;
+  const int32_t* e = ends ? ends + (r * row_tables + g * group_tables) * rows : nullptr;
+  counts[i] = visible_count(positions[r], rows, cluster_block, block_buckets, e);
+}
+
+// ------------------------------------------------------------------ scores
+
+template <typename QT, typename CT, int SPAN>
+__global__ __launch_bounds__(LSA_BLOCK) void score_rows_kernel(const QT* q, int G, const CT* cent, int N,
+                                                               int64_t row_tables, int64_t group_tables,
+                                                               bool bf16_mode, float* out) {
+  constexpr int D = 16 * SPAN;
+  const int64_t i = blockIdx.x;
+  const int64_t r = i / G, g = i % G;
+  const int p = threadIdx.x & 15, grp = threadIdx.x >> 4;
+  float qs[SPAN];
+  load_query_slice<QT, SPAN>(q + i * D, p, bf16_mode, qs);
+  const CT* tab = cent + (r * row_tables + g * group_tables) * (int64_t)N * D;
+  const int c = blockIdx.y * (LSA_BLOCK / 16) + grp;
+  if (c < N) {
+    const float s = canonical_score<CT, SPAN>(qs, tab + (int64_t)c * D, p);
+    if (p == 0) out[i * N + c] = s;
+  }
+}
+
+// ------------------------------------------------------------------ listing / unpack
+
+__global__ void pack_listing_kernel(const float* scores, const int32_t* counts, int64_t R, int N, int64_t* keys) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= R * N) return;
+  const int64_t r = i / N;
+  const int c = (int)(i % N);
+  keys[i] = c < counts[r] ? pack_key(scores[i], c) : kEmpty;
+}
+
+__global__ void unpack_kernel(const int64_t* keys, int64_t n, int32_t* ids) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i < n) ids[i] = key_column(keys[i]);
+}
+
+// ------------------------------------------------------------------ top-k
+
+struct KeySource {  // best_first_keys: existing keys, optional listing counts
+  const int64_t* keys;
+  const int32_t* counts;
+  int W;
+  __device__ uint64_t get(int64_t row, int i) const {
+    if (counts && i >= counts[row]) return 0;
+    return key_to_u(keys[row * W + i]);
+  }
+};
+
+struct ScoreSource {  // select_topk_scores: pack from fp32 scores, EMPTY past length
+  const float* scores;
+  const int32_t* lengths;
+  int W;
+  __device__ uint64_t get(int64_t row, int i) const {
+    if (i >= lengths[row]) return 0;
+    return key_to_u(pack_key(scores[row * W + i], i));
+  }
+};
+
+// One row per workgroup: radix-select the k-th best key, collect the k best, bitonic
+// sort them descending, write k_out keys (EMPTY past k). LDS mode keeps the row in LDS.
+template <typename Src, bool LDS_ROW>
+__global__ __launch_bounds__(LSA_BLOCK) void topk_kernel(Src src, int W, int k, int kp, int k_out, int64_t* out) {
+  extern __shared__ uint64_t smem[];
+  __shared__ RadixState st;
+  const int64_t row = blockIdx.x;
+  uint64_t* buf = smem;
+  uint64_t* row_keys = smem + kp;
+  if (LDS_ROW) {
+    for (int i = threadIdx.x; i < W; i += LSA_BLOCK) row_keys[i] = src.get(row, i);
+    __syncthreads();
+  }
+  auto get = [&](int i) -> uint64_t { return LDS_ROW ? row_keys[i] : src.get(row, i); };
+  radix_select(get, W, k, &st);
+  radix_collect(get, W, k, &st, buf);
+  for (int i = k + threadIdx.x; i < kp; i += LSA_BLOCK) buf[i] = 0;
+  __syncthreads();
+  bitonic_sort_desc(buf, kp);
+  for (int i = threadIdx.x; i < k_out; i += LSA_BLOCK) out[row * k_out + i] = i < k ? u_to_key(buf[i]) : kEmpty;
+}
+
+// ------------------------------------------------------------------ expansion
+
+template <bool KEYS>
+__global__ __launch_bounds__(LSA_BLOCK) void expand_kernel(const void* picks, int G, int P, const int32_t* members,
+                                                           int rows, int cap, int64_t row_tables,
+                                                           int64_t group_tables, const int32_t* positions,
+                                                           int window, int sink, int top_k, int32_t* lists,
+                                                           int32_t* lengths) {
+  extern __shared__ int32_t pk[];
+  __shared__ int scan[LSA_WAVES];
+  const int64_t i = blockIdx.x;
+  const int64_t r = i / G, g = i % G;
+  for (int j = threadIdx.x; j < P; j += LSA_BLOCK) {
+    pk[j] = KEYS ? key_column(((const int64_t*)picks)[i * P + j]) : ((const int32_t*)picks)[i * P + j];
+  }
+  __syncthreads();
+  const int32_t* tab = members + (r * row_tables + g * group_tables) * (int64_t)rows * cap;
+  const int width = top_k + window + sink;
+  const int len = expand_walk(pk, P, tab, rows, cap, positions[r], window, sink, top_k, lists + i * width, width,
+                              scan);
+  if (threadIdx.x == 0) lengths[i] = len;
+}
+
+// ------------------------------------------------------------------ fused flat select
+
+struct FlatArgs {
+  int64_t R;
+  int G;
+  int rows, cap;
+  int64_t row_tables, group_tables;
+  const void* centroids;
+  const int32_t* members;
+  const int32_t* ends;
+  const int32_t* positions;
+  int cluster_block, block_buckets;
+  int K, kp;          // picks kept (min(top_p, rows)) and its power of two
+  int window, sink, top_k;
+  int S, cs;          // splits and columns per split
+  int keys_cap;       // LDS keys slots: max(cs, S*K)
+  uint64_t* ws_keys;  // [R*G, S, K]
+  int* ws_count;      // [R*G]
+  int32_t* lists;
+  int32_t* lengths;
+};
+
+// grid (R*G, S). Each workgroup scores its column slice and keeps its best K keys; with
+// S > 1 the last workgroup of a (row, group) merges the S sorted lists. The winner
+// expands the picks into the read list.
+template <typename QT, typename CT, int SPAN>
+__global__ __launch_bounds__(LSA_BLOCK) void select_flat_kernel(const QT* q, bool bf16_mode, FlatArgs a) {
+  constexpr int D = 16 * SPAN;
+  extern __shared__ uint64_t smem[];
+  __shared__ RadixState st;
+  __shared__ int scan[LSA_WAVES];
+  __shared__ int is_last;
+  uint64_t* keys = smem;
+  uint64_t* best = smem + a.keys_cap;
+  const int64_t i = blockIdx.x;
+  const int s = blockIdx.y;
+  const int64_t r = i / a.G, g = i % a.G;
+  const int64_t position = a.positions[r];
+  const int64_t t = r * a.row_tables + g * a.group_tables;
+  const int visible = visible_count(position, a.rows, a.cluster_block, a.block_buckets,
+                                    a.ends ? a.ends + t * a.rows : nullptr);
+  const CT* cent = (const CT*)a.centroids + t * a.rows * (int64_t)D;
+  const int c0 = s * a.cs;
+  const int c1 = min(c0 + a.cs, a.rows);
+  const int n_local = c1 > c0 ? c1 - c0 : 0;
+
+  float qs[SPAN];
+  load_query_slice<QT, SPAN>(q + i * D, threadIdx.x & 15, bf16_mode, qs);
+  score_slice_keys<CT, SPAN>(qs, cent, D, c0, c1, visible, keys);
+  __syncthreads();
+  const int k_loc = min(a.K, n_local);
+  if (k_loc > 0) {
+    auto get = [&](int j) -> uint64_t { return keys[j]; };
+    radix_select(get, n_local, k_loc, &st);
+    radix_collect(get, n_local, k_loc, &st, best);
+  }
+  for (int j = k_loc + threadIdx.x; j < a.kp; j += LSA_BLOCK) best[j] = 0;
+  __syncthreads();
+  bitonic_sort_desc(best, a.kp);
+
+  if (a.S > 1) {
+    uint64_t* mine = a.ws_keys + (i * a.S + s) * (int64_t)a.K;
+    for (int j = threadIdx.x; j < a.K; j += LSA_BLOCK) mine[j] = best[j];
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) is_last = (atomicAdd(&a.ws_count[i], 1) == a.S - 1);
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    if (threadIdx.x == 0) a.ws_count[i] = 0;  // every split has arrived: reset for the next launch
+    const uint64_t* all = a.ws_keys + i * a.S * (int64_t)a.K;
+    for (int j = threadIdx.x; j < a.S * a.K; j += LSA_BLOCK) keys[j] = all[j];
+    __syncthreads();
+    merge_sorted_lists(keys, a.S, a.K, best);
+  }
+  int32_t* pk = (int32_t*)keys;
+  for (int j = threadIdx.x; j < a.K; j += LSA_BLOCK) pk[j] = key_column(u_to_key(best[j]));
+  __syncthreads();
+  const int width = a.top_k + a.window + a.sink;
+  const int32_t* tab = a.members + t * a.rows * (int64_t)a.cap;
+  const int len = expand_walk(pk, a.K, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k,
+                              a.lists + i * width, width, scan);
+  if (threadIdx.x == 0) a.lengths[i] = len;
+}
+
+// ------------------------------------------------------------------ two-level tree select
+
+struct TreeArgs {
+  int64_t R;
+  int G;
+  const void* node_centroids;
+  const int32_t* children;
+  int n_nodes, node_size;
+  const void* centroids;
+  const int32_t* members;
+  const int32_t* ends;
+  int rows, cap;
+  int64_t row_tables, group_tables;
+  const int32_t* positions;
+  int cluster_block, block_buckets;
+  int covered, beam, top_p;
+  int nodes_pow2, beam_pow2, cand_cap, cand_pow2, top_pow2;
+  int window, sink, top_k;
+  int32_t* lists;
+  int32_t* lengths;
+};
+
+template <typename QT, typename CT, int SPAN>
+__global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, bool bf16_mode, TreeArgs a) {
+  constexpr int D = 16 * SPAN;
+  extern __shared__ uint64_t smem[];
+  __shared__ RadixState st;
+  __shared__ int scan[LSA_WAVES];
+  uint64_t* keys = smem;                    // [max(nodes_pow2, cand_pow2)]
+  uint64_t* best = keys + max(a.nodes_pow2, a.cand_pow2);  // [max(beam_pow2, top_pow2)]
+  int32_t* cand = (int32_t*)(best + max(a.beam_pow2, a.top_pow2));  // [cand_cap]
+  const int64_t i = blockIdx.x;
+  const int64_t r = i / a.G, g = i % a.G;
+  const int64_t position = a.positions[r];
+  const int64_t t = r * a.row_tables + g * a.group_tables;
+  const int p = threadIdx.x & 15, grp = threadIdx.x >> 4;
+  float qs[SPAN];
+  load_query_slice<QT, SPAN>(q + i * D, p, bf16_mode, qs);
+
+  // level 1: every node, the best `beam` (a tie to the lower node)
+  const CT* ncent = (const CT*)a.node_centroids + t * (int64_t)a.n_nodes * D;
+  score_slice_keys<CT, SPAN>(qs, ncent, D, 0, a.n_nodes, a.n_nodes, keys);
+  __syncthreads();
+  const int beam = min(a.beam, a.n_nodes);
+  {
+    auto get = [&](int j) -> uint64_t { return keys[j]; };
+    radix_select(get, a.n_nodes, beam, &st);
+    radix_collect(get, a.n_nodes, beam, &st, best);
+  }
+  for (int j = beam + threadIdx.x; j < a.beam_pow2; j += LSA_BLOCK) best[j] = 0;
+  __syncthreads();
+  bitonic_sort_desc(best, a.beam_pow2);
+
+  // level 0 candidates: the kept nodes' children, then the uncovered visible buckets
+  const int visible = visible_count(position, a.rows, a.cluster_block, a.block_buckets,
+                                    a.ends ? a.ends + t * a.rows : nullptr);
+  const int n_fresh = max(0, visible - a.covered);
+  const int n_kids = beam * a.node_size;
+  const int n_cand = n_kids + n_fresh;
+  const int32_t* kids = a.children + t * (int64_t)a.n_nodes * a.node_size;
+  for (int j = threadIdx.x; j < a.cand_pow2; j += LSA_BLOCK) {
+    int32_t c = -1;
+    if (j < n_kids) {
+      const int node = key_column(u_to_key(best[j / a.node_size]));
+      if (node >= 0) c = kids[(int64_t)node * a.node_size + j % a.node_size];
+    } else if (j < n_cand) {
+      c = a.covered + (j - n_kids);
+    }
+    keys[j] = (c >= 0 && c < a.rows) ? (uint64_t)c + 1 : 0;  // id + 1, 0 = none
+  }
+  __syncthreads();
+  bitonic_sort_desc(keys, a.cand_pow2);  // equal ids adjacent: keep the first
+  for (int j = threadIdx.x; j < a.cand_pow2; j += LSA_BLOCK) {
+    const uint64_t v = keys[j];
+    cand[j] = (v != 0 && (j == 0 || keys[j - 1] != v)) ? (int32_t)(v - 1) : -1;
+  }
+  __syncthreads();
+  const CT* bcent = (const CT*)a.centroids + t * (int64_t)a.rows * D;
+  for (int j = grp; j < a.cand_pow2; j += LSA_BLOCK / 16) {
+    const int32_t c = cand[j];
+    uint64_t u = 0;
+    if (c >= 0) {
+      const float s = canonical_score<CT, SPAN>(qs, bcent + (int64_t)c * D, p);
+      u = key_to_u(pack_key(s, c));
+    }
+    if (p == 0) keys[j] = u;
+  }
+  __syncthreads();
+  const int k = min(a.top_p, a.cand_pow2);
+  {
+    auto get = [&](int j) -> uint64_t { return keys[j]; };
+    radix_select(get, a.cand_pow2, k, &st);
+    radix_collect(get, a.cand_pow2, k, &st, best);
+  }
+  for (int j = k + threadIdx.x; j < a.top_pow2; j += LSA_BLOCK) best[j] = 0;
+  __syncthreads();
+  bitonic_sort_desc(best, a.top_pow2);
+  for (int j = threadIdx.x; j < a.top_p; j += LSA_BLOCK) cand[j] = j < k ? key_column(u_to_key(best[j])) : -1;
+  __syncthreads();
+  const int width = a.top_k + a.window + a.sink;
+  const int32_t* tab = a.members + t * (int64_t)a.rows * a.cap;
+  const int len = expand_walk(cand, a.top_p, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k,
+                              a.lists + i * width, width, scan);
+  if (threadIdx.x == 0) a.lengths[i] = len;
+}
+
+// ------------------------------------------------------------------ index queries / centroids
+
+template <typename QT>
+__global__ void index_queries_kernel(const QT* q, int64_t B, int64_t T, int Hq, int Hkv, int D, int chunk,
+                                     float* out) {
+  const int64_t C = T / chunk;
+  const int64_t n = B * C * Hkv * D;
+  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (idx >= n) return;
+  const int d = (int)(idx % D);
+  const int g = (int)((idx / D) % Hkv);
+  const int64_t c = (idx / ((int64_t)D * Hkv)) % C;
+  const int64_t b = idx / ((int64_t)D * Hkv * C);
+  const int G = Hq / Hkv;
+  float acc = 0.0f;
+  for (int t = 0; t < chunk; ++t) {
+    const int64_t base = ((b * T + c * chunk + t) * Hq + (int64_t)g * G) * D + d;
+    for (int h = 0; h < G; ++h) acc += elem<QT>::load(q, base + (int64_t)h * D);
+  }
+  out[idx] = acc / (float)(chunk * G);
+}
+
+template <typename KT>
+__global__ __launch_bounds__(LSA_BLOCK) void centroids_kernel(const KT* keys, int64_t tokens, int64_t token_stride,
+                                                              int64_t batch_stride, int kv_heads, int D,
+                                                              const int32_t* members, int rows, int cap,
+                                                              int mode, float* out_f32, uint16_t* out_bf16) {
+  __shared__ float sums[512];
+  __shared__ float norm;
+  const int64_t bucket = blockIdx.x;
+  const int64_t table = bucket / rows;
+  const KT* kb = keys + (table / kv_heads) * batch_stride + (table % kv_heads) * (int64_t)D;
+  const int32_t* m = members + bucket * cap;
+  int count = 0;
+  for (int j = 0; j < cap; ++j) count += (m[j] >= 0 && m[j] < tokens) ? 1 : 0;
+  for (int d = threadIdx.x; d < D; d += LSA_BLOCK) {
+    float acc = 0.0f;
+    for (int j = 0; j < cap; ++j) {
+      const int32_t id = m[j];
+      if (id >= 0 && id < tokens) acc += elem<KT>::load(kb, (int64_t)id * token_stride + d);
+    }
+    sums[d] = acc;
+  }
+  __syncthreads();
+  if (mode == LSA_CENTROID_NORMALIZED && threadIdx.x == 0) {
+    double sq = 0.0;
+    for (int d = 0; d < D; ++d) sq += (double)sums[d] * (double)sums[d];
+    norm = fmaxf((float)sqrt(sq), 1e-12f);
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += LSA_BLOCK) {
+    float c;
+    if (mode == LSA_CENTROID_NORMALIZED) c = sums[d] / norm;
+    else c = count > 0 ? sums[d] / (float)count : 0.0f;
+    out_f32[bucket * D + d] = c;
+    if (out_bf16) out_bf16[bucket * D + d] = f32_to_bf16(c);
+  }
+}
+
+int check_tables(int32_t rows, int32_t cap, int64_t row_tables, int64_t group_tables) {
+  LSA_REQUIRE(rows >= 1, LSA_ERR_SHAPE, "bucket table needs >= 1 row, got %d", rows);
+  LSA_REQUIRE(cap >= 1, LSA_ERR_SHAPE, "bucket cap must be >= 1, got %d", cap);
+  LSA_REQUIRE(row_tables >= 0 && group_tables >= 0, LSA_ERR_SHAPE, "table strides must be >= 0");
+  return LSA_OK;
+}
+
+int check_dim(int32_t D) {
+  LSA_REQUIRE(D >= 16 && D <= 256 && is_pow2(D), LSA_ERR_SHAPE,
+              "index dim must be a power of two in [16, 256], got %d", D);
+  return LSA_OK;
+}
+
+int check_dtype(int dtype) {
+  LSA_REQUIRE(dtype == LSA_F32 || dtype == LSA_BF16 || dtype == LSA_F16, LSA_ERR_DTYPE, "unknown dtype %d", dtype);
+  return LSA_OK;
+}
+
+}  // namespace
+
+#define LSA_TRY(expr)            \
+  do {                           \
+    int rc_ = (expr);            \
+    if (rc_ != LSA_OK) return rc_; \
+  } while (0)
+
+extern "C" int lsa_visible_counts(const int32_t* positions, int64_t R, int32_t G, int32_t rows,
+                                  int32_t cluster_block_size, int32_t block_buckets, const int32_t* ends,
+                                  int64_t row_tables, int64_t group_tables, int32_t* counts, void* stream) {
+  LSA_REQUIRE(positions && counts, LSA_ERR_NULL, "lsa_visible_counts: positions/counts NULL");
+  LSA_REQUIRE(R >= 0 && G >= 1 && rows >= 0, LSA_ERR_SHAPE, "lsa_visible_counts: bad sizes");
+  LSA_REQUIRE(ends || (cluster_block_size >= 1 && block_buckets >= 0), LSA_ERR_SHAPE,
+              "lsa_visible_counts: cluster_block_size must be >= 1");
+  if (R * G == 0) return LSA_OK;
+  const int64_t n = R * G;
+  visible_counts_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream>>>(
+      positions, R, G, rows, cluster_block_size, block_buckets, ends, row_tables, group_tables, counts);
+  LSA_LAUNCHED("lsa_visible_counts");
+  return LSA_OK;
+}
+
+extern "C" int lsa_score_rows(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D,
+                              const void* centroids, int32_t N, int64_t row_tables, int64_t group_tables,
+                              int score_mode, float* scores, void* stream) {
+  LSA_REQUIRE(queries && centroids && scores, LSA_ERR_NULL, "lsa_score_rows: NULL pointer");
+  LSA_TRY(check_dtype(q_dtype));
+  LSA_TRY(check_dim(D));
+  LSA_REQUIRE(score_mode == LSA_SCORE_BF16 || score_mode == LSA_SCORE_F32, LSA_ERR_DTYPE, "bad score mode");
+  LSA_REQUIRE(R >= 0 && G >= 1 && N >= 0 && R * G <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_score_rows: bad sizes");
+  if (R * G == 0 || N == 0) return LSA_OK;
+  LSA_REQUIRE((N + 15) / 16 <= 65535, LSA_ERR_SHAPE, "lsa_score_rows: %d columns exceed the grid", N);
+  const dim3 grid((unsigned)(R * G), (unsigned)((N + 15) / 16));
+  const bool bf16 = score_mode == LSA_SCORE_BF16;
+  hipStream_t s = (hipStream_t)stream;
+  LSA_DISPATCH_QT(q_dtype, LSA_DISPATCH_SPAN(D / 16, {
+    if (bf16)
+      score_rows_kernel<QT, bf16_t, SPAN><<<grid, LSA_BLOCK, 0, s>>>((const QT*)queries, G,
+                                                                    (const bf16_t*)centroids, N, row_tables,
+                                                                    group_tables, true, scores);
+    else
+      score_rows_kernel<QT, float, SPAN><<<grid, LSA_BLOCK, 0, s>>>((const QT*)queries, G, (const float*)centroids,
+                                                                   N, row_tables, group_tables, false, scores);
+  }))
+  LSA_LAUNCHED("lsa_score_rows");
+  return LSA_OK;
+}
+
+extern "C" int lsa_pack_listing(const float* scores, const int32_t* counts, int64_t R, int32_t N, int64_t* keys,
+                                void* stream) {
+  LSA_REQUIRE(scores && counts && keys, LSA_ERR_NULL, "lsa_pack_listing: NULL pointer");
+  LSA_REQUIRE(R >= 0 && N >= 0, LSA_ERR_SHAPE, "lsa_pack_listing: bad sizes");
+  const int64_t n = R * N;
+  if (n == 0) return LSA_OK;
+  pack_listing_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream>>>(scores, counts, R,
+                                                                                               N, keys);
+  LSA_LAUNCHED("lsa_pack_listing");
+  return LSA_OK;
+}
+
+extern "C" int lsa_unpack_ids(const int64_t* keys, int64_t n, int32_t* ids, void* stream) {
+  LSA_REQUIRE(keys && ids, LSA_ERR_NULL, "lsa_unpack_ids: NULL pointer");
+  LSA_REQUIRE(n >= 0, LSA_ERR_SHAPE, "lsa_unpack_ids: bad size");
+  if (n == 0) return LSA_OK;
+  unpack_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream>>>(keys, n, ids);
+  LSA_LAUNCHED("lsa_unpack_ids");
+  return LSA_OK;
+}
+
+template <typename Src>
+static int launch_topk(Src src, int64_t R, int32_t W, int32_t k, int32_t k_out, int64_t* out, hipStream_t s) {
+  const int kp = next_pow2(k_out);
+  const bool lds_row = W <= kMaxLdsKeys;
+  const size_t shmem = sizeof(uint64_t) * ((size_t)kp + (lds_row ? (size_t)W : 0));
+  if (lds_row)
+    topk_kernel<Src, true><<<dim3((unsigned)R), LSA_BLOCK, shmem, s>>>(src, W, k, kp, k_out, out);
+  else
+    topk_kernel<Src, false><<<dim3((unsigned)R), LSA_BLOCK, shmem, s>>>(src, W, k, kp, k_out, out);
+  return LSA_OK;
+}
+
+extern "C" int lsa_topk_keys(const int64_t* keys, const int32_t* counts, int64_t R, int32_t W, int32_t k,
+                             int64_t* out, void* stream) {
+  LSA_REQUIRE(keys && out, LSA_ERR_NULL, "lsa_topk_keys: NULL pointer");
+  LSA_REQUIRE(R >= 0 && W >= 1 && k >= 1 && k <= W, LSA_ERR_SHAPE, "lsa_topk_keys: need 1 <= k <= W (k=%d W=%d)", k,
+              W);
+  LSA_REQUIRE(k <= kMaxLdsKeys, LSA_ERR_SHAPE, "lsa_topk_keys: k=%d exceeds %d", k, kMaxLdsKeys);
+  LSA_REQUIRE(R <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_topk_keys: too many rows");
+  if (R == 0) return LSA_OK;
+  launch_topk(KeySource{keys, counts, W}, R, W, k, k, out, (hipStream_t)stream);
+  LSA_LAUNCHED("lsa_topk_keys");
+  return LSA_OK;
+}
+
+extern "C" int lsa_select_topk_scores(const float* scores, const int32_t* lengths, int64_t R, int32_t N,
+                                      int32_t top_p, int64_t* out, void* stream) {
+  LSA_REQUIRE(scores && lengths && out, LSA_ERR_NULL, "lsa_select_topk_scores: NULL pointer");
+  LSA_REQUIRE(R >= 0 && N >= 1 && top_p >= 1, LSA_ERR_SHAPE, "lsa_select_topk_scores: bad sizes");
+  const int keep = top_p < N ? top_p : N;
+  LSA_REQUIRE(next_pow2(keep) <= kMaxLdsKeys, LSA_ERR_SHAPE, "lsa_select_topk_scores: top_p %d too large", top_p);
+  LSA_REQUIRE(R <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_select_topk_scores: too many rows");
+  if (R == 0) return LSA_OK;
+  launch_topk(ScoreSource{scores, lengths, N}, R, N, keep, next_pow2(keep), out, (hipStream_t)stream);
+  LSA_LAUNCHED("lsa_select_topk_scores");
+  return LSA_OK;
+}
+
+extern "C" int lsa_expand(const void* picks, int picks_are_keys, int64_t R, int32_t G, int32_t P,
+                          const int32_t* members, int32_t rows, int32_t cap, int64_t row_tables, int64_t group_tables,
+                          const int32_t* positions, int32_t window, int32_t sink, int32_t top_k, int32_t* lists,
+                          int32_t* lengths, void* stream) {
+  LSA_REQUIRE(picks && members && positions && lists && lengths, LSA_ERR_NULL, "lsa_expand: NULL pointer");
+  LSA_TRY(check_tables(rows, cap, row_tables, group_tables));
+  LSA_REQUIRE(R >= 0 && G >= 1 && P >= 0 && P <= 16384, LSA_ERR_SHAPE, "lsa_expand: bad sizes (P=%d)", P);
+  LSA_REQUIRE(window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE, "lsa_expand: window/sink/top_k must be >= 0");
+  LSA_REQUIRE(R * G <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_expand: too many rows");
+  if (R * G == 0) return LSA_OK;
+  const size_t shmem = sizeof(int32_t) * (size_t)(P > 0 ? P : 1);
+  hipStream_t s = (hipStream_t)stream;
+  if (picks_are_keys)
+    expand_kernel<true><<<dim3((unsigned)(R * G)), LSA_BLOCK, shmem, s>>>(picks, G, P, members, rows, cap, row_tables,
+                                                                        group_tables, positions, window, sink,
+                                                                        top_k, lists, lengths);
+  else
+    expand_kernel<false><<<dim3((unsigned)(R * G)), LSA_BLOCK, shmem, s>>>(picks, G, P, members, rows, cap,
+                                                                         row_tables, group_tables, positions, window,
+                                                                         sink, top_k, lists, lengths);
+  LSA_LAUNCHED("lsa_expand");
+  return LSA_OK;
+}
+
+static int flat_picks(int32_t top_p, int32_t rows) { return top_p < rows ? top_p : rows; }
+
+extern "C" size_t lsa_select_flat_scratch_bytes(int64_t R, int32_t G, int32_t top_p, int32_t N, int32_t splits) {
+  if (splits <= 1 || R <= 0 || G <= 0) return 0;
+  const int64_t K = flat_picks(top_p, N);
+  return (size_t)(R * G) * (size_t)splits * (size_t)K * sizeof(uint64_t);
+}
+
+extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D,
+                               const void* centroids, const int32_t* members, const int32_t* ends, int32_t rows,
+                               int32_t cap, int64_t row_tables, int64_t group_tables, int score_mode,
+                               const int32_t* positions, int32_t cluster_block_size, int32_t block_buckets,
+                               int32_t top_p, int32_t window, int32_t sink, int32_t top_k, int32_t splits,
+                               int32_t* counters, void* scratch, size_t scratch_bytes, int32_t* lists,
+                               int32_t* lengths, void* stream) {
+  LSA_REQUIRE(queries && centroids && members && positions && lists && lengths, LSA_ERR_NULL,
+              "lsa_select_flat: NULL pointer");
+  LSA_TRY(check_dtype(q_dtype));
+  LSA_TRY(check_dim(D));
+  LSA_TRY(check_tables(rows, cap, row_tables, group_tables));
+  LSA_REQUIRE(score_mode == LSA_SCORE_BF16 || score_mode == LSA_SCORE_F32, LSA_ERR_DTYPE, "bad score mode");
+  LSA_REQUIRE(R >= 0 && G >= 1 && R * G <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_select_flat: bad sizes");
+  LSA_REQUIRE(top_p >= 1 && window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE,
+              "lsa_select_flat: top_p >= 1, window/sink/top_k >= 0");
+  LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "lsa_select_flat: cluster_block_size must be >= 1");
+  LSA_REQUIRE(splits >= 1 && splits <= 256, LSA_ERR_SHAPE, "lsa_select_flat: splits in [1, 256], got %d", splits);
+  const int K = flat_picks(top_p, rows);
+  const int cs = (rows + splits - 1) / splits;
+  const int kp = next_pow2(K);
+  const int keys_cap = cs > splits * K ? cs : splits * K;
+  LSA_REQUIRE(cs <= kMaxLdsKeys && splits * K <= kMaxLdsKeys && kp <= kMaxLdsKeys, LSA_ERR_SHAPE,
+              "lsa_select_flat: %d columns per split / %d merged keys exceed %d", cs, splits * K, kMaxLdsKeys);
+  const size_t need = lsa_select_flat_scratch_bytes(R, G, top_p, rows, splits);
+  LSA_REQUIRE(need == 0 || (scratch && counters && scratch_bytes >= need), LSA_ERR_WORKSPACE,
+              "lsa_select_flat: counters/scratch missing or scratch %zu < %zu bytes", scratch_bytes, need);
+  if (R * G == 0) return LSA_OK;
+  FlatArgs a;
+  a.R = R; a.G = G; a.rows = rows; a.cap = cap; a.row_tables = row_tables; a.group_tables = group_tables;
+  a.centroids = centroids; a.members = members; a.ends = ends; a.positions = positions;
+  a.cluster_block = cluster_block_size; a.block_buckets = block_buckets;
+  a.K = K; a.kp = kp; a.window = window; a.sink = sink; a.top_k = top_k;
+  a.S = splits; a.cs = cs; a.keys_cap = keys_cap;
+  a.ws_count = counters;
+  a.ws_keys = need ? (uint64_t*)scratch : nullptr;
+  a.lists = lists; a.lengths = lengths;
+  const size_t shmem = sizeof(uint64_t) * ((size_t)keys_cap + kp);
+  const dim3 grid((unsigned)(R * G), (unsigned)splits);
+  const bool bf16 = score_mode == LSA_SCORE_BF16;
+  hipStream_t s = (hipStream_t)stream;
+  LSA_DISPATCH_QT(q_dtype, LSA_DISPATCH_SPAN(D / 16, {
+    if (bf16) select_flat_kernel<QT, bf16_t, SPAN><<<grid, LSA_BLOCK, shmem, s>>>((const QT*)queries, true, a);
+    else select_flat_kernel<QT, float, SPAN><<<grid, LSA_BLOCK, shmem, s>>>((const QT*)queries, false, a);
+  }))
+  LSA_LAUNCHED("lsa_select_flat");
+  return LSA_OK;
+}
+
+extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D,
+                               const void* node_centroids, const int32_t* children, int32_t n_nodes,
+                               int32_t node_size, const void* centroids, const int32_t* members, const int32_t* ends,
+                               int32_t rows, int32_t cap, int64_t row_tables, int64_t group_tables, int score_mode,
+                               const int32_t* positions, int32_t cluster_block_size, int32_t block_buckets,
+                               int32_t covered, int32_t beam_width, int32_t top_p, int32_t window, int32_t sink,
+                               int32_t top_k, int32_t* lists, int32_t* lengths, void* stream) {
+  LSA_REQUIRE(queries && node_centroids && children && centroids && members && positions && lists && lengths,
+              LSA_ERR_NULL, "lsa_select_tree: NULL pointer");
+  LSA_TRY(check_dtype(q_dtype));
+  LSA_TRY(check_dim(D));
+  LSA_TRY(check_tables(rows, cap, row_tables, group_tables));
+  LSA_REQUIRE(score_mode == LSA_SCORE_BF16 || score_mode == LSA_SCORE_F32, LSA_ERR_DTYPE, "bad score mode");
+  LSA_REQUIRE(R >= 0 && G >= 1 && R * G <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_select_tree: bad sizes");
+  LSA_REQUIRE(n_nodes >= 1 && node_size >= 1 && beam_width >= 1 && top_p >= 1 && covered >= 0, LSA_ERR_SHAPE,
+              "lsa_select_tree: n_nodes, node_size, beam_width, top_p >= 1");
+  LSA_REQUIRE(window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE, "lsa_select_tree: window/sink/top_k >= 0");
+  LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "lsa_select_tree: cluster_block_size must be >= 1");
+  const int beam = beam_width < n_nodes ? beam_width : n_nodes;
+  const int64_t max_fresh = rows - covered > 0 ? rows - covered : 0;
+  const int64_t cand_cap = (int64_t)beam * node_size + max_fresh;
+  LSA_REQUIRE(n_nodes <= kMaxLdsKeys && cand_cap <= kMaxLdsKeys && top_p <= kMaxLdsKeys, LSA_ERR_SHAPE,
+              "lsa_select_tree: %d nodes / %lld candidates exceed %d", n_nodes, (long long)cand_cap, kMaxLdsKeys);
+  if (R * G == 0) return LSA_OK;
+  TreeArgs a;
+  a.R = R; a.G = G; a.node_centroids = node_centroids; a.children = children; a.n_nodes = n_nodes;
+  a.node_size = node_size; a.centroids = centroids; a.members = members; a.ends = ends; a.rows = rows; a.cap = cap;
+  a.row_tables = row_tables; a.group_tables = group_tables; a.positions = positions;
+  a.cluster_block = cluster_block_size; a.block_buckets = block_buckets; a.covered = covered;
+  a.beam = beam_width; a.top_p = top_p;
+  a.nodes_pow2 = next_pow2(n_nodes); a.beam_pow2 = next_pow2(beam); a.cand_cap = (int)cand_cap;
+  a.cand_pow2 = next_pow2((int)(cand_cap > 0 ? cand_cap : 1)); a.top_pow2 = next_pow2(top_p);
+  a.window = window; a.sink = sink; a.top_k = top_k; a.lists = lists; a.lengths = lengths;
+  const int keys_slots = a.nodes_pow2 > a.cand_pow2 ? a.nodes_pow2 : a.cand_pow2;
+  const int best_slots = a.beam_pow2 > a.top_pow2 ? a.beam_pow2 : a.top_pow2;
+  const int cand_slots = a.cand_pow2 > top_p ? a.cand_pow2 : top_p;
+  const size_t shmem = sizeof(uint64_t) * (size_t)(keys_slots + best_slots) + sizeof(int32_t) * (size_t)cand_slots;
+  LSA_REQUIRE(shmem <= 65536, LSA_ERR_SHAPE, "lsa_select_tree: %zu bytes of LDS needed", shmem);
+  const bool bf16 = score_mode == LSA_SCORE_BF16;
+  hipStream_t s = (hipStream_t)stream;
+  LSA_DISPATCH_QT(q_dtype, LSA_DISPATCH_SPAN(D / 16, {
+    if (bf16) select_tree_kernel<QT, bf16_t, SPAN><<<dim3((unsigned)(R * G)), LSA_BLOCK, shmem, s>>>((const QT*)queries,
+                                                                                                   true, a);
+    else select_tree_kernel<QT, float, SPAN><<<dim3((unsigned)(R * G)), LSA_BLOCK, shmem, s>>>((const QT*)queries,
+                                                                                             false, a);
+  }))
+  LSA_LAUNCHED("lsa_select_tree");
+  return LSA_OK;
+}
+
+extern "C" int lsa_index_queries(const void* q, int q_dtype, int64_t B, int64_t T, int32_t Hq, int32_t Hkv, int32_t D,
+                                 int32_t chunk, float* out, void* stream) {
+  LSA_REQUIRE(q && out, LSA_ERR_NULL, "lsa_index_queries: NULL pointer");
+  LSA_TRY(check_dtype(q_dtype));
+  LSA_REQUIRE(B >= 0 && T >= 0 && Hq >= 1 && Hkv >= 1 && D >= 1 && chunk >= 1, LSA_ERR_SHAPE,
+              "lsa_index_queries: bad sizes");
+  LSA_REQUIRE(Hq % Hkv == 0, LSA_ERR_SHAPE, "lsa_index_queries: Hq %d not a multiple of Hkv %d", Hq, Hkv);
+  const int64_t n = B * (T / chunk) * Hkv * D;
+  if (n == 0) return LSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  LSA_DISPATCH_QT(q_dtype, { index_queries_kernel<QT><<<grid, 256, 0, s>>>((const QT*)q, B, T, Hq, Hkv, D, chunk, out); })
+  LSA_LAUNCHED("lsa_index_queries");
+  return LSA_OK;
+}
+
+extern "C" int lsa_bucket_centroids(const void* keys, int k_dtype, int64_t tokens, int64_t token_stride,
+                                    int64_t batch_stride,
+                                    int32_t kv_heads, int32_t D, const int32_t* members, int64_t n_tables,
+                                    int32_t rows, int32_t cap, int centroid_mode, float* out_f32, uint16_t* out_bf16,
+                                    void* stream) {
+  LSA_REQUIRE(keys && members && out_f32, LSA_ERR_NULL, "lsa_bucket_centroids: NULL pointer");
+  LSA_TRY(check_dtype(k_dtype));
+  LSA_REQUIRE(D >= 1 && D <= 512 && kv_heads >= 1 && n_tables >= 0 && rows >= 0 && cap >= 1 && tokens >= 0,
+              LSA_ERR_SHAPE,
+              "lsa_bucket_centroids: bad sizes");
+  LSA_REQUIRE(centroid_mode == LSA_CENTROID_MEAN || centroid_mode == LSA_CENTROID_NORMALIZED, LSA_ERR_SHAPE,
+              "lsa_bucket_centroids: bad centroid mode");
+  const int64_t n = n_tables * rows;
+  if (n == 0) return LSA_OK;
+  LSA_REQUIRE(n <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_bucket_centroids: too many buckets");
+  hipStream_t s = (hipStream_t)stream;
+  LSA_DISPATCH_QT(k_dtype, {
+    centroids_kernel<QT><<<dim3((unsigned)n), LSA_BLOCK, 0, s>>>((const QT*)keys, tokens, token_stride, batch_stride,
+                                                                kv_heads,
+                                                                D, members, rows, cap, centroid_mode, out_f32,
+                                                                out_bf16);
+  })
+  LSA_LAUNCHED("lsa_bucket_centroids");
+  return LSA_OK;
+}

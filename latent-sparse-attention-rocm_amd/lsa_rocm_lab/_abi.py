@@ -1,0 +1,171 @@
+"""ctypes binding of liblsa_rocm.so (the C ABI in include/lsa_rocm.h).
+
+The library is loaded after ``torch`` so that it shares torch's HIP runtime (one
+device context, one set of streams). Every call passes raw device pointers and
+``torch.cuda.current_stream().cuda_stream``; nothing here computes on the host.
+If the library is missing the first call raises ``ExtensionMissing`` - there is
+no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import threading
+
+import torch
+
+LIB_PATH = pathlib.Path(os.environ.get("LSA_ROCM_LIB", pathlib.Path(__file__).parent / "_lib" / "liblsa_rocm.so"))
+
+LSA_F32, LSA_BF16, LSA_F16 = 0, 1, 2
+SCORE_BF16, SCORE_F32 = 0, 1
+CENTROID_MEAN, CENTROID_NORMALIZED = 0, 1
+
+_ERRORS = {
+    -1: "LSA_ERR_NULL",
+    -2: "LSA_ERR_SHAPE",
+    -3: "LSA_ERR_DTYPE",
+    -4: "LSA_ERR_POW2",
+    -5: "LSA_ERR_WORKSPACE",
+    -6: "LSA_ERR_LAUNCH",
+    -7: "LSA_ERR_ALIGN",
+}
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/lsa_rocm.h
+SIGNATURES = {
+    "lsa_abi_version": (_int, []),
+    "lsa_last_error": (ctypes.c_char_p, []),
+    "lsa_visible_counts": (_int, [_p, _i64, _i32, _i32, _i32, _i32, _p, _i64, _i64, _p, _p]),
+    "lsa_score_rows": (_int, [_p, _int, _i64, _i32, _i32, _p, _i32, _i64, _i64, _int, _p, _p]),
+    "lsa_pack_listing": (_int, [_p, _p, _i64, _i32, _p, _p]),
+    "lsa_topk_keys": (_int, [_p, _p, _i64, _i32, _i32, _p, _p]),
+    "lsa_select_topk_scores": (_int, [_p, _p, _i64, _i32, _i32, _p, _p]),
+    "lsa_unpack_ids": (_int, [_p, _i64, _p, _p]),
+    "lsa_expand": (_int, [_p, _int, _i64, _i32, _i32, _p, _i32, _i32, _i64, _i64, _p, _i32, _i32, _i32, _p, _p, _p]),
+    "lsa_select_flat_scratch_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
+    "lsa_select_flat": (_int, [_p, _int, _i64, _i32, _i32, _p, _p, _p, _i32, _i32, _i64, _i64, _int, _p, _i32, _i32,
+                               _i32, _i32, _i32, _i32, _i32, _p, _p, _sz, _p, _p, _p]),
+    "lsa_select_tree": (_int, [_p, _int, _i64, _i32, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i32, _i32, _i64, _i64,
+                               _int, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
+    "lsa_index_queries": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p]),
+    "lsa_bucket_centroids": (_int, [_p, _int, _i64, _i64, _i64, _i32, _i32, _p, _i64, _i32, _i32, _int, _p, _p, _p]),
+    "lsa_read_scratch_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
+    "lsa_read": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _i32, _int, _f32, _int, _i32,
+                        _p, _p, _sz, _p, _p]),
+    "lsa_read_chunked": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _i32, _i32, _f32, _p,
+                                _p]),
+}
+
+
+class ExtensionMissing(RuntimeError):
+    """liblsa_rocm.so is not built or cannot be loaded: the HIP path cannot run."""
+
+
+class LsaError(RuntimeError):
+    """A launch-level failure reported by the C ABI."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{_ERRORS.get(code, code)}: {message}")
+        self.code = code
+
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads the library once (after torch) and binds every signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.is_file():
+                raise ExtensionMissing(
+                    f"{LIB_PATH} is missing - build it with __graft_entry__.build() "
+                    "(hipcc --offload-arch=gfx950); the select+read path has no CPU fallback")
+            try:
+                lib = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_LOCAL)
+            except OSError as exc:
+                raise ExtensionMissing(f"cannot load {LIB_PATH}: {exc}") from exc
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def call(name: str, *args):
+    """Calls an entry point; a nonzero status raises (ValueError for argument errors)."""
+    rc = getattr(load(), name)(*args)
+    if rc != 0:
+        msg = load().lsa_last_error().decode(errors="replace")
+        if rc in (-1, -2, -3, -4, -7):
+            raise ValueError(f"{name}: {_ERRORS.get(rc, rc)}: {msg}")
+        raise LsaError(rc, f"{name}: {msg}")
+    return rc
+
+
+def size(name: str, *args) -> int:
+    return int(getattr(load(), name)(*args))
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream(device: torch.device | None = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return LSA_F32
+    if dtype == torch.bfloat16:
+        return LSA_BF16
+    if dtype == torch.float16:
+        return LSA_F16
+    raise ValueError(f"unsupported dtype {dtype} (fp32, bf16, fp16)")
+
+
+class Workspace:
+    """Scratch per (device, stream, purpose), grown on demand; kernels fully write the
+    part they read, so it needs no initialisation. Calls sharing it are stream-ordered."""
+
+    _buffers: dict[tuple, torch.Tensor] = {}
+
+    @classmethod
+    def get(cls, device: torch.device, purpose: str, nbytes: int) -> torch.Tensor | None:
+        if nbytes <= 0:
+            return None
+        key = (device.index, stream(device), purpose)
+        buf = cls._buffers.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            cls._buffers[key] = buf
+        return buf
+
+
+class Counters:
+    """Split-arrival counters per (device, stream): int32 that every kernel finds zero at
+    launch and leaves zero, so the buffer is zero-filled only when it is (re)allocated."""
+
+    _buffers: dict[tuple, torch.Tensor] = {}
+
+    @classmethod
+    def get(cls, device: torch.device, n: int) -> torch.Tensor:
+        key = (device.index, stream(device))
+        buf = cls._buffers.get(key)
+        if buf is None or buf.numel() < n:
+            buf = torch.zeros(max(n, 4096), dtype=torch.int32, device=device)
+            cls._buffers[key] = buf
+        return buf

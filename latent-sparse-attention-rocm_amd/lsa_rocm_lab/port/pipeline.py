@@ -1,0 +1,480 @@
+"""The LSA select+read call surface on MI355X (reference src/lsa_rocm_lab/port/pipeline.py).
+
+Same names, arguments and errors as the reference's composition layer; every stage is
+a HIP kernel in liblsa_rocm.so:
+
+* ``visible_counts`` (pipeline.py:184-186), ``_production_scores`` (:217-232),
+  ``best_first_keys`` (:189-214), ``flat_select_reference`` (:248-271) - the unfused
+  chain: score kernel -> listing pack -> radix top-k -> unpack -> expansion walk;
+* ``flat_select`` (:274-316) with the ``LSA_SELECT_IMPL`` switch: ``fused`` is ONE
+  kernel from the index queries to the read lists (score + top-k + expansion, split
+  over workgroups when there are few rows); ``fused_unpack`` keeps the listing +
+  top-k and expands from the keys; ``reference`` is the unfused chain;
+* ``tree_select`` (:319-337), ``lsa_read`` (:373-375), ``position_buckets`` (:378-403);
+* ``dense_read`` (:340-370) stays torch SDPA - it is the dense comparator.
+
+Per-kv-head selection (the benchmark geometry) extends the shapes: index queries
+[R, G, D] against tables with a leading group axis [G, rows, ...] (one table per
+kv-head) or [R, G, rows, ...] (one per sequence and kv-head) give lists [R, G, W] and
+lengths [R, G]. ``Buckets.ends`` (optional) carries each bucket's exclusive span end
+for tables whose buckets are not the reference's fixed blocks; visibility is then the
+buckets ending at or before ``position + 1``.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+from dataclasses import dataclass, field
+
+import torch
+import torch.nn.functional as F
+
+from lsa_rocm_lab import _abi
+from lsa_rocm_lab.port import keys as keys_mod
+
+
+@dataclass(frozen=True)
+class PortConfig:
+    """The design's knobs (reference pipeline.py:32-54), same names and defaults."""
+
+    cluster_block_size: int = 512
+    pool_size: int = 4
+    bucket_size: int = 8
+    bucket_cap: int = 16
+    top_p: int = 1024
+    top_k: int = 4096
+    window_size: int = 512
+    sink_size: int = 4
+    node_bucket_size: int = 4
+    top_level: int = 3
+    node_cluster_block_size: int = 64
+    beam_width: int = 64
+    start_nodes: int | None = None
+
+    @property
+    def block_bucket_count(self) -> int:
+        return self.cluster_block_size // self.bucket_size
+
+
+@dataclass
+class Buckets:
+    """A cache's bucket tables on the GPU (reference pipeline.py:57-68) plus optional
+    span ends. Shapes: [rows, ...] (one table), [G, rows, ...] or [R, G, rows, ...]."""
+
+    centroids: torch.Tensor  # [..., rows, index_dim] bf16 - what production scoring reads
+    members: torch.Tensor  # [..., rows, bucket_cap] int32, absolute positions, -1 padded
+    sizes: torch.Tensor  # [..., rows] int32
+    centroids_f32: torch.Tensor | None = None  # [..., rows, index_dim] fp32 - fp32 scoring
+    ends: torch.Tensor | None = None  # [..., rows] int32 exclusive span end, nondecreasing
+
+    @property
+    def rows(self) -> int:
+        return self.centroids.shape[-2]
+
+
+@dataclass
+class NodeLevel:
+    """One node level over the buckets (reference pipeline.py:119-125)."""
+
+    centroids: torch.Tensor  # [..., N, index_dim] fp32
+    children: torch.Tensor  # [..., N, node_bucket_size] bucket rows
+    key_sums: torch.Tensor | None = None
+    centroids_bf16: torch.Tensor | None = None
+
+
+@dataclass
+class Hierarchy:
+    """Node levels over a cache's buckets (reference pipeline.py:128-133)."""
+
+    levels: list[NodeLevel] = field(default_factory=list)
+    bucket_key_sums: torch.Tensor | None = None
+
+
+# ----------------------------------------------------------------------------- helpers
+
+
+def _on_device(what: str, *tensors: torch.Tensor | None) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError(f"{what} is a ROCm kernel, got device {t.device}")
+        device = t.device
+    return device
+
+
+class _Layout:
+    """How query rows and groups map onto a stack of bucket tables."""
+
+    def __init__(self, index_queries: torch.Tensor, table: torch.Tensor):
+        if index_queries.dim() == 2:
+            self.R, self.D = index_queries.shape
+            self.G = 1
+            self.grouped = False
+        elif index_queries.dim() == 3:
+            self.R, self.G, self.D = index_queries.shape
+            self.grouped = True
+        else:
+            raise ValueError(f"index queries must be [R, d] or [R, G, D], got {tuple(index_queries.shape)}")
+        lead = table.dim() - 2
+        if lead == 0:
+            self.row_tables, self.group_tables = 0, 0
+        elif lead == 1:
+            if table.shape[0] != self.G:
+                raise ValueError(f"{table.shape[0]} tables for {self.G} groups")
+            self.row_tables, self.group_tables = 0, 1
+        elif lead == 2:
+            if tuple(table.shape[:2]) != (self.R, self.G):
+                raise ValueError(f"tables {tuple(table.shape[:2])} for rows x groups {(self.R, self.G)}")
+            self.row_tables, self.group_tables = self.G, 1
+        else:
+            raise ValueError(f"bucket tables must have at most two leading axes, got {tuple(table.shape)}")
+        self.rows = table.shape[-2]
+
+    def out_shape(self, *tail: int) -> tuple[int, ...]:
+        return (self.R, self.G, *tail) if self.grouped else (self.R, *tail)
+
+
+def _positions32(positions: torch.Tensor, device) -> torch.Tensor:
+    p = positions.to(device=device)
+    return (p if p.dtype == torch.int32 else p.to(torch.int32)).contiguous()
+
+
+def _score_table(buckets: Buckets, score_dtype: str) -> tuple[torch.Tensor, int]:
+    if score_dtype == "fp32":
+        if buckets.centroids_f32 is None:
+            raise ValueError("fp32 scoring needs buckets.centroids_f32")
+        return buckets.centroids_f32.float().contiguous(), _abi.SCORE_F32
+    if score_dtype != "bf16":
+        raise ValueError(f"score_dtype must be bf16|fp32, got {score_dtype!r}")
+    return buckets.centroids.to(torch.bfloat16).contiguous(), _abi.SCORE_BF16
+
+
+def _ends(buckets: Buckets) -> torch.Tensor | None:
+    return None if buckets.ends is None else buckets.ends.to(torch.int32).contiguous()
+
+
+def _queries(index_queries: torch.Tensor) -> torch.Tensor:
+    if index_queries.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        index_queries = index_queries.float()
+    return index_queries.contiguous()
+
+
+# ----------------------------------------------------------------------------- selection
+
+
+def visible_counts(positions: torch.Tensor, buckets: Buckets, config: PortConfig,
+                   groups: int | None = None) -> torch.Tensor:
+    """Buckets each query sees - the closed blocks before its own (reference pipeline.py:184-186).
+
+    With ``buckets.ends`` the buckets whose span ends at or before ``position + 1``.
+    Returns [R] int32, or [R, G] for per-group tables.
+    """
+    device = _on_device("visible_counts", buckets.centroids)
+    pos = _positions32(positions, device)
+    R = pos.shape[0]
+    lead = buckets.centroids.dim() - 2
+    G = groups or (buckets.centroids.shape[-3] if lead >= 1 else 1)
+    row_tables, group_tables = (0, 0) if lead == 0 else ((0, 1) if lead == 1 else (G, 1))
+    counts = torch.empty(R * G, dtype=torch.int32, device=device)
+    ends = _ends(buckets)
+    _abi.call("lsa_visible_counts", pos.data_ptr(), R, G, buckets.rows, config.cluster_block_size,
+              config.block_bucket_count, _abi.ptr(ends), row_tables, group_tables, counts.data_ptr(),
+              _abi.stream(device))
+    return counts.view(R, G) if (lead or G > 1) else counts
+
+
+def best_first_keys(keys: torch.Tensor, top_p: int, counts: torch.Tensor | None = None) -> torch.Tensor:
+    """The best ``top_p`` packed keys per row, best first (reference pipeline.py:189-214).
+
+    A radix select plus bitonic sort per row on the GPU; keys are unique per column, so
+    the result is exactly ``torch.sort(keys, descending=True).values[:, :top_p]``.
+    ``counts`` masks slots at or past each row's count to EMPTY first.
+    """
+    _on_device("best_first_keys", keys)
+    keys = keys.contiguous()
+    rows, width = keys.shape
+    k = min(top_p, width)
+    out = torch.empty(rows, k, dtype=torch.int64, device=keys.device)
+    if rows == 0 or k == 0:
+        return out
+    cnt = None if counts is None else counts.to(device=keys.device, dtype=torch.int32).reshape(rows).contiguous()
+    _abi.call("lsa_topk_keys", keys.data_ptr(), _abi.ptr(cnt), rows, width, k, out.data_ptr(),
+              _abi.stream(keys.device))
+    return out
+
+
+def _production_scores(index_queries, positions, buckets, config, score_dtype):
+    """The canonical scoring both select implementations share (reference pipeline.py:217-232).
+
+    fp32 scores = the index queries (rounded to bf16 for ``score_dtype="bf16"``) against
+    the bf16 centroids (or fp32 against ``centroids_f32``), products and partial sums
+    in fp64 in a fixed order, one rounding to fp32.
+    """
+    if positions.shape[0] != index_queries.shape[0]:
+        raise ValueError(
+            f"a position a query: {index_queries.shape[0]} queries, {positions.shape[0]} positions"
+        )
+    device = _on_device("_production_scores", index_queries, buckets.centroids)
+    layout = _Layout(index_queries, buckets.centroids)
+    table, mode = _score_table(buckets, score_dtype)
+    q = _queries(index_queries)
+    counts = visible_counts(positions, buckets, config, layout.G)
+    scores = torch.empty(layout.out_shape(layout.rows), dtype=torch.float32, device=device)
+    _abi.call("lsa_score_rows", q.data_ptr(), _abi.dtype_code(q.dtype), layout.R, layout.G, layout.D,
+              table.data_ptr(), layout.rows, layout.row_tables, layout.group_tables, mode, scores.data_ptr(),
+              _abi.stream(device))
+    return scores, counts
+
+
+def _mask_for(scores: torch.Tensor, config: PortConfig, listed: torch.Tensor) -> torch.Tensor | None:
+    """Listing counts for ``best_first_keys`` - None on the whole path (reference pipeline.py:235-245)."""
+    return None if scores.shape[-1] <= keys_mod.WHOLE * config.top_p else listed
+
+
+def _expand(picks: torch.Tensor, picks_are_keys: bool, layout: _Layout, members: torch.Tensor,
+            positions: torch.Tensor, window: int, sink: int, top_k: int):
+    device = picks.device
+    picks = picks.contiguous()
+    members = members.to(device=device, dtype=torch.int32).contiguous()
+    P = picks.shape[-1]
+    width = top_k + window + sink
+    lists = torch.empty(layout.out_shape(width), dtype=torch.int32, device=device)
+    lengths = torch.empty(layout.out_shape(), dtype=torch.int32, device=device)
+    _abi.call("lsa_expand", picks.data_ptr(), 1 if picks_are_keys else 0, layout.R, layout.G, P,
+              members.data_ptr(), members.shape[-2], members.shape[-1], layout.row_tables, layout.group_tables,
+              positions.data_ptr(), window, sink, top_k, lists.data_ptr(), lengths.data_ptr(), _abi.stream(device))
+    return lists, lengths
+
+
+def flat_select_reference(
+    index_queries: torch.Tensor,
+    positions: torch.Tensor,
+    buckets: Buckets,
+    config: PortConfig,
+    top_k: int | None = None,
+    score_dtype: str = "bf16",
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """The unfused select chain (reference pipeline.py:248-271): scores, the whole-path
+    listing, best-first keys, unpack, rank-order expansion - one HIP kernel each."""
+    top_k = config.top_k if top_k is None else top_k
+    scores, counts = _production_scores(index_queries, positions, buckets, config, score_dtype)
+    layout = _Layout(index_queries, buckets.centroids)
+    flat_scores = scores.reshape(-1, layout.rows)
+    keys, listed = keys_mod.listed(flat_scores, counts.reshape(-1))
+    picked = keys_mod.unpack_ids(best_first_keys(keys, config.top_p, counts=_mask_for(flat_scores, config, listed)))
+    pos = _positions32(positions, scores.device)
+    return _expand(picked, False, layout, buckets.members, pos, config.window_size, config.sink_size, top_k)
+
+
+def _select_splits(R: int, G: int, rows: int, top_p: int) -> int:
+    """Workgroups per (row, group) of the fused select: split the columns when there are
+    too few rows to fill the GPU (decode), keep >= 64 columns per split."""
+    env = os.environ.get("LSA_SELECT_SPLITS")
+    k = min(top_p, rows)
+    cap = max(1, min(4096 // max(k, 1), 256))
+    if env:
+        return max(1, min(int(env), cap))
+    units = R * G
+    if units >= 256:
+        return 1
+    s = min(max(1, 512 // units), max(1, rows // 64), cap)
+    while s > 1 and math.ceil(rows / s) > 4096:
+        s -= 1
+    return max(1, s)
+
+
+def _fused_select(index_queries, positions, buckets, config, top_k, score_dtype):
+    device = _on_device("flat_select", index_queries, buckets.centroids, buckets.members)
+    if positions.shape[0] != index_queries.shape[0]:
+        raise ValueError(
+            f"a position a query: {index_queries.shape[0]} queries, {positions.shape[0]} positions"
+        )
+    layout = _Layout(index_queries, buckets.centroids)
+    table, mode = _score_table(buckets, score_dtype)
+    q = _queries(index_queries)
+    members = buckets.members.to(device=device, dtype=torch.int32).contiguous()
+    ends = _ends(buckets)
+    pos = _positions32(positions, device)
+    splits = _select_splits(layout.R, layout.G, layout.rows, config.top_p)
+    width = top_k + config.window_size + config.sink_size
+    lists = torch.empty(layout.out_shape(width), dtype=torch.int32, device=device)
+    lengths = torch.empty(layout.out_shape(), dtype=torch.int32, device=device)
+    nbytes = _abi.size("lsa_select_flat_scratch_bytes", layout.R, layout.G, config.top_p, layout.rows, splits)
+    ws = _abi.Workspace.get(device, "select", nbytes)
+    counters = _abi.Counters.get(device, layout.R * layout.G) if nbytes else None
+    _abi.call("lsa_select_flat", q.data_ptr(), _abi.dtype_code(q.dtype), layout.R, layout.G, layout.D,
+              table.data_ptr(), members.data_ptr(), _abi.ptr(ends), layout.rows, members.shape[-1],
+              layout.row_tables, layout.group_tables, mode, pos.data_ptr(), config.cluster_block_size,
+              config.block_bucket_count, config.top_p, config.window_size, config.sink_size, top_k, splits,
+              _abi.ptr(counters), _abi.ptr(ws), nbytes, lists.data_ptr(), lengths.data_ptr(), _abi.stream(device))
+    return lists, lengths
+
+
+def flat_select(
+    index_queries: torch.Tensor,
+    positions: torch.Tensor,
+    buckets: Buckets,
+    config: PortConfig,
+    top_k: int | None = None,
+    score_dtype: str = "bf16",
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Select each query's keys - the production composition, implementation-switched.
+
+    ``LSA_SELECT_IMPL`` picks the implementation (default ``reference``):
+    ``reference`` is the unfused chain (``flat_select_reference``); ``fused`` is one HIP
+    kernel from the index queries to the read lists (canonical score, packed-key top-k,
+    rank-order expansion); ``fused_unpack`` keeps the listing and best-first top-k and
+    expands from the keys. All three produce byte-identical lists and lengths; unknown
+    values fail loudly.
+    """
+    impl = os.environ.get("LSA_SELECT_IMPL", "reference")
+    if impl not in ("reference", "fused", "fused_unpack"):
+        raise ValueError(
+            f"LSA_SELECT_IMPL must be reference|fused|fused_unpack, got {impl!r}"
+        )
+    if impl == "reference":
+        return flat_select_reference(index_queries, positions, buckets, config, top_k, score_dtype)
+    top_k = config.top_k if top_k is None else top_k
+    if impl == "fused":
+        return _fused_select(index_queries, positions, buckets, config, top_k, score_dtype)
+    if impl == "fused_unpack":
+        scores, counts = _production_scores(index_queries, positions, buckets, config, score_dtype)
+        layout = _Layout(index_queries, buckets.centroids)
+        flat_scores = scores.reshape(-1, layout.rows)
+        keys, listed = keys_mod.listed(flat_scores, counts.reshape(-1))
+        ordered = best_first_keys(keys, config.top_p, counts=_mask_for(flat_scores, config, listed))
+        pos = _positions32(positions, scores.device)
+        return _expand(ordered, True, layout, buckets.members, pos, config.window_size, config.sink_size, top_k)
+    raise AssertionError(f"unreachable impl {impl!r}")
+
+
+def tree_select(
+    index_queries: torch.Tensor,
+    positions: torch.Tensor,
+    buckets: Buckets,
+    hierarchy: Hierarchy,
+    config: PortConfig,
+    top_k: int | None = None,
+    score_dtype: str = "fp32",
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Select each query's keys by a beam down a one-level node tree (reference pipeline.py:319-337).
+
+    See ``_tree.tree_select_batched``.
+    """
+    from lsa_rocm_lab.port._tree import tree_select_batched
+
+    return tree_select_batched(index_queries, positions, buckets, hierarchy, config, top_k, score_dtype)
+
+
+# ----------------------------------------------------------------------------- reading
+
+
+def dense_read(q, k, v, scale):
+    """The dense causal baseline - torch SDPA (reference pipeline.py:340-370), the comparator.
+
+    Query rows are the tail ``q_len`` positions of the ``kv_len`` cache: the square case
+    keeps the fused causal flag, one row attends the whole cache unmasked, a chunk gets
+    an explicit bottom-right-aligned causal mask (never top-left ``is_causal``).
+    """
+    heads_q, heads_kv = q.shape[2], k.shape[2]
+    q_len, kv_len = q.shape[1], k.shape[1]
+    if q_len > kv_len:
+        raise ValueError(f"query rows {q_len} exceed the cache {kv_len}: no causal read exists")
+    queries, keys, values = q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3)
+    gqa = heads_q != heads_kv
+    if q_len == kv_len:
+        out = F.scaled_dot_product_attention(queries, keys, values, is_causal=True, scale=scale, enable_gqa=gqa)
+    elif q_len == 1:
+        out = F.scaled_dot_product_attention(queries, keys, values, scale=scale, enable_gqa=gqa)
+    else:
+        causal = torch.arange(kv_len, device=q.device)[None, :] <= torch.arange(
+            kv_len - q_len, kv_len, device=q.device
+        )[:, None]
+        out = F.scaled_dot_product_attention(
+            queries, keys, values, attn_mask=causal, scale=scale, enable_gqa=gqa
+        )
+    return out.permute(0, 2, 1, 3)
+
+
+def lsa_read(q, k, v, read_lists, lengths, scale):
+    """The sparse read over selected lists (reference pipeline.py:373-375)."""
+    from lsa_rocm_lab.port.read_kernel_tiled import sparse_read_auto
+
+    return sparse_read_auto(q, k, v, read_lists, lengths, scale)
+
+
+def lsa_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale, chunk_size: int = 64):
+    """Chunked prefill read: every query row of a ``chunk_size`` chunk reads the chunk's
+    shared per-kv-head list plus the chunk's own causal block.
+
+    q [B, T, Hq, D] (query row t at cache position t), k/v [B, Tk, Hkv, D], chunk_lists
+    [B, C, Hkv, W] / chunk_lengths [B, C, Hkv] (or without B for B == 1).
+    """
+    from lsa_rocm_lab.port.read_kernel_tiled import sparse_read_chunked
+
+    return sparse_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale, chunk_size)
+
+
+# ----------------------------------------------------------------------------- index build
+
+
+def index_queries(q: torch.Tensor, heads_kv: int, chunk: int = 1) -> torch.Tensor:
+    """Per-kv-head index queries: the fp32 mean over each GQA group and ``chunk``
+    consecutive tokens. q [B, T, Hq, D] -> [B, T // chunk, Hkv, D] fp32."""
+    device = _on_device("index_queries", q)
+    q = q.contiguous()
+    B, T, Hq, D = q.shape
+    out = torch.empty(B, T // chunk, heads_kv, D, dtype=torch.float32, device=device)
+    _abi.call("lsa_index_queries", q.data_ptr(), _abi.dtype_code(q.dtype), B, T, Hq, heads_kv, D, chunk,
+              out.data_ptr(), _abi.stream(device))
+    return out
+
+
+def bucket_centroids(keys: torch.Tensor, members: torch.Tensor, centroid: str = "mean"):
+    """Bucket centroids (fp32, bf16) from member keys: the mean key, or the L2-normalized
+    sum (reference pipeline.py:108-115). keys [T, d] with members [rows, cap], or keys
+    [B, T, Hkv, D] with members [Hkv, rows, cap] (B == 1) / [B, Hkv, rows, cap]."""
+    device = _on_device("bucket_centroids", keys, members)
+    keys = keys.contiguous()
+    members = members.to(torch.int32).contiguous()
+    mode = {"mean": _abi.CENTROID_MEAN, "normalized": _abi.CENTROID_NORMALIZED}[centroid]
+    rows, cap = members.shape[-2:]
+    if keys.dim() == 2:
+        T, D = keys.shape
+        kv_heads, token_stride, batch_stride, n_tables = 1, D, 0, 1
+    else:
+        B, T, kv_heads, D = keys.shape
+        token_stride, batch_stride = kv_heads * D, T * kv_heads * D
+        n_tables = B * kv_heads
+        if members.numel() != n_tables * rows * cap:
+            raise ValueError(f"members {tuple(members.shape)} do not give one table per (batch, kv-head)")
+    out32 = torch.empty(*members.shape[:-1], D, dtype=torch.float32, device=device)
+    out16 = torch.empty(*members.shape[:-1], D, dtype=torch.bfloat16, device=device)
+    _abi.call("lsa_bucket_centroids", keys.data_ptr(), _abi.dtype_code(keys.dtype), T, token_stride, batch_stride,
+              kv_heads, D, members.data_ptr(), n_tables, rows, cap, mode, out32.data_ptr(), out16.data_ptr(),
+              _abi.stream(device))
+    return out32, out16
+
+
+def position_buckets(index_keys: torch.Tensor, config: PortConfig, centroid: str = "normalized") -> Buckets:
+    """Positional block-sparse buckets - runs of ``bucket_size`` consecutive keys (reference
+    pipeline.py:378-403). index_keys [T, d] gives one table; [B, T, Hkv, D] one table per
+    kv-head ([Hkv, rows, ...] for B == 1, else [B, Hkv, rows, ...]). ``centroid`` is the
+    reference's normalized sum or the bucket-mean key."""
+    device = _on_device("position_buckets", index_keys)
+    block, size, cap = config.cluster_block_size, config.bucket_size, config.bucket_cap
+    T = index_keys.shape[0] if index_keys.dim() == 2 else index_keys.shape[1]
+    blocks = T // block
+    rows = blocks * config.block_bucket_count
+    local = torch.arange(rows * size, device=device, dtype=torch.int32).view(rows, size)
+    members = F.pad(local, (0, cap - size), value=-1)
+    if index_keys.dim() == 4:
+        B, _, Hkv, _ = index_keys.shape
+        lead = (Hkv,) if B == 1 else (B, Hkv)
+        members = members.expand(*lead, rows, cap).contiguous()
+    sizes = (members >= 0).sum(-1, dtype=torch.int32)
+    c32, c16 = bucket_centroids(index_keys, members, centroid)
+    return Buckets(c16, members, sizes, centroids_f32=c32)

@@ -1,0 +1,82 @@
+"""The C ABI without a GPU: the library loads, exports every symbol include/lsa_rocm.h
+declares, and its host-side validation rejects bad arguments before any HIP call."""
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+from lsa_rocm_lab import _abi
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "lsa_rocm.h"
+
+
+def declared() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(lsa_\w+)\(", text, flags=re.M)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _abi.load()
+    names = declared()
+    assert len(names) >= 15
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _abi.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_abi.SIGNATURES) == set(names)
+
+
+def test_version_and_error_string():
+    lib = _abi.load()
+    assert lib.lsa_abi_version() == 1
+    assert isinstance(lib.lsa_last_error(), bytes)
+
+
+def test_null_pointers_rejected_before_launch():
+    with pytest.raises(ValueError, match="NULL"):
+        _abi.call("lsa_read", None, None, None, 1, 1, 1, 8, 8, 2, 64, None, None, 4, 0, 0.1, 0, 1, None, None, 0,
+                  None, None)
+    with pytest.raises(ValueError, match="NULL"):
+        _abi.call("lsa_select_flat", None, 1, 1, 8, 128, None, None, None, 512, 256, 0, 1, 0, None, 64, 1, 32, 0, 0,
+                  8192, 8, None, None, 0, None, None, None)
+
+
+@pytest.mark.parametrize("dim", [8, 100, 512])
+def test_bad_index_dim_rejected(dim):
+    with pytest.raises(ValueError, match="index dim"):
+        _abi.call("lsa_score_rows", 1, 1, 1, 1, dim, 1, 4, 0, 0, 0, 1, None)
+
+
+def test_bad_head_dim_group_and_alignment_rejected():
+    with pytest.raises(ValueError, match="head dim"):
+        _abi.call("lsa_read", 16, 16, 16, 1, 1, 1, 8, 8, 2, 48, 16, 16, 4, 0, 0.1, 0, 1, None, None, 0, 16, None)
+    with pytest.raises(ValueError, match="group"):
+        _abi.call("lsa_read", 16, 16, 16, 1, 1, 1, 8, 6, 4, 64, 16, 16, 4, 0, 0.1, 0, 1, None, None, 0, 16, None)
+    with pytest.raises(ValueError, match="aligned"):
+        _abi.call("lsa_read", 18, 16, 16, 1, 1, 1, 8, 8, 2, 64, 16, 16, 4, 0, 0.1, 0, 1, None, None, 0, 16, None)
+
+
+def test_workspace_required_for_split_reads():
+    need = _abi.size("lsa_read_scratch_bytes", 1, 32, 8, 128, 32)
+    assert need == 8 * 32 * 4 * 130 * 4
+    with pytest.raises(_abi.LsaError, match="WORKSPACE"):
+        _abi.call("lsa_read", 16, 16, 16, 1, 1, 1, 8, 32, 8, 128, 16, 16, 4, 1, 0.1, 0, 32, None, None, 0, 16, None)
+    with pytest.raises(_abi.LsaError, match="WORKSPACE"):  # scratch without counters
+        _abi.call("lsa_read", 16, 16, 16, 1, 1, 1, 8, 32, 8, 128, 16, 16, 4, 1, 0.1, 0, 32, None, 16, need, 16, None)
+    assert _abi.size("lsa_select_flat_scratch_bytes", 1, 8, 32, 512, 8) == 8 * 8 * 32 * 8
+    assert _abi.size("lsa_select_flat_scratch_bytes", 1, 8, 32, 512, 1) == 0
+
+
+def test_select_limits_rejected():
+    # 8192 columns in one split exceed the LDS key budget
+    with pytest.raises(ValueError, match="exceed"):
+        _abi.call("lsa_select_flat", 16, 1, 1, 1, 128, 16, 16, None, 8192, 16, 0, 0, 0, 16, 512, 64, 32, 0, 0, 64, 1,
+                  None, None, 0, 16, 16, None)
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_abi, "_lib", None)
+    monkeypatch.setattr(_abi, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(_abi.ExtensionMissing):
+        _abi.load()
