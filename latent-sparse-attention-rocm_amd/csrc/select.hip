@@ -12,7 +12,7 @@ using namespace lsa;
 
 namespace {
 
-constexpr int kMaxLdsKeys = 4096;  // u64 keys a workgroup holds in LDS (32 KiB)
+constexpr int kMaxLdsKeys = 6144;  // u64 keys a workgroup holds in LDS (48 KiB, under the 64 KiB default)
 
 // ------------------------------------------------------------------ visible counts
 
@@ -469,7 +469,7 @@ extern "C" int lsa_unpack_ids(const int64_t* keys, int64_t n, int32_t* ids, void
 template <typename Src>
 static int launch_topk(Src src, int64_t R, int32_t W, int32_t k, int32_t k_out, int64_t* out, hipStream_t s) {
   const int kp = next_pow2(k_out);
-  const bool lds_row = W <= kMaxLdsKeys;
+  const bool lds_row = W + kp <= kMaxLdsKeys;
   const size_t shmem = sizeof(uint64_t) * ((size_t)kp + (lds_row ? (size_t)W : 0));
   if (lds_row)
     topk_kernel<Src, true><<<dim3((unsigned)R), LSA_BLOCK, shmem, s>>>(src, W, k, kp, k_out, out);
@@ -510,7 +510,7 @@ extern "C" int lsa_expand(const void* picks, int picks_are_keys, int64_t R, int3
                           int32_t* lengths, void* stream) {
   LSA_REQUIRE(picks && members && positions && lists && lengths, LSA_ERR_NULL, "lsa_expand: NULL pointer");
   LSA_TRY(check_tables(rows, cap, row_tables, group_tables));
-  LSA_REQUIRE(R >= 0 && G >= 1 && P >= 0 && P <= 16384, LSA_ERR_SHAPE, "lsa_expand: bad sizes (P=%d)", P);
+  LSA_REQUIRE(R >= 0 && G >= 1 && P >= 0 && P <= 2 * kMaxLdsKeys, LSA_ERR_SHAPE, "lsa_expand: bad sizes (P=%d)", P);
   LSA_REQUIRE(window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE, "lsa_expand: window/sink/top_k must be >= 0");
   LSA_REQUIRE(R * G <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_expand: too many rows");
   if (R * G == 0) return LSA_OK;
@@ -558,8 +558,9 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
   const int cs = (rows + splits - 1) / splits;
   const int kp = next_pow2(K);
   const int keys_cap = cs > splits * K ? cs : splits * K;
-  LSA_REQUIRE(cs <= kMaxLdsKeys && splits * K <= kMaxLdsKeys && kp <= kMaxLdsKeys, LSA_ERR_SHAPE,
-              "lsa_select_flat: %d columns per split / %d merged keys exceed %d", cs, splits * K, kMaxLdsKeys);
+  LSA_REQUIRE(keys_cap + kp <= kMaxLdsKeys, LSA_ERR_SHAPE,
+              "lsa_select_flat: %d columns per split / %d merged keys + %d picks exceed %d LDS keys", cs, splits * K,
+              kp, kMaxLdsKeys);
   const size_t need = lsa_select_flat_scratch_bytes(R, G, top_p, rows, splits);
   LSA_REQUIRE(need == 0 || (scratch && counters && scratch_bytes >= need), LSA_ERR_WORKSPACE,
               "lsa_select_flat: counters/scratch missing or scratch %zu < %zu bytes", scratch_bytes, need);
@@ -622,7 +623,7 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
   const int best_slots = a.beam_pow2 > a.top_pow2 ? a.beam_pow2 : a.top_pow2;
   const int cand_slots = a.cand_pow2 > top_p ? a.cand_pow2 : top_p;
   const size_t shmem = sizeof(uint64_t) * (size_t)(keys_slots + best_slots) + sizeof(int32_t) * (size_t)cand_slots;
-  LSA_REQUIRE(shmem <= 65536, LSA_ERR_SHAPE, "lsa_select_tree: %zu bytes of LDS needed", shmem);
+  LSA_REQUIRE(shmem <= 8 * (size_t)kMaxLdsKeys, LSA_ERR_SHAPE, "lsa_select_tree: %zu bytes of LDS needed", shmem);
   const bool bf16 = score_mode == LSA_SCORE_BF16;
   hipStream_t s = (hipStream_t)stream;
   LSA_DISPATCH_QT(q_dtype, LSA_DISPATCH_SPAN(D / 16, {
