@@ -1,0 +1,420 @@
+#!/usr/bin/env python3
+"""Select+read benchmark on one MI355X: 32k bf16 decode µs/step + HBM GB/s, prefill tok/s.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Decode workload (the headline): D-LSA Flat at B=1, context 32768, Hq=32, Hkv=8, D=128,
+bf16, keys from 512 Gaussian clusters per kv-head (sigma 0.3, runs of 16-128 tokens),
+512 Ward-style buckets per kv-head (16-256 tokens, mean 64) with bucket-mean centroids,
+top-32 buckets per kv-head, rank-order expansion, split-K sparse read. One step is what
+a decode layer pays: GQA-collapsed index queries, the fused select kernel and the
+read kernel (reference port/bench.py:147-153 ``step``: select + read on a built index).
+
+Timing: the K timed steps are replayed from HIP graphs (one graph = a rotation of
+``--rotate`` steps, each on its own resident copy of the cache, so consecutive steps
+never find their K/V rows in the 256 MiB MALL) between ``torch.cuda.synchronize()``
+brackets; ``value`` = wall µs per step. The dominant kernel (the sparse read) is also
+timed alone, with HIP events around each launch on the stream it runs on, for the
+roofline: algorithmic bytes (gathered K and V rows) / average launch duration.
+
+Comparators in the same run: dense SDPA decode on the same GPU (same rotation), the
+chunked prefill (configs' prefill row) as tok/s beside dense causal SDPA, and the CPU
+oracle on the host cores (a bounded sample of decode steps; its lists are also checked
+bit-exact against the GPU's, and its output within the bf16 bar).
+
+One GPU only: ``--gpus N`` with N > 1 exits with a message.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for p in (ROOT / "latent-sparse-attention-rocm_amd", ROOT):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+METRIC = "32k bf16 decode select+read µs/step + HBM GB/s; prefill select+read tok/s"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+T_CTX, HQ, HKV, D = 32768, 32, 8, 128
+N_BUCKETS = 512
+CHUNK = 64
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2048, help="timed decode steps")
+    ap.add_argument("--warmup", type=int, default=256, help="untimed decode steps first")
+    ap.add_argument("--rotate", type=int, default=64, help="resident cache copies cycled through")
+    ap.add_argument("--kernel-launches", type=int, default=512, help="event-timed read launches")
+    ap.add_argument("--prefill-steps", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+# ----------------------------------------------------------------------------- workload
+
+
+class DecodeCache:
+    """One resident copy of everything a decode step reads."""
+
+    def __init__(self, q_last, k, v, buckets, pos):
+        self.q = q_last
+        self.k = k
+        self.v = v
+        self.buckets = buckets
+        self.pos = pos
+
+
+def copy_cache(c: DecodeCache):
+    from lsa_rocm_lab.port.pipeline import Buckets
+
+    b = c.buckets
+    nb = Buckets(b.centroids.clone(), b.members.clone(), b.sizes.clone(), centroids_f32=None,
+                 ends=None if b.ends is None else b.ends.clone())
+    return DecodeCache(c.q.clone(), c.k.clone(), c.v.clone(), nb, c.pos.clone())
+
+
+def decode_step(c: DecodeCache, config):
+    from lsa_rocm_lab.port import pipeline
+    from lsa_rocm_lab.port.read_kernel_tiled import sparse_read_auto
+
+    idx = pipeline.index_queries(c.q, HKV)[0]  # [1, Hkv, D] fp32
+    lists, lengths = pipeline.flat_select(idx, c.pos, c.buckets, config)
+    out = sparse_read_auto(c.q, c.k, c.v, lists.unsqueeze(0), lengths.unsqueeze(0), D ** -0.5)
+    return lists, lengths, out
+
+
+def capture(fn, n: int, torch):
+    """A HIP graph of fn(0..n-1); warm-up runs on a side stream first (torch's recipe)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(n):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    torch.cuda.synchronize()
+    return g
+
+
+def run_steps(graphs, n_steps: int, per_graph: int, torch):
+    """Replays exactly n_steps steps: full-rotation graphs, then the remainder graph."""
+    full, rem = divmod(n_steps, per_graph)
+    for _ in range(full):
+        graphs["full"].replay()
+    if rem:
+        graphs[rem].replay()
+
+
+def event_launch_times(fn, n: int, torch) -> list[float]:
+    """Milliseconds between HIP events recorded right before and after each launch."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        fn(i)
+        b.record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in evs]
+
+
+def dense_decode_fn(torch):
+    """Dense SDPA decode over the whole cache, restricted to fused kernels (no math path)."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    def make(backend, gqa):
+        def fn(q, k, v):
+            qq = q.permute(0, 2, 1, 3)
+            if gqa:
+                kk, vv = k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3)
+            else:
+                kk = k.permute(0, 2, 1, 3).repeat_interleave(HQ // HKV, dim=1)
+                vv = v.permute(0, 2, 1, 3).repeat_interleave(HQ // HKV, dim=1)
+            with sdpa_kernel([backend]):
+                return F.scaled_dot_product_attention(qq, kk, vv, scale=D ** -0.5, enable_gqa=gqa)
+        return fn
+
+    return [("flash+gqa", make(SDPBackend.FLASH_ATTENTION, True)),
+            ("efficient+gqa", make(SDPBackend.EFFICIENT_ATTENTION, True)),
+            ("flash+expanded_kv", make(SDPBackend.FLASH_ATTENTION, False))]
+
+
+# ----------------------------------------------------------------------------- main
+
+
+def main() -> int:
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: the select+read path shards by kv-head with no exchange "
+              "inside the step, and this build runs on a single MI355X; use --gpus 1.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from lsa_rocm_lab import _abi, workloads
+    from lsa_rocm_lab.port import pipeline
+    from lsa_rocm_lab.port.read_kernel_tiled import sparse_read_auto
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    _abi.load()  # fails loudly without the HIP library
+    torch.cuda.set_device(0)
+    dev = "cuda"
+    os.environ["LSA_SELECT_IMPL"] = "fused"
+    config = workloads.FLAT_32K
+
+    # ---- workload (seeded CPU draw, identical on every machine)
+    t0 = time.perf_counter()
+    data = workloads.clustered(T_CTX, HQ, HKV, D, n_clusters=512, seed=0, device=dev)
+    buckets = workloads.cluster_buckets(data, target=N_BUCKETS)
+    log(f"workload built in {time.perf_counter() - t0:.1f}s")
+    pos = torch.tensor([T_CTX - 1], device=dev, dtype=torch.int32)
+    base = DecodeCache(data.q[:, -1:].contiguous(), data.k, data.v, buckets, pos)
+    lists0, lengths0, out0 = decode_step(base, config)
+    torch.cuda.synchronize()
+    n_tok = lengths0.cpu().numpy().astype(np.int64)  # tokens read per kv-head
+    gathered = int(n_tok.sum()) * D * 2 * 2          # K and V rows, bf16
+    cand_bytes = HKV * N_BUCKETS * D * 2             # centroid scan, bf16
+    ids_bytes = int(n_tok.sum()) * 4                 # member ids
+    qo_bytes = 2 * HQ * D * 2
+    total_bytes = gathered + cand_bytes + ids_bytes + qo_bytes
+
+    # ---- rotation copies
+    R = max(1, args.rotate)
+    caches = [base] + [copy_cache(base) for _ in range(R - 1)]
+    torch.cuda.synchronize()
+    log(f"{R} resident cache copies ({R * 2 * data.k.numel() * 2 / 2**30:.1f} GiB of K/V)")
+
+    step = lambda i: decode_step(caches[i % R], config)
+    graphs = {"full": capture(step, R, torch)}
+    rem = args.steps % R
+    if rem:
+        graphs[rem] = capture(step, rem, torch)
+    wrem = args.warmup % R
+    if wrem and wrem not in graphs:
+        graphs[wrem] = capture(step, wrem, torch)
+
+    # ---- warmup + timed region
+    run_steps(graphs, args.warmup, R, torch)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    ev0.record()
+    run_steps(graphs, args.steps, R, torch)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - w0
+    us_step = wall_s / args.steps * 1e6
+    dev_us_step = ev0.elapsed_time(ev1) * 1e3 / args.steps
+    log(f"decode step {us_step:.2f} us (device {dev_us_step:.2f} us)")
+
+    # warm (MALL-resident) variant: the same graph recipe on one copy
+    warm_graph = capture(lambda i: decode_step(base, config), R, torch)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    for _ in range(max(1, args.steps // R)):
+        warm_graph.replay()
+    torch.cuda.synchronize()
+    warm_us = (time.perf_counter() - w0) / (max(1, args.steps // R) * R) * 1e6
+
+    # ---- dominant kernel alone (the sparse read), HIP events around each launch
+    sel = [pipeline.flat_select(pipeline.index_queries(c.q, HKV)[0], c.pos, c.buckets, config) for c in caches]
+    torch.cuda.synchronize()
+    read_fn = lambda i: sparse_read_auto(caches[i % R].q, caches[i % R].k, caches[i % R].v,
+                                         sel[i % R][0].unsqueeze(0), sel[i % R][1].unsqueeze(0), D ** -0.5)
+    event_launch_times(read_fn, 32, torch)
+    read_ms = event_launch_times(read_fn, args.kernel_launches, torch)
+    read_us = statistics.mean(read_ms) * 1e3
+    read_p50 = statistics.median(read_ms) * 1e3
+    sel_fn = lambda i: pipeline.flat_select(pipeline.index_queries(caches[i % R].q, HKV)[0], caches[i % R].pos,
+                                            caches[i % R].buckets, config)
+    event_launch_times(sel_fn, 32, torch)
+    sel_ms = event_launch_times(sel_fn, args.kernel_launches, torch)
+    sel_us = statistics.mean(sel_ms) * 1e3
+    achieved = gathered / (read_us * 1e-6) / 1e9
+    log(f"read kernel {read_us:.2f} us mean ({read_p50:.2f} p50): {achieved:.0f} GB/s on gathered bytes; "
+        f"select (index queries + fused select) {sel_us:.2f} us")
+
+    # ---- dense SDPA comparator on the same rotation
+    dense = {"backend": None}
+    for name, fn in dense_decode_fn(torch):
+        try:
+            fn(caches[0].q, caches[0].k, caches[0].v)
+            torch.cuda.synchronize()
+        except RuntimeError as exc:
+            log(f"dense {name} unavailable: {str(exc).splitlines()[0][:120]}")
+            continue
+        dfn = lambda i, fn=fn: fn(caches[i % R].q, caches[i % R].k, caches[i % R].v)
+        event_launch_times(dfn, 16, torch)
+        try:
+            dgraph = capture(dfn, R, torch)
+            torch.cuda.synchronize()
+            w0 = time.perf_counter()
+            n_rep = max(1, 256 // R)
+            for _ in range(n_rep):
+                dgraph.replay()
+            torch.cuda.synchronize()
+            dense_us = (time.perf_counter() - w0) / (n_rep * R) * 1e6
+            how = "graph"
+        except RuntimeError as exc:
+            log(f"dense graph capture failed ({str(exc).splitlines()[0][:80]}); event-timed launches instead")
+            dense_us = statistics.mean(event_launch_times(dfn, 256, torch)) * 1e3
+            how = "events"
+        dense = {"backend": name, "us_per_step": round(dense_us, 3), "timing": how,
+                 "kv_bytes": 2 * T_CTX * HKV * D * 2}
+        break
+    speedup = dense["us_per_step"] / us_step if dense.get("us_per_step") else None
+    log(f"dense decode {dense}")
+
+    # ---- prefill (chunked, shared selection per 64-token chunk)
+    prefill = None
+    if not args.no_prefill:
+        C = T_CTX // CHUNK
+        ppos = torch.arange(C, device=dev, dtype=torch.int32) * CHUNK - 1
+
+        def prefill_step():
+            idx = pipeline.index_queries(data.q, HKV, CHUNK)[0]  # [C, Hkv, D]
+            pl, pn = pipeline.flat_select(idx, ppos, buckets, config)
+            return pipeline.lsa_read_chunked(data.q, data.k, data.v, pl.unsqueeze(0), pn.unsqueeze(0), D ** -0.5,
+                                             CHUNK), pn
+
+        _, pn = prefill_step()
+        torch.cuda.synchronize()
+        keys_per_row = pn.float().mean().item()
+        ms = event_launch_times(lambda i: prefill_step(), args.prefill_steps, torch)
+        p_ms = statistics.median(ms)
+        # flops: 4*D per (q-head row, key); shared list + the causal local triangle
+        list_pairs = float(pn.to(torch.float64).sum().item()) * CHUNK * (HQ // HKV)
+        local_pairs = C * HQ * CHUNK * (CHUNK + 1) / 2
+        flops = 4.0 * D * (list_pairs + local_pairs)
+        dense_p = None
+        try:
+            import torch.nn.functional as F
+            from torch.nn.attention import SDPBackend, sdpa_kernel
+
+            qq, kk, vv = (t.permute(0, 2, 1, 3) for t in (data.q, data.k, data.v))
+
+            def dfn(i):
+                with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                    return F.scaled_dot_product_attention(qq, kk, vv, is_causal=True, scale=D ** -0.5,
+                                                          enable_gqa=True)
+
+            dfn(0)
+            torch.cuda.synchronize()
+            dense_p = statistics.median(event_launch_times(dfn, args.prefill_steps, torch))
+        except RuntimeError as exc:
+            log(f"dense prefill unavailable: {str(exc).splitlines()[0][:120]}")
+        prefill = {"workload": "flat_prefill_32k", "chunk": CHUNK, "ms_per_step": round(p_ms, 3),
+                   "tok_per_s": round(T_CTX / (p_ms * 1e-3), 1), "keys_per_row": round(keys_per_row + CHUNK / 2, 1),
+                   "flops": flops, "tflops": round(flops / (p_ms * 1e-3) / 1e12, 2),
+                   "mfma_frac": round(flops / (p_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                   "read": "gather kernel (fp32 FMA)",
+                   "dense_sdpa_ms": None if dense_p is None else round(dense_p, 3),
+                   "speedup_vs_dense": None if dense_p is None else round(dense_p / p_ms, 3)}
+        log(f"prefill {prefill}")
+
+    # ---- CPU baseline: the oracle on the host, bounded sample; doubles as the parity check
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        import oracle
+        from threadpoolctl import threadpool_limits
+
+        q_np = base.q.float().cpu().numpy()
+        k_np, v_np = data.k.float().cpu().numpy(), data.v.float().cpu().numpy()
+        cents = buckets.centroids.float().cpu().numpy()
+        members = buckets.members.cpu().numpy()
+        ends = buckets.ends.cpu().numpy()
+
+        def cpu_step():
+            idx = oracle.index_queries(q_np, HKV)[0, 0]
+            ls, ns = [], []
+            for g in range(HKV):
+                lst, n = oracle.flat_select(idx[g][None], np.array([T_CTX - 1]), cents[g], members[g],
+                                            cluster_block_size=config.cluster_block_size,
+                                            block_buckets=config.block_bucket_count, top_p=config.top_p,
+                                            top_k=config.top_k, window=config.window_size,
+                                            sink=config.sink_size, mode="bf16", ends=ends[g])
+                ls.append(lst[0])
+                ns.append(n[0])
+            ls, ns = np.stack(ls), np.array(ns)
+            out = oracle.sparse_read(q_np, k_np, v_np, ls[None, None], ns[None, None], D ** -0.5)
+            return ls, ns, out
+
+        times = []
+        with threadpool_limits(limits=1):
+            t_end = time.perf_counter() + args.cpu_seconds
+            while time.perf_counter() < t_end or len(times) < 2:
+                c0 = time.perf_counter()
+                ls, ns, out_cpu = cpu_step()
+                times.append(time.perf_counter() - c0)
+        cpu = {"value": round(statistics.median(times) * 1e6, 1), "unit": "us/step", "cores": 1, "kind": "port",
+               "sample": f"{len(times)} full flat_decode_32k steps (index queries, select, read) of the numpy "
+                         f"oracle, one BLAS thread, median"}
+        err = np.abs(out0.float().cpu().numpy() - out_cpu)
+        parity = {"lists_bit_exact": bool(np.array_equal(lists0[0].cpu().numpy(), ls)),
+                  "lengths_bit_exact": bool(np.array_equal(lengths0[0].cpu().numpy(), ns)),
+                  "read_max_abs": float(err.max()), "read_mean_abs": float(err.mean())}
+        log(f"cpu {cpu} parity {parity}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(us_step, 3),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_step / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded clustered keys (512 clusters/kv-head, sigma 0.3), q/v ~ N(0,1)",
+        "config": {"workload": "flat_decode_32k", "batch": 1, "context": T_CTX, "heads_q": HQ, "heads_kv": HKV,
+                   "head_dim": D, "buckets_per_kv_head": N_BUCKETS, "top_buckets": config.top_p,
+                   "tokens_read": n_tok.tolist(), "rotated_copies": R, "timing": "hip graphs, wall clock"},
+        "gbps": round(gathered / (us_step * 1e-6) / 1e9, 1),
+        "gbps_total": round(total_bytes / (us_step * 1e-6) / 1e9, 1),
+        "device_us_per_step": round(dev_us_step, 3),
+        "warm_us_per_step": round(warm_us, 3),
+        "select_us": round(sel_us, 3),
+        "read_us": round(read_us, 3),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "read_kernel<bf16,128,4>", "bytes_per_launch": gathered},
+        "dense": dense,
+        "speedup_vs_dense": None if speedup is None else round(speedup, 3),
+        "prefill": prefill,
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

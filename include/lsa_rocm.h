@@ -132,25 +132,32 @@ int lsa_bucket_centroids(const void* keys, int k_dtype, int64_t tokens, int64_t 
                          int32_t cap, int centroid_mode, float* out_f32, uint16_t* out_bf16, void* stream);
 
 /* Sparse gather read (reference read_kernel_tiled.py:30-156 sparse_read_auto / tiled,
- * read_kernel.py:26-120 v1): q [B, Tq, Hq, D], k/v [B, Tk, Hkv, D] (dtype), ids
+ * read_kernel.py:26-120 v1): q [B, Tq, Hq, D] dense; k/v [B, Tk, Hkv, D] (dtype) with the
+ * given element strides of batch, token and head (shared by K and V; rows of D contiguous
+ * elements, 16-byte aligned), so a view into a larger cache is read in place; ids
  * [B*Tq, W] shared by all heads (ids_per_head == 0) or [B*Tq, Hkv, W] per kv-head, and
- * lengths likewise. Each (row, kv-head) list is split over `splits` workgroups whose
- * online-softmax partials the last one to arrive combines. empty_nan: a row with no key
+ * lengths likewise. Each (row, kv-head) list is cut into spans of whole tiles, at most
+ * `splits` (<= 256) of them; the online-softmax partials of a row's active spans are
+ * combined by the last workgroup to arrive. empty_nan: a row with no key
  * gives NaN (v1 contract) instead of 0. Ids outside [0, Tk) are skipped.
  * counters: B*Tq*Hkv int32 that read zero at launch, left zero (splits > 1 only);
  * scratch: lsa_read_scratch_bytes(), no initialisation. */
 size_t lsa_read_scratch_bytes(int64_t rows, int32_t Hq, int32_t Hkv, int32_t D, int32_t splits);
+/* List slots one read workgroup covers per tile for (dtype, head dim, query heads per
+ * kv-head); a split spans ceil(ceil(W / tile) / splits) tiles. 0 for unsupported dims. */
+int32_t lsa_read_tile_tokens(int dtype, int32_t D, int32_t group);
 int lsa_read(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t Tq, int64_t Tk, int32_t Hq,
-             int32_t Hkv, int32_t D, const int32_t* ids, const int32_t* lengths, int32_t W, int ids_per_head,
-             float scale, int empty_nan, int32_t splits, int32_t* counters, void* scratch, size_t scratch_bytes,
-             void* out, void* stream);
+             int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride, int64_t kv_head_stride,
+             const int32_t* ids, const int32_t* lengths, int32_t W, int ids_per_head, float scale, int empty_nan,
+             int32_t splits, int32_t* counters, void* scratch, size_t scratch_bytes, void* out, void* stream);
 
 /* Chunked prefill read on MFMA (bf16): query row t of chunk c = t / chunk reads chunk
  * c's per-kv-head list ids [B, C, Hkv, W] (first lengths[b, c, g] slots) plus the
  * chunk's causal block [c*chunk, t]. q [B, T, Hq, D], k/v [B, Tk, Hkv, D], out like q. */
 int lsa_read_chunked(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t T, int64_t Tk,
-                     int32_t Hq, int32_t Hkv, int32_t D, const int32_t* ids, const int32_t* lengths, int32_t W,
-                     int32_t chunk, float scale, void* out, void* stream);
+                     int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride,
+                     int64_t kv_head_stride, const int32_t* ids, const int32_t* lengths, int32_t W, int32_t chunk,
+                     float scale, void* out, void* stream);
 
 #ifdef __cplusplus
 }

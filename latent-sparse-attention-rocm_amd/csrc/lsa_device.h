@@ -119,7 +119,7 @@ struct RadixState {
 //   done == 0: every value > prefix plus `need` copies of prefix (ties).
 // 1 <= k <= n. Every thread of the block must call it.
 template <typename Get>
-__device__ void radix_select(Get get, int n, int k, RadixState* st) {
+__device__ __forceinline__ void radix_select(Get get, int n, int k, RadixState* st) {
   const int tid = threadIdx.x;
   if (tid == 0) { st->prefix = 0; st->mask = 0; st->need = k; st->done = 0; }
   for (int pass = 0; pass < 8; ++pass) {
@@ -159,7 +159,7 @@ __device__ void radix_select(Get get, int n, int k, RadixState* st) {
 
 // Appends the selected values (see radix_select) to out[0..k) in arbitrary order.
 template <typename Get>
-__device__ void radix_collect(Get get, int n, int k, RadixState* st, uint64_t* out) {
+__device__ __forceinline__ void radix_collect(Get get, int n, int k, RadixState* st, uint64_t* out) {
   const int tid = threadIdx.x;
   if (tid == 0) st->slot = 0;
   __syncthreads();
@@ -179,7 +179,7 @@ __device__ void radix_collect(Get get, int n, int k, RadixState* st, uint64_t* o
 }
 
 // Sorts a[0..n) descending in LDS; n is a power of two. Every thread must call it.
-__device__ void bitonic_sort_desc(uint64_t* a, int n) {
+__device__ __forceinline__ void bitonic_sort_desc(uint64_t* a, int n) {
   const int tid = threadIdx.x;
   for (int size = 2; size <= n; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
@@ -214,6 +214,106 @@ __device__ __forceinline__ uint64_t wave_sort64_desc(uint64_t v) {
     }
   }
   return v;
+}
+
+// ---------------------------------------------------------------- cross-workgroup exchange
+
+// Values handed between workgroups that may sit on different XCDs (whose L2s are not
+// coherent with each other) go through system-coherent accesses: write-through stores and
+// cache-bypassing loads. Publishing then needs only the stores' completion (s_waitcnt)
+// before an arrival counter, never a device-scope fence (a whole-L2 writeback on gfx950).
+__device__ __forceinline__ void coherent_store_u64(uint64_t* p, uint64_t x) { *(volatile uint64_t*)p = x; }
+__device__ __forceinline__ uint64_t coherent_load_u64(const uint64_t* p) { return *(const volatile uint64_t*)p; }
+
+// Every thread's coherent stores complete, then one arrival on `counter`; returns (to
+// every thread) whether this workgroup arrived last of `expected`. The last one resets the
+// counter to zero for the next launch. Contains barriers: every thread calls it.
+__device__ __forceinline__ bool arrive_last(int* counter, int expected, int* flag) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = before == expected - 1;
+    if (before == expected - 1) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  const bool last = *flag != 0;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  return last;
+}
+
+// ---------------------------------------------------------------- wave top-k
+
+// One wave selects the K (<= 64) largest of keys[0..n) (u-ordered, n <= 64 * KPL) and
+// writes them sorted descending to out[0..kp), u == 0 past K. Nonzero keys are distinct
+// (a packed key carries its column); only u == 0 (EMPTY) repeats. The K-th largest value
+// T is found bit by bit, high word first, by wave-wide counts (ballot + popcount, no
+// barriers); the keys above T and then copies of T are compacted into tmp[0..K) and
+// ranked into place. Called by the 64 threads of one wave.
+template <int KPL>
+__device__ __forceinline__ void wave_topk_sorted(const uint64_t* keys, int n, int K, int kp, uint64_t* out,
+                                                 uint64_t* tmp) {
+  const int lane = threadIdx.x & (LSA_WAVE - 1);
+  uint32_t vh[KPL], vl[KPL];
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    const int idx = lane + LSA_WAVE * j;
+    const uint64_t v = idx < n ? keys[idx] : 0;
+    vh[j] = (uint32_t)(v >> 32);
+    vl[j] = (uint32_t)v;
+  }
+  // high word of T: the largest h with #(high >= h) >= K
+  uint32_t hi = 0;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = hi | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) cnt += __popcll(__ballot(vh[j] >= cand));
+    if (cnt >= K) hi = cand;
+  }
+  int above = 0, at_hi = 0;
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    above += __popcll(__ballot(vh[j] > hi));
+    at_hi += __popcll(__ballot(vh[j] == hi));
+  }
+  uint32_t lo = 0;
+  if (above + at_hi > K) {  // the K-th key shares its high word with keys below it
+    const int need = K - above;
+    for (int b = 31; b >= 0; --b) {
+      const uint32_t cand = lo | (1u << b);
+      int cnt = 0;
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) cnt += __popcll(__ballot(vh[j] == hi && vl[j] >= cand));
+      if (cnt >= need) lo = cand;
+    }
+  }
+  const uint64_t T = ((uint64_t)hi << 32) | lo;
+  // compact the keys above T, then fill with T (repeats only when T is EMPTY)
+  int base = 0;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (LSA_WAVE - lane));
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    const uint64_t v = ((uint64_t)vh[j] << 32) | vl[j];
+    const bool take = v > T;
+    const uint64_t m = __ballot(take);
+    if (take) tmp[base + __popcll(m & below)] = v;
+    base += __popcll(m);
+  }
+  for (int m = base + lane; m < K; m += LSA_WAVE) tmp[m] = T;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  if (lane < K) {
+    const uint64_t x = tmp[lane];
+    int rank = 0;
+    for (int m = 0; m < K; ++m) {
+      const uint64_t y = tmp[m];
+      rank += (y > x || (y == x && m < lane)) ? 1 : 0;
+    }
+    out[rank] = x;
+  }
+  for (int m = K + lane; m < kp; m += LSA_WAVE) out[m] = 0;
 }
 
 // ---------------------------------------------------------------- canonical score

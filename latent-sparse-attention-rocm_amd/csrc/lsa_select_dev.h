@@ -42,15 +42,7 @@ __device__ __forceinline__ int visible_count(int64_t position, int rows, int clu
   return lo;
 }
 
-// Loads one lane's slice of a query row, rounded to the scoring type.
-template <typename QT, int SPAN>
-__device__ __forceinline__ void load_query_slice(const QT* q, int p, bool bf16_mode, float* out) {
-#pragma unroll
-  for (int j = 0; j < SPAN; ++j) {
-    float x = elem<QT>::load(q, (int64_t)p * SPAN + j);
-    out[j] = bf16_mode ? bf16_round(x) : x;
-  }
-}
+
 
 // fp64 partial over the lane's slice, then the 16-lane tree: the canonical score.
 template <typename CT, int SPAN>
@@ -62,58 +54,321 @@ __device__ __forceinline__ float canonical_score(const float* qs, const CT* row,
   return score_tree16(acc);
 }
 
+// SPAN consecutive elements of a centroid row, loaded raw with the widest aligned vector
+// loads (a lane's slice starts at a multiple of SPAN elements of a row whose length is
+// 16 * SPAN elements, so SPAN * sizeof(CT) bytes of alignment hold for an aligned table).
+template <typename CT, int SPAN>
+struct SpanRaw {
+  static constexpr int BYTES = SPAN * (int)sizeof(CT);
+  static constexpr int WORDS = BYTES >= 4 ? BYTES / 4 : 1;
+  uint32_t w[WORDS];
+  __device__ __forceinline__ void load(const CT* p) {
+    if constexpr (BYTES >= 16) {
+#pragma unroll
+      for (int i = 0; i < BYTES / 16; ++i) {
+        const uint4 v = ((const uint4*)p)[i];
+        w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+      }
+    } else if constexpr (BYTES == 8) {
+      const uint2 v = *(const uint2*)p;
+      w[0] = v.x; w[1] = v.y;
+    } else if constexpr (BYTES == 4) {
+      w[0] = *(const uint32_t*)p;
+    } else {
+      w[0] = *(const uint16_t*)p;
+    }
+  }
+  __device__ __forceinline__ float at(int j) const {
+    if constexpr (sizeof(CT) == 4) {
+      return __uint_as_float(w[j]);
+    } else if constexpr (__is_same(CT, _Float16)) {
+      const uint16_t h = (uint16_t)((j & 1) ? (w[j >> 1] >> 16) : (w[j >> 1] & 0xFFFFu));
+      _Float16 f;
+      __builtin_memcpy(&f, &h, 2);
+      return (float)f;
+    } else {  // bf16
+      const uint32_t x = w[j >> 1];
+      return __uint_as_float((j & 1) ? (x & 0xFFFF0000u) : (x << 16));
+    }
+  }
+};
+
+// Loads one lane's slice of a query row (all loads first), rounded to the scoring type.
+template <typename QT, int SPAN>
+__device__ __forceinline__ void load_query_slice(const QT* q, int p, bool bf16_mode, float* out) {
+  SpanRaw<QT, SPAN> raw;
+  raw.load(q + (int64_t)p * SPAN);
+#pragma unroll
+  for (int j = 0; j < SPAN; ++j) {
+    const float x = raw.at(j);
+    out[j] = bf16_mode ? bf16_round(x) : x;
+  }
+}
+
+// One batch size of score_keys: each 16-lane group scores CB columns per round trip.
+template <typename CT, int SPAN, int CB, typename ColOf, typename KeepOf>
+__device__ __forceinline__ void score_keys_cb(const float* qs, const CT* cent, int dim, int n, ColOf col_of,
+                                              KeepOf keep_of, uint64_t* out) {
+  constexpr int GROUPS = LSA_BLOCK / 16;
+  const int grp = threadIdx.x >> 4, p = threadIdx.x & 15;
+  for (int jb = 0; jb < n; jb += GROUPS * CB) {
+    SpanRaw<CT, SPAN> raw[CB];
+    int col[CB];
+    bool keep[CB];
+#pragma unroll
+    for (int k = 0; k < CB; ++k) {
+      const int j = jb + k * GROUPS + grp;
+      col[k] = j < n ? col_of(j) : -1;
+      raw[k].load(cent + (int64_t)(col[k] >= 0 ? col[k] : 0) * dim + p * SPAN);
+      keep[k] = keep_of(j < n ? j : n - 1) && j < n;
+    }
+#pragma unroll
+    for (int k = 0; k < CB; ++k) {
+      const int j = jb + k * GROUPS + grp;
+      double acc = 0.0;
+#pragma unroll
+      for (int e = 0; e < SPAN; ++e) acc = fma((double)qs[e], (double)raw[k].at(e), acc);
+      const float s = score_tree16(acc);
+      if (p == 0 && j < n) out[j] = (col[k] >= 0 && keep[k]) ? key_to_u(pack_key(s, col[k])) : 0;
+    }
+  }
+}
+
+// Scores entries j < n of a column list into u-ordered keys out[j]: col_of(j) is a
+// column of `cent` or -1 (EMPTY key, u == 0), keep_of(j) masks a scored column to EMPTY
+// (its load is issued with the centroid rows, so it costs no extra round trip). Each
+// 16-lane group scores one column per step; a batch of columns (sized to n, at most 256
+// bytes of rows per lane) is loaded unconditionally (invalid ones read row 0) before any
+// arithmetic, so a batch costs one memory round trip. Every thread calls it.
+template <typename CT, int SPAN, typename ColOf, typename KeepOf>
+__device__ __forceinline__ void score_keys(const float* qs, const CT* cent, int dim, int n, ColOf col_of,
+                                           KeepOf keep_of, uint64_t* out) {
+  constexpr int GROUPS = LSA_BLOCK / 16;
+  constexpr int BYTES = SPAN * (int)sizeof(CT);
+  constexpr int CBMAX = BYTES >= 256 ? 1 : (256 / BYTES > 16 ? 16 : 256 / BYTES);
+  if (n <= GROUPS) score_keys_cb<CT, SPAN, 1>(qs, cent, dim, n, col_of, keep_of, out);
+  else if (n <= 2 * GROUPS || CBMAX < 4) score_keys_cb<CT, SPAN, (CBMAX < 2 ? CBMAX : 2)>(qs, cent, dim, n, col_of, keep_of, out);
+  else if (n <= 4 * GROUPS || CBMAX < 8) score_keys_cb<CT, SPAN, (CBMAX < 4 ? CBMAX : 4)>(qs, cent, dim, n, col_of, keep_of, out);
+  else if (n <= 8 * GROUPS || CBMAX < 16) score_keys_cb<CT, SPAN, (CBMAX < 8 ? CBMAX : 8)>(qs, cent, dim, n, col_of, keep_of, out);
+  else score_keys_cb<CT, SPAN, CBMAX>(qs, cent, dim, n, col_of, keep_of, out);
+}
+
+template <typename CT, int SPAN, typename ColOf>
+__device__ __forceinline__ void score_keys(const float* qs, const CT* cent, int dim, int n, ColOf col_of,
+                                           uint64_t* out) {
+  score_keys<CT, SPAN>(qs, cent, dim, n, col_of, [](int) { return true; }, out);
+}
+
 // Scores columns [c0, c1) of one table into u-ordered keys out[c - c0]; columns at or
 // past `visible` become EMPTY (u == 0). Every thread of the block calls it.
 template <typename CT, int SPAN>
-__device__ void score_slice_keys(const float* qs, const CT* cent, int dim, int c0, int c1, int visible,
-                                 uint64_t* out) {
-  const int grp = threadIdx.x >> 4, p = threadIdx.x & 15;
-  for (int c = c0 + grp; c < c1; c += LSA_BLOCK / 16) {
-    uint64_t u = 0;
-    if (c < visible) {  // uniform over the 16-lane group
-      float s = canonical_score<CT, SPAN>(qs, cent + (int64_t)c * dim, p);
-      u = key_to_u(pack_key(s, c));
-    }
-    if (p == 0) out[c - c0] = u;
+__device__ __forceinline__ void score_slice_keys(const float* qs, const CT* cent, int dim, int c0, int c1,
+                                                 int visible, uint64_t* out) {
+  const int n = c1 > c0 ? c1 - c0 : 0;
+  score_keys<CT, SPAN>(qs, cent, dim, n, [&](int j) { return c0 + j < visible ? c0 + j : -1; }, out);
+}
+
+// Shared state of the histogram top-k (one per workgroup, in LDS).
+struct TopkScratch {
+  int hist[256];
+  int off[256];   // first candidate slot of each bin (bins from the top down)
+  int fill[256];  // candidates placed so far per bin
+  uint64_t cand[LSA_WAVE];
+  float wmin[LSA_WAVES], wmax[LSA_WAVES];
+  int wcnt[LSA_WAVES], wbad[LSA_WAVES];
+  int cut, ok;
+};
+
+// The score a u-ordered key was packed from (inverse of ordered_bits).
+__device__ __forceinline__ float key_score(uint64_t u) {
+  const int32_t ob = (int32_t)((uint32_t)(u >> 32) ^ 0x80000000u);
+  return __int_as_float(ob ^ ((ob >> 31) & 0x7FFFFFFF));
+}
+
+// Histogram cut for a small K (<= 64). The nonempty keys are binned linearly by score over
+// [min, max] into 256 bins (a monotone map: a higher bin never holds a lower key). The bins
+// from the top down to the one holding the min(K, nonempty)-th key are the candidates;
+// each is placed at its bin's offset (bins in descending order), so its rank is that
+// offset plus the larger keys of its own bin - usually none. Returns false (every thread)
+// when a score is not finite or more than 64 keys survive the cut (ties, a degenerate
+// spread); the caller then uses the radix select. Every thread calls it. Designed for
+// latency: five barriers and no loop longer than a bin's occupancy.
+__device__ __forceinline__ bool block_topk_hist(const uint64_t* keys, int n, int K, int kp, uint64_t* out,
+                                                TopkScratch* sc) {
+  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
+  float mn = INFINITY, mx = -INFINITY;
+  int cnt = 0, bad = 0;
+  for (int j = tid; j < n; j += LSA_BLOCK) {
+    const uint64_t k = keys[j];
+    const float x = key_score(k);
+    const bool live = k != 0;
+    bad |= (live && x - x != 0.0f) ? 1 : 0;  // NaN or infinite
+    mn = live ? fminf(mn, x) : mn;
+    mx = live ? fmaxf(mx, x) : mx;
+    cnt += live ? 1 : 0;
   }
+  sc->hist[tid] = 0;  // LSA_BLOCK == 256 bins
+  sc->fill[tid] = 0;
+#pragma unroll
+  for (int x = LSA_WAVE / 2; x >= 1; x >>= 1) {
+    mn = fminf(mn, __shfl_xor(mn, x, LSA_WAVE));
+    mx = fmaxf(mx, __shfl_xor(mx, x, LSA_WAVE));
+    cnt += __shfl_xor(cnt, x, LSA_WAVE);
+    bad |= __shfl_xor(bad, x, LSA_WAVE);
+  }
+  if (lane == 0) { sc->wmin[w] = mn; sc->wmax[w] = mx; sc->wcnt[w] = cnt; sc->wbad[w] = bad; }
+  __syncthreads();
+  mn = fminf(fminf(sc->wmin[0], sc->wmin[1]), fminf(sc->wmin[2], sc->wmin[3]));
+  mx = fmaxf(fmaxf(sc->wmax[0], sc->wmax[1]), fmaxf(sc->wmax[2], sc->wmax[3]));
+  cnt = sc->wcnt[0] + sc->wcnt[1] + sc->wcnt[2] + sc->wcnt[3];
+  bad = sc->wbad[0] | sc->wbad[1] | sc->wbad[2] | sc->wbad[3];
+  if (bad) return false;  // uniform: every thread sees the same totals
+  const int kc = cnt < K ? cnt : K;
+  const float scale = mx > mn ? 256.0f / (mx - mn) : 0.0f;
+  auto bin_of = [&](uint64_t k) {
+    const int b = (int)((key_score(k) - mn) * scale);
+    return b < 0 ? 0 : (b > 255 ? 255 : b);
+  };
+  for (int j = tid; j < n; j += LSA_BLOCK) {
+    const uint64_t k = keys[j];
+    if (k != 0) atomicAdd(&sc->hist[bin_of(k)], 1);
+  }
+  __syncthreads();
+  if (w == 0) {
+    // lane l owns bins 255-4l .. 252-4l; exclusive suffix offsets from the top bin
+    const int c0 = sc->hist[255 - 4 * lane], c1 = sc->hist[254 - 4 * lane];
+    const int c2 = sc->hist[253 - 4 * lane], c3 = sc->hist[252 - 4 * lane];
+    const int mine = c0 + c1 + c2 + c3;
+    const int inc = wave_inclusive_sum(mine);
+    const int o0 = inc - mine, o1 = o0 + c0, o2 = o1 + c1, o3 = o2 + c2;
+    sc->off[255 - 4 * lane] = o0;
+    sc->off[254 - 4 * lane] = o1;
+    sc->off[253 - 4 * lane] = o2;
+    sc->off[252 - 4 * lane] = o3;
+    // the bin holding the kc-th key, and the keys in it and above
+    const bool here = kc > 0 && o0 < kc && kc <= inc;
+    const int d = o1 >= kc ? 255 - 4 * lane : (o2 >= kc ? 254 - 4 * lane : (o3 >= kc ? 253 - 4 * lane : 252 - 4 * lane));
+    const int total = o1 >= kc ? o1 : (o2 >= kc ? o2 : (o3 >= kc ? o3 : inc));
+    const uint64_t m = __ballot(here);
+    const int src = m ? __ffsll((long long)m) - 1 : 0;
+    const int cut = __shfl(d, src, LSA_WAVE);
+    const int tot = __shfl(total, src, LSA_WAVE);
+    if (lane == 0) { sc->cut = m ? cut : 256; sc->ok = (m == 0 || tot <= LSA_WAVE) ? 1 : 0; }
+  }
+  __syncthreads();
+  if (!sc->ok) return false;
+  const int cut = sc->cut;
+  for (int j = tid; j < n; j += LSA_BLOCK) {
+    const uint64_t k = keys[j];
+    const int b = bin_of(k);
+    if (k != 0 && b >= cut) sc->cand[sc->off[b] + atomicAdd(&sc->fill[b], 1)] = k;
+  }
+  __syncthreads();
+  if (w == 0) {
+    const int nc = cut < 256 ? sc->off[cut] + sc->hist[cut] : 0;
+    if (lane < nc) {
+      const uint64_t x = sc->cand[lane];
+      const int b = bin_of(x);
+      const int lo = sc->off[b], hi = lo + sc->hist[b];
+      int rank = lo;
+      for (int m = lo; m < hi; ++m) rank += sc->cand[m] > x ? 1 : 0;  // nonempty keys are distinct
+      if (rank < K) out[rank] = x;
+    }
+    for (int m = kc + lane; m < kp; m += LSA_WAVE) out[m] = 0;  // EMPTY past the nonempty keys
+  }
+  __syncthreads();
+  return true;
+}
+
+// The K best of keys[0..n) (u-ordered, in LDS), sorted descending into out[0..kp) with
+// u == 0 past K (kp = next_pow2(K)). K <= 64 takes the histogram cut when it leaves at
+// most 64 candidates; otherwise a radix select + bitonic sort. 1 <= K <= n. Every thread
+// calls it.
+__device__ __forceinline__ void block_topk_sorted(const uint64_t* keys, int n, int K, int kp, uint64_t* out,
+                                                  TopkScratch* sc, RadixState* st) {
+  if (K <= LSA_WAVE && block_topk_hist(keys, n, K, kp, out, sc)) return;
+  auto get = [&](int j) -> uint64_t { return keys[j]; };
+  radix_select(get, n, K, st);
+  radix_collect(get, n, K, st, out);
+  for (int j = K + threadIdx.x; j < kp; j += LSA_BLOCK) out[j] = 0;
+  __syncthreads();
+  bitonic_sort_desc(out, kp);
+}
+
+// Value of tail slot i (after the kept ids) of a read list: the window [window_start,
+// position], then the sinks [0, min(sink, window_start)), then -1.
+__device__ __forceinline__ int32_t tail_id(int64_t i, int64_t window_start, int64_t n_win, int64_t n_sink) {
+  return i < n_win ? (int32_t)(window_start + i) : (i < n_win + n_sink ? (int32_t)(i - n_win) : -1);
 }
 
 // Rank-order expansion of one row (reference select_fused.py:172-214): picks in rank
 // order, member slots in table order, keep ids with sink <= id < window_start until
 // top_k are stored; then the window [window_start, position] and the sinks
 // [0, min(sink, window_start)). Slots past the length are -1. Returns the length.
-// picks lives in LDS (bucket ids, -1 = none). Every thread of the block calls it.
-__device__ int expand_walk(const int32_t* picks, int n_picks, const int32_t* members, int rows, int cap,
-                           int64_t position, int window, int sink, int top_k, int32_t* out, int width,
-                           int* scan) {
-  constexpr int E = 8;  // consecutive slots per thread per tile
+// picks lives in LDS (bucket ids, -1 = none). Each thread owns 32 consecutive slots of a
+// 8192-slot super-tile, all loaded before one block-wide prefix sum (as 16-byte vectors
+// when the cap is a multiple of 32, so a thread's slots lie in one member row; the table
+// is then 16-byte aligned). With `stage` (LDS for width + 4 ints, width % 4 == 0, `out`
+// 16-byte aligned) the kept ids are scattered into the LDS row without branches and the
+// whole row - ids, tail and padding - leaves in coalesced 16-byte stores; without it they
+// are stored directly. Every thread of the block calls it.
+__device__ __forceinline__ int expand_walk(const int32_t* picks, int n_picks, const int32_t* members, int rows,
+                                           int cap, int64_t position, int window, int sink, int top_k,
+                                           int32_t* out, int width, int* scan, int32_t* stage) {
+  constexpr int E = 32;
   const int tid = threadIdx.x;
-  int64_t ws = position + 1 - window;
+  const int64_t ws = position + 1 - window;
   const int64_t window_start = ws > 0 ? ws : 0;
   const int64_t total_slots = (int64_t)n_picks * cap;
+  const bool rowwise = (cap % E) == 0;
   int filled = 0;
   for (int64_t base = 0; base < total_slots && filled < top_k; base += (int64_t)LSA_BLOCK * E) {
     int32_t ids[E];
-    int count = 0;
+    const int64_t s0 = base + (int64_t)tid * E;
+    if (rowwise) {
+      const int32_t b = s0 < total_slots ? picks[s0 / cap] : -1;
+      const bool okb = b >= 0 && b < rows;
+      const int4* src = (const int4*)(members + (int64_t)(okb ? b : 0) * cap + (okb ? s0 % cap : 0));
+#pragma unroll
+      for (int v = 0; v < E / 4; ++v) {
+        const int4 x = src[v];
+        ids[4 * v] = okb ? x.x : -1;
+        ids[4 * v + 1] = okb ? x.y : -1;
+        ids[4 * v + 2] = okb ? x.z : -1;
+        ids[4 * v + 3] = okb ? x.w : -1;
+      }
+    } else {
+      for (int e = 0; e < E; ++e) {
+        const int64_t s = s0 + e;
+        const int32_t b = s < total_slots ? picks[(int)(s / cap)] : -1;
+        const bool okb = b >= 0 && b < rows;
+        const int32_t id = members[(int64_t)(okb ? b : 0) * cap + (okb ? (int)(s % cap) : 0)];
+        ids[e] = okb ? id : -1;
+      }
+    }
+    uint32_t keep = 0;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const int64_t s = base + (int64_t)tid * E + e;
-      int32_t id = -1;
-      if (s < total_slots) {
-        const int32_t b = picks[s / cap];
-        if (b >= 0 && b < rows) id = members[(int64_t)b * cap + (s % cap)];
-      }
-      const bool ok = (id >= sink) && ((int64_t)id < window_start);
-      ids[e] = ok ? id : -1;
-      count += ok ? 1 : 0;
+      const bool ok = (ids[e] >= sink) && ((int64_t)ids[e] < window_start);
+      keep |= ok ? (1u << e) : 0u;
     }
     int total;
-    int at = filled + block_exclusive_sum(count, scan, &total);
+    const int at = filled + block_exclusive_sum(__popc(keep), scan, &total);
+    if (stage) {
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      if (ids[e] >= 0) {
-        if (at < top_k) out[at] = ids[e];
-        ++at;
+      for (int e = 0; e < E; ++e) {
+        const int pos = at + __popc(keep & ((1u << e) - 1u));
+        const bool put = ((keep >> e) & 1u) && pos < top_k;
+        stage[put ? pos : width] = ids[e];  // slot `width` is a sink for the unkept
+      }
+    } else {
+      int pos = at;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        if ((keep >> e) & 1u) {
+          if (pos < top_k) out[pos] = ids[e];
+          ++pos;
+        }
       }
     }
     filled += total;
@@ -122,40 +377,30 @@ __device__ int expand_walk(const int32_t* picks, int n_picks, const int32_t* mem
   const int64_t n_win = position + 1 - window_start > 0 ? position + 1 - window_start : 0;
   const int64_t n_sink = sink < window_start ? sink : window_start;
   const int length = filled + (int)n_win + (int)n_sink;
-  for (int i = tid; i < width - filled; i += LSA_BLOCK) {
-    const int at = filled + i;
-    int32_t v = -1;
-    if (i < n_win) v = (int32_t)(window_start + i);
-    else if (i < n_win + n_sink) v = (int32_t)(i - n_win);
-    out[at] = v;
+  if (stage) {
+    __syncthreads();
+    for (int c = tid; c < width / 4; c += LSA_BLOCK) {
+      const int s0 = 4 * c;
+      int4 v;
+      if (s0 + 4 <= filled) {
+        v = ((const int4*)stage)[c];
+      } else if (s0 >= length) {
+        v = make_int4(-1, -1, -1, -1);
+      } else {
+        int e[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int slot = s0 + k;
+          e[k] = slot < filled ? stage[slot] : tail_id(slot - filled, window_start, n_win, n_sink);
+        }
+        v = make_int4(e[0], e[1], e[2], e[3]);
+      }
+      ((int4*)out)[c] = v;
+    }
+  } else {
+    for (int i = tid; i < width - filled; i += LSA_BLOCK) out[filled + i] = tail_id(i, window_start, n_win, n_sink);
   }
   return length;
-}
-
-// Merges S descending lists (each K long, u-ordered, u == 0 padding) into the best K,
-// descending, by rank: an element's rank is its index plus, for every other list, the
-// number of its elements that beat it (ties to the lower list). Every thread calls it.
-__device__ void merge_sorted_lists(const uint64_t* lists, int S, int K, uint64_t* out) {
-  const int total = S * K;
-  for (int e = threadIdx.x; e < total; e += LSA_BLOCK) {
-    const int s = e / K, j = e % K;
-    const uint64_t x = lists[e];
-    int rank = j;
-    for (int o = 0; o < S; ++o) {
-      if (o == s) continue;
-      const uint64_t* l = lists + (int64_t)o * K;
-      // count of elements in l that beat x: > x, or >= x when o < s
-      int lo = 0, hi = K;
-      while (lo < hi) {
-        int mid = (lo + hi) >> 1;
-        bool beats = (o < s) ? (l[mid] >= x) : (l[mid] > x);
-        if (beats) lo = mid + 1; else hi = mid;
-      }
-      rank += lo;
-    }
-    if (rank < K) out[rank] = x;
-  }
-  __syncthreads();
 }
 
 }  // namespace lsa

@@ -13,6 +13,7 @@ using namespace lsa;
 namespace {
 
 constexpr int kMaxLdsKeys = 6144;  // u64 keys a workgroup holds in LDS (48 KiB, under the 64 KiB default)
+constexpr size_t kMaxDynLds = 56 * 1024;  // dynamic LDS of a select workgroup, beside ~6 KiB of static state
 
 // ------------------------------------------------------------------ visible counts
 
@@ -124,7 +125,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void expand_kernel(const void* picks, in
   const int32_t* tab = members + (r * row_tables + g * group_tables) * (int64_t)rows * cap;
   const int width = top_k + window + sink;
   const int len = expand_walk(pk, P, tab, rows, cap, positions[r], window, sink, top_k, lists + i * width, width,
-                              scan);
+                              scan, nullptr);
   if (threadIdx.x == 0) lengths[i] = len;
 }
 
@@ -143,73 +144,84 @@ struct FlatArgs {
   int K, kp;          // picks kept (min(top_p, rows)) and its power of two
   int window, sink, top_k;
   int S, cs;          // splits and columns per split
-  int keys_cap;       // LDS keys slots: max(cs, S*K)
-  uint64_t* ws_keys;  // [R*G, S, K]
-  int* ws_count;      // [R*G]
+  int stage;          // 1: the list row is assembled in LDS after keys and picks
+  uint64_t* ws_keys;  // [R*G, rows] every column's key (S > 1)
+  int* ws_count;      // [R*G] arrival counters (S > 1)
   int32_t* lists;
   int32_t* lengths;
 };
 
-// grid (R*G, S). Each workgroup scores its column slice and keeps its best K keys; with
-// S > 1 the last workgroup of a (row, group) merges the S sorted lists. The winner
-// expands the picks into the read list.
+// Closed-form visible count without span ends (reference pipeline.py:184-186).
+__device__ __forceinline__ int visible_closed(int64_t position, int rows, int cluster_block, int block_buckets) {
+  const int64_t blocks =
+      position >= 0 ? position / cluster_block : -((-position + cluster_block - 1) / cluster_block);
+  int64_t v = blocks * block_buckets;
+  return (int)(v > rows ? rows : v);
+}
+
+// grid (R*G, S). Split s scores columns [s*cs, (s+1)*cs) of its table in one batch of
+// loads (query slice, centroid rows and the columns' span ends together); with S > 1 it
+// publishes the keys and the last split to arrive takes every column's key from the
+// workspace. That workgroup selects the K best keys, sorted, and expands the picks into
+// the read list in rank order (reference pipeline.py:248-316, select_fused.py:52-280).
 template <typename QT, typename CT, int SPAN>
 __global__ __launch_bounds__(LSA_BLOCK) void select_flat_kernel(const QT* q, bool bf16_mode, FlatArgs a) {
   constexpr int D = 16 * SPAN;
   extern __shared__ uint64_t smem[];
   __shared__ RadixState st;
+  __shared__ TopkScratch tks;
   __shared__ int scan[LSA_WAVES];
-  __shared__ int is_last;
-  uint64_t* keys = smem;
-  uint64_t* best = smem + a.keys_cap;
+  __shared__ int flag;
+  uint64_t* keys = smem;            // [rows]
+  uint64_t* best = smem + a.rows;   // [kp]
   const int64_t i = blockIdx.x;
   const int s = blockIdx.y;
   const int64_t r = i / a.G, g = i % a.G;
   const int64_t position = a.positions[r];
   const int64_t t = r * a.row_tables + g * a.group_tables;
-  const int visible = visible_count(position, a.rows, a.cluster_block, a.block_buckets,
-                                    a.ends ? a.ends + t * a.rows : nullptr);
   const CT* cent = (const CT*)a.centroids + t * a.rows * (int64_t)D;
+  const int32_t* ends = a.ends ? a.ends + t * a.rows : nullptr;
   const int c0 = s * a.cs;
   const int c1 = min(c0 + a.cs, a.rows);
   const int n_local = c1 > c0 ? c1 - c0 : 0;
+  const int vis = ends ? 0 : visible_closed(position, a.rows, a.cluster_block, a.block_buckets);
+  const int64_t lim = position + 1;
 
   float qs[SPAN];
   load_query_slice<QT, SPAN>(q + i * D, threadIdx.x & 15, bf16_mode, qs);
-  score_slice_keys<CT, SPAN>(qs, cent, D, c0, c1, visible, keys);
-  __syncthreads();
-  const int k_loc = min(a.K, n_local);
-  if (k_loc > 0) {
-    auto get = [&](int j) -> uint64_t { return keys[j]; };
-    radix_select(get, n_local, k_loc, &st);
-    radix_collect(get, n_local, k_loc, &st, best);
-  }
-  for (int j = k_loc + threadIdx.x; j < a.kp; j += LSA_BLOCK) best[j] = 0;
-  __syncthreads();
-  bitonic_sort_desc(best, a.kp);
+  score_keys<CT, SPAN>(
+      qs, cent, D, n_local, [&](int j) { return c0 + j; },
+      [&](int j) { return ends ? (int64_t)ends[c0 + j] <= lim : c0 + j < vis; }, keys + c0);
 
   if (a.S > 1) {
-    uint64_t* mine = a.ws_keys + (i * a.S + s) * (int64_t)a.K;
-    for (int j = threadIdx.x; j < a.K; j += LSA_BLOCK) mine[j] = best[j];
-    __threadfence();
     __syncthreads();
-    if (threadIdx.x == 0) is_last = (atomicAdd(&a.ws_count[i], 1) == a.S - 1);
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    if (threadIdx.x == 0) a.ws_count[i] = 0;  // every split has arrived: reset for the next launch
-    const uint64_t* all = a.ws_keys + i * a.S * (int64_t)a.K;
-    for (int j = threadIdx.x; j < a.S * a.K; j += LSA_BLOCK) keys[j] = all[j];
-    __syncthreads();
-    merge_sorted_lists(keys, a.S, a.K, best);
+    uint64_t* mine = a.ws_keys + i * (int64_t)a.rows;
+    for (int j = threadIdx.x; j < n_local; j += LSA_BLOCK) coherent_store_u64(mine + c0 + j, keys[c0 + j]);
+    if (!arrive_last(&a.ws_count[i], a.S, &flag)) return;
+    for (int jb = 0; jb < a.rows; jb += 4 * LSA_BLOCK) {  // four coherent loads in flight per thread
+      uint64_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = jb + u * LSA_BLOCK + threadIdx.x;
+        v[u] = coherent_load_u64(mine + (j < a.rows ? j : 0));
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = jb + u * LSA_BLOCK + threadIdx.x;
+        if (j < a.rows) keys[j] = v[u];
+      }
+    }
   }
+  __syncthreads();
+  block_topk_sorted(keys, a.rows, a.K, a.kp, best, &tks, &st);
   int32_t* pk = (int32_t*)keys;
   for (int j = threadIdx.x; j < a.K; j += LSA_BLOCK) pk[j] = key_column(u_to_key(best[j]));
   __syncthreads();
   const int width = a.top_k + a.window + a.sink;
   const int32_t* tab = a.members + t * a.rows * (int64_t)a.cap;
+  int32_t* stage = a.stage ? (int32_t*)(smem + ((a.rows + a.kp + 1) & ~1)) : nullptr;  // 16-byte aligned
   const int len = expand_walk(pk, a.K, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k,
-                              a.lists + i * width, width, scan);
+                              a.lists + i * width, width, scan, stage);
   if (threadIdx.x == 0) a.lengths[i] = len;
 }
 
@@ -240,6 +252,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
   constexpr int D = 16 * SPAN;
   extern __shared__ uint64_t smem[];
   __shared__ RadixState st;
+  __shared__ TopkScratch tks;
   __shared__ int scan[LSA_WAVES];
   uint64_t* keys = smem;                    // [max(nodes_pow2, cand_pow2)]
   uint64_t* best = keys + max(a.nodes_pow2, a.cand_pow2);  // [max(beam_pow2, top_pow2)]
@@ -257,18 +270,13 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
   score_slice_keys<CT, SPAN>(qs, ncent, D, 0, a.n_nodes, a.n_nodes, keys);
   __syncthreads();
   const int beam = min(a.beam, a.n_nodes);
-  {
-    auto get = [&](int j) -> uint64_t { return keys[j]; };
-    radix_select(get, a.n_nodes, beam, &st);
-    radix_collect(get, a.n_nodes, beam, &st, best);
-  }
-  for (int j = beam + threadIdx.x; j < a.beam_pow2; j += LSA_BLOCK) best[j] = 0;
-  __syncthreads();
-  bitonic_sort_desc(best, a.beam_pow2);
+  block_topk_sorted(keys, a.n_nodes, beam, a.beam_pow2, best, &tks, &st);
 
-  // level 0 candidates: the kept nodes' children, then the uncovered visible buckets
-  const int visible = visible_count(position, a.rows, a.cluster_block, a.block_buckets,
-                                    a.ends ? a.ends + t * a.rows : nullptr);
+  // level 0 candidates: the kept nodes' children, then the uncovered visible buckets (none
+  // when the nodes cover every bucket, which needs no visibility count)
+  const int visible = a.covered >= a.rows ? a.rows
+                                          : visible_count(position, a.rows, a.cluster_block, a.block_buckets,
+                                                          a.ends ? a.ends + t * a.rows : nullptr);
   const int n_fresh = max(0, visible - a.covered);
   const int n_kids = beam * a.node_size;
   const int n_cand = n_kids + n_fresh;
@@ -291,31 +299,16 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
   }
   __syncthreads();
   const CT* bcent = (const CT*)a.centroids + t * (int64_t)a.rows * D;
-  for (int j = grp; j < a.cand_pow2; j += LSA_BLOCK / 16) {
-    const int32_t c = cand[j];
-    uint64_t u = 0;
-    if (c >= 0) {
-      const float s = canonical_score<CT, SPAN>(qs, bcent + (int64_t)c * D, p);
-      u = key_to_u(pack_key(s, c));
-    }
-    if (p == 0) keys[j] = u;
-  }
+  score_keys<CT, SPAN>(qs, bcent, D, a.cand_pow2, [&](int j) { return cand[j]; }, keys);
   __syncthreads();
   const int k = min(a.top_p, a.cand_pow2);
-  {
-    auto get = [&](int j) -> uint64_t { return keys[j]; };
-    radix_select(get, a.cand_pow2, k, &st);
-    radix_collect(get, a.cand_pow2, k, &st, best);
-  }
-  for (int j = k + threadIdx.x; j < a.top_pow2; j += LSA_BLOCK) best[j] = 0;
-  __syncthreads();
-  bitonic_sort_desc(best, a.top_pow2);
+  block_topk_sorted(keys, a.cand_pow2, k, a.top_pow2, best, &tks, &st);
   for (int j = threadIdx.x; j < a.top_p; j += LSA_BLOCK) cand[j] = j < k ? key_column(u_to_key(best[j])) : -1;
   __syncthreads();
   const int width = a.top_k + a.window + a.sink;
   const int32_t* tab = a.members + t * (int64_t)a.rows * a.cap;
   const int len = expand_walk(cand, a.top_p, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k,
-                              a.lists + i * width, width, scan);
+                              a.lists + i * width, width, scan, nullptr);
   if (threadIdx.x == 0) a.lengths[i] = len;
 }
 
@@ -396,6 +389,26 @@ int check_dtype(int dtype) {
   return LSA_OK;
 }
 
+// The scoring loads a lane's D/16 centroid elements with vector loads and the expansion
+// loads member rows as 16-byte vectors when cap % 32 == 0: both need aligned tables.
+int check_query_aligned(const void* q, int q_dtype, int D) {
+  size_t need = (size_t)(D / 16) * (q_dtype == LSA_F32 ? 4 : 2);
+  need = need > 16 ? 16 : need;
+  LSA_REQUIRE(((uintptr_t)q % need) == 0, LSA_ERR_ALIGN, "query rows must be %zu-byte aligned", need);
+  return LSA_OK;
+}
+
+int check_aligned(const void* centroids, int D, int score_mode, const int32_t* members, int cap) {
+  const size_t esize = score_mode == LSA_SCORE_F32 ? 4 : 2;
+  size_t need = (size_t)(D / 16) * esize;
+  need = need > 16 ? 16 : need;
+  LSA_REQUIRE(centroids == nullptr || ((uintptr_t)centroids % need) == 0, LSA_ERR_ALIGN,
+              "centroid table must be %zu-byte aligned", need);
+  LSA_REQUIRE(members == nullptr || cap % 32 != 0 || ((uintptr_t)members % 16) == 0, LSA_ERR_ALIGN,
+              "member table must be 16-byte aligned");
+  return LSA_OK;
+}
+
 }  // namespace
 
 #define LSA_TRY(expr)            \
@@ -426,6 +439,7 @@ extern "C" int lsa_score_rows(const void* queries, int q_dtype, int64_t R, int32
   LSA_TRY(check_dtype(q_dtype));
   LSA_TRY(check_dim(D));
   LSA_REQUIRE(score_mode == LSA_SCORE_BF16 || score_mode == LSA_SCORE_F32, LSA_ERR_DTYPE, "bad score mode");
+  LSA_TRY(check_query_aligned(queries, q_dtype, D));
   LSA_REQUIRE(R >= 0 && G >= 1 && N >= 0 && R * G <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_score_rows: bad sizes");
   if (R * G == 0 || N == 0) return LSA_OK;
   LSA_REQUIRE((N + 15) / 16 <= 65535, LSA_ERR_SHAPE, "lsa_score_rows: %d columns exceed the grid", N);
@@ -510,6 +524,7 @@ extern "C" int lsa_expand(const void* picks, int picks_are_keys, int64_t R, int3
                           int32_t* lengths, void* stream) {
   LSA_REQUIRE(picks && members && positions && lists && lengths, LSA_ERR_NULL, "lsa_expand: NULL pointer");
   LSA_TRY(check_tables(rows, cap, row_tables, group_tables));
+  LSA_TRY(check_aligned(nullptr, 16, LSA_SCORE_BF16, members, cap));
   LSA_REQUIRE(R >= 0 && G >= 1 && P >= 0 && P <= 2 * kMaxLdsKeys, LSA_ERR_SHAPE, "lsa_expand: bad sizes (P=%d)", P);
   LSA_REQUIRE(window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE, "lsa_expand: window/sink/top_k must be >= 0");
   LSA_REQUIRE(R * G <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_expand: too many rows");
@@ -531,9 +546,9 @@ extern "C" int lsa_expand(const void* picks, int picks_are_keys, int64_t R, int3
 static int flat_picks(int32_t top_p, int32_t rows) { return top_p < rows ? top_p : rows; }
 
 extern "C" size_t lsa_select_flat_scratch_bytes(int64_t R, int32_t G, int32_t top_p, int32_t N, int32_t splits) {
-  if (splits <= 1 || R <= 0 || G <= 0) return 0;
-  const int64_t K = flat_picks(top_p, N);
-  return (size_t)(R * G) * (size_t)splits * (size_t)K * sizeof(uint64_t);
+  (void)top_p;
+  if (splits <= 1 || R <= 0 || G <= 0 || N <= 0) return 0;
+  return (size_t)(R * G) * (size_t)N * sizeof(uint64_t);
 }
 
 extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D,
@@ -549,18 +564,19 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
   LSA_TRY(check_dim(D));
   LSA_TRY(check_tables(rows, cap, row_tables, group_tables));
   LSA_REQUIRE(score_mode == LSA_SCORE_BF16 || score_mode == LSA_SCORE_F32, LSA_ERR_DTYPE, "bad score mode");
+  LSA_TRY(check_aligned(centroids, D, score_mode, members, cap));
+  LSA_TRY(check_query_aligned(queries, q_dtype, D));
   LSA_REQUIRE(R >= 0 && G >= 1 && R * G <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_select_flat: bad sizes");
   LSA_REQUIRE(top_p >= 1 && window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE,
               "lsa_select_flat: top_p >= 1, window/sink/top_k >= 0");
   LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "lsa_select_flat: cluster_block_size must be >= 1");
-  LSA_REQUIRE(splits >= 1 && splits <= 256, LSA_ERR_SHAPE, "lsa_select_flat: splits in [1, 256], got %d", splits);
+  LSA_REQUIRE(splits >= 1 && splits <= 256 && splits <= rows, LSA_ERR_SHAPE,
+              "lsa_select_flat: splits in [1, min(256, rows)], got %d", splits);
   const int K = flat_picks(top_p, rows);
   const int cs = (rows + splits - 1) / splits;
   const int kp = next_pow2(K);
-  const int keys_cap = cs > splits * K ? cs : splits * K;
-  LSA_REQUIRE(keys_cap + kp <= kMaxLdsKeys, LSA_ERR_SHAPE,
-              "lsa_select_flat: %d columns per split / %d merged keys + %d picks exceed %d LDS keys", cs, splits * K,
-              kp, kMaxLdsKeys);
+  LSA_REQUIRE(rows + kp <= kMaxLdsKeys, LSA_ERR_SHAPE,
+              "lsa_select_flat: %d columns + %d picks exceed %d LDS keys", rows, kp, kMaxLdsKeys);
   const size_t need = lsa_select_flat_scratch_bytes(R, G, top_p, rows, splits);
   LSA_REQUIRE(need == 0 || (scratch && counters && scratch_bytes >= need), LSA_ERR_WORKSPACE,
               "lsa_select_flat: counters/scratch missing or scratch %zu < %zu bytes", scratch_bytes, need);
@@ -570,11 +586,16 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
   a.centroids = centroids; a.members = members; a.ends = ends; a.positions = positions;
   a.cluster_block = cluster_block_size; a.block_buckets = block_buckets;
   a.K = K; a.kp = kp; a.window = window; a.sink = sink; a.top_k = top_k;
-  a.S = splits; a.cs = cs; a.keys_cap = keys_cap;
+  a.S = splits; a.cs = cs;
   a.ws_count = counters;
   a.ws_keys = need ? (uint64_t*)scratch : nullptr;
   a.lists = lists; a.lengths = lengths;
-  const size_t shmem = sizeof(uint64_t) * ((size_t)keys_cap + kp);
+  // the list row is staged in LDS when it fits beside the keys (coalesced row stores)
+  const int width = top_k + window + sink;
+  const size_t base_lds = sizeof(uint64_t) * (((size_t)rows + kp + 1) & ~(size_t)1);
+  const size_t stage_lds = sizeof(int32_t) * ((size_t)width + 4);
+  a.stage = (width % 4 == 0 && ((uintptr_t)lists % 16) == 0 && base_lds + stage_lds <= kMaxDynLds) ? 1 : 0;
+  const size_t shmem = base_lds + (a.stage ? stage_lds : 0);
   const dim3 grid((unsigned)(R * G), (unsigned)splits);
   const bool bf16 = score_mode == LSA_SCORE_BF16;
   hipStream_t s = (hipStream_t)stream;
@@ -599,6 +620,9 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
   LSA_TRY(check_dim(D));
   LSA_TRY(check_tables(rows, cap, row_tables, group_tables));
   LSA_REQUIRE(score_mode == LSA_SCORE_BF16 || score_mode == LSA_SCORE_F32, LSA_ERR_DTYPE, "bad score mode");
+  LSA_TRY(check_aligned(centroids, D, score_mode, members, cap));
+  LSA_TRY(check_aligned(node_centroids, D, score_mode, nullptr, cap));
+  LSA_TRY(check_query_aligned(queries, q_dtype, D));
   LSA_REQUIRE(R >= 0 && G >= 1 && R * G <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_select_tree: bad sizes");
   LSA_REQUIRE(n_nodes >= 1 && node_size >= 1 && beam_width >= 1 && top_p >= 1 && covered >= 0, LSA_ERR_SHAPE,
               "lsa_select_tree: n_nodes, node_size, beam_width, top_p >= 1");

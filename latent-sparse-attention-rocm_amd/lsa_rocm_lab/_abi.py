@@ -58,10 +58,11 @@ SIGNATURES = {
     "lsa_index_queries": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p]),
     "lsa_bucket_centroids": (_int, [_p, _int, _i64, _i64, _i64, _i32, _i32, _p, _i64, _i32, _i32, _int, _p, _p, _p]),
     "lsa_read_scratch_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
-    "lsa_read": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _i32, _int, _f32, _int, _i32,
-                        _p, _p, _sz, _p, _p]),
-    "lsa_read_chunked": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _i32, _i32, _f32, _p,
-                                _p]),
+    "lsa_read_tile_tokens": (_i32, [_int, _i32, _i32]),
+    "lsa_read": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _i32, _int,
+                        _f32, _int, _i32, _p, _p, _sz, _p, _p]),
+    "lsa_read_chunked": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _i32,
+                                _i32, _f32, _p, _p]),
 }
 
 

@@ -270,20 +270,19 @@ def flat_select_reference(
 
 
 def _select_splits(R: int, G: int, rows: int, top_p: int) -> int:
-    """Workgroups per (row, group) of the fused select: split the columns when there are
-    too few rows to fill the GPU (decode), keep >= 64 columns per split."""
+    """Workgroups per (row, group) of the fused select. A CU keeps only so many misses in
+    flight, so with few rows the centroid scan is cut into ~32-column slices on separate
+    CUs, whose keys the last slice to finish collects; with many rows each workgroup scores
+    its whole table. ``LSA_SELECT_SPLITS`` overrides."""
     env = os.environ.get("LSA_SELECT_SPLITS")
-    k = min(top_p, rows)
-    cap = max(1, min(4096 // max(k, 1), 256))
+    cap = max(1, min(rows, 256))
     if env:
         return max(1, min(int(env), cap))
     units = R * G
-    if units >= 256:
+    if units >= 256:  # enough rows to fill the GPU: one workgroup per (row, group)
         return 1
-    s = min(max(1, 512 // units), max(1, rows // 64), cap)
-    while s > 1 and math.ceil(rows / s) > 4096:
-        s -= 1
-    return max(1, s)
+    # few rows (decode): ~32 columns per workgroup, so the centroid scan spreads over CUs
+    return max(1, min(math.ceil(rows / 32), cap, max(1, 2048 // max(units, 1))))
 
 
 def _fused_select(index_queries, positions, buckets, config, top_k, score_dtype):

@@ -23,14 +23,26 @@ from lsa_rocm_lab import _abi
 DECODE_ROW_LIMIT = 32
 
 
-def _read_splits(units: int, width: int) -> int:
-    """Workgroups per (row, kv-head): split long lists when there are few rows."""
+MAX_SPLITS = 256
+
+
+def _read_splits(units: int, width: int, tile: int) -> int:
+    """Spans per (row, kv-head): with few rows (decode) a list is cut into spans of one
+    tile so ~every CU gets a workgroup; with many rows each list stays whole or nearly."""
     env = os.environ.get("LSA_READ_SPLITS")
     if env:
-        return max(1, min(int(env), 1024))
-    if units >= 512 or width <= 64:
-        return 1
-    return max(1, min(512 // units, math.ceil(width / 64), 1024))
+        return max(1, min(int(env), MAX_SPLITS))
+    tiles = max(1, math.ceil(width / tile))
+    return max(1, min(tiles, max(1, 4096 // max(units, 1)), MAX_SPLITS))
+
+
+def _kv_layout(k: torch.Tensor, v: torch.Tensor):
+    """K/V as the kernel reads them: rows of D contiguous elements at shared batch/token/
+    head strides, read in place (a cache view costs no copy); other layouts are made dense."""
+    aligned = all(x % 16 == 0 for x in (k.data_ptr(), v.data_ptr()))
+    if k.stride(-1) != 1 or v.stride(-1) != 1 or k.stride() != v.stride() or not aligned:
+        k, v = k.contiguous(), v.contiguous()
+    return k, v, k.stride(0), k.stride(1), k.stride(2)
 
 
 def _sparse_read(q, k, v, read_ids, lengths, scale, empty_nan: bool, splits: int | None = None):
@@ -40,7 +52,8 @@ def _sparse_read(q, k, v, read_ids, lengths, scale, empty_nan: bool, splits: int
     assert Hq % Hkv == 0, "query heads must group evenly onto KV heads"
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError(f"q/k/v dtypes differ: {q.dtype} {k.dtype} {v.dtype}")
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    q = q.contiguous()
+    k, v, sb, st, sh = _kv_layout(k, v)
     rows = B * Tq
     width = read_ids.shape[-1]
     per_head = Hkv > 1 and lengths.numel() == rows * Hkv and lengths.numel() != rows
@@ -54,12 +67,13 @@ def _sparse_read(q, k, v, read_ids, lengths, scale, empty_nan: bool, splits: int
     if rows == 0:
         return out
     if splits is None:
-        splits = _read_splits(rows * Hkv, width)
+        tile = _abi.size("lsa_read_tile_tokens", _abi.dtype_code(q.dtype), D, Hq // Hkv)
+        splits = _read_splits(rows * Hkv, width, max(tile, 1))
     nbytes = _abi.size("lsa_read_scratch_bytes", rows, Hq, Hkv, D, splits)
     ws = _abi.Workspace.get(q.device, "read", nbytes)
     counters = _abi.Counters.get(q.device, rows * Hkv) if nbytes else None
     _abi.call("lsa_read", q.data_ptr(), k.data_ptr(), v.data_ptr(), _abi.dtype_code(q.dtype), B, Tq, Tk, Hq, Hkv, D,
-              ids.data_ptr(), lens.data_ptr(), width, 1 if per_head else 0, float(D ** -0.5 if scale is None else scale),
+              sb, st, sh, ids.data_ptr(), lens.data_ptr(), width, 1 if per_head else 0, float(D ** -0.5 if scale is None else scale),
               1 if empty_nan else 0, splits, _abi.ptr(counters), _abi.ptr(ws), nbytes, out.data_ptr(),
               _abi.stream(q.device))
     return out
@@ -104,11 +118,12 @@ def sparse_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale=None, chunk_s
     width = chunk_lists.shape[-1]
     ids = chunk_lists.to(torch.int32).reshape(B * C * Hkv, width).contiguous()
     lens = chunk_lengths.to(device=q.device, dtype=torch.int32).reshape(B * C * Hkv).contiguous()
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    q = q.contiguous()
+    k, v, sb, st, sh = _kv_layout(k, v)
     out = torch.empty_like(q)
     if B * T == 0:
         return out
     _abi.call("lsa_read_chunked", q.data_ptr(), k.data_ptr(), v.data_ptr(), _abi.dtype_code(q.dtype), B, T, Tk, Hq,
-              Hkv, D, ids.data_ptr(), lens.data_ptr(), width, chunk_size,
+              Hkv, D, sb, st, sh, ids.data_ptr(), lens.data_ptr(), width, chunk_size,
               float(D ** -0.5 if scale is None else scale), out.data_ptr(), _abi.stream(q.device))
     return out

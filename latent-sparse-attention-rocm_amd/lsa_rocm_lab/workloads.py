@@ -82,7 +82,7 @@ def clustered(T: int, Hq: int, Hkv: int, D: int, n_clusters: int = 512, sigma: f
     cdev = centers.to(gen_device)
     idx = cluster_of_token.to(gen_device)
     base = torch.gather(cdev, 2, idx[..., None].expand(B, Hkv, T, D))  # [B, Hkv, T, D]
-    k = (base.permute(0, 2, 1, 3) + sigma * noise).to(dtype)
+    k = (base.permute(0, 2, 1, 3) + sigma * noise).to(dtype).contiguous()
     del base, noise
     v = torch.randn(B, T, Hkv, D, generator=gd, device=gen_device).to(dtype)
     return Clustered(q.to(device), k.to(device), v.to(device), centers, run_lengths, run_clusters)

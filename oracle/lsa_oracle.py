@@ -373,8 +373,8 @@ def sparse_read(q: np.ndarray, k: np.ndarray, v: np.ndarray, ids: np.ndarray, le
     returned fp32.
     """
     q = np.asarray(q, dtype=np.float64)
-    k = np.asarray(k, dtype=np.float64)
-    v = np.asarray(v, dtype=np.float64)
+    k = np.asarray(k)
+    v = np.asarray(v)
     b_, tq, hq, d = q.shape
     hkv = k.shape[2]
     group = hq // hkv
@@ -391,13 +391,15 @@ def sparse_read(q: np.ndarray, k: np.ndarray, v: np.ndarray, ids: np.ndarray, le
                 n = int(lengths[b, t, g] if per_head else lengths[b, t])
                 sel = row[: max(0, min(n, width))]
                 sel = sel[sel >= 0]
+                keys = k[b, sel, g].astype(np.float64)
+                vals = v[b, sel, g].astype(np.float64)
                 for h in range(g * group, (g + 1) * group):
                     if sel.size == 0:
                         out[b, t, h] = np.nan if empty == "nan" else 0.0
                         continue
-                    s = (k[b, sel, g] @ q[b, t, h]) * scale
+                    s = (keys @ q[b, t, h]) * scale
                     p = np.exp(s - s.max())
-                    out[b, t, h] = (p @ v[b, sel, g]) / p.sum()
+                    out[b, t, h] = (p @ vals) / p.sum()
     return out.astype(np.float32)
 
 

@@ -35,8 +35,8 @@ def test_version_and_error_string():
 
 def test_null_pointers_rejected_before_launch():
     with pytest.raises(ValueError, match="NULL"):
-        _abi.call("lsa_read", None, None, None, 1, 1, 1, 8, 8, 2, 64, None, None, 4, 0, 0.1, 0, 1, None, None, 0,
-                  None, None)
+        _abi.call("lsa_read", None, None, None, 1, 1, 1, 8, 8, 2, 64, 1024, 128, 64, None, None, 4, 0, 0.1, 0, 1, None,
+                  None, 0, None, None)
     with pytest.raises(ValueError, match="NULL"):
         _abi.call("lsa_select_flat", None, 1, 1, 8, 128, None, None, None, 512, 256, 0, 1, 0, None, 64, 1, 32, 0, 0,
                   8192, 8, None, None, 0, None, None, None)
@@ -50,21 +50,21 @@ def test_bad_index_dim_rejected(dim):
 
 def test_bad_head_dim_group_and_alignment_rejected():
     with pytest.raises(ValueError, match="head dim"):
-        _abi.call("lsa_read", 16, 16, 16, 1, 1, 1, 8, 8, 2, 48, 16, 16, 4, 0, 0.1, 0, 1, None, None, 0, 16, None)
+        _abi.call("lsa_read", 16, 16, 16, 1, 1, 1, 8, 8, 2, 48, 768, 96, 48, 16, 16, 4, 0, 0.1, 0, 1, None, None, 0, 16, None)
     with pytest.raises(ValueError, match="group"):
-        _abi.call("lsa_read", 16, 16, 16, 1, 1, 1, 8, 6, 4, 64, 16, 16, 4, 0, 0.1, 0, 1, None, None, 0, 16, None)
+        _abi.call("lsa_read", 16, 16, 16, 1, 1, 1, 8, 6, 4, 64, 2048, 256, 64, 16, 16, 4, 0, 0.1, 0, 1, None, None, 0, 16, None)
     with pytest.raises(ValueError, match="aligned"):
-        _abi.call("lsa_read", 18, 16, 16, 1, 1, 1, 8, 8, 2, 64, 16, 16, 4, 0, 0.1, 0, 1, None, None, 0, 16, None)
+        _abi.call("lsa_read", 18, 16, 16, 1, 1, 1, 8, 8, 2, 64, 1024, 128, 64, 16, 16, 4, 0, 0.1, 0, 1, None, None, 0, 16, None)
 
 
 def test_workspace_required_for_split_reads():
     need = _abi.size("lsa_read_scratch_bytes", 1, 32, 8, 128, 32)
     assert need == 8 * 32 * 4 * 130 * 4
     with pytest.raises(_abi.LsaError, match="WORKSPACE"):
-        _abi.call("lsa_read", 16, 16, 16, 1, 1, 1, 8, 32, 8, 128, 16, 16, 4, 1, 0.1, 0, 32, None, None, 0, 16, None)
+        _abi.call("lsa_read", 16, 16, 16, 1, 1, 1, 8, 32, 8, 128, 8192, 1024, 128, 16, 16, 4, 1, 0.1, 0, 32, None, None, 0, 16, None)
     with pytest.raises(_abi.LsaError, match="WORKSPACE"):  # scratch without counters
-        _abi.call("lsa_read", 16, 16, 16, 1, 1, 1, 8, 32, 8, 128, 16, 16, 4, 1, 0.1, 0, 32, None, 16, need, 16, None)
-    assert _abi.size("lsa_select_flat_scratch_bytes", 1, 8, 32, 512, 8) == 8 * 8 * 32 * 8
+        _abi.call("lsa_read", 16, 16, 16, 1, 1, 1, 8, 32, 8, 128, 8192, 1024, 128, 16, 16, 4, 1, 0.1, 0, 32, None, 16, need, 16, None)
+    assert _abi.size("lsa_select_flat_scratch_bytes", 1, 8, 32, 512, 8) == 8 * 512 * 8  # every column key
     assert _abi.size("lsa_select_flat_scratch_bytes", 1, 8, 32, 512, 1) == 0
 
 

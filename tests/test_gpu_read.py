@@ -216,3 +216,22 @@ def test_dense_decode_and_chunk_equal_prefill_tail():
     assert torch.allclose(tail.float(), prefill[:, -16:].float(), atol=2e-2, rtol=2e-2)
     with pytest.raises(ValueError):
         pipeline.dense_read(q, k[:, :32], v[:, :32], scale)
+
+
+def test_kv_views_are_read_in_place():
+    """K/V given as views into a larger cache (token stride of a longer buffer, every other
+    kv-head) give the same output as their dense copies, and nothing is copied."""
+    q, k, v = geometry(torch.bfloat16, T=256, Hq=8, Hkv=4, D=128)
+    big_k = torch.zeros(1, 512, 4, 128, dtype=torch.bfloat16)
+    big_v = torch.zeros(1, 512, 4, 128, dtype=torch.bfloat16)
+    big_k[:, :256], big_v[:, :256] = k, v
+    g = torch.Generator().manual_seed(29)
+    ids = torch.randint(-1, 256, (1, 1, 2, 600), generator=g, dtype=torch.int32)
+    lengths = torch.tensor([[[600, 333]]], dtype=torch.int32)
+    bk, bv = big_k.to(DEV), big_v.to(DEV)
+    kview, vview = bk[:, :256, ::2], bv[:, :256, ::2]  # 2 kv-heads, strided tokens and heads
+    assert not kview.is_contiguous()
+    got = sparse_read_auto(q[:, -1:].to(DEV)[:, :, :4].contiguous(), kview, vview, ids.to(DEV), lengths.to(DEV))
+    want = oracle.sparse_read(q[:, -1:, :4].float().numpy(), k[:, :, ::2].float().numpy(),
+                              v[:, :, ::2].float().numpy(), ids.numpy(), lengths.numpy())
+    check(got, want, torch.bfloat16)

@@ -321,3 +321,48 @@ def test_per_kv_head_flat_select_clustered():
         for impl, (l, n) in results.items():
             assert np.array_equal(_np(l[:, g]), want_l), f"{impl} kv-head {g}"
             assert np.array_equal(_np(n[:, g]), want_n), f"{impl} kv-head {g}"
+
+
+@pytest.mark.parametrize("splits", ["1", "2", "3", "16", "64"])
+def test_fused_split_counts_and_repeat_launches(splits, monkeypatch):
+    """Every split count of the fused select gives the oracle's lists, on two launches in a
+    row with different queries (the split keys and arrival counters are reused)."""
+    T, Hq, Hkv, D = 8192, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=128, seed=4, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    config = workloads.FLAT_32K
+    monkeypatch.setenv("LSA_SELECT_SPLITS", splits)
+    for rows in (slice(-1, None), slice(-3, -1)):
+        idx = pipeline.index_queries(data.q[:, rows], Hkv)[0]
+        positions = torch.full((idx.shape[0],), T - 1, dtype=torch.int32)
+        got_l, got_n = _switched("fused", idx, positions.to(DEV), buckets, config)
+        for g in range(Hkv):
+            cent = buckets.centroids[g].float().cpu().numpy()
+            want_l, want_n = oracle.flat_select(_np(idx[:, g]), positions.numpy(), cent, _np(buckets.members[g]),
+                                                cluster_block_size=64, block_buckets=1, top_p=32, top_k=8192,
+                                                window=0, sink=0, mode="bf16", ends=_np(buckets.ends[g]))
+            assert np.array_equal(_np(got_l[:, g]), want_l), (splits, g)
+            assert np.array_equal(_np(got_n[:, g]), want_n), (splits, g)
+
+
+@pytest.mark.parametrize("rows_visible", [512, 20])
+def test_fused_all_tied_scores_break_to_lower_bucket(rows_visible):
+    """A zero index query ties every score: the picks are the lowest visible bucket ids, in
+    ascending order (the packed key's column term), and EMPTY past the visible ones."""
+    T, Hkv, D = 32768, 2, 128
+    cap = 64
+    members = torch.arange(512 * cap, dtype=torch.int32).view(512, cap).expand(Hkv, 512, cap).contiguous()
+    cent = torch.randn(Hkv, 512, D, generator=torch.Generator().manual_seed(9)).bfloat16()
+    buckets = Buckets(cent.to(DEV), members.to(DEV), torch.full((Hkv, 512), cap, dtype=torch.int32).to(DEV))
+    config = PortConfig(cluster_block_size=64, bucket_size=64, bucket_cap=64, top_p=32, top_k=4096,
+                        window_size=0, sink_size=0)
+    pos = torch.tensor([rows_visible * 64 - 1], dtype=torch.int32)
+    idx = torch.zeros(1, Hkv, D, device=DEV)
+    got_l, got_n = _switched("fused", idx, pos.to(DEV), buckets, config)
+    for g in range(Hkv):
+        want_l, want_n = oracle.flat_select(np.zeros((1, D), np.float32), pos.numpy(), cent[g].float().numpy(),
+                                            members[g].numpy(), cluster_block_size=64, block_buckets=1, top_p=32,
+                                            top_k=4096, window=0, sink=0, mode="bf16")
+        assert np.array_equal(_np(got_l[:, g]), want_l) and np.array_equal(_np(got_n[:, g]), want_n)
+        first = min(32, rows_visible - 1)  # a position sees the closed blocks before its own
+        assert np.array_equal(want_l[0][: first * cap], np.arange(first * cap))
