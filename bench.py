@@ -14,8 +14,10 @@ Timing: the K timed steps are replayed from HIP graphs (one graph = a rotation o
 ``--rotate`` steps, each on its own resident copy of the cache, so consecutive steps
 never find their K/V rows in the 256 MiB MALL) between ``torch.cuda.synchronize()``
 brackets; ``value`` = wall µs per step. The dominant kernel (the sparse read) is also
-timed alone, with HIP events around each launch on the stream it runs on, for the
-roofline: algorithmic bytes (gathered K and V rows) / average launch duration.
+timed alone for the roofline: a HIP graph of back-to-back launches over the rotation,
+HIP events around its replays on the stream it runs on; algorithmic bytes (gathered K
+and V rows) / average launch duration (which includes the dispatch gap, so it is an upper
+bound on the kernel's own duration, which rocprofv3's kernel trace reports).
 
 Comparators in the same run: dense SDPA decode on the same GPU (same rotation), the
 chunked prefill (configs' prefill row) as tok/s beside dense causal SDPA, and the CPU
@@ -64,6 +66,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="also run 3 plain device copies of this many MiB (calibrates HBM byte counters)")
     return ap.parse_args()
 
 
@@ -135,6 +139,33 @@ def event_launch_times(fn, n: int, torch) -> list[float]:
         b.record()
     torch.cuda.synchronize()
     return [a.elapsed_time(b) for a, b in evs]
+
+
+def profiled_traffic() -> int | None:
+    """HBM bytes per read launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    (profiles/read_decode_flat32k_pmc.md); None when it is absent."""
+    path = ROOT / "profiles" / "read_decode_flat32k_pmc.md"
+    if not path.is_file():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch read_kernel:"):
+            return int(line.split(":")[1])
+    return None
+
+
+def graph_launch_us(fn, n: int, replays: int, torch) -> float:
+    """Average µs per launch of fn(0..n-1) replayed back to back from one HIP graph, timed
+    with HIP events on the stream the graph runs on (kernel time plus the dispatch gap)."""
+    g = capture(fn, n, torch)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (n * replays)
 
 
 def dense_decode_fn(torch):
@@ -241,23 +272,20 @@ def main() -> int:
     torch.cuda.synchronize()
     warm_us = (time.perf_counter() - w0) / (max(1, args.steps // R) * R) * 1e6
 
-    # ---- dominant kernel alone (the sparse read), HIP events around each launch
+    # ---- the two kernels alone: each replayed back to back from a HIP graph over the
+    # rotation, HIP events around the replays on the stream they run on
     sel = [pipeline.flat_select(pipeline.index_queries(c.q, HKV)[0], c.pos, c.buckets, config) for c in caches]
+    idxs = [pipeline.index_queries(c.q, HKV)[0] for c in caches]
     torch.cuda.synchronize()
     read_fn = lambda i: sparse_read_auto(caches[i % R].q, caches[i % R].k, caches[i % R].v,
                                          sel[i % R][0].unsqueeze(0), sel[i % R][1].unsqueeze(0), D ** -0.5)
-    event_launch_times(read_fn, 32, torch)
-    read_ms = event_launch_times(read_fn, args.kernel_launches, torch)
-    read_us = statistics.mean(read_ms) * 1e3
-    read_p50 = statistics.median(read_ms) * 1e3
-    sel_fn = lambda i: pipeline.flat_select(pipeline.index_queries(caches[i % R].q, HKV)[0], caches[i % R].pos,
-                                            caches[i % R].buckets, config)
-    event_launch_times(sel_fn, 32, torch)
-    sel_ms = event_launch_times(sel_fn, args.kernel_launches, torch)
-    sel_us = statistics.mean(sel_ms) * 1e3
+    sel_fn = lambda i: pipeline.flat_select(idxs[i % R], caches[i % R].pos, caches[i % R].buckets, config)
+    reps = max(1, args.kernel_launches // R)
+    read_us = graph_launch_us(read_fn, R, reps, torch)
+    sel_us = graph_launch_us(sel_fn, R, reps, torch)
     achieved = gathered / (read_us * 1e-6) / 1e9
-    log(f"read kernel {read_us:.2f} us mean ({read_p50:.2f} p50): {achieved:.0f} GB/s on gathered bytes; "
-        f"select (index queries + fused select) {sel_us:.2f} us")
+    log(f"read kernel {read_us:.2f} us per launch: {achieved:.0f} GB/s on gathered bytes; "
+        f"fused select {sel_us:.2f} us per launch")
 
     # ---- dense SDPA comparator on the same rotation
     dense = {"backend": None}
@@ -381,6 +409,14 @@ def main() -> int:
                   "read_max_abs": float(err.max()), "read_mean_abs": float(err.mean())}
         log(f"cpu {cpu} parity {parity}")
 
+    if args.copy_mib:  # a plain copy of known size, for scaling FETCH_SIZE / WRITE_SIZE counters
+        src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {args.copy_mib} MiB three times")
+
     line = {
         "metric": METRIC,
         "value": round(us_step, 3),
@@ -403,8 +439,9 @@ def main() -> int:
         "warm_us_per_step": round(warm_us, 3),
         "select_us": round(sel_us, 3),
         "read_us": round(read_us, 3),
+        "kernel_timing": "per launch, HIP graph of back-to-back launches over the rotation, HIP events",
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
                      "kernel": "read_kernel<bf16,128,4>", "bytes_per_launch": gathered},
         "dense": dense,
         "speedup_vs_dense": None if speedup is None else round(speedup, 3),

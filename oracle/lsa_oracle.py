@@ -11,7 +11,7 @@ latent-sparse-attention @ 5ebea732d639576d2a7579b0de40e6252f9001f5), the
 restatement follows the reference's call sites and docs, and the header of the
 function says what pins it.
 
-Pinning (what each function is checked against in tests/test_oracle_*.py):
+Pinning (what each function is checked against in tests/test_oracle.py):
   ordered_bits / pack_keys       monotone vs float order (argsort), ties -> lower column,
                                  EMPTY sorts last; closed form on special values
   best_first_keys                numpy/torch full sort + slice (library routine)

@@ -1,0 +1,275 @@
+"""Pins the CPU oracle before it is trusted as the checker (CPU only, no GPU).
+
+Every oracle function is checked against something that does not share its code: a
+library routine (torch sort / SDPA / bf16 conversion / normalize), exact fp64 or rational
+arithmetic, or a brute-force statement of the reference's rule on tiny inputs. Each check
+is chosen so that a plausible slip (a dropped term, a flipped tie rule, an off-by-one in
+the window, a transposed operand) fails it. The reference ships no golden vectors for this
+path (its tests regenerate seeded tensors through the absent upstream package), so the
+fixtures under tests/golden/ are written from this oracle and pinned here by these checks.
+"""
+
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+
+RNG = np.random.default_rng(20261201)
+
+
+# ----------------------------------------------------------------------------- keys
+
+
+def brute_order(scores, length):
+    """Best-first columns by the packed-key contract: score descending, a tie to the lower
+    column (reference select_fused.py:71-77 key layout), columns < length only."""
+    cols = [c for c in range(length)]
+    return sorted(cols, key=lambda c: (-float(scores[c]), c))
+
+
+def test_ordered_bits_is_the_float_order():
+    vals = np.array([-np.inf, -3e38, -1.0, -1e-30, -1e-45, -0.0, 0.0, 1e-45, 1e-30, 1.0, 3e38, np.inf],
+                    dtype=np.float32)
+    bits = oracle.ordered_bits(vals)
+    assert (np.diff(bits.astype(np.int64)) > 0).all()  # strictly increasing, -0.0 just below +0.0
+    x = RNG.standard_normal(10_000).astype(np.float32) * 10.0 ** RNG.integers(-30, 30, 10_000)
+    order_bits = np.argsort(oracle.ordered_bits(x), kind="stable")
+    assert np.array_equal(np.sort(x, kind="stable"), x[order_bits])
+
+
+@pytest.mark.parametrize("rows,cols,top_p", [(3, 17, 5), (4, 64, 64), (2, 40, 100), (5, 128, 33)])
+def test_select_topk_scores_equals_brute_force(rows, cols, top_p):
+    scores = RNG.integers(-4, 5, (rows, cols)).astype(np.float32)  # many ties
+    lengths = RNG.integers(0, cols + 1, rows)
+    got = oracle.select_topk_scores(scores, lengths, top_p)
+    keep = min(top_p, cols)
+    assert got.shape == (rows, oracle.next_pow2(keep))
+    ids = oracle.unpack_ids(got)
+    for r in range(rows):
+        want = brute_order(scores[r], int(lengths[r]))[:keep]
+        assert ids[r, : len(want)].tolist() == want
+        assert (got[r, len(want):] == oracle.EMPTY).all()
+
+
+def test_all_tied_scores_pick_ids_in_ascending_order():
+    got = oracle.unpack_ids(oracle.select_topk_scores(np.zeros((2, 300), np.float32), np.array([300, 7]), 64))
+    assert got[0].tolist() == list(range(64))
+    assert got[1, :7].tolist() == list(range(7)) and (got[1, 7:] == -1).all()
+
+
+def test_best_first_keys_is_sort_slice_and_masks_unlisted():
+    keys = oracle.pack_keys(RNG.standard_normal((4, 50)).astype(np.float32), np.array([50, 20, 0, 50]))
+    want = torch.sort(torch.from_numpy(keys), dim=1, descending=True).values[:, :16].numpy()
+    assert np.array_equal(oracle.best_first_keys(keys, 16), want)
+    poisoned = keys.copy()
+    poisoned[:, 30:] = np.int64((1 << 63) - 1)  # unlisted slots hold garbage larger than any key
+    got = oracle.best_first_keys(poisoned, 16, counts=np.array([30, 30, 30, 30]))
+    masked = keys.copy()
+    masked[:, 30:] = oracle.EMPTY
+    want = torch.sort(torch.from_numpy(masked), dim=1, descending=True).values[:, :16].numpy()
+    assert np.array_equal(got, want)
+
+
+def test_unpack_round_trip():
+    scores = RNG.standard_normal((3, 33)).astype(np.float32)
+    keys = oracle.pack_keys(scores, np.array([33, 10, 0]))
+    ids = oracle.unpack_ids(keys)
+    assert np.array_equal(ids[0], np.arange(33))
+    assert np.array_equal(ids[1, :10], np.arange(10)) and (ids[1, 10:] == -1).all()
+    assert (ids[2] == -1).all()
+
+
+# ----------------------------------------------------------------------------- expansion
+
+
+def literal_expand(picks, members, position, window, sink, top_k):
+    """The reference's walk (select_fused.py:172-214) as a literal loop: picks in rank order,
+    slots in table order, keep sink <= id < window_start up to top_k; then the window, then
+    the sinks that are not in it."""
+    window_start = max(0, position + 1 - window)
+    kept = []
+    for b in picks:
+        if b < 0 or b >= len(members):
+            continue
+        for m in members[b]:
+            if m >= sink and m < window_start and len(kept) < top_k:
+                kept.append(int(m))
+    tail = list(range(window_start, position + 1)) + list(range(0, min(sink, window_start)))
+    row = kept + tail
+    return row + [-1] * (top_k + window + sink - len(row)), len(row)
+
+
+@pytest.mark.parametrize("window,sink,top_k", [(8, 2, 20), (0, 0, 50), (16, 4, 3), (100, 4, 64)])
+def test_expand_matches_literal_walk(window, sink, top_k):
+    members = RNG.integers(-1, 120, (12, 6)).astype(np.int32)
+    picks = RNG.integers(-1, 14, (5, 7)).astype(np.int32)  # includes -1 and out-of-range picks
+    positions = np.array([0, 3, 40, 90, 119])
+    lists, lengths = oracle.expand_in_order(picks, members, positions, window, sink, top_k)
+    for r in range(5):
+        want, n = literal_expand(picks[r].tolist(), members.tolist(), int(positions[r]), window, sink, top_k)
+        assert lists[r].tolist() == want and int(lengths[r]) == n
+
+
+def test_expand_invariants_causal_and_counts():
+    members = RNG.integers(0, 1000, (64, 16)).astype(np.int32)
+    picks = RNG.permutation(64)[None, :32].astype(np.int32)
+    for pos in (0, 5, 511, 999):
+        lst, n = oracle.expand_in_order(picks, members, np.array([pos]), 512, 4, 4096)
+        sel = lst[0, : n[0]]
+        assert (sel <= pos).all() and (lst[0, n[0]:] == -1).all()
+        window_start = max(0, pos + 1 - 512)
+        assert sorted(sel[sel >= window_start].tolist())[-(pos + 1 - window_start):] == list(range(window_start, pos + 1))
+
+
+def test_visible_counts_rule():
+    pos = np.array([-1, 0, 511, 512, 1023, 1024, 100000])
+    assert oracle.visible_counts(pos, 64, 512, 8).tolist() == [-8, 0, 0, 8, 8, 16, 64]
+    ends = np.array([10, 20, 20, 35, 64])
+    assert oracle.visible_counts(np.array([8, 9, 19, 34, 63, 500]), 5, 1, 1, ends).tolist() == [0, 1, 3, 4, 5, 5]
+
+
+# ----------------------------------------------------------------------------- numbers
+
+
+def test_bf16_round_matches_torch():
+    x = np.concatenate([RNG.standard_normal(5000).astype(np.float32) * 1e3,
+                        np.array([0.0, -0.0, 1.0, 1.00390625, 1.005859375, 65504.0, 3.4e38, 1e-40], np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(oracle.bf16_round(x).view(np.uint32), want.view(np.uint32))
+
+
+def test_canonical_scores_exact_on_integers_and_close_to_fp64():
+    q = RNG.integers(-8, 9, (3, 64)).astype(np.float32)
+    c = RNG.integers(-8, 9, (10, 64)).astype(np.float32)
+    assert np.array_equal(oracle.canonical_scores(q, c, "fp32"), (q.astype(np.int64) @ c.astype(np.int64).T))
+    q = RNG.standard_normal((4, 128)).astype(np.float32)
+    c = RNG.standard_normal((50, 128)).astype(np.float32)
+    for mode in ("fp32", "bf16"):
+        qq, cc = (q, c) if mode == "fp32" else (oracle.bf16_round(q), oracle.bf16_round(c))
+        exact = qq.astype(np.float64) @ cc.astype(np.float64).T
+        got = oracle.canonical_scores(q, c, mode).astype(np.float64)
+        assert np.all(np.abs(got - exact) <= np.abs(exact) * 2.0 ** -23 + 1e-30)
+
+
+def test_canonical_scores_follow_the_documented_order():
+    """fp32 rounding happens once, after the fp64 tree: a rational computation of the same
+    value rounds to the same float."""
+    q = RNG.standard_normal((2, 32)).astype(np.float32)
+    c = RNG.standard_normal((3, 32)).astype(np.float32)
+    got = oracle.canonical_scores(q, c, "fp32")
+    for i in range(2):
+        for j in range(3):
+            exact = sum(Fraction(float(a)) * Fraction(float(b)) for a, b in zip(q[i], c[j]))
+            assert abs(float(got[i, j]) - float(exact)) <= abs(float(exact)) * 2.0 ** -24 + 1e-38
+
+
+def test_index_queries_is_group_mean():
+    q = RNG.standard_normal((2, 128, 8, 16)).astype(np.float32)
+    got = oracle.index_queries(q, 2, chunk=4)
+    want = torch.from_numpy(q).double().view(2, 32, 4, 2, 4, 16).mean(dim=(2, 4)).numpy()
+    assert got.shape == (2, 32, 2, 16)
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-6)
+    exact = np.full((1, 8, 4, 4), 0.5, np.float32)  # exactly representable sums and quotient
+    assert np.array_equal(oracle.index_queries(exact, 2, 2), np.full((1, 4, 2, 4), 0.5, np.float32))
+
+
+def test_bucket_centroids_mean_and_normalized():
+    keys = RNG.standard_normal((40, 8)).astype(np.float32)
+    members = np.array([[0, 1, 2, -1], [5, -1, 7, 9], [-1, -1, -1, -1]], np.int32)
+    mean = oracle.bucket_centroids(keys, members, "mean")
+    assert np.allclose(mean[0], keys[[0, 1, 2]].mean(0), atol=1e-6)
+    assert np.allclose(mean[1], keys[[5, 7, 9]].mean(0), atol=1e-6)
+    assert (mean[2] == 0).all()
+    norm = oracle.bucket_centroids(keys, members, "normalized")
+    want = F.normalize(torch.from_numpy(keys[[5, 7, 9]]).sum(0, keepdim=True).double(), dim=-1).numpy()[0]
+    assert np.allclose(norm[1], want, atol=1e-6)
+
+
+# ----------------------------------------------------------------------------- reading
+
+
+def test_sparse_read_full_causal_equals_torch_sdpa():
+    T, Hq, Hkv, D = 24, 4, 2, 16
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(1, T, h, D, generator=g) for h in (Hq, Hkv, Hkv))
+    ids = np.tile(np.arange(T, dtype=np.int32), (T, 1))
+    ids = np.where(ids <= np.arange(T)[:, None], ids, -1)[None]
+    lengths = (np.arange(T) + 1)[None]
+    got = oracle.sparse_read(q.numpy(), k.numpy(), v.numpy(), ids, lengths)
+    kk = k.repeat_interleave(2, dim=2).permute(0, 2, 1, 3).double()
+    vv = v.repeat_interleave(2, dim=2).permute(0, 2, 1, 3).double()
+    want = F.scaled_dot_product_attention(q.permute(0, 2, 1, 3).double(), kk, vv, is_causal=True)
+    assert np.allclose(got, want.permute(0, 2, 1, 3).numpy(), atol=1e-6)
+
+
+def test_sparse_read_edge_semantics():
+    q = RNG.standard_normal((1, 2, 2, 8)).astype(np.float32)
+    k = RNG.standard_normal((1, 10, 1, 8)).astype(np.float32)
+    v = RNG.standard_normal((1, 10, 1, 8)).astype(np.float32)
+    dup = np.array([[[4, 4, -1], [-1, -1, -1]]], np.int32)
+    lengths = np.array([[3, 0]])
+    out = oracle.sparse_read(q, k, v, dup, lengths)
+    assert np.allclose(out[0, 0, 0], v[0, 4, 0]) and np.allclose(out[0, 0, 1], v[0, 4, 0])  # duplicate -> V row
+    assert (out[0, 1] == 0).all()
+    assert np.isnan(oracle.sparse_read(q, k, v, dup, lengths, empty="nan")[0, 1]).all()
+    # duplicates count per occurrence: ids [1, 1, 2] weight row 1 twice
+    ids = np.array([[[1, 1, 2], [1, 2, -1]]], np.int32)
+    out = oracle.sparse_read(q, k, v, ids, np.array([[3, 2]]))
+    s = (k[0, [1, 1, 2], 0] @ q[0, 0, 0]) / np.sqrt(8.0)
+    p = np.exp(s - s.max()) / np.exp(s - s.max()).sum()
+    assert np.allclose(out[0, 0, 0], p @ v[0, [1, 1, 2], 0], atol=1e-6)
+
+
+def test_chunked_read_is_shared_list_plus_causal_block():
+    q = RNG.standard_normal((1, 8, 2, 8)).astype(np.float32)
+    k = RNG.standard_normal((1, 8, 1, 8)).astype(np.float32)
+    v = RNG.standard_normal((1, 8, 1, 8)).astype(np.float32)
+    chunk_ids = np.array([[[[-1, -1]], [[0, 2]]]], np.int32)  # [B, C=2, Hkv, W]
+    chunk_len = np.array([[[0], [2]]])
+    got = oracle.sparse_read_chunked(q, k, v, chunk_ids, chunk_len, chunk=4)
+    row = 6  # chunk 1: list {0, 2} + its causal block {4, 5, 6}
+    ids = np.array([[[[0, 2, 4, 5, 6]]]], np.int32)
+    want = oracle.sparse_read(q[:, [row]], k, v, ids, np.array([[[5]]]))
+    assert np.allclose(got[:, row], want[:, 0])
+
+
+# ----------------------------------------------------------------------------- selection end to end
+
+
+def test_flat_select_equals_brute_force():
+    q = RNG.standard_normal((3, 32)).astype(np.float32)
+    cents = RNG.standard_normal((20, 32)).astype(np.float32)
+    members = RNG.permutation(400).astype(np.int32).reshape(20, 20)
+    positions = np.array([399, 250, 100])
+    ends = np.arange(20, 401, 20)
+    lists, lengths = oracle.flat_select(q, positions, cents, members, cluster_block_size=1, block_buckets=1,
+                                        top_p=5, top_k=60, window=16, sink=2, mode="fp32", ends=ends)
+    exact = q.astype(np.float64) @ cents.astype(np.float64).T
+    for r in range(3):
+        visible = int(np.sum(ends <= positions[r] + 1))
+        order = sorted(range(visible), key=lambda c: (-exact[r, c], c))[:5]
+        want, n = literal_expand(order, members.tolist(), int(positions[r]), 16, 2, 60)
+        assert lists[r].tolist() == want and int(lengths[r]) == n
+
+
+def test_tree_select_row_equals_brute_force():
+    D, n_nodes, size = 16, 6, 4
+    q = RNG.standard_normal(D).astype(np.float32)
+    bcent = RNG.standard_normal((n_nodes * size, D)).astype(np.float32)
+    children = np.arange(n_nodes * size, dtype=np.int32).reshape(n_nodes, size)
+    ncent = bcent.reshape(n_nodes, size, D).mean(1)
+    members = np.arange(n_nodes * size * 3, dtype=np.int32).reshape(n_nodes * size, 3)
+    lst, n, picks = oracle.tree_select_row(q, ncent, children, bcent, members, position=10_000,
+                                           visible=n_nodes * size, covered=n_nodes * size, beam_width=2, top_p=5,
+                                           top_k=100, window=0, sink=0, mode="fp32")
+    ns = ncent.astype(np.float64) @ q.astype(np.float64)
+    beam = sorted(range(n_nodes), key=lambda j: (-ns[j], j))[:2]
+    cand = sorted(children[beam].ravel().tolist())
+    bs = bcent.astype(np.float64) @ q.astype(np.float64)
+    want = sorted(cand, key=lambda c: (-bs[c], c))[:5]
+    assert picks.tolist() == want
+    assert lst[:n].tolist() == [int(m) for b in want for m in members[b]]
