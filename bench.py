@@ -7,17 +7,18 @@ Decode workload (the headline): D-LSA Flat at B=1, context 32768, Hq=32, Hkv=8, 
 bf16, keys from 512 Gaussian clusters per kv-head (sigma 0.3, runs of 16-128 tokens),
 512 Ward-style buckets per kv-head (16-256 tokens, mean 64) with bucket-mean centroids,
 top-32 buckets per kv-head, rank-order expansion, split-K sparse read. One step is what
-a decode layer pays: GQA-collapsed index queries, the fused select kernel and the
-read kernel (reference port/bench.py:147-153 ``step``: select + read on a built index).
+a decode layer pays: GQA-collapsed index queries, the flat select and the sparse read
+(reference port/bench.py:147-153 ``step``: select + read on a built index), here fused
+into one kernel launch; the unfused three-launch composition is timed beside it.
 
 Timing: the K timed steps are replayed from HIP graphs (one graph = a rotation of
 ``--rotate`` steps, each on its own resident copy of the cache, so consecutive steps
 never find their K/V rows in the 256 MiB MALL) between ``torch.cuda.synchronize()``
-brackets; ``value`` = wall µs per step. The dominant kernel (the sparse read) is also
-timed alone for the roofline: a HIP graph of back-to-back launches over the rotation,
-HIP events around its replays on the stream it runs on; algorithmic bytes (gathered K
-and V rows) / average launch duration (which includes the dispatch gap, so it is an upper
-bound on the kernel's own duration, which rocprofv3's kernel trace reports).
+brackets; ``value`` = wall µs per step. The step's kernel is also timed alone for the
+roofline: a HIP graph of back-to-back launches over the rotation, HIP events around its
+replays on the stream it runs on; algorithmic bytes (gathered K and V rows) / average
+launch duration (which includes the dispatch gap, so it is an upper bound on the
+kernel's own duration, which rocprofv3's kernel trace reports).
 
 Comparators in the same run: dense SDPA decode on the same GPU (same rotation), the
 chunked prefill (configs' prefill row) as tok/s beside dense causal SDPA, and the CPU
@@ -95,6 +96,16 @@ def copy_cache(c: DecodeCache):
 
 
 def decode_step(c: DecodeCache, config):
+    """The decode step as one launch: group-mean index queries, flat select, sparse read."""
+    from lsa_rocm_lab.port import pipeline
+
+    out, lists, lengths = pipeline.flat_decode(c.q, c.k, c.v, c.pos, c.buckets, config, scale=D ** -0.5)
+    return lists, lengths, out
+
+
+def unfused_step(c: DecodeCache, config):
+    """The same step as the reference composes it: index queries, flat select, sparse read
+    (three launches)."""
     from lsa_rocm_lab.port import pipeline
     from lsa_rocm_lab.port.read_kernel_tiled import sparse_read_auto
 
@@ -141,14 +152,14 @@ def event_launch_times(fn, n: int, torch) -> list[float]:
     return [a.elapsed_time(b) for a, b in evs]
 
 
-def profiled_traffic() -> int | None:
-    """HBM bytes per read launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
-    (profiles/read_decode_flat32k_pmc.md); None when it is absent."""
-    path = ROOT / "profiles" / "read_decode_flat32k_pmc.md"
+def profiled_traffic(kernel: str) -> int | None:
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (profiles/decode_flat32k_pmc.md); None when it is absent."""
+    path = ROOT / "profiles" / "decode_flat32k_pmc.md"
     if not path.is_file():
         return None
     for line in path.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch read_kernel:"):
+        if line.startswith(f"traffic_bytes_per_launch {kernel}:"):
             return int(line.split(":")[1])
     return None
 
@@ -229,9 +240,11 @@ def main() -> int:
     n_tok = lengths0.cpu().numpy().astype(np.int64)  # tokens read per kv-head
     gathered = int(n_tok.sum()) * D * 2 * 2          # K and V rows, bf16
     cand_bytes = HKV * N_BUCKETS * D * 2             # centroid scan, bf16
-    ids_bytes = int(n_tok.sum()) * 4                 # member ids
+    cap = buckets.members.shape[-1]
+    ids_bytes = HKV * config.top_p * cap * 4         # member rows of the picked buckets
+    list_bytes = lists0.numel() * 4 + lengths0.numel() * 4  # the lists handed back
     qo_bytes = 2 * HQ * D * 2
-    total_bytes = gathered + cand_bytes + ids_bytes + qo_bytes
+    total_bytes = gathered + cand_bytes + ids_bytes + list_bytes + qo_bytes
 
     # ---- rotation copies
     R = max(1, args.rotate)
@@ -272,20 +285,27 @@ def main() -> int:
     torch.cuda.synchronize()
     warm_us = (time.perf_counter() - w0) / (max(1, args.steps // R) * R) * 1e6
 
-    # ---- the two kernels alone: each replayed back to back from a HIP graph over the
-    # rotation, HIP events around the replays on the stream they run on
+    # ---- kernels alone: each replayed back to back from a HIP graph over the rotation, HIP
+    # events around the replays on the stream they run on. The fused decode kernel is the
+    # step's only kernel; the unfused path's select and read kernels are timed beside it.
+    reps = max(1, args.kernel_launches // R)
+    fused_us = graph_launch_us(step, R, reps, torch)
+    achieved = gathered / (fused_us * 1e-6) / 1e9
     sel = [pipeline.flat_select(pipeline.index_queries(c.q, HKV)[0], c.pos, c.buckets, config) for c in caches]
     idxs = [pipeline.index_queries(c.q, HKV)[0] for c in caches]
     torch.cuda.synchronize()
     read_fn = lambda i: sparse_read_auto(caches[i % R].q, caches[i % R].k, caches[i % R].v,
                                          sel[i % R][0].unsqueeze(0), sel[i % R][1].unsqueeze(0), D ** -0.5)
     sel_fn = lambda i: pipeline.flat_select(idxs[i % R], caches[i % R].pos, caches[i % R].buckets, config)
-    reps = max(1, args.kernel_launches // R)
     read_us = graph_launch_us(read_fn, R, reps, torch)
     sel_us = graph_launch_us(sel_fn, R, reps, torch)
-    achieved = gathered / (read_us * 1e-6) / 1e9
-    log(f"read kernel {read_us:.2f} us per launch: {achieved:.0f} GB/s on gathered bytes; "
-        f"fused select {sel_us:.2f} us per launch")
+    unfused_us = graph_launch_us(lambda i: unfused_step(caches[i % R], config), R, reps, torch)
+    u_lists, u_lengths, u_out = unfused_step(base, config)
+    torch.cuda.synchronize()
+    unfused_same = bool(torch.equal(u_lists, lists0) and torch.equal(u_lengths, lengths0))
+    log(f"fused decode kernel {fused_us:.2f} us per launch: {achieved:.0f} GB/s on gathered bytes; "
+        f"unfused step {unfused_us:.2f} us (select {sel_us:.2f} + read {read_us:.2f} + index queries); "
+        f"unfused lists identical: {unfused_same}")
 
     # ---- dense SDPA comparator on the same rotation
     dense = {"backend": None}
@@ -437,12 +457,14 @@ def main() -> int:
         "gbps_total": round(total_bytes / (us_step * 1e-6) / 1e9, 1),
         "device_us_per_step": round(dev_us_step, 3),
         "warm_us_per_step": round(warm_us, 3),
-        "select_us": round(sel_us, 3),
-        "read_us": round(read_us, 3),
+        "fused_kernel_us": round(fused_us, 3),
+        "unfused": {"us_per_step": round(unfused_us, 3), "select_us": round(sel_us, 3), "read_us": round(read_us, 3),
+                    "lists_identical": unfused_same},
         "kernel_timing": "per launch, HIP graph of back-to-back launches over the rotation, HIP events",
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
-                     "kernel": "read_kernel<bf16,128,4>", "bytes_per_launch": gathered},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("decode_flat_kernel"),
+                     "kernel": "decode_flat_kernel<bf16,bf16,128,4>", "bytes_per_launch": gathered,
+                     "all_bytes_per_launch": total_bytes},
         "dense": dense,
         "speedup_vs_dense": None if speedup is None else round(speedup, 3),
         "prefill": prefill,

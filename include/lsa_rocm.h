@@ -159,6 +159,37 @@ int lsa_read_chunked(const void* q, const void* k, const void* v, int dtype, int
                      int64_t kv_head_stride, const int32_t* ids, const int32_t* lengths, int32_t W, int32_t chunk,
                      float scale, void* out, void* stream);
 
+/* Fused decode step: the flat select and the sparse read of one decode token per batch
+ * row in ONE launch (reference port/bench.py:147-153 `step` = pipeline.flat_select then
+ * read_kernel_tiled.sparse_read_auto; pipeline.py:248-316, select_fused.py:52-280,
+ * read_kernel_tiled.py:92-156). Row r's index query is the fp32 mean of its query group
+ * (make_index_space, gates.py:50-59). q [R, Hq, D] (one token per batch row), k/v
+ * [R, Tk, Hkv, D] at the given element strides, tables as lsa_select_flat's; writes
+ * lists [R, Hkv, top_k + window + sink] and lengths [R, Hkv] (identical to
+ * lsa_select_flat's) and out [R, Hq, D] (the read of those lists).
+ *
+ * readers: reader workgroups per (row, kv-head), 0 = default (2 * picks + the window/sink
+ * parts), at most 256; each reads its share of the list in tiles of
+ * lsa_read_tile_tokens() slots. counters: lsa_decode_flat_counters() int32 words, zero
+ * before the first launch; every launch leaves them zero. scratch:
+ * lsa_decode_flat_scratch_bytes(), 16-byte aligned. Launches sharing counters must be
+ * stream-ordered. status (optional, int32) is set to 1 if a reader workgroup gave up
+ * waiting for its unit's selection (not expected: readers wait only on lower-numbered
+ * workgroups, which never wait); the counters must then be zeroed again.
+ * Limits: top_p (capped at rows) <= 64; head dim {32,64,128,256}; group {1,2,4,8}. */
+int64_t lsa_decode_flat_counters(int64_t R, int32_t Hkv, int32_t rows, int32_t top_p);
+size_t lsa_decode_flat_scratch_bytes(int dtype, int64_t R, int32_t Hq, int32_t Hkv, int32_t D, int32_t rows,
+                                     int32_t top_p, int32_t window, int32_t sink, int32_t select_splits,
+                                     int32_t readers);
+int lsa_decode_flat(const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk, int32_t Hq,
+                    int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride, int64_t kv_head_stride,
+                    const void* centroids, const int32_t* members, const int32_t* ends, int32_t rows, int32_t cap,
+                    int64_t row_tables, int64_t group_tables, int score_mode, const int32_t* positions,
+                    int32_t cluster_block_size, int32_t block_buckets, int32_t top_p, int32_t window, int32_t sink,
+                    int32_t top_k, float scale, int32_t select_splits, int32_t readers, int32_t* counters,
+                    int64_t n_counters, void* scratch, size_t scratch_bytes, int32_t* lists, int32_t* lengths,
+                    void* out, int32_t* status, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

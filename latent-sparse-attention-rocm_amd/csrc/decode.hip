@@ -1,0 +1,211 @@
+// Fused decode step for gfx950: group-mean index queries, flat select and the split sparse
+// read in one launch (reference port/bench.py:147-153, the decode step = flat_select then
+// the sparse read; pipeline.py:248-316, select_fused.py:52-280, read_kernel_tiled.py:92-156).
+//
+// A unit is one (query row, kv-head). The 1-D grid holds the select workgroups of every
+// unit first, then the readers.
+//
+// Select workgroup (unit i, split s), id s * units + i: the unit's index query is the fp32
+// mean of its query group's rows (summed in head order, divided by the group size, as the
+// separate index-query kernel does); it scores columns [s*cs, (s+1)*cs) of the unit's
+// bucket table (the canonical score), publishes the keys and arrives. The last split of a
+// unit takes every key, selects the K best buckets in rank order, counts each picked
+// bucket's kept members (sink <= id < window start, in table order) and publishes the
+// unit's record: per pick, word A = bucket + 2 and word B = end of the pick's slots in the
+// list (the clipped inclusive prefix of kept counts) + 1. Both words are nonzero once
+// written, so a reader that sees all 2K words nonzero holds the whole record: no flag and
+// no fence. It also writes the unit's list length.
+//
+// Reader workgroup (unit i, pick j, part u) or (unit i, tail part t): waits for the record
+// with a bounded poll (past the limit it sets *status and exits), expands its share of the
+// list - the kept members of pick j at ranks [u*span, u*span + span), or a slice of the
+// window-then-sinks tail - into LDS and into the list, gathers those K/V rows and publishes
+// a split partial (or writes the output when the unit has one active part). Every reader
+// of the unit then arrives; the last one combines the partials, clears the record and
+// resets the counter, so the workspace is ready for the next launch.
+//
+// Readers wait only on select workgroups, which hold lower ids. Workgroups are dispatched
+// in id order, so every select workgroup is resident (or done) before any reader can
+// occupy a slot, and it never waits itself: the readers' wait ends.
+#include "lsa_abi_common.h"
+#include "decode_dev.h"
+
+using namespace lsa;
+using namespace lsa::decode;
+
+namespace {
+
+// ------------------------------------------------------------------ host
+
+struct Plan {
+  int K, kp, span, NR;
+  int64_t cstride;  // words between record copies
+  size_t keys_bytes, part_bytes, shmem;
+};
+
+template <int D, int GQ>
+size_t reader_lds(int span) {
+  return rd_ids_offset<D, GQ>() + sizeof(int32_t) * (size_t)span;
+}
+
+template <int D>
+size_t reader_lds_gq(int gq, int span) {
+  switch (gq) {
+    case 1: return reader_lds<D, 1>(span);
+    case 2: return reader_lds<D, 2>(span);
+    case 4: return reader_lds<D, 4>(span);
+    default: return reader_lds<D, 8>(span);
+  }
+}
+
+size_t reader_lds_d(int D, int gq, int span) {
+  switch (D) {
+    case 32: return reader_lds_gq<32>(gq, span);
+    case 64: return reader_lds_gq<64>(gq, span);
+    case 128: return reader_lds_gq<128>(gq, span);
+    default: return reader_lds_gq<256>(gq, span);
+  }
+}
+
+// Record copies sit one 4 KiB page plus 256 bytes apart, so readers polling different
+// copies load from different memory channels.
+int64_t record_stride(int64_t units, int K) {
+  const int64_t words = units * 2 * K;
+  return ((words + 1023) / 1024) * 1024 + 64;
+}
+
+// Readers per unit: enough that each typically reads one part of `span` slots (two per
+// pick, plus the tail's parts), at most kMaxReaders.
+int default_readers(int K, int span, int window, int sink) {
+  const int64_t tail = ((int64_t)window + sink + span - 1) / span;
+  const int64_t nr = 2 * (int64_t)K + tail;
+  return (int)(nr < kMaxReaders ? nr : kMaxReaders);
+}
+
+int plan_decode(int dtype, int D, int gq, int64_t units, int rows, int top_p, int window, int sink, int splits,
+                int readers, Plan* p) {
+  p->K = top_p < rows ? top_p : rows;
+  p->kp = next_pow2(p->K);
+  p->span = lsa_read_tile_tokens(dtype, D, gq);
+  LSA_REQUIRE(p->span > 0, LSA_ERR_SHAPE, "lsa_decode_flat: no read tile for D=%d group=%d", D, gq);
+  LSA_REQUIRE(readers >= 0 && readers <= kMaxReaders, LSA_ERR_SHAPE, "lsa_decode_flat: readers in [0, %d], got %d",
+              kMaxReaders, readers);
+  p->NR = readers > 0 ? readers : default_readers(p->K, p->span, window, sink);
+  p->cstride = record_stride(units, p->K);
+  p->keys_bytes = splits > 1 ? (size_t)units * rows * sizeof(uint64_t) : 0;
+  p->part_bytes = p->NR > 1 ? (size_t)units * p->NR * (size_t)(gq * (D + 2)) * sizeof(float) : 0;
+  const size_t sel = sel_keys_offset() + sizeof(uint64_t) * ((size_t)rows + p->kp);
+  const size_t rd = reader_lds_d(D, gq, p->span);
+  p->shmem = sel > rd ? sel : rd;
+  return LSA_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t lsa_decode_flat_counters(int64_t R, int32_t Hkv, int32_t rows, int32_t top_p) {
+  if (R <= 0 || Hkv <= 0 || rows <= 0 || top_p <= 0) return 0;
+  const int K = top_p < rows ? top_p : rows;
+  if (K > kMaxPicks) return 0;
+  const int64_t units = R * Hkv;
+  return 2 * units + kRecordCopies * record_stride(units, K);
+}
+
+extern "C" size_t lsa_decode_flat_scratch_bytes(int dtype, int64_t R, int32_t Hq, int32_t Hkv, int32_t D,
+                                                int32_t rows, int32_t top_p, int32_t window, int32_t sink,
+                                                int32_t select_splits, int32_t readers) {
+  if (R <= 0 || Hkv <= 0 || Hq < Hkv || rows <= 0 || top_p <= 0) return 0;
+  Plan p;
+  if (plan_decode(dtype, D, Hq / Hkv, R * Hkv, rows, top_p, window < 0 ? 0 : window, sink < 0 ? 0 : sink,
+                  select_splits, readers, &p) != LSA_OK)
+    return 0;
+  return ((p.keys_bytes + 255) & ~(size_t)255) + p.part_bytes;
+}
+
+extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk,
+                               int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride,
+                               int64_t kv_head_stride, const void* centroids, const int32_t* members,
+                               const int32_t* ends, int32_t rows, int32_t cap, int64_t row_tables,
+                               int64_t group_tables, int score_mode, const int32_t* positions,
+                               int32_t cluster_block_size, int32_t block_buckets, int32_t top_p, int32_t window,
+                               int32_t sink, int32_t top_k, float scale, int32_t select_splits, int32_t readers,
+                               int32_t* counters, int64_t n_counters, void* scratch, size_t scratch_bytes,
+                               int32_t* lists, int32_t* lengths, void* out, int32_t* status, void* stream) {
+  LSA_REQUIRE(q && k && v && centroids && members && positions && lists && lengths && out && counters, LSA_ERR_NULL,
+              "lsa_decode_flat: NULL pointer");
+  LSA_REQUIRE(dtype == LSA_F32 || dtype == LSA_BF16 || dtype == LSA_F16, LSA_ERR_DTYPE,
+              "lsa_decode_flat: dtype %d", dtype);
+  LSA_REQUIRE(D == 32 || D == 64 || D == 128 || D == 256, LSA_ERR_SHAPE,
+              "lsa_decode_flat: head dim %d not in {32,64,128,256}", D);
+  LSA_REQUIRE(Hq >= 1 && Hkv >= 1 && Hq % Hkv == 0, LSA_ERR_SHAPE, "lsa_decode_flat: Hq %d must group onto Hkv %d",
+              Hq, Hkv);
+  const int gq = Hq / Hkv;
+  LSA_REQUIRE(gq == 1 || gq == 2 || gq == 4 || gq == 8, LSA_ERR_SHAPE,
+              "lsa_decode_flat: group size %d not in {1,2,4,8}", gq);
+  LSA_REQUIRE(score_mode == LSA_SCORE_BF16 || score_mode == LSA_SCORE_F32, LSA_ERR_DTYPE,
+              "lsa_decode_flat: bad score mode");
+  LSA_REQUIRE(rows >= 1 && cap >= 1 && row_tables >= 0 && group_tables >= 0, LSA_ERR_SHAPE,
+              "lsa_decode_flat: bad table sizes");
+  LSA_REQUIRE(R >= 0 && Tk >= 0 && Tk <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_decode_flat: bad sizes");
+  LSA_REQUIRE(top_p >= 1 && window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE,
+              "lsa_decode_flat: top_p >= 1, window/sink/top_k >= 0");
+  LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "lsa_decode_flat: cluster_block_size must be >= 1");
+  const int K = top_p < rows ? top_p : rows;
+  LSA_REQUIRE(K <= kMaxPicks, LSA_ERR_SHAPE, "lsa_decode_flat: %d picks exceed %d", K, kMaxPicks);
+  LSA_REQUIRE((int64_t)K * cap < 0x7FFFFFFF && (int64_t)top_k + window + sink <= 0x7FFFFFFF, LSA_ERR_SHAPE,
+              "lsa_decode_flat: list too wide");
+  LSA_REQUIRE(select_splits >= 1 && select_splits <= 256 && select_splits <= rows, LSA_ERR_SHAPE,
+              "lsa_decode_flat: select splits in [1, min(256, rows)], got %d", select_splits);
+  const uintptr_t mis = ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)centroids) & 15;
+  LSA_REQUIRE(mis == 0, LSA_ERR_ALIGN, "lsa_decode_flat: q/k/v/centroids must be 16-byte aligned");
+  const int64_t esize = dtype == LSA_F32 ? 4 : 2;
+  LSA_REQUIRE(kv_batch_stride >= 0 && kv_token_stride >= D && kv_head_stride >= D, LSA_ERR_SHAPE,
+              "lsa_decode_flat: K/V strides must leave rows of %d elements apart", D);
+  LSA_REQUIRE(((kv_batch_stride | kv_token_stride | kv_head_stride) * esize) % 16 == 0, LSA_ERR_ALIGN,
+              "lsa_decode_flat: K/V strides must keep rows 16-byte aligned");
+  const int64_t units = R * Hkv;
+  if (units == 0) return LSA_OK;
+  Plan p;
+  LSA_TRY(plan_decode(dtype, D, gq, units, rows, top_p, window, sink, select_splits, readers, &p));
+  LSA_REQUIRE(p.kp + rows <= 6144, LSA_ERR_SHAPE, "lsa_decode_flat: %d columns + %d picks exceed 6144 LDS keys", rows,
+              p.kp);
+  LSA_REQUIRE(p.shmem <= kMaxLds, LSA_ERR_SHAPE, "lsa_decode_flat: %zu bytes of LDS exceed %zu", p.shmem, kMaxLds);
+  const int64_t grid = units * (select_splits + p.NR);
+  LSA_REQUIRE(grid <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_decode_flat: too many workgroups");
+  const int64_t need_counters = lsa_decode_flat_counters(R, Hkv, rows, top_p);
+  LSA_REQUIRE(need_counters > 0 && n_counters >= need_counters, LSA_ERR_WORKSPACE,
+              "lsa_decode_flat: %lld counters < %lld", (long long)n_counters, (long long)need_counters);
+  const size_t keys_at = (p.keys_bytes + 255) & ~(size_t)255;
+  const size_t need = keys_at + p.part_bytes;
+  LSA_REQUIRE(need == 0 || (scratch && scratch_bytes >= need), LSA_ERR_WORKSPACE,
+              "lsa_decode_flat: scratch %zu < %zu bytes", scratch_bytes, need);
+  LSA_REQUIRE(((uintptr_t)scratch % 16) == 0, LSA_ERR_ALIGN, "lsa_decode_flat: scratch must be 16-byte aligned");
+
+  DecodeArgs a;
+  a.q = q; a.k = k; a.v = v; a.out = out;
+  a.R = R; a.G = Hkv; a.Hq = Hq;
+  a.Tk = Tk; a.kv_sb = kv_batch_stride; a.kv_st = kv_token_stride; a.kv_sh = kv_head_stride;
+  a.centroids = centroids; a.members = members; a.ends = ends; a.rows = rows; a.cap = cap;
+  a.vec_rows = (cap % 4 == 0 && ((uintptr_t)members % 16) == 0) ? 1 : 0;
+  a.row_tables = row_tables; a.group_tables = group_tables; a.positions = positions;
+  a.cluster_block = cluster_block_size; a.block_buckets = block_buckets;
+  a.K = p.K; a.kp = p.kp; a.window = window; a.sink = sink; a.top_k = top_k; a.W = top_k + window + sink;
+  a.S = select_splits; a.cs = (rows + select_splits - 1) / select_splits;
+  a.span = p.span; a.NR = p.NR;
+  a.scale_log2 = scale * kLog2e;
+  a.spin_limit = 1 << 22;  // polls of about a microsecond each: seconds
+  a.sel_count = counters;
+  a.rd_count = counters + units;
+  a.record = counters + 2 * units;
+  a.cstride = p.cstride;
+  a.ws_keys = p.keys_bytes ? (uint64_t*)scratch : nullptr;
+  a.ws_part = p.part_bytes ? (float*)((char*)scratch + keys_at) : nullptr;
+  a.lists = lists; a.lengths = lengths; a.status = status;
+  const dim3 g3((unsigned)grid);
+  hipStream_t s = (hipStream_t)stream;
+  const bool bf16 = score_mode == LSA_SCORE_BF16;
+  if (dtype == LSA_BF16) decode::launch_bf16(a, bf16, D, gq, g3, p.shmem, s);
+  else if (dtype == LSA_F16) decode::launch_f16(a, bf16, D, gq, g3, p.shmem, s);
+  else decode::launch_f32(a, bf16, D, gq, g3, p.shmem, s);
+  LSA_LAUNCHED("lsa_decode_flat");
+  return LSA_OK;
+}

@@ -1,0 +1,12 @@
+// Fused decode kernels with _Float16 queries and K/V rows.
+#include "decode_dev.h"
+
+namespace lsa {
+namespace decode {
+
+void launch_f16(const DecodeArgs& a, bool bf16_table, int D, int gq, dim3 grid, size_t shmem, hipStream_t s) {
+  launch_type<_Float16>(a, bf16_table, D, gq, grid, shmem, s);
+}
+
+}  // namespace decode
+}  // namespace lsa

@@ -35,6 +35,13 @@ inline int next_pow2(int x) {
     if (err_ != hipSuccess) return ::lsa::fail(LSA_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(err_)); \
   } while (0)
 
+// Propagates a nonzero status of a host-side check.
+#define LSA_TRY(expr)              \
+  do {                             \
+    int rc_ = (expr);              \
+    if (rc_ != LSA_OK) return rc_; \
+  } while (0)
+
 // Query / key element type dispatch: binds QT.
 #define LSA_DISPATCH_QT(dtype, ...)                       \
   switch (dtype) {                                        \

@@ -219,11 +219,42 @@ __device__ __forceinline__ uint64_t wave_sort64_desc(uint64_t v) {
 // ---------------------------------------------------------------- cross-workgroup exchange
 
 // Values handed between workgroups that may sit on different XCDs (whose L2s are not
-// coherent with each other) go through system-coherent accesses: write-through stores and
-// cache-bypassing loads. Publishing then needs only the stores' completion (s_waitcnt)
-// before an arrival counter, never a device-scope fence (a whole-L2 writeback on gfx950).
-__device__ __forceinline__ void coherent_store_u64(uint64_t* p, uint64_t x) { *(volatile uint64_t*)p = x; }
-__device__ __forceinline__ uint64_t coherent_load_u64(const uint64_t* p) { return *(const volatile uint64_t*)p; }
+// coherent with each other) go through device-scope accesses (the sc1 cache policy):
+// relaxed agent-scope atomic loads and stores, coherent across the XCDs. Publishing then
+// needs only the stores' completion (s_waitcnt) before an arrival counter, never a
+// device-scope release fence (a whole-L2 writeback on gfx950). System-scope (volatile,
+// sc0 sc1) accesses would also be coherent but move data ~3x slower per workgroup.
+__device__ __forceinline__ void coherent_store_u64(uint64_t* p, uint64_t x) {
+  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t coherent_load_u64(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coherent_store_i32(int32_t* p, int32_t x) {
+  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t coherent_load_i32(const int32_t* p) {
+  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coherent_store(float* p, float x) {
+  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float coherent_load(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 16-byte device-scope loads from a workgroup-uniform base: a buffer resource over `base`
+// and per-lane byte offsets (buffer_load_dwordx4 ... sc1).
+struct CoherentRows {
+  __amdgpu_buffer_rsrc_t rsrc;
+  __device__ __forceinline__ explicit CoherentRows(const float* base)
+      : rsrc(__builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7FFFFFFF, 0x00020000)) {}
+  __device__ __forceinline__ float4 load4(int byte_offset) const {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, byte_offset, 0, 16 /* sc1 */);
+    return make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
 
 // Every thread's coherent stores complete, then one arrival on `counter`; returns (to
 // every thread) whether this workgroup arrived last of `expected`. The last one resets the

@@ -1,0 +1,461 @@
+// Device code of the sparse gather read, shared by the read kernel and the fused decode
+// kernel: row loads and conversions, lane reductions, the tile loop of one list span
+// (online softmax over gathered K/V rows), the wave merge, and the split-K partial
+// publish / combine.
+#pragma once
+
+#include <math.h>
+
+#include "lsa_device.h"
+
+namespace lsa {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegBig = -3.0e38f;  // finite "minus infinity" for the running max
+constexpr int kMaxSplits = 256;
+
+// 16 raw bytes of a row -> VEC floats.
+template <typename T> struct Row16;
+template <> struct Row16<bf16_t> {
+  static constexpr int N = 8;
+  static __device__ __forceinline__ void cvt(const uint4& u, float* f) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(w[i] << 16);
+      f[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
+};
+template <> struct Row16<_Float16> {
+  static constexpr int N = 8;
+  static __device__ __forceinline__ void cvt(const uint4& u, float* f) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      _Float16 lo, hi;
+      const uint16_t a = (uint16_t)(w[i] & 0xFFFFu), b = (uint16_t)(w[i] >> 16);
+      __builtin_memcpy(&lo, &a, 2);
+      __builtin_memcpy(&hi, &b, 2);
+      f[2 * i] = (float)lo;
+      f[2 * i + 1] = (float)hi;
+    }
+  }
+};
+template <> struct Row16<float> {
+  static constexpr int N = 4;
+  static __device__ __forceinline__ void cvt(const uint4& u, float* f) {
+    f[0] = __uint_as_float(u.x); f[1] = __uint_as_float(u.y);
+    f[2] = __uint_as_float(u.z); f[3] = __uint_as_float(u.w);
+  }
+};
+
+// Launch geometry of one (dtype, head dim) instance.
+// Tiles of 64 tokens: 8 16-byte K/V loads per lane in flight (bf16, D=128). A CU keeps
+// only so many misses in flight, so a decode read spreads its tiles over as many CUs as
+// possible rather than giving each workgroup more rows.
+template <typename T, int D, int GQ>
+struct ReadShape {
+  static constexpr int VEC = Row16<T>::N;
+  static constexpr int LPT = D / VEC;                        // lanes per token row
+  static constexpr int TPW = LSA_WAVE / LPT;                 // tokens per wave per load step
+  static constexpr int U0 = 64 / (LSA_WAVES * TPW);
+  static constexpr int U = U0 < 1 ? 1 : (U0 > 8 ? 8 : U0);   // load steps per tile
+  static constexpr int NT = LSA_WAVES * TPW * U;             // tokens per tile
+};
+
+// exp2 on the hardware unit (v_exp_f32): softmax weights that would be denormal flush
+// to zero, which the normaliser never notices.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// DPP lane exchange inside a row of 16: dpp_ctrl quad_perm / row mirrors.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+// The partner value of lane ^ x for x in {16, 32} (v_permlane16/32_swap on gfx950), else
+// a bpermute shuffle.
+__device__ __forceinline__ float lane_xor(float v, int x) {
+  const int iv = __builtin_bit_cast(int, v);
+  const int row = (threadIdx.x & (LSA_WAVE - 1)) >> 4;
+  if (x == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+    return __builtin_bit_cast(float, (row & 1) ? r[0] : r[1]);
+  }
+  if (x == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+    return __builtin_bit_cast(float, (row & 2) ? r[0] : r[1]);
+  }
+  return __shfl_xor(v, x, LSA_WAVE);
+}
+
+// Sum over each group of N consecutive lanes (N a power of two <= 64), in every lane of
+// the group: DPP adds inside rows of 16, lane swaps across rows.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp_mov<0xB1>(x);   // quad_perm [1,0,3,2]
+  if constexpr (N >= 4) x += dpp_mov<0x4E>(x);   // quad_perm [2,3,0,1]
+  if constexpr (N >= 8) x += dpp_mov<0x141>(x);  // row_half_mirror
+  if constexpr (N >= 16) x += dpp_mov<0x140>(x); // row_mirror
+  if constexpr (N >= 32) x += lane_xor(x, 16);
+  if constexpr (N >= 64) x += lane_xor(x, 32);
+  return x;
+}
+
+// Dot product of 8 packed 16-bit elements (two uint4-halves' worth of words): fp32
+// accumulation of exact products (v_dot2c).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ __forceinline__ float dot8(const uint32_t* q, const uint4& k) {
+  const uint32_t kw[4] = {k.x, k.y, k.z, k.w};
+  float p = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (__is_same(T, bf16_t))
+      p = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, q[i]), __builtin_bit_cast(bf16x2_t, kw[i]), p,
+                                          false);
+    else
+      p = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q[i]), __builtin_bit_cast(f16x2_t, kw[i]), p, false);
+  }
+  return p;
+}
+
+template <typename T> __device__ __forceinline__ void store_out(T* p, float x);
+template <> __device__ __forceinline__ void store_out<float>(float* p, float x) { *p = x; }
+template <> __device__ __forceinline__ void store_out<bf16_t>(bf16_t* p, float x) { p->bits = f32_to_bf16(x); }
+template <> __device__ __forceinline__ void store_out<_Float16>(_Float16* p, float x) { *p = (_Float16)x; }
+
+
+// LDS of the read finish: per-wave states, split weights, reduction buffers.
+template <int D, int GQ, int MAXS>
+struct ReadLds {
+  static constexpr int COLS = GQ * D / 4;
+  static constexpr int RPT = COLS >= LSA_BLOCK ? 1 : LSA_BLOCK / COLS;
+  float acc[LSA_WAVES][GQ][D];
+  float m[LSA_WAVES][GQ];
+  float l[LSA_WAVES][GQ];
+  float w[MAXS][GQ];
+  float pl[MAXS][GQ];
+  float ltot[GQ];
+  float4 red[RPT > 1 ? RPT : 1][RPT > 1 ? COLS : 1];
+  int flag;
+};
+
+// The GQ query rows of one kv-head as this lane holds them: raw 16-byte words (16-bit
+// rows score with packed dot products on them, the scale applied to the fp32 sum) and, for
+// fp32 rows, floats pre-scaled by scale_log2. qrow points at the GQ contiguous rows.
+template <typename T, int D, int GQ>
+struct QueryRegs {
+  static constexpr bool PACKED = sizeof(T) == 2;
+  uint32_t qw[GQ][4];
+  float qf[GQ][ReadShape<T, D, GQ>::VEC];
+
+  __device__ __forceinline__ void load(const T* qrow, float scale_log2) {
+    using S = ReadShape<T, D, GQ>;
+    const int lp = (threadIdx.x & (LSA_WAVE - 1)) % S::LPT;
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) {
+      const uint4 raw = *(const uint4*)(qrow + (int64_t)h * D + lp * S::VEC);
+      qw[h][0] = raw.x; qw[h][1] = raw.y; qw[h][2] = raw.z; qw[h][3] = raw.w;
+      if constexpr (!PACKED) {
+        Row16<T>::cvt(raw, qf[h]);
+#pragma unroll
+        for (int e = 0; e < S::VEC; ++e) qf[h][e] *= scale_log2;
+      }
+    }
+  }
+};
+
+// Per-lane running softmax state of the GQ heads over this lane's VEC dims.
+template <typename T, int D, int GQ>
+struct AttnState {
+  float m[GQ], l[GQ], acc[GQ][ReadShape<T, D, GQ>::VEC];
+
+  __device__ __forceinline__ void clear() {
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) {
+      m[h] = kNegBig;
+      l[h] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < ReadShape<T, D, GQ>::VEC; ++e) acc[h][e] = 0.0f;
+    }
+  }
+};
+
+// Online-softmax attention over list slots [lo, hi), tile by tile: id_of(j) is the token of
+// slot j, or -1 (skipped); it must be cheap and unconditional (a clamped load or an LDS
+// read). kb / vb point at the kv-head's row 0 plus this lane's VEC-element offset. fresh:
+// the state is empty, so the first tile needs no rescale.
+template <typename T, int D, int GQ, typename IdOf>
+__device__ __forceinline__ void attend_tiles(const QueryRegs<T, D, GQ>& q, const T* kb, const T* vb, int64_t tstride,
+                                             int64_t Tk, int lo, int hi, IdOf id_of, float scale_log2, bool fresh,
+                                             AttnState<T, D, GQ>& st) {
+  using S = ReadShape<T, D, GQ>;
+  constexpr int VEC = S::VEC, LPT = S::LPT, TPW = S::TPW, U = S::U, NT = S::NT;
+  constexpr bool PACKED = QueryRegs<T, D, GQ>::PACKED;
+  const int lane = threadIdx.x & (LSA_WAVE - 1);
+  const int w = threadIdx.x / LSA_WAVE;
+  const int tg = lane / LPT;
+
+  int32_t id[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) id[u] = id_of(lo + (u * LSA_WAVES + w) * TPW + tg);
+  for (int base = lo; base < hi; base += NT) {
+    // all K/V rows of the tile in flight at once
+    bool ok[U];
+    uint4 kr[U], vr[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      ok[u] = id[u] >= 0 && id[u] < Tk;
+      const uint64_t off = (uint64_t)(uint32_t)(ok[u] ? id[u] : 0) * (uint32_t)tstride;
+      kr[u] = *(const uint4*)(kb + off);
+      vr[u] = *(const uint4*)(vb + off);
+    }
+    // next tile's ids while this one computes
+    const int nb = base + NT;
+#pragma unroll
+    for (int u = 0; u < U; ++u) id[u] = id_of(nb + (u * LSA_WAVES + w) * TPW + tg);
+
+    float sc[GQ][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) {
+        float p;
+        if constexpr (PACKED) {
+          p = dot8<T>(q.qw[h], kr[u]);
+        } else {
+          float kf[VEC];
+          Row16<T>::cvt(kr[u], kf);
+          p = 0.0f;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) p = fmaf(q.qf[h][e], kf[e], p);
+        }
+        p = group_sum<LPT>(p);
+        if constexpr (PACKED) p *= scale_log2;
+        sc[h][u] = ok[u] ? p : -INFINITY;
+      }
+    }
+    const bool rescale = !(fresh && base == lo);  // an empty state needs no rescale
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) {
+      float mt = st.m[h];
+#pragma unroll
+      for (int u = 0; u < U; ++u) mt = fmaxf(mt, sc[h][u]);
+      if (rescale) {
+        const float alpha = fast_exp2(st.m[h] - mt);
+        st.l[h] *= alpha;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) st.acc[h][e] *= alpha;
+      }
+      st.m[h] = mt;
+#pragma unroll
+      for (int u = 0; u < U; ++u) sc[h][u] = fast_exp2(sc[h][u] - mt);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float vf[VEC];
+      Row16<T>::cvt(vr[u], vf);
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) {
+        st.l[h] += sc[h][u];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) st.acc[h][e] = fmaf(sc[h][u], vf[e], st.acc[h][e]);
+      }
+    }
+  }
+}
+
+// Merges the token groups of each wave (lanes that hold the same dims): afterwards every
+// lane of a group holds the wave's state for its dims.
+template <typename T, int D, int GQ>
+__device__ __forceinline__ void merge_token_groups(AttnState<T, D, GQ>& st) {
+  using S = ReadShape<T, D, GQ>;
+  constexpr int VEC = S::VEC, LPT = S::LPT;
+#pragma unroll
+  for (int x = LPT; x < LSA_WAVE; x <<= 1) {
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) {
+      const float mo = lane_xor(st.m[h], x);
+      const float lo_ = lane_xor(st.l[h], x);
+      const float mn = fmaxf(st.m[h], mo);
+      const float a1 = fast_exp2(st.m[h] - mn), a2 = fast_exp2(mo - mn);
+      st.l[h] = st.l[h] * a1 + lo_ * a2;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float ao = lane_xor(st.acc[h][e], x);
+        st.acc[h][e] = st.acc[h][e] * a1 + ao * a2;
+      }
+      st.m[h] = mn;
+    }
+  }
+}
+
+// Attention of the GQ query heads of one kv-head over list slots [lo, hi) from an empty
+// state, token groups merged (qrow: the GQ contiguous query rows).
+template <typename T, int D, int GQ, typename IdOf>
+__device__ __forceinline__ void attend_span(const T* qrow, const T* kb, const T* vb, int64_t tstride, int64_t Tk,
+                                            int lo, int hi, IdOf id_of, float scale_log2, AttnState<T, D, GQ>& st) {
+  QueryRegs<T, D, GQ> q;
+  q.load(qrow, scale_log2);
+  st.clear();
+  attend_tiles<T, D, GQ>(q, kb, vb, tstride, Tk, lo, hi, id_of, scale_log2, true, st);
+  merge_token_groups<T, D, GQ>(st);
+}
+
+// Merges the four waves' states of a span. direct: writes the normalised output to outp
+// (GQ rows of D); otherwise publishes the partial (m[GQ], l[GQ], acc[GQ][D]) at part with
+// write-through stores. Every thread calls it.
+template <typename T, int D, int GQ, int MAXS>
+__device__ __forceinline__ void finish_span(ReadLds<D, GQ, MAXS>& sh, const AttnState<T, D, GQ>& st, bool direct,
+                                            T* outp, float* part, int empty_nan) {
+  using S = ReadShape<T, D, GQ>;
+  constexpr int VEC = S::VEC, LPT = S::LPT;
+  const int lane = threadIdx.x & (LSA_WAVE - 1);
+  const int w = threadIdx.x / LSA_WAVE;
+  const int tg = lane / LPT, lp = lane % LPT;
+  if (tg == 0) {
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sh.acc[w][h][lp * VEC + e] = st.acc[h][e];
+      if (lp == 0) { sh.m[w][h] = st.m[h]; sh.l[w][h] = st.l[h]; }
+    }
+  }
+  __syncthreads();
+  // thread j owns (head, dim) pairs j, j + 256, ...
+  for (int j = threadIdx.x; j < GQ * D; j += LSA_BLOCK) {
+    const int h = j / D, d = j % D;
+    float M = kNegBig;
+#pragma unroll
+    for (int ww = 0; ww < LSA_WAVES; ++ww) M = fmaxf(M, sh.m[ww][h]);
+    float L = 0.0f, A = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < LSA_WAVES; ++ww) {
+      const float f = fast_exp2(sh.m[ww][h] - M);
+      L += sh.l[ww][h] * f;
+      A += sh.acc[ww][h][d] * f;
+    }
+    if (direct) {
+      store_out<T>(outp + j, L > 0.0f ? A / L : (empty_nan ? NAN : 0.0f));
+    } else {
+      coherent_store(part + 2 * GQ + j, A);
+      if (d == 0) { coherent_store(part + h, M); coherent_store(part + GQ + h, L); }
+    }
+  }
+}
+
+// Combines n_act published partials (stride GQ*(D+2) floats from parts) into outp. The
+// first batch of accumulator columns and every (m, l) are loaded together; per-head
+// maxima and normalisers are wave reductions (a fixed order: deterministic). Every
+// thread calls it; n_act <= MAXS.
+template <typename T, int D, int GQ, int MAXS>
+__device__ __forceinline__ void combine_partials(ReadLds<D, GQ, MAXS>& sh, const float* parts, int n_act, T* outp,
+                                                 int empty_nan) {
+  constexpr int COLS = GQ * D / 4;                                // float4 columns of a partial
+  constexpr int RPT = COLS >= LSA_BLOCK ? 1 : LSA_BLOCK / COLS;   // threads per column
+  constexpr int CPT = COLS >= LSA_BLOCK ? COLS / LSA_BLOCK : 1;   // columns per thread
+  constexpr int PSTRIDE = GQ * (D + 2);
+  constexpr int BATCH = 16 / CPT;
+  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
+  const int r = tid / COLS % RPT;
+  const CoherentRows rows(parts);  // partials of one unit span < 2 GiB
+  float4 first[CPT][BATCH];
+#pragma unroll
+  for (int cc = 0; cc < CPT; ++cc) {
+    const int c = (tid % COLS) + cc * LSA_BLOCK;
+#pragma unroll
+    for (int bb = 0; bb < BATCH; ++bb) {
+      const int sp = r + bb * RPT;
+      const int sl = sp < n_act ? sp : 0;
+      first[cc][bb] = rows.load4(4 * (sl * PSTRIDE + 2 * GQ + 4 * c));
+    }
+  }
+  for (int t = tid; t < n_act * GQ; t += LSA_BLOCK) {
+    const int sp = t / GQ, h = t % GQ;
+    const float* ps = parts + (int64_t)sp * PSTRIDE;
+    const float pm = coherent_load(ps + h), pl = coherent_load(ps + GQ + h);
+    sh.w[sp][h] = pm;
+    sh.pl[sp][h] = pl;
+  }
+  __syncthreads();
+  // per-head maximum and normaliser: wave w reduces heads w, w + 4, ... with the splits
+  // strided over its lanes
+  for (int h = w; h < GQ; h += LSA_WAVES) {
+    float M = kNegBig;
+    for (int sp = lane; sp < n_act; sp += LSA_WAVE) M = fmaxf(M, sh.w[sp][h]);
+#pragma unroll
+    for (int x = LSA_WAVE / 2; x >= 1; x >>= 1) M = fmaxf(M, __shfl_xor(M, x, LSA_WAVE));
+    float L = 0.0f;
+    for (int sp = lane; sp < n_act; sp += LSA_WAVE) {
+      const float f = fast_exp2(sh.w[sp][h] - M);
+      L += sh.pl[sp][h] * f;
+      sh.w[sp][h] = f;
+    }
+#pragma unroll
+    for (int x = LSA_WAVE / 2; x >= 1; x >>= 1) L += __shfl_xor(L, x, LSA_WAVE);
+    if (lane == 0) sh.ltot[h] = L;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int cc = 0; cc < CPT; ++cc) {
+    const int c = (tid % COLS) + cc * LSA_BLOCK;
+    const int h = (4 * c) / D;
+    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int bb = 0; bb < BATCH; ++bb) {
+      const int sp = r + bb * RPT;
+      const float f = sp < n_act ? sh.w[sp][h] : 0.0f;
+      sum.x += f * first[cc][bb].x; sum.y += f * first[cc][bb].y;
+      sum.z += f * first[cc][bb].z; sum.w += f * first[cc][bb].w;
+    }
+    for (int sb = BATCH * RPT; sb < n_act; sb += BATCH * RPT) {  // more splits than one batch
+      float4 x[BATCH];
+#pragma unroll
+      for (int bb = 0; bb < BATCH; ++bb) {
+        const int sp = r + sb + bb * RPT;
+        x[bb] = rows.load4(4 * ((sp < n_act ? sp : 0) * PSTRIDE + 2 * GQ + 4 * c));
+      }
+#pragma unroll
+      for (int bb = 0; bb < BATCH; ++bb) {
+        const int sp = r + sb + bb * RPT;
+        const float f = sp < n_act ? sh.w[sp][h] : 0.0f;
+        sum.x += f * x[bb].x; sum.y += f * x[bb].y; sum.z += f * x[bb].z; sum.w += f * x[bb].w;
+      }
+    }
+    if (RPT > 1) {
+      sh.red[r][c] = sum;
+    } else {
+      const float L = sh.ltot[h];
+      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+      const float e = empty_nan ? NAN : 0.0f;
+      store_out<T>(outp + 4 * c + 0, L > 0.0f ? sum.x * inv : e);
+      store_out<T>(outp + 4 * c + 1, L > 0.0f ? sum.y * inv : e);
+      store_out<T>(outp + 4 * c + 2, L > 0.0f ? sum.z * inv : e);
+      store_out<T>(outp + 4 * c + 3, L > 0.0f ? sum.w * inv : e);
+    }
+  }
+  if (RPT > 1) {
+    __syncthreads();
+    for (int c = tid; c < COLS; c += LSA_BLOCK) {
+      float4 sum = sh.red[0][c];
+#pragma unroll
+      for (int rr = 1; rr < RPT; ++rr) {
+        const float4 x = sh.red[rr][c];
+        sum.x += x.x; sum.y += x.y; sum.z += x.z; sum.w += x.w;
+      }
+      const int h = (4 * c) / D;
+      const float L = sh.ltot[h];
+      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+      const float e = empty_nan ? NAN : 0.0f;
+      store_out<T>(outp + 4 * c + 0, L > 0.0f ? sum.x * inv : e);
+      store_out<T>(outp + 4 * c + 1, L > 0.0f ? sum.y * inv : e);
+      store_out<T>(outp + 4 * c + 2, L > 0.0f ? sum.z * inv : e);
+      store_out<T>(outp + 4 * c + 3, L > 0.0f ? sum.w * inv : e);
+    }
+  }
+}
+
+}  // namespace lsa

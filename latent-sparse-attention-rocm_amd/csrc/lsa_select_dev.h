@@ -295,6 +295,14 @@ __device__ __forceinline__ void block_topk_sorted(const uint64_t* keys, int n, i
   bitonic_sort_desc(out, kp);
 }
 
+// Closed-form visible count without span ends (reference pipeline.py:184-186).
+__device__ __forceinline__ int visible_closed(int64_t position, int rows, int cluster_block, int block_buckets) {
+  const int64_t blocks =
+      position >= 0 ? position / cluster_block : -((-position + cluster_block - 1) / cluster_block);
+  int64_t v = blocks * block_buckets;
+  return (int)(v > rows ? rows : v);
+}
+
 // Value of tail slot i (after the kept ids) of a read list: the window [window_start,
 // position], then the sinks [0, min(sink, window_start)), then -1.
 __device__ __forceinline__ int32_t tail_id(int64_t i, int64_t window_start, int64_t n_win, int64_t n_sink) {

@@ -151,14 +151,6 @@ struct FlatArgs {
   int32_t* lengths;
 };
 
-// Closed-form visible count without span ends (reference pipeline.py:184-186).
-__device__ __forceinline__ int visible_closed(int64_t position, int rows, int cluster_block, int block_buckets) {
-  const int64_t blocks =
-      position >= 0 ? position / cluster_block : -((-position + cluster_block - 1) / cluster_block);
-  int64_t v = blocks * block_buckets;
-  return (int)(v > rows ? rows : v);
-}
-
 // grid (R*G, S). Split s scores columns [s*cs, (s+1)*cs) of its table in one batch of
 // loads (query slice, centroid rows and the columns' span ends together); with S > 1 it
 // publishes the keys and the last split to arrive takes every column's key from the
@@ -410,12 +402,6 @@ int check_aligned(const void* centroids, int D, int score_mode, const int32_t* m
 }
 
 }  // namespace
-
-#define LSA_TRY(expr)            \
-  do {                           \
-    int rc_ = (expr);            \
-    if (rc_ != LSA_OK) return rc_; \
-  } while (0)
 
 extern "C" int lsa_visible_counts(const int32_t* positions, int64_t R, int32_t G, int32_t rows,
                                   int32_t cluster_block_size, int32_t block_buckets, const int32_t* ends,

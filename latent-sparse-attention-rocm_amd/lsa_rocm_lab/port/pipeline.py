@@ -405,6 +405,79 @@ def lsa_read(q, k, v, read_lists, lengths, scale):
     return sparse_read_auto(q, k, v, read_lists, lengths, scale)
 
 
+def flat_decode(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    positions: torch.Tensor,
+    buckets: Buckets,
+    config: PortConfig,
+    scale: float | None = None,
+    top_k: int | None = None,
+    score_dtype: str = "bf16",
+    splits: int | None = None,
+    readers: int | None = None,
+    status: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """One decode step - index queries, flat select, sparse read - in one HIP launch.
+
+    The reference's decode step (port/bench.py:147-153) is ``flat_select`` on the GQA
+    group-mean index queries followed by ``lsa_read``; this is that composition fused.
+    q [B, 1, Hq, D] (the token being decoded, at ``positions[b]``), k/v [B, Tk, Hkv, D],
+    bucket tables per kv-head ([Hkv, rows, ...]) or per row and kv-head. Returns
+    ``(out [B, 1, Hq, D], lists [B, Hkv, W], lengths [B, Hkv])``; lists and lengths are
+    byte-identical to ``flat_select(index_queries(q, Hkv)[:, 0], ...)``'s. ``splits``: select
+    workgroups per (row, kv-head) (default as ``flat_select``); ``readers``: reader
+    workgroups per (row, kv-head) (default: ``LSA_DECODE_READERS`` or the library's
+    choice); ``status`` (optional int32 [1] on the device) is set to 1 if a reader gave up
+    waiting.
+    """
+    from lsa_rocm_lab.port.read_kernel_tiled import _kv_layout
+
+    device = _on_device("flat_decode", q, k, v, buckets.centroids, buckets.members)
+    if q.dim() != 4 or q.shape[1] != 1:
+        raise ValueError(f"flat_decode takes one query token per batch row: q [B, 1, Hq, D], got {tuple(q.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"q/k/v dtypes differ: {q.dtype} {k.dtype} {v.dtype}")
+    B, _, Hq, D = q.shape
+    Tk, Hkv = k.shape[1], k.shape[2]
+    if k.dim() != 4 or k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
+        raise ValueError(f"k/v must be [B={B}, Tk, Hkv, D={D}], got {tuple(k.shape)} / {tuple(v.shape)}")
+    if Hq % Hkv:
+        raise ValueError(f"{Hq} query heads do not group onto {Hkv} kv-heads")
+    q = q.contiguous()
+    k, v, sb, st, sh = _kv_layout(k, v)
+    layout = _Layout(torch.empty((B, Hkv, D), device="meta"), buckets.centroids)
+    table, mode = _score_table(buckets, score_dtype)
+    members = buckets.members.to(device=device, dtype=torch.int32).contiguous()
+    ends = _ends(buckets)
+    pos = _positions32(positions, device)
+    if pos.numel() != B:
+        raise ValueError(f"a position a batch row: {B} rows, {pos.numel()} positions")
+    top_k = config.top_k if top_k is None else top_k
+    scale = D ** -0.5 if scale is None else scale
+    splits = _select_splits(B, Hkv, layout.rows, config.top_p) if splits is None else splits
+    rows, cap = layout.rows, members.shape[-1]
+    width = top_k + config.window_size + config.sink_size
+    lists = torch.empty(B, Hkv, width, dtype=torch.int32, device=device)
+    lengths = torch.empty(B, Hkv, dtype=torch.int32, device=device)
+    out = torch.empty_like(q)
+    dt = _abi.dtype_code(q.dtype)
+    readers = int(os.environ.get("LSA_DECODE_READERS", "0")) if readers is None else readers
+    n_counters = _abi.size("lsa_decode_flat_counters", B, Hkv, rows, config.top_p)
+    nbytes = _abi.size("lsa_decode_flat_scratch_bytes", dt, B, Hq, Hkv, D, rows, config.top_p,
+                       config.window_size, config.sink_size, splits, readers)
+    ws = _abi.Workspace.get(device, "decode", nbytes)
+    counters = _abi.Counters.get(device, max(n_counters, 1))
+    _abi.call("lsa_decode_flat", q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, Tk, Hq, Hkv, D, sb, st, sh,
+              table.data_ptr(), members.data_ptr(), _abi.ptr(ends), rows, cap, layout.row_tables,
+              layout.group_tables, mode, pos.data_ptr(), config.cluster_block_size, config.block_bucket_count,
+              config.top_p, config.window_size, config.sink_size, top_k, float(scale), splits, readers,
+              counters.data_ptr(), counters.numel(), _abi.ptr(ws), nbytes, lists.data_ptr(), lengths.data_ptr(),
+              out.data_ptr(), _abi.ptr(status), _abi.stream(device))
+    return out, lists, lengths
+
+
 def lsa_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale, chunk_size: int = 64):
     """Chunked prefill read: every query row of a ``chunk_size`` chunk reads the chunk's
     shared per-kv-head list plus the chunk's own causal block.

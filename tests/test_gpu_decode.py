@@ -1,0 +1,165 @@
+"""The fused decode step (index queries + flat select + sparse read in one launch) on the GPU.
+
+Lists and lengths must equal, bit for bit, the oracle's flat select on the group-mean index
+queries (and so the unfused HIP select's); the output must match the oracle's sparse read of
+those lists within the dtype's bar (max-abs / mean-abs vs fp64: fp32 1e-4 / 1e-5, bf16
+2e-2 / 2e-3). Cases: the clustered decode geometry up to 32k, positional buckets with
+window and sink tails, top_k cutting a bucket short, fewer visible buckets than picks,
+nothing visible (zeros), batch rows with their own tables and positions, every select
+split count, both scoring dtypes, and repeated launches (the record, counters and
+partials are reused and must come back clean).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from lsa_rocm_lab import workloads
+from lsa_rocm_lab.port import pipeline
+from lsa_rocm_lab.port.pipeline import PortConfig
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float32: (1e-4, 1e-5), torch.bfloat16: (2e-2, 2e-3), torch.float16: (5e-3, 5e-4)}
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def oracle_decode(q, k, v, positions, buckets, config, score_dtype, top_k=None):
+    """Oracle lists/lengths [B, Hkv, W] / [B, Hkv] and output [B, 1, Hq, D]."""
+    top_k = config.top_k if top_k is None else top_k
+    B, _, Hq, D = q.shape
+    Hkv = k.shape[2]
+    idx = oracle.index_queries(q.float().cpu().numpy(), Hkv)[:, 0]  # [B, Hkv, D]
+    per_row = buckets.members.dim() == 4
+    cents = buckets.centroids_f32 if score_dtype == "fp32" else buckets.centroids.float()
+    lists, lengths = [], []
+    for b in range(B):
+        lb, nb = [], []
+        for g in range(Hkv):
+            sel = (b, g) if per_row else (g,)
+            ends = None if buckets.ends is None else _np(buckets.ends[sel])
+            l, n = oracle.flat_select(idx[b, g][None], np.array([int(positions[b])]), _np(cents[sel]),
+                                      _np(buckets.members[sel]), cluster_block_size=config.cluster_block_size,
+                                      block_buckets=config.block_bucket_count, top_p=config.top_p, top_k=top_k,
+                                      window=config.window_size, sink=config.sink_size, mode=score_dtype, ends=ends)
+            lb.append(l[0])
+            nb.append(n[0])
+        lists.append(np.stack(lb))
+        lengths.append(np.array(nb))
+    lists, lengths = np.stack(lists), np.stack(lengths)
+    out = oracle.sparse_read(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
+                             lists[:, None], lengths[:, None], D ** -0.5)
+    return lists, lengths, out
+
+
+def check_decode(q, k, v, positions, buckets, config, score_dtype="bf16", top_k=None, splits=None, label=""):
+    print(f"case {label} B={q.shape[0]} Hq={q.shape[2]} D={q.shape[3]} {q.dtype} {score_dtype} splits={splits}",
+          flush=True)
+    status = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out, lists, lengths = pipeline.flat_decode(q, k, v, positions.to(DEV), buckets, config, top_k=top_k,
+                                               score_dtype=score_dtype, splits=splits, status=status)
+    want_l, want_n, want_o = oracle_decode(q, k, v, positions, buckets, config, score_dtype, top_k)
+    assert int(status.item()) == 0
+    assert np.array_equal(_np(lengths), want_n), label
+    assert np.array_equal(_np(lists), want_l), label
+    max_abs, mean_abs = TOL[q.dtype]
+    err = np.abs(_np(out.float()) - want_o)
+    assert np.isfinite(err).all(), label
+    assert err.max() <= max_abs and err.mean() <= mean_abs, (label, err.max(), err.mean())
+    return out, lists, lengths
+
+
+@pytest.mark.parametrize("splits", [1, 3, 16, None])
+def test_clustered_decode_matches_oracle(splits):
+    T, Hq, Hkv, D = 8192, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=128, seed=4, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    pos = torch.tensor([T - 1], dtype=torch.int32)
+    check_decode(data.q[:, -1:], data.k, data.v, pos, buckets, workloads.FLAT_32K, splits=splits,
+                 label=f"clustered splits={splits}")
+
+
+def test_decode_32k_geometry_matches_unfused_path(monkeypatch):
+    """The benchmark geometry: 32k context, Hq 32 / Hkv 8, 512 buckets per kv-head."""
+    T, Hq, Hkv, D = 32768, 32, 8, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=512, seed=1, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=512)
+    config = workloads.FLAT_32K
+    pos = torch.tensor([T - 1], dtype=torch.int32)
+    q = data.q[:, -1:]
+    out, lists, lengths = check_decode(q, data.k, data.v, pos, buckets, config, label="32k")
+    monkeypatch.setenv("LSA_SELECT_IMPL", "fused")
+    idx = pipeline.index_queries(q, Hkv)[0]
+    l2, n2 = pipeline.flat_select(idx, pos.to(DEV), buckets, config)
+    assert torch.equal(lists, l2) and torch.equal(lengths, n2)  # [1, Hkv, W], [1, Hkv]
+    o2 = pipeline.lsa_read(q, data.k, data.v, l2.unsqueeze(0), n2.unsqueeze(0), D ** -0.5)
+    assert (out.float() - o2.float()).abs().max().item() <= 2e-2
+
+
+@pytest.mark.parametrize("top_k", [100, 2000])
+@pytest.mark.parametrize("score_dtype", ["bf16", "fp32"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_positional_window_sink_and_truncation(score_dtype, dtype, top_k):
+    """Window + sink tails, top_k cutting the expansion inside a bucket (100), positions that
+    see fewer buckets than picks (32 per closed block, 48 picks) or none (only the window) -
+    one launch over batch rows with their own tables."""
+    T, Hq, Hkv, D = 4096, 8, 2, 64
+    g = torch.Generator().manual_seed(20261201)
+    B = 3
+    q = (torch.randn(B, 1, Hq, D, generator=g) * 0.5).to(dtype).to(DEV)
+    k = (torch.randn(B, T, Hkv, D, generator=g) * 0.5).to(dtype).to(DEV)
+    v = torch.randn(B, T, Hkv, D, generator=g).to(dtype).to(DEV)
+    config = PortConfig(cluster_block_size=512, bucket_size=16, bucket_cap=16, top_p=48, top_k=top_k,
+                        window_size=128, sink_size=4)
+    buckets = pipeline.position_buckets(k, config, centroid="mean")  # [B, Hkv, rows, ...]
+    for positions in ([T - 1, 1500, 700], [5, 513, 4000]):
+        pos = torch.tensor(positions, dtype=torch.int32)
+        check_decode(q, k, v, pos, buckets, config, score_dtype=score_dtype,
+                     label=f"positional {positions} top_k={top_k}")
+
+
+def test_nothing_visible_gives_zeros_and_empty_lists():
+    T, Hq, Hkv, D = 2048, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=32, seed=6, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    pos = torch.tensor([3], dtype=torch.int32)  # no bucket ends at or before position 4
+    out, lists, lengths = check_decode(data.q[:, :1], data.k, data.v, pos, buckets, workloads.FLAT_32K,
+                                       label="nothing visible")
+    assert int(lengths.max().item()) == 0 and torch.all(lists == -1)
+    assert torch.all(out == 0)
+
+
+def test_repeated_launches_reuse_workspace():
+    """Three launches in a row on one stream with different queries and positions: the
+    record, the arrival counters and the partials left by one launch serve the next."""
+    T, Hq, Hkv, D = 8192, 16, 4, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=64, seed=7, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    for step, p in enumerate((T - 1, T - 300, 5000)):
+        pos = torch.tensor([p], dtype=torch.int32)
+        check_decode(data.q[:, p:p + 1], data.k, data.v, pos, buckets, workloads.FLAT_32K, label=f"repeat {step}")
+
+
+def test_decode_deterministic():
+    T, Hq, Hkv, D = 4096, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=64, seed=8, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    pos = torch.tensor([T - 1], dtype=torch.int32, device=DEV)
+    first = pipeline.flat_decode(data.q[:, -1:], data.k, data.v, pos, buckets, workloads.FLAT_32K)
+    for _ in range(3):
+        again = pipeline.flat_decode(data.q[:, -1:], data.k, data.v, pos, buckets, workloads.FLAT_32K)
+        assert all(torch.equal(a, b) for a, b in zip(first, again))
+
+
+def test_rejects_cpu_tensors_and_bad_shapes():
+    data = workloads.clustered(1024, 8, 2, 128, n_clusters=16, seed=9, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=16)
+    pos = torch.tensor([1023], dtype=torch.int32, device=DEV)
+    with pytest.raises(ValueError):
+        pipeline.flat_decode(data.q[:, -1:].cpu(), data.k, data.v, pos, buckets, workloads.FLAT_32K)
+    with pytest.raises(ValueError):
+        pipeline.flat_decode(data.q[:, -2:], data.k, data.v, pos, buckets, workloads.FLAT_32K)
