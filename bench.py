@@ -355,6 +355,16 @@ def main() -> int:
         keys_per_row = pn.float().mean().item()
         ms = event_launch_times(lambda i: prefill_step(), args.prefill_steps, torch)
         p_ms = statistics.median(ms)
+        # the stages alone: chunk index queries + select, and the read kernel
+        pidx = pipeline.index_queries(data.q, HKV, CHUNK)[0]
+        plists, plens = pipeline.flat_select(pidx, ppos, buckets, config)
+        torch.cuda.synchronize()
+        sel_ms = statistics.median(event_launch_times(
+            lambda i: pipeline.flat_select(pipeline.index_queries(data.q, HKV, CHUNK)[0], ppos, buckets, config),
+            args.prefill_steps, torch))
+        read_ms = statistics.median(event_launch_times(
+            lambda i: pipeline.lsa_read_chunked(data.q, data.k, data.v, plists.unsqueeze(0), plens.unsqueeze(0),
+                                                D ** -0.5, CHUNK), args.prefill_steps, torch))
         # flops: 4*D per (q-head row, key); shared list + the causal local triangle
         list_pairs = float(pn.to(torch.float64).sum().item()) * CHUNK * (HQ // HKV)
         local_pairs = C * HQ * CHUNK * (CHUNK + 1) / 2
@@ -380,7 +390,10 @@ def main() -> int:
                    "tok_per_s": round(T_CTX / (p_ms * 1e-3), 1), "keys_per_row": round(keys_per_row + CHUNK / 2, 1),
                    "flops": flops, "tflops": round(flops / (p_ms * 1e-3) / 1e12, 2),
                    "mfma_frac": round(flops / (p_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-                   "read": "gather kernel (fp32 FMA)",
+                   "select_ms": round(sel_ms, 3), "read_ms": round(read_ms, 3),
+                   "read_tflops": round(flops / (read_ms * 1e-3) / 1e12, 2),
+                   "read_mfma_frac": round(flops / (read_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                   "read": "MFMA tile kernel (bf16 v_mfma_f32_32x32x16, fp32 accumulate)",
                    "dense_sdpa_ms": None if dense_p is None else round(dense_p, 3),
                    "speedup_vs_dense": None if dense_p is None else round(dense_p / p_ms, 3)}
         log(f"prefill {prefill}")

@@ -151,13 +151,22 @@ int lsa_read(const void* q, const void* k, const void* v, int dtype, int64_t B, 
              const int32_t* ids, const int32_t* lengths, int32_t W, int ids_per_head, float scale, int empty_nan,
              int32_t splits, int32_t* counters, void* scratch, size_t scratch_bytes, void* out, void* stream);
 
-/* Chunked prefill read on MFMA (bf16): query row t of chunk c = t / chunk reads chunk
- * c's per-kv-head list ids [B, C, Hkv, W] (first lengths[b, c, g] slots) plus the
- * chunk's causal block [c*chunk, t]. q [B, T, Hq, D], k/v [B, Tk, Hkv, D], out like q. */
+/* Chunked prefill read: query row t of chunk c = t / chunk reads chunk c's per-kv-head
+ * list ids [B, C, Hkv, W] (first lengths[b, c, g] slots) plus the chunk's causal block
+ * [c*chunk, t]. q [B, T, Hq, D], k/v [B, Tk, Hkv, D], out like q; T <= Tk.
+ * path: LSA_CHUNKED_AUTO (the MFMA tile kernel when lsa_read_chunked_mfma_ok, else the
+ * gather kernel), LSA_CHUNKED_GATHER, or LSA_CHUNKED_MFMA (an error where it does not
+ * apply). */
+#define LSA_CHUNKED_AUTO 0
+#define LSA_CHUNKED_GATHER 1
+#define LSA_CHUNKED_MFMA 2
 int lsa_read_chunked(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t T, int64_t Tk,
                      int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride,
                      int64_t kv_head_stride, const int32_t* ids, const int32_t* lengths, int32_t W, int32_t chunk,
-                     float scale, void* out, void* stream);
+                     float scale, int32_t path, void* out, void* stream);
+/* 1 when the MFMA tile kernel serves lsa_read_chunked for this shape: bf16/fp16 rows, head
+ * dim 64 or 128, chunk in {16, 32, 64, 128, 256}. */
+int lsa_read_chunked_mfma_ok(int dtype, int32_t D, int32_t chunk);
 
 /* Fused decode step: the flat select and the sparse read of one decode token per batch
  * row in ONE launch (reference port/bench.py:147-153 `step` = pipeline.flat_select then

@@ -24,6 +24,13 @@
 
 using namespace lsa;
 
+namespace lsa {
+int launch_read_chunked_mfma(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t T, int64_t Tk,
+                             int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
+                             const int32_t* ids, const int32_t* lengths, int32_t W, int32_t chunk, float scale,
+                             void* out, hipStream_t s);
+}  // namespace lsa
+
 namespace {
 
 struct ReadArgs {
@@ -246,8 +253,8 @@ extern "C" int lsa_read(const void* q, const void* k, const void* v, int dtype, 
 extern "C" int lsa_read_chunked(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t T,
                                 int64_t Tk, int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride,
                                 int64_t kv_token_stride, int64_t kv_head_stride, const int32_t* ids,
-                                const int32_t* lengths, int32_t W, int32_t chunk, float scale, void* out,
-                                void* stream) {
+                                const int32_t* lengths, int32_t W, int32_t chunk, float scale, int32_t path,
+                                void* out, void* stream) {
   int rc = check_read_common(q, k, v, dtype, B, T, Tk, Hq, Hkv, D, kv_batch_stride, kv_token_stride,
                              kv_head_stride, ids, lengths, W, out);
   if (rc != LSA_OK) return rc;
@@ -255,7 +262,14 @@ extern "C" int lsa_read_chunked(const void* q, const void* k, const void* v, int
   LSA_REQUIRE(T <= Tk, LSA_ERR_SHAPE, "lsa_read_chunked: %lld query rows exceed the cache %lld", (long long)T,
               (long long)Tk);
   LSA_REQUIRE(B * T * Hkv <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_read_chunked: too many rows");
+  LSA_REQUIRE(path >= LSA_CHUNKED_AUTO && path <= LSA_CHUNKED_MFMA, LSA_ERR_SHAPE, "lsa_read_chunked: path %d", path);
+  const int mfma_ok = lsa_read_chunked_mfma_ok(dtype, D, chunk);
+  LSA_REQUIRE(path != LSA_CHUNKED_MFMA || mfma_ok, LSA_ERR_SHAPE,
+              "lsa_read_chunked: the MFMA path needs bf16/fp16 rows, D 64/128 and a power-of-two chunk 16..256");
   if (B * T * Hkv == 0) return LSA_OK;
+  if (mfma_ok && path != LSA_CHUNKED_GATHER)
+    return launch_read_chunked_mfma(q, k, v, dtype, B, T, Tk, Hq, Hkv, D, kv_batch_stride, kv_token_stride,
+                                    kv_head_stride, ids, lengths, W, chunk, scale, out, (hipStream_t)stream);
   ReadArgs a;
   a.q = q; a.k = k; a.v = v; a.out = out; a.ids = ids; a.lengths = lengths;
   a.Tq = T; a.Tk = Tk; a.Hq = Hq; a.Hkv = Hkv; a.W = W; a.ids_per_head = 1; a.chunk = chunk;

@@ -1,2 +1,361 @@
-// MFMA tile kernel for the chunked prefill read (bf16, head dim 128).
+// MFMA tile kernel for the chunked prefill read (16-bit rows, head dim 64 or 128).
+//
+// Query row t of chunk c = t / chunk reads chunk c's per-kv-head list (its first lengths
+// slots) and then the chunk's own causal block [c*chunk, t] (the reference read of the
+// config-4 prefill: read_kernel_tiled.py:30-89 over these lists). Every row of a chunk
+// shares the list, so one workgroup serves (batch, chunk, kv-head, head group): the
+// chunk's rows of up to 256 / chunk query heads of the group - 256 query rows, 64 per
+// wave - and every K/V row of the list is gathered once for all of them.
+//
+// Per 32-key tile: the K rows land in LDS row-major and the V rows transposed (V^T), double
+// buffered, the next tile's ids and rows in flight while this one computes. Each wave then
+// computes S^T = K Q^T (v_mfma_f32_32x32x16: the K rows are the A operand read straight
+// from LDS, Q^T the B operand held in registers for the whole kernel), masks invalid and
+// non-causal keys, runs the online softmax in the exp2 domain per query column, and
+// accumulates O^T += V^T P^T: the S^T accumulator layout is exactly the P^T B operand
+// (lane (h, q) holds keys 8(r/4) + 4h + r%4 of column q), so P needs no shuffle; the V^T
+// A operand pairs the same key order from LDS. The running max is rescaled lazily: only
+// when a column's max grows by more than 2^8 is the state rescaled, so P stays below 256
+// in the 16-bit operand and most tiles skip the 128-register rescale.
+#include <math.h>
+
 #include "lsa_abi_common.h"
+#include "lsa_read_dev.h"
+
+using namespace lsa;
+
+namespace {
+
+constexpr int TK = 32;     // keys per tile
+constexpr int KPAD = 8;    // LDS row padding of the K tile (elements)
+constexpr int VPAD = 8;    // of the V^T tile
+constexpr float kRescale = 8.0f;  // log2 growth of a column max that forces a rescale
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+template <typename T> struct Mfma;
+template <> struct Mfma<bf16_t> {
+  typedef bf16x8_t op_t;
+  static __device__ __forceinline__ f32x16_t run(op_t a, op_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t bits(float x) { return f32_to_bf16(x); }
+};
+template <> struct Mfma<_Float16> {
+  typedef f16x8_t op_t;
+  static __device__ __forceinline__ f32x16_t run(op_t a, op_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t bits(float x) {
+    const _Float16 h = (_Float16)x;
+    uint16_t u;
+    __builtin_memcpy(&u, &h, 2);
+    return u;
+  }
+};
+
+template <int D>
+struct alignas(16) PrefillLds {
+  uint16_t k[2][TK][D + KPAD];   // K rows, raw 16-bit elements
+  uint16_t vt[2][D][TK + VPAD];  // V^T
+  int info[2][TK];               // per key: -2 skipped, -1 list key (every row), o >= 0 local offset
+};
+
+struct PrefillArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  const int32_t* ids;
+  const int32_t* lengths;
+  int64_t T, Tk;
+  int64_t kv_sb, kv_st, kv_sh;
+  int Hq, Hkv, W, chunk, C;
+  int hpw;   // query heads per workgroup (256 / chunk, at most the group)
+  int n_hg;  // head groups per kv-head
+  float scale_log2;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) {
+  using M = Mfma<T>;
+  using op_t = typename M::op_t;
+  constexpr int KS = D / 16;              // k-steps of S^T
+  constexpr int DB = D / 32;              // dim blocks of O^T
+  constexpr int SEGS = D / 8;             // 16-byte segments of a row
+  constexpr int KPP = LSA_BLOCK / SEGS;   // keys loaded per pass
+  constexpr int PASSES = TK / KPP;
+  __shared__ PrefillLds<D> sh;
+
+  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
+  const int hh = lane / 32, ln = lane % 32;
+  int64_t x = blockIdx.x;
+  const int hg = (int)(x % a.n_hg); x /= a.n_hg;
+  const int g = (int)(x % a.Hkv); x /= a.Hkv;
+  const int c = (int)(x % a.C);
+  const int64_t b = x / a.C;
+  const int gq = a.Hq / a.Hkv;
+  const int64_t c0 = (int64_t)c * a.chunk;
+  const int n_loc = (int)min((int64_t)a.chunk, a.T - c0);  // rows of this chunk
+  const int64_t li = (b * a.C + c) * a.Hkv + g;
+  int n_list = a.W > 0 ? a.lengths[li] : 0;
+  n_list = n_list < 0 ? 0 : (n_list > a.W ? a.W : n_list);
+  const int32_t* list = a.ids + li * a.W;
+  const int n_tot = n_list + n_loc;
+  const int n_tiles = (n_tot + TK - 1) / TK;
+  const T* kb = (const T*)a.k + b * a.kv_sb + (int64_t)g * a.kv_sh;
+  const T* vb = (const T*)a.v + b * a.kv_sb + (int64_t)g * a.kv_sh;
+
+  // this lane's query columns: qi = 64 w + 32 qb + ln -> (local head, token)
+  int tok[2];
+  bool qok[2];
+  int64_t qrow[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int qi = 64 * w + 32 * qb + ln;
+    const int hl = qi / a.chunk;
+    tok[qb] = qi % a.chunk;
+    const int head_in_group = hg * a.hpw + hl;
+    qok[qb] = hl < a.hpw && head_in_group < gq && tok[qb] < n_loc;
+    const int head = g * gq + (qok[qb] ? head_in_group : 0);
+    const int64_t t = c0 + (qok[qb] ? tok[qb] : 0);
+    qrow[qb] = ((b * a.T + t) * a.Hq + head) * (int64_t)D;
+  }
+  // Q^T B operands, whole kernel: 16 bytes of row q at dims [16 s + 8 hh, +8)
+  op_t qop[2][KS];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const uint4 raw = *(const uint4*)((const T*)a.q + qrow[qb] + 16 * s + 8 * hh);
+      qop[qb][s] = __builtin_bit_cast(op_t, raw);
+    }
+  }
+
+  // tile loads: key kk = pass * KPP + tid / SEGS, segment seg = tid % SEGS. A tile's list
+  // ids are fetched one tile ahead of its K/V rows (an unconditional, clamped load), and
+  // its rows one tile ahead of their use.
+  const int seg = tid % SEGS;
+  const int32_t* lsrc = a.W > 0 ? list : a.lengths + li;  // always a valid address
+  int32_t idq[PASSES];
+  int infq[PASSES];
+  auto fetch_ids = [&](int tile) {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int j = tile * TK + p * KPP + tid / SEGS;
+      const int jl = j < n_list ? j : (n_list > 0 ? n_list - 1 : 0);
+      const int32_t lid = lsrc[jl];
+      const int o = j - n_list;
+      infq[p] = j < n_list ? ((lid >= 0 && lid < a.Tk) ? -1 : -2) : (j < n_tot ? o : -2);
+      idq[p] = j < n_list ? lid : (int32_t)(c0 + o);
+    }
+  };
+  uint4 kreg[PASSES], vreg[PASSES];
+  int kinfo[PASSES];
+  auto load_tile = [&]() {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const uint64_t off = (uint64_t)(uint32_t)(infq[p] >= -1 ? idq[p] : 0) * (uint64_t)a.kv_st + seg * 8;
+      kreg[p] = *(const uint4*)(kb + off);
+      vreg[p] = *(const uint4*)(vb + off);
+      kinfo[p] = infq[p];
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int kk = p * KPP + tid / SEGS;
+      const bool ok = kinfo[p] >= -1;
+      const uint4 kr = ok ? kreg[p] : make_uint4(0, 0, 0, 0);
+      const uint4 vr = ok ? vreg[p] : make_uint4(0, 0, 0, 0);
+      *(uint4*)&sh.k[buf][kk][seg * 8] = kr;
+      const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sh.vt[buf][seg * 8 + 2 * e][kk] = (uint16_t)(vw[e] & 0xFFFFu);
+        sh.vt[buf][seg * 8 + 2 * e + 1][kk] = (uint16_t)(vw[e] >> 16);
+      }
+      if (seg == 0) sh.info[buf][kk] = kinfo[p];
+    }
+  };
+
+  f32x16_t o[DB][2];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[d][qb][r] = 0.0f;
+    }
+  }
+  float m_run[2] = {kNegBig, kNegBig}, l_run[2] = {0.0f, 0.0f};
+
+  fetch_ids(0);
+  load_tile();
+  fetch_ids(1);
+  for (int tile = 0; tile < n_tiles; ++tile) {
+    const int buf = tile & 1;
+    store_tile(buf);
+    __syncthreads();
+    if (tile + 1 < n_tiles) {  // in flight during this tile's math
+      load_tile();
+      fetch_ids(tile + 2);
+    }
+
+    // S^T = K Q^T: rows = the tile's 32 keys, columns = this wave's 64 query rows
+    f32x16_t st[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st[qb][r] = 0.0f;
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const op_t ka = __builtin_bit_cast(op_t, *(const uint4*)&sh.k[buf][ln][16 * s + 8 * hh]);
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) st[qb] = M::run(ka, qop[qb][s], st[qb]);
+    }
+    // the lane's 16 keys: 8 (r / 4) + 4 hh + r % 4, four runs of four
+    int kinf[16];
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int4 v4 = *(const int4*)&sh.info[buf][8 * r4 + 4 * hh];
+      kinf[4 * r4 + 0] = v4.x; kinf[4 * r4 + 1] = v4.y; kinf[4 * r4 + 2] = v4.z; kinf[4 * r4 + 3] = v4.w;
+    }
+    // masked, scaled scores; column max over both lane halves
+    float mt[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int inf = kinf[r];
+        const bool vis = inf == -1 || (inf >= 0 && inf <= tok[qb]);
+        const float sv = vis ? st[qb][r] * a.scale_log2 : -INFINITY;
+        st[qb][r] = sv;
+        mx = fmaxf(mx, sv);
+      }
+      mt[qb] = fmaxf(mx, lane_xor(mx, 32));
+    }
+    // lazy rescale: only when some column's max grew by more than 2^kRescale
+    bool grow = false;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) grow |= mt[qb] > m_run[qb] + kRescale;
+    if (__any(grow)) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const float mn = fmaxf(m_run[qb], mt[qb]);
+        const float alpha = fast_exp2(m_run[qb] - mn);
+        m_run[qb] = mn;
+        l_run[qb] *= alpha;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[d][qb][r] *= alpha;
+        }
+      }
+    }
+    // P^T as the B operand: regs 8 s' .. 8 s' + 7 of the accumulator are keys
+    // 16 s' + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}
+    op_t pb[2][2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      uint16_t pbits[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(st[qb][r] - m_run[qb]);
+        l_run[qb] += p;
+        pbits[r] = M::bits(p);
+      }
+#pragma unroll
+      for (int sp = 0; sp < 2; ++sp) {
+        uint4 u;
+        u.x = pbits[8 * sp + 0] | ((uint32_t)pbits[8 * sp + 1] << 16);
+        u.y = pbits[8 * sp + 2] | ((uint32_t)pbits[8 * sp + 3] << 16);
+        u.z = pbits[8 * sp + 4] | ((uint32_t)pbits[8 * sp + 5] << 16);
+        u.w = pbits[8 * sp + 6] | ((uint32_t)pbits[8 * sp + 7] << 16);
+        pb[qb][sp] = __builtin_bit_cast(op_t, u);
+      }
+    }
+    // O^T += V^T P^T: A = V^T rows (dims) at the same key order, two 8-byte LDS reads
+#pragma unroll
+    for (int sp = 0; sp < 2; ++sp) {
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const int dim = 32 * d + ln;
+        const uint2 lo = *(const uint2*)&sh.vt[buf][dim][16 * sp + 4 * hh];
+        const uint2 hi = *(const uint2*)&sh.vt[buf][dim][16 * sp + 8 + 4 * hh];
+        const op_t va = __builtin_bit_cast(op_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) o[d][qb] = M::run(va, pb[qb][sp], o[d][qb]);
+      }
+    }
+  }
+
+  // normalise and store: lane (hh, q) holds dims 32 d + 8 (r / 4) + 4 hh + r % 4 of column q
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const float lt = l_run[qb] + lane_xor(l_run[qb], 32);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    if (!qok[qb]) continue;
+    T* op = (T*)a.out + qrow[qb];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int dim = 32 * d + 8 * r4 + 4 * hh;
+        uint2 u;
+        u.x = M::bits(o[d][qb][4 * r4 + 0] * inv) | ((uint32_t)M::bits(o[d][qb][4 * r4 + 1] * inv) << 16);
+        u.y = M::bits(o[d][qb][4 * r4 + 2] * inv) | ((uint32_t)M::bits(o[d][qb][4 * r4 + 3] * inv) << 16);
+        *(uint2*)(op + dim) = u;
+      }
+    }
+  }
+}
+
+template <typename T>
+void launch_prefill(const PrefillArgs& a, int D, dim3 grid, hipStream_t s) {
+  if (D == 64) prefill_mfma_kernel<T, 64><<<grid, LSA_BLOCK, 0, s>>>(a);
+  else prefill_mfma_kernel<T, 128><<<grid, LSA_BLOCK, 0, s>>>(a);
+}
+
+}  // namespace
+
+// Whether the MFMA tile kernel serves a chunked read of this shape: 16-bit rows, head dim
+// 64 or 128, chunk in {16, 32, 64, 128, 256} (a workgroup holds 256 query rows).
+extern "C" int lsa_read_chunked_mfma_ok(int dtype, int32_t D, int32_t chunk) {
+  const bool type_ok = dtype == LSA_BF16 || dtype == LSA_F16;
+  const bool d_ok = D == 64 || D == 128;
+  const bool c_ok = chunk == 16 || chunk == 32 || chunk == 64 || chunk == 128 || chunk == 256;
+  return (type_ok && d_ok && c_ok) ? 1 : 0;
+}
+
+namespace lsa {
+
+// Launches the MFMA chunked read (arguments already checked by lsa_read_chunked).
+int launch_read_chunked_mfma(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t T, int64_t Tk,
+                             int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
+                             const int32_t* ids, const int32_t* lengths, int32_t W, int32_t chunk, float scale,
+                             void* out, hipStream_t s) {
+  PrefillArgs a;
+  a.q = q; a.k = k; a.v = v; a.out = out; a.ids = ids; a.lengths = lengths;
+  a.T = T; a.Tk = Tk; a.kv_sb = kv_sb; a.kv_st = kv_st; a.kv_sh = kv_sh;
+  a.Hq = Hq; a.Hkv = Hkv; a.W = W; a.chunk = chunk;
+  a.C = (int)((T + chunk - 1) / chunk);
+  const int gq = Hq / Hkv;
+  const int per = LSA_BLOCK / chunk;  // heads that fill 256 rows
+  a.hpw = per < gq ? per : gq;
+  a.n_hg = (gq + a.hpw - 1) / a.hpw;
+  a.scale_log2 = scale * kLog2e;
+  const int64_t n = B * a.C * Hkv * a.n_hg;
+  LSA_REQUIRE(n <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_read_chunked: too many workgroups");
+  if (n == 0) return LSA_OK;
+  if (dtype == LSA_BF16) launch_prefill<bf16_t>(a, D, dim3((unsigned)n), s);
+  else launch_prefill<_Float16>(a, D, dim3((unsigned)n), s);
+  LSA_LAUNCHED("lsa_read_chunked (mfma)");
+  return LSA_OK;
+}
+
+}  // namespace lsa

@@ -104,10 +104,14 @@ def sparse_read_auto(q, k, v, read_ids, lengths, scale=None):
     return _sparse_read(q, k, v, read_ids, lengths, scale, empty_nan=False)
 
 
-def sparse_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale=None, chunk_size: int = 64):
+def sparse_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale=None, chunk_size: int = 64, path: str | None = None):
     """Chunked-prefill read: query row t reads chunk ``t // chunk_size``'s per-kv-head list
     and the chunk's causal block [chunk start, t]. chunk_lists [B, C, Hkv, W] (or
-    [C, Hkv, W] for B == 1), chunk_lengths [B, C, Hkv] (or [C, Hkv])."""
+    [C, Hkv, W] for B == 1), chunk_lengths [B, C, Hkv] (or [C, Hkv]).
+
+    ``path`` (default ``LSA_PREFILL_READ`` or ``auto``): ``auto`` runs the MFMA tile kernel
+    where it applies (bf16/fp16, D 64/128, power-of-two chunk 16..256) and the gather kernel
+    elsewhere; ``gather`` / ``mfma`` force one (``mfma`` raises where it does not apply)."""
     assert q.is_cuda and k.is_cuda and v.is_cuda, "the sparse read is a GPU kernel"
     B, T, Hq, D = q.shape
     Tk, Hkv = k.shape[1], k.shape[2]
@@ -123,7 +127,11 @@ def sparse_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale=None, chunk_s
     out = torch.empty_like(q)
     if B * T == 0:
         return out
+    path = os.environ.get("LSA_PREFILL_READ", "auto") if path is None else path
+    codes = {"auto": _abi.CHUNKED_AUTO, "gather": _abi.CHUNKED_GATHER, "mfma": _abi.CHUNKED_MFMA}
+    if path not in codes:
+        raise ValueError(f"chunked read path must be auto|gather|mfma, got {path!r}")
     _abi.call("lsa_read_chunked", q.data_ptr(), k.data_ptr(), v.data_ptr(), _abi.dtype_code(q.dtype), B, T, Tk, Hq,
               Hkv, D, sb, st, sh, ids.data_ptr(), lens.data_ptr(), width, chunk_size,
-              float(D ** -0.5 if scale is None else scale), out.data_ptr(), _abi.stream(q.device))
+              float(D ** -0.5 if scale is None else scale), codes[path], out.data_ptr(), _abi.stream(q.device))
     return out
