@@ -41,27 +41,37 @@ template <> struct Mfma<bf16_t> {
   static __device__ __forceinline__ f32x16_t run(op_t a, op_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint16_t bits(float x) { return f32_to_bf16(x); }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {  // v_cvt_pk_bf16_f32 (RNE)
+    typedef __bf16 v2_t __attribute__((ext_vector_type(2)));
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    const f2_t f = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2_t));
+  }
 };
 template <> struct Mfma<_Float16> {
   typedef f16x8_t op_t;
   static __device__ __forceinline__ f32x16_t run(op_t a, op_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint16_t bits(float x) {
-    const _Float16 h = (_Float16)x;
-    uint16_t u;
-    __builtin_memcpy(&u, &h, 2);
-    return u;
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef _Float16 v2_t __attribute__((ext_vector_type(2)));
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    const f2_t f = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2_t));
   }
 };
 
 template <int D>
 struct alignas(16) PrefillLds {
   uint16_t k[2][TK][D + KPAD];   // K rows, raw 16-bit elements
-  uint16_t vt[2][D][TK + VPAD];  // V^T
+  uint16_t vt[2][D][TK + VPAD];  // V^T, swizzled (vt_col)
   int info[2][TK];               // per key: -2 skipped, -1 list key (every row), o >= 0 local offset
 };
+
+// Column of key `key` in V^T row `dim`: groups of 4 keys (8 bytes) XOR-swizzled by the
+// row's eighth, so the transposed stores (16 dims apart per lane group) and the operand
+// reads spread over the LDS banks (2-way instead of 16-way on the stores).
+__device__ __forceinline__ int vt_col(int dim, int key) { return 4 * ((key >> 2) ^ ((dim >> 3) & 7)) + (key & 3); }
 
 struct PrefillArgs {
   const void* q;
@@ -139,28 +149,33 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
   // its rows one tile ahead of their use.
   const int seg = tid % SEGS;
   const int32_t* lsrc = a.W > 0 ? list : a.lengths + li;  // always a valid address
-  int32_t idq[PASSES];
-  int infq[PASSES];
-  auto fetch_ids = [&](int tile) {
+  // raw list ids: `lidq` of the next tile to gather, `lidn` of the one after, issued
+  // before that gather and handed over at the end of the iteration, so every wait for a
+  // load falls after the math that hides it (the vector-memory counter retires in order)
+  int32_t lidq[PASSES], lidn[PASSES];
+  auto fetch_ids = [&](int tile, int32_t (&dst)[PASSES]) {
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       const int j = tile * TK + p * KPP + tid / SEGS;
       const int jl = j < n_list ? j : (n_list > 0 ? n_list - 1 : 0);
-      const int32_t lid = lsrc[jl];
-      const int o = j - n_list;
-      infq[p] = j < n_list ? ((lid >= 0 && lid < a.Tk) ? -1 : -2) : (j < n_tot ? o : -2);
-      idq[p] = j < n_list ? lid : (int32_t)(c0 + o);
+      dst[p] = lsrc[jl];
     }
   };
   uint4 kreg[PASSES], vreg[PASSES];
   int kinfo[PASSES];
-  auto load_tile = [&]() {
+  auto load_tile = [&](int tile) {
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
-      const uint64_t off = (uint64_t)(uint32_t)(infq[p] >= -1 ? idq[p] : 0) * (uint64_t)a.kv_st + seg * 8;
+      const int j = tile * TK + p * KPP + tid / SEGS;
+      const int32_t lid = lidq[p];
+      const int o = j - n_list;
+      const bool in_list = j < n_list;
+      const int info = in_list ? (((lid >= 0) & (lid < a.Tk)) ? -1 : -2) : (j < n_tot ? o : -2);
+      const int32_t id = in_list ? lid : (int32_t)(c0 + o);
+      const uint64_t off = (uint64_t)(uint32_t)(info >= -1 ? id : 0) * (uint64_t)a.kv_st + seg * 8;
       kreg[p] = *(const uint4*)(kb + off);
       vreg[p] = *(const uint4*)(vb + off);
-      kinfo[p] = infq[p];
+      kinfo[p] = info;
     }
   };
   auto store_tile = [&](int buf) {
@@ -174,8 +189,9 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
       const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        sh.vt[buf][seg * 8 + 2 * e][kk] = (uint16_t)(vw[e] & 0xFFFFu);
-        sh.vt[buf][seg * 8 + 2 * e + 1][kk] = (uint16_t)(vw[e] >> 16);
+        const int d0 = seg * 8 + 2 * e;
+        sh.vt[buf][d0][vt_col(d0, kk)] = (uint16_t)(vw[e] & 0xFFFFu);
+        sh.vt[buf][d0 + 1][vt_col(d0 + 1, kk)] = (uint16_t)(vw[e] >> 16);
       }
       if (seg == 0) sh.info[buf][kk] = kinfo[p];
     }
@@ -192,16 +208,16 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
   }
   float m_run[2] = {kNegBig, kNegBig}, l_run[2] = {0.0f, 0.0f};
 
-  fetch_ids(0);
-  load_tile();
-  fetch_ids(1);
+  fetch_ids(0, lidq);
+  load_tile(0);
+  fetch_ids(1, lidq);
   for (int tile = 0; tile < n_tiles; ++tile) {
     const int buf = tile & 1;
     store_tile(buf);
     __syncthreads();
     if (tile + 1 < n_tiles) {  // in flight during this tile's math
-      load_tile();
-      fetch_ids(tile + 2);
+      fetch_ids(tile + 2, lidn);
+      load_tile(tile + 1);
     }
 
     // S^T = K Q^T: rows = the tile's 32 keys, columns = this wave's 64 query rows
@@ -224,19 +240,34 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
       const int4 v4 = *(const int4*)&sh.info[buf][8 * r4 + 4 * hh];
       kinf[4 * r4 + 0] = v4.x; kinf[4 * r4 + 1] = v4.y; kinf[4 * r4 + 2] = v4.z; kinf[4 * r4 + 3] = v4.w;
     }
-    // masked, scaled scores; column max over both lane halves
+    // scaled scores; the mask only where this wave sees a skipped or local key (a uniform
+    // branch: most tiles are list keys every row sees)
+    int odd = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) odd |= kinf[r] != -1;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st[qb][r] *= a.scale_log2;
+    }
+    if (__any(odd)) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int inf = kinf[r];
+          const bool vis = (inf == -1) | ((unsigned)inf <= (unsigned)tok[qb]);
+          st[qb][r] = vis ? st[qb][r] : -INFINITY;
+        }
+      }
+    }
+    // column max over both lane halves
     float mt[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      float mx = -INFINITY;
+      float mx = st[qb][0];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int inf = kinf[r];
-        const bool vis = inf == -1 || (inf >= 0 && inf <= tok[qb]);
-        const float sv = vis ? st[qb][r] * a.scale_log2 : -INFINITY;
-        st[qb][r] = sv;
-        mx = fmaxf(mx, sv);
-      }
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, st[qb][r]);
       mt[qb] = fmaxf(mx, lane_xor(mx, 32));
     }
     // lazy rescale: only when some column's max grew by more than 2^kRescale
@@ -262,20 +293,19 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
     op_t pb[2][2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      uint16_t pbits[16];
+      float pv[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(st[qb][r] - m_run[qb]);
-        l_run[qb] += p;
-        pbits[r] = M::bits(p);
+        pv[r] = fast_exp2(st[qb][r] - m_run[qb]);
+        l_run[qb] += pv[r];
       }
 #pragma unroll
       for (int sp = 0; sp < 2; ++sp) {
         uint4 u;
-        u.x = pbits[8 * sp + 0] | ((uint32_t)pbits[8 * sp + 1] << 16);
-        u.y = pbits[8 * sp + 2] | ((uint32_t)pbits[8 * sp + 3] << 16);
-        u.z = pbits[8 * sp + 4] | ((uint32_t)pbits[8 * sp + 5] << 16);
-        u.w = pbits[8 * sp + 6] | ((uint32_t)pbits[8 * sp + 7] << 16);
+        u.x = M::pack2(pv[8 * sp + 0], pv[8 * sp + 1]);
+        u.y = M::pack2(pv[8 * sp + 2], pv[8 * sp + 3]);
+        u.z = M::pack2(pv[8 * sp + 4], pv[8 * sp + 5]);
+        u.w = M::pack2(pv[8 * sp + 6], pv[8 * sp + 7]);
         pb[qb][sp] = __builtin_bit_cast(op_t, u);
       }
     }
@@ -285,13 +315,15 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
         const int dim = 32 * d + ln;
-        const uint2 lo = *(const uint2*)&sh.vt[buf][dim][16 * sp + 4 * hh];
-        const uint2 hi = *(const uint2*)&sh.vt[buf][dim][16 * sp + 8 + 4 * hh];
+        const uint2 lo = *(const uint2*)&sh.vt[buf][dim][vt_col(dim, 16 * sp + 4 * hh)];
+        const uint2 hi = *(const uint2*)&sh.vt[buf][dim][vt_col(dim, 16 * sp + 8 + 4 * hh)];
         const op_t va = __builtin_bit_cast(op_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) o[d][qb] = M::run(va, pb[qb][sp], o[d][qb]);
       }
     }
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) lidq[p] = lidn[p];
   }
 
   // normalise and store: lane (hh, q) holds dims 32 d + 8 (r / 4) + 4 hh + r % 4 of column q
@@ -307,8 +339,8 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
       for (int r4 = 0; r4 < 4; ++r4) {
         const int dim = 32 * d + 8 * r4 + 4 * hh;
         uint2 u;
-        u.x = M::bits(o[d][qb][4 * r4 + 0] * inv) | ((uint32_t)M::bits(o[d][qb][4 * r4 + 1] * inv) << 16);
-        u.y = M::bits(o[d][qb][4 * r4 + 2] * inv) | ((uint32_t)M::bits(o[d][qb][4 * r4 + 3] * inv) << 16);
+        u.x = M::pack2(o[d][qb][4 * r4 + 0] * inv, o[d][qb][4 * r4 + 1] * inv);
+        u.y = M::pack2(o[d][qb][4 * r4 + 2] * inv, o[d][qb][4 * r4 + 3] * inv);
         *(uint2*)(op + dim) = u;
       }
     }
