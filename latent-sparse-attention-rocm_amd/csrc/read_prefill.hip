@@ -30,6 +30,7 @@ constexpr int TK = 32;     // keys per tile
 constexpr int KPAD = 8;    // LDS row padding of the K tile (elements)
 constexpr int VPAD = 8;    // of the V^T tile
 constexpr float kRescale = 8.0f;  // log2 growth of a column max that forces a rescale
+constexpr int kRows = 256;       // query rows of a workgroup
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -63,9 +64,9 @@ template <> struct Mfma<_Float16> {
 
 template <int D>
 struct alignas(16) PrefillLds {
-  uint16_t k[2][TK][D + KPAD];   // K rows, raw 16-bit elements
-  uint16_t vt[2][D][TK + VPAD];  // V^T, swizzled (vt_col)
-  int info[2][TK];               // per key: -2 skipped, -1 list key (every row), o >= 0 local offset
+  uint16_t k[3][TK][D + KPAD];   // K rows, raw 16-bit elements (three tiles in flight)
+  uint16_t vt[3][D][TK + VPAD];  // V^T, swizzled (vt_col)
+  int info[3][TK];               // per key: -2 skipped, -1 list key (every row), o >= 0 local offset
 };
 
 // Column of key `key` in V^T row `dim`: groups of 4 keys (8 bytes) XOR-swizzled by the
@@ -88,15 +89,17 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-template <typename T, int D>
-__global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) {
+// QB query blocks of 32 columns per wave; 8 / QB waves hold the workgroup's 256 rows.
+template <typename T, int D, int QB>
+__global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs a) {
   using M = Mfma<T>;
   using op_t = typename M::op_t;
+  constexpr int NTH = 64 * (8 / QB);      // threads
   constexpr int KS = D / 16;              // k-steps of S^T
   constexpr int DB = D / 32;              // dim blocks of O^T
   constexpr int SEGS = D / 8;             // 16-byte segments of a row
-  constexpr int KPP = LSA_BLOCK / SEGS;   // keys loaded per pass
-  constexpr int PASSES = TK / KPP;
+  constexpr int KPP = NTH / SEGS;         // keys loaded per pass
+  constexpr int PASSES = TK >= KPP ? TK / KPP : 1;
   __shared__ PrefillLds<D> sh;
 
   const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
@@ -118,13 +121,13 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
   const T* kb = (const T*)a.k + b * a.kv_sb + (int64_t)g * a.kv_sh;
   const T* vb = (const T*)a.v + b * a.kv_sb + (int64_t)g * a.kv_sh;
 
-  // this lane's query columns: qi = 64 w + 32 qb + ln -> (local head, token)
-  int tok[2];
-  bool qok[2];
-  int64_t qrow[2];
+  // this lane's query columns: qi = 32 QB w + 32 qb + ln -> (local head, token)
+  int tok[QB];
+  bool qok[QB];
+  int64_t qrow[QB];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int qi = 64 * w + 32 * qb + ln;
+  for (int qb = 0; qb < QB; ++qb) {
+    const int qi = 32 * QB * w + 32 * qb + ln;
     const int hl = qi / a.chunk;
     tok[qb] = qi % a.chunk;
     const int head_in_group = hg * a.hpw + hl;
@@ -134,9 +137,9 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
     qrow[qb] = ((b * a.T + t) * a.Hq + head) * (int64_t)D;
   }
   // Q^T B operands, whole kernel: 16 bytes of row q at dims [16 s + 8 hh, +8)
-  op_t qop[2][KS];
+  op_t qop[QB][KS];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const uint4 raw = *(const uint4*)((const T*)a.q + qrow[qb] + 16 * s + 8 * hh);
@@ -153,10 +156,11 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
   // before that gather and handed over at the end of the iteration, so every wait for a
   // load falls after the math that hides it (the vector-memory counter retires in order)
   int32_t lidq[PASSES], lidn[PASSES];
+  const bool loader = KPP <= TK || tid / SEGS < TK;  // threads with a key to load
   auto fetch_ids = [&](int tile, int32_t (&dst)[PASSES]) {
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
-      const int j = tile * TK + p * KPP + tid / SEGS;
+      const int j = tile * TK + p * KPP + (loader ? tid / SEGS : 0);
       const int jl = j < n_list ? j : (n_list > 0 ? n_list - 1 : 0);
       dst[p] = lsrc[jl];
     }
@@ -166,7 +170,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
   auto load_tile = [&](int tile) {
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
-      const int j = tile * TK + p * KPP + tid / SEGS;
+      const int j = tile * TK + p * KPP + (loader ? tid / SEGS : 0);
       const int32_t lid = lidq[p];
       const int o = j - n_list;
       const bool in_list = j < n_list;
@@ -179,6 +183,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
     }
   };
   auto store_tile = [&](int buf) {
+    if (!loader) return;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       const int kk = p * KPP + tid / SEGS;
@@ -197,33 +202,28 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
     }
   };
 
-  f32x16_t o[DB][2];
+  f32x16_t o[DB][QB];
 #pragma unroll
   for (int d = 0; d < DB; ++d) {
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[d][qb][r] = 0.0f;
     }
   }
-  float m_run[2] = {kNegBig, kNegBig}, l_run[2] = {0.0f, 0.0f};
-
-  fetch_ids(0, lidq);
-  load_tile(0);
-  fetch_ids(1, lidq);
-  for (int tile = 0; tile < n_tiles; ++tile) {
-    const int buf = tile & 1;
-    store_tile(buf);
-    __syncthreads();
-    if (tile + 1 < n_tiles) {  // in flight during this tile's math
-      fetch_ids(tile + 2, lidn);
-      load_tile(tile + 1);
-    }
-
-    // S^T = K Q^T: rows = the tile's 32 keys, columns = this wave's 64 query rows
-    f32x16_t st[2];
+  float m_run[QB], l_run[QB];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
+    m_run[qb] = kNegBig;
+    l_run[qb] = 0.0f;
+  }
+
+  // S^T = K Q^T of the tile in LDS buffer `buf`: rows = its 32 keys, columns = this wave's
+  // query rows. Issued a tile ahead of its softmax, so the matrix core runs while the VALU
+  // does the previous tile's softmax.
+  auto scores = [&](int buf, f32x16_t (&st)[QB]) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) st[qb][r] = 0.0f;
     }
@@ -231,8 +231,11 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
     for (int s = 0; s < KS; ++s) {
       const op_t ka = __builtin_bit_cast(op_t, *(const uint4*)&sh.k[buf][ln][16 * s + 8 * hh]);
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) st[qb] = M::run(ka, qop[qb][s], st[qb]);
+      for (int qb = 0; qb < QB; ++qb) st[qb] = M::run(ka, qop[qb][s], st[qb]);
     }
+  };
+  // online softmax of the tile in `buf` (raw scores st), then O^T += V^T P^T
+  auto softmax_pv = [&](int buf, f32x16_t (&st)[QB]) {
     // the lane's 16 keys: 8 (r / 4) + 4 hh + r % 4, four runs of four
     int kinf[16];
 #pragma unroll
@@ -240,19 +243,14 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
       const int4 v4 = *(const int4*)&sh.info[buf][8 * r4 + 4 * hh];
       kinf[4 * r4 + 0] = v4.x; kinf[4 * r4 + 1] = v4.y; kinf[4 * r4 + 2] = v4.z; kinf[4 * r4 + 3] = v4.w;
     }
-    // scaled scores; the mask only where this wave sees a skipped or local key (a uniform
-    // branch: most tiles are list keys every row sees)
+    // the mask only where this wave sees a skipped or local key (a uniform branch: most
+    // tiles are list keys every row sees)
     int odd = 0;
 #pragma unroll
     for (int r = 0; r < 16; ++r) odd |= kinf[r] != -1;
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) st[qb][r] *= a.scale_log2;
-    }
     if (__any(odd)) {
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
+      for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int inf = kinf[r];
@@ -261,22 +259,22 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
         }
       }
     }
-    // column max over both lane halves
-    float mt[2];
+    // column max (raw scores; the scale is positive) over both lane halves, in log2 units
+    float mt[QB];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       float mx = st[qb][0];
 #pragma unroll
       for (int r = 1; r < 16; ++r) mx = fmaxf(mx, st[qb][r]);
-      mt[qb] = fmaxf(mx, lane_xor(mx, 32));
+      mt[qb] = fmaxf(mx, lane_xor(mx, 32)) * a.scale_log2;
     }
     // lazy rescale: only when some column's max grew by more than 2^kRescale
     bool grow = false;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) grow |= mt[qb] > m_run[qb] + kRescale;
+    for (int qb = 0; qb < QB; ++qb) grow |= mt[qb] > m_run[qb] + kRescale;
     if (__any(grow)) {
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
+      for (int qb = 0; qb < QB; ++qb) {
         const float mn = fmaxf(m_run[qb], mt[qb]);
         const float alpha = fast_exp2(m_run[qb] - mn);
         m_run[qb] = mn;
@@ -289,14 +287,14 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
       }
     }
     // P^T as the B operand: regs 8 s' .. 8 s' + 7 of the accumulator are keys
-    // 16 s' + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}
-    op_t pb[2][2];
+    // 16 s' + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}; p = exp2(s * scale - m)
+    op_t pb[QB][2];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       float pv[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        pv[r] = fast_exp2(st[qb][r] - m_run[qb]);
+        pv[r] = fast_exp2(fmaf(st[qb][r], a.scale_log2, -m_run[qb]));
         l_run[qb] += pv[r];
       }
 #pragma unroll
@@ -319,16 +317,47 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
         const uint2 hi = *(const uint2*)&sh.vt[buf][dim][vt_col(dim, 16 * sp + 8 + 4 * hh)];
         const op_t va = __builtin_bit_cast(op_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) o[d][qb] = M::run(va, pb[qb][sp], o[d][qb]);
+        for (int qb = 0; qb < QB; ++qb) o[d][qb] = M::run(va, pb[qb][sp], o[d][qb]);
       }
     }
+  };
+
+  // Pipeline, one barrier per tile over three LDS buffers: iteration t stores tile t + 1
+  // (gathered an iteration earlier), issues the gather of tile t + 2 and the scores of
+  // tile t + 1, then runs tile t's softmax and P V. A buffer is rewritten two iterations
+  // after its last reader, which the intervening barrier has let finish.
+  f32x16_t st_cur[QB], st_next[QB];
+  fetch_ids(0, lidq);
+  load_tile(0);
+  fetch_ids(1, lidq);
+  store_tile(0);
+  __syncthreads();
+  if (n_tiles > 1) {
+    fetch_ids(2, lidn);
+    load_tile(1);
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) lidq[p] = lidn[p];
+  }
+  scores(0, st_cur);
+  for (int tile = 0; tile < n_tiles; ++tile) {
+    const bool more = tile + 1 < n_tiles;
+    if (more) store_tile((tile + 1) % 3);
+    __syncthreads();
+    if (tile + 2 < n_tiles) {  // in flight during this tile's math
+      fetch_ids(tile + 3, lidn);
+      load_tile(tile + 2);
+    }
+    if (more) scores((tile + 1) % 3, st_next);
+    softmax_pv(tile % 3, st_cur);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) st_cur[qb] = st_next[qb];
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) lidq[p] = lidn[p];
   }
 
   // normalise and store: lane (hh, q) holds dims 32 d + 8 (r / 4) + 4 hh + r % 4 of column q
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     const float lt = l_run[qb] + lane_xor(l_run[qb], 32);
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     if (!qok[qb]) continue;
@@ -347,10 +376,13 @@ __global__ __launch_bounds__(LSA_BLOCK) void prefill_mfma_kernel(PrefillArgs a) 
   }
 }
 
+constexpr int kQB = 1;  // 8 waves of 32 query columns: two waves per SIMD hide each other's latency
+
 template <typename T>
 void launch_prefill(const PrefillArgs& a, int D, dim3 grid, hipStream_t s) {
-  if (D == 64) prefill_mfma_kernel<T, 64><<<grid, LSA_BLOCK, 0, s>>>(a);
-  else prefill_mfma_kernel<T, 128><<<grid, LSA_BLOCK, 0, s>>>(a);
+  constexpr int nth = 64 * (8 / kQB);
+  if (D == 64) prefill_mfma_kernel<T, 64, kQB><<<grid, nth, 0, s>>>(a);
+  else prefill_mfma_kernel<T, 128, kQB><<<grid, nth, 0, s>>>(a);
 }
 
 }  // namespace
@@ -377,7 +409,7 @@ int launch_read_chunked_mfma(const void* q, const void* k, const void* v, int dt
   a.Hq = Hq; a.Hkv = Hkv; a.W = W; a.chunk = chunk;
   a.C = (int)((T + chunk - 1) / chunk);
   const int gq = Hq / Hkv;
-  const int per = LSA_BLOCK / chunk;  // heads that fill 256 rows
+  const int per = kRows / chunk;  // heads that fill the workgroup's rows
   a.hpw = per < gq ? per : gq;
   a.n_hg = (gq + a.hpw - 1) / a.hpw;
   a.scale_log2 = scale * kLog2e;
