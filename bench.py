@@ -66,6 +66,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-tree", action="store_true", help="skip the B=32 x 131k tree decode leg")
+    ap.add_argument("--tree-steps", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run 3 plain device copies of this many MiB (calibrates HBM byte counters)")
@@ -199,6 +201,112 @@ def dense_decode_fn(torch):
     return [("flash+gqa", make(SDPBackend.FLASH_ATTENTION, True)),
             ("efficient+gqa", make(SDPBackend.EFFICIENT_ATTENTION, True)),
             ("flash+expanded_kv", make(SDPBackend.FLASH_ATTENTION, False))]
+
+
+# ----------------------------------------------------------------------------- tree decode
+
+
+def tree_decode_leg(args, torch, np):
+    """Batched tree decode (B=32, context 131072, 2048 buckets = 128 nodes x 16 per
+    sequence and kv-head, top-8 nodes then top-32 of their children): index queries + tree
+    select + split read per step, rotating over 4 query tokens so that consecutive steps
+    gather different rows (the 17 GB cache is far beyond the 256 MB MALL anyway)."""
+    import oracle
+    from lsa_rocm_lab import workloads
+    from lsa_rocm_lab.port import pipeline
+    from lsa_rocm_lab.port.read_kernel_tiled import sparse_read_auto
+
+    B, T, NQ = 32, 131072, 4
+    t0 = time.perf_counter()
+    data = workloads.clustered(T, HQ, HKV, D, n_clusters=2048, seed=0, B=B, device="cuda", gen_device="cuda",
+                               q_tokens=NQ)
+    buckets = workloads.cluster_buckets(data, target=2048, workers=16)
+    tree = workloads.node_tree(buckets, node_size=16)
+    config = workloads.TREE_131K
+    torch.cuda.synchronize()
+    log(f"tree workload built in {time.perf_counter() - t0:.1f}s "
+        f"(K/V {2 * data.k.numel() * 2 / 1e9:.1f} GB)")
+    pos = torch.full((B,), T - 1, device="cuda", dtype=torch.int32)
+    qs = [data.q[:, i:i + 1].contiguous() for i in range(NQ)]
+
+    def step(i):
+        q = qs[i % NQ]
+        idx = pipeline.index_queries(q, HKV)[:, 0]  # [B, Hkv, D]
+        lists, lengths = pipeline.tree_select(idx, pos, buckets, tree, config, score_dtype="bf16")
+        out = sparse_read_auto(q, data.k, data.v, lists.unsqueeze(1), lengths.unsqueeze(1), D ** -0.5)
+        return lists, lengths, out
+
+    res = [step(i) for i in range(NQ)]
+    torch.cuda.synchronize()
+    toks = [int(r[1].to(torch.int64).sum().item()) for r in res]
+    gathered = statistics.mean(toks) * D * 2 * 2
+    g = capture(step, NQ, torch)
+    g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, args.tree_steps // NQ)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - w0) / (reps * NQ) * 1e6
+    dev_us = e0.elapsed_time(e1) * 1e3 / (reps * NQ)
+    # the kernels alone
+    idxs = [pipeline.index_queries(q, HKV)[:, 0] for q in qs]
+    sel_us = graph_launch_us(lambda i: pipeline.tree_select(idxs[i % NQ], pos, buckets, tree, config,
+                                                            score_dtype="bf16"), NQ, reps, torch)
+    read_us = graph_launch_us(lambda i: sparse_read_auto(qs[i % NQ], data.k, data.v, res[i % NQ][0].unsqueeze(1),
+                                                         res[i % NQ][1].unsqueeze(1), D ** -0.5), NQ, reps, torch)
+    read_gbps = gathered / (read_us * 1e-6) / 1e9
+    log(f"tree decode {us:.1f} us/step (select {sel_us:.1f} + read {read_us:.1f} us); read {read_gbps:.0f} GB/s "
+        f"on {gathered / 1e6:.1f} MB gathered")
+    # dense SDPA decode over the whole 17 GB cache
+    dense_us = None
+    try:
+        import torch.nn.functional as F
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        kk, vv = data.k.permute(0, 2, 1, 3), data.v.permute(0, 2, 1, 3)
+
+        def dfn(i):
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                return F.scaled_dot_product_attention(qs[i % NQ].permute(0, 2, 1, 3), kk, vv, scale=D ** -0.5,
+                                                      enable_gqa=True)
+
+        dfn(0)
+        torch.cuda.synchronize()
+        dense_us = statistics.median(event_launch_times(dfn, 5, torch)) * 1e3
+    except RuntimeError as exc:
+        log(f"dense tree decode unavailable: {str(exc).splitlines()[0][:120]}")
+    # parity sample: two (sequence, kv-head) selections and sequence 0's read vs the oracle
+    lists0, lengths0, out0 = res[0]
+    lvl = tree.levels[0]
+    idx0 = idxs[0]
+    exact = True
+    for b, gg in ((0, 0), (B - 1, HKV - 1)):
+        l, n, _ = oracle.tree_select_row(
+            idx0[b, gg].float().cpu().numpy(), lvl.centroids_bf16[b, gg].float().cpu().numpy(),
+            lvl.children[b, gg].cpu().numpy(), buckets.centroids[b, gg].float().cpu().numpy(),
+            buckets.members[b, gg].cpu().numpy(), T - 1, visible=buckets.rows, covered=buckets.rows,
+            beam_width=config.beam_width, top_p=config.top_p, top_k=config.top_k, window=0, sink=0, mode="bf16")
+        exact &= bool(np.array_equal(lists0[b, gg].cpu().numpy(), l)) and int(lengths0[b, gg]) == n
+    k0, v0 = data.k[:1].float().cpu().numpy(), data.v[:1].float().cpu().numpy()
+    want = oracle.sparse_read(qs[0][:1].float().cpu().numpy(), k0, v0, lists0[:1, None].cpu().numpy(),
+                              lengths0[:1, None].cpu().numpy(), D ** -0.5)
+    err = np.abs(out0[:1].float().cpu().numpy() - want)
+    del k0, v0, data
+    return {"workload": "tree_decode_131k_b32", "batch": B, "context": T, "buckets": 2048, "nodes": 128,
+            "beam": config.beam_width, "top_buckets": config.top_p, "us_per_step": round(us, 2),
+            "device_us_per_step": round(dev_us, 2), "select_us": round(sel_us, 2), "read_us": round(read_us, 2),
+            "gathered_bytes": int(gathered), "read_gbps": round(read_gbps, 1),
+            "read_roofline_frac": round(read_gbps / HBM_PEAK_GBS, 4),
+            "step_gbps": round(gathered / (us * 1e-6) / 1e9, 1),
+            "dense_us": None if dense_us is None else round(dense_us, 1),
+            "speedup_vs_dense": None if dense_us is None else round(dense_us / us, 2),
+            "parity": {"lists_bit_exact_sampled": exact, "read_max_abs": float(err.max()),
+                       "read_mean_abs": float(err.mean())}}
 
 
 # ----------------------------------------------------------------------------- main
@@ -398,6 +506,12 @@ def main() -> int:
                    "speedup_vs_dense": None if dense_p is None else round(dense_p / p_ms, 3)}
         log(f"prefill {prefill}")
 
+    # ---- batched tree decode (B=32 x 131k): the bandwidth-bound regime of the read
+    tree = None
+    if not args.no_tree:
+        tree = tree_decode_leg(args, torch, np)
+        log(f"tree {tree}")
+
     # ---- CPU baseline: the oracle on the host, bounded sample; doubles as the parity check
     cpu = None
     parity = None
@@ -481,6 +595,7 @@ def main() -> int:
         "dense": dense,
         "speedup_vs_dense": None if speedup is None else round(speedup, 3),
         "prefill": prefill,
+        "tree_decode": tree,
         "cpu_baseline": cpu,
         "parity": parity,
     }

@@ -57,7 +57,8 @@ def geometry(T: int, Hq: int, Hkv: int, D: int, dtype=torch.bfloat16, seed: int 
 
 def clustered(T: int, Hq: int, Hkv: int, D: int, n_clusters: int = 512, sigma: float = 0.3,
               dtype=torch.bfloat16, seed: int = 0, B: int = 1, device: str = "cuda",
-              run_min: int = 16, run_max: int = 128, gen_device: str = "cpu") -> Clustered:
+              run_min: int = 16, run_max: int = 128, gen_device: str = "cpu",
+              q_tokens: int | None = None) -> Clustered:
     """Keys from a mixture of Gaussian clusters: per (batch, kv-head) ``n_clusters`` centers
     ~ N(0, 1); the sequence is cut into runs of U{run_min..run_max} tokens, each run
     drawn from a cluster ~ U{0..n_clusters-1}; key = center + sigma * N(0, 1). q, v ~ N(0, 1).
@@ -65,10 +66,12 @@ def clustered(T: int, Hq: int, Hkv: int, D: int, n_clusters: int = 512, sigma: f
     Draw order on the generator: q, centers, run lengths, run clusters, key noise, v.
     ``gen_device="cuda"`` draws the large tensors on the GPU's generator instead (fast
     for the 131k x 32 batch; reproducible on the same GPU, not bit-equal to the CPU draw).
+    ``q_tokens``: draw only that many query rows (the last positions of a decode step,
+    q [B, q_tokens, Hq, D]); a different draw from the full q.
     """
     g = torch.Generator().manual_seed(seed)
     gd = g if gen_device == "cpu" else torch.Generator(device=gen_device).manual_seed(seed)
-    q = torch.randn(B, T, Hq, D, generator=gd, device=gen_device).to(dtype)
+    q = torch.randn(B, T if q_tokens is None else q_tokens, Hq, D, generator=gd, device=gen_device).to(dtype)
     centers = torch.randn(B, Hkv, n_clusters, D, generator=g)
     max_runs = T // run_min + 1
     run_lengths = torch.randint(run_min, run_max + 1, (B, Hkv, max_runs), generator=g)
@@ -172,15 +175,28 @@ def segment_tables(starts: np.ndarray, cap: int, device) -> tuple[torch.Tensor, 
     return members.contiguous(), sizes.contiguous(), end.to(torch.int32).contiguous()
 
 
-def cluster_buckets(data: Clustered, target: int, cap: int = 256, max_size: int = 256) -> Buckets:
+def cluster_buckets(data: Clustered, target: int, cap: int = 256, max_size: int = 256,
+                    workers: int = 1) -> Buckets:
     """Ward-style buckets per (batch, kv-head) with bucket-mean centroids. Tables are
-    [Hkv, rows, ...] for B == 1, else [B, Hkv, rows, ...]."""
+    [Hkv, rows, ...] for B == 1, else [B, Hkv, rows, ...]. ``workers`` > 1 builds the
+    tables in that many spawned CPU processes (they never touch the GPU)."""
     B, T, Hkv, D = data.k.shape
     starts = np.empty((B, Hkv, target + 1), dtype=np.int64)
     centers = data.centers.numpy()
     rl, rc = data.run_lengths.numpy(), data.run_clusters.numpy()
-    for b in range(B):
-        for g in range(Hkv):
+    jobs = [(b, g) for b in range(B) for g in range(Hkv)]
+    if workers > 1 and len(jobs) > 1:
+        import concurrent.futures
+        import multiprocessing
+
+        ctx = multiprocessing.get_context("spawn")
+        with concurrent.futures.ProcessPoolExecutor(max_workers=workers, mp_context=ctx) as pool:
+            futs = {pool.submit(ward_segments, rl[b, g], rc[b, g], centers[b, g], T, target, max_size): (b, g)
+                    for b, g in jobs}
+            for f, (b, g) in futs.items():
+                starts[b, g] = f.result()
+    else:
+        for b, g in jobs:
             starts[b, g] = ward_segments(rl[b, g], rc[b, g], centers[b, g], T, target, max_size)
     if B == 1:
         starts = starts[0]
