@@ -75,6 +75,63 @@ def test_select_limits_rejected():
                   None, None, 0, 16, 16, None)
 
 
+def _decode_args(**kw):
+    """lsa_decode_flat arguments for a flat 32k decode shape with fake (never dereferenced)
+    pointers; kw overrides by name."""
+    args = dict(q=16, k=16, v=16, dtype=_abi.LSA_BF16, R=1, Tk=32768, Hq=32, Hkv=8, D=128, sb=0, st=1024, sh=128,
+                cent=16, members=16, ends=None, rows=512, cap=256, row_tables=0, group_tables=1,
+                mode=_abi.SCORE_BF16, pos=16, cbs=64, bb=1, top_p=32, window=0, sink=0, top_k=8192, scale=0.088,
+                splits=16, readers=0, counters=16, n_counters=1 << 20, scratch=16, scratch_bytes=1 << 30, lists=16,
+                lengths=16, out=16, status=None, stream=None)
+    args.update(kw)
+    return list(args.values())
+
+
+def test_decode_workspace_sizes():
+    n = _abi.size("lsa_decode_flat_counters", 1, 8, 512, 32)
+    units, K = 8, 32
+    stride = ((units * 2 * K + 1023) // 1024) * 1024 + 64
+    assert n == 2 * units + 8 * stride  # arrival counters + 8 record copies
+    keys = 8 * 512 * 8  # every column key of 16 select splits
+    parts = 8 * 64 * 4 * 130 * 4  # 64 readers' partials per unit
+    got = _abi.size("lsa_decode_flat_scratch_bytes", _abi.LSA_BF16, 1, 32, 8, 128, 512, 32, 0, 0, 16, 0)
+    assert got == ((keys + 255) // 256) * 256 + parts
+    assert _abi.size("lsa_decode_flat_counters", 1, 8, 512, 65) == 0  # more than 64 picks is not served
+
+
+def test_decode_arguments_rejected_before_launch():
+    with pytest.raises(ValueError, match="NULL"):
+        _abi.call("lsa_decode_flat", *_decode_args(q=None))
+    with pytest.raises(ValueError, match="picks exceed"):
+        _abi.call("lsa_decode_flat", *_decode_args(top_p=65))
+    with pytest.raises(ValueError, match="group size"):
+        _abi.call("lsa_decode_flat", *_decode_args(Hq=24, Hkv=8))
+    with pytest.raises(ValueError, match="aligned"):
+        _abi.call("lsa_decode_flat", *_decode_args(q=18))
+    with pytest.raises(ValueError, match="select splits"):
+        _abi.call("lsa_decode_flat", *_decode_args(splits=513))
+    with pytest.raises(ValueError, match="readers"):
+        _abi.call("lsa_decode_flat", *_decode_args(readers=257))
+    with pytest.raises(_abi.LsaError, match="WORKSPACE"):
+        _abi.call("lsa_decode_flat", *_decode_args(n_counters=10))
+    with pytest.raises(_abi.LsaError, match="WORKSPACE"):
+        _abi.call("lsa_decode_flat", *_decode_args(scratch_bytes=1024))
+
+
+def test_chunked_read_paths():
+    lib = _abi.load()
+    assert lib.lsa_read_chunked_mfma_ok(_abi.LSA_BF16, 128, 64) == 1
+    assert lib.lsa_read_chunked_mfma_ok(_abi.LSA_F16, 64, 16) == 1
+    assert lib.lsa_read_chunked_mfma_ok(_abi.LSA_F32, 128, 64) == 0
+    assert lib.lsa_read_chunked_mfma_ok(_abi.LSA_BF16, 256, 64) == 0
+    assert lib.lsa_read_chunked_mfma_ok(_abi.LSA_BF16, 128, 48) == 0
+    base = [16, 16, 16, _abi.LSA_F32, 1, 128, 128, 8, 2, 64, 0, 128, 64, 16, 16, 8, 64, 0.125]
+    with pytest.raises(ValueError, match="MFMA path"):
+        _abi.call("lsa_read_chunked", *base, _abi.CHUNKED_MFMA, 16, None)
+    with pytest.raises(ValueError, match="path"):
+        _abi.call("lsa_read_chunked", *base, 7, 16, None)
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_abi, "_lib", None)
     monkeypatch.setattr(_abi, "LIB_PATH", tmp_path / "absent.so")
