@@ -227,11 +227,15 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
 #pragma unroll
       for (int r = 0; r < 16; ++r) st[qb][r] = 0.0f;
     }
+    // every K operand in flight before the first MFMA (LDS latency paid once)
+    op_t ka[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) ka[s] = __builtin_bit_cast(op_t, *(const uint4*)&sh.k[buf][ln][16 * s + 8 * hh]);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      const op_t ka = __builtin_bit_cast(op_t, *(const uint4*)&sh.k[buf][ln][16 * s + 8 * hh]);
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) st[qb] = M::run(ka, qop[qb][s], st[qb]);
+      for (int qb = 0; qb < QB; ++qb) st[qb] = M::run(ka[s], qop[qb][s], st[qb]);
     }
   };
   // online softmax of the tile in `buf` (raw scores st), then O^T += V^T P^T
@@ -307,7 +311,9 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
         pb[qb][sp] = __builtin_bit_cast(op_t, u);
       }
     }
-    // O^T += V^T P^T: A = V^T rows (dims) at the same key order, two 8-byte LDS reads
+    // O^T += V^T P^T: A = V^T rows (dims) at the same key order, two 8-byte LDS reads,
+    // all in flight before the first MFMA
+    op_t va[2][DB];
 #pragma unroll
     for (int sp = 0; sp < 2; ++sp) {
 #pragma unroll
@@ -315,9 +321,16 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
         const int dim = 32 * d + ln;
         const uint2 lo = *(const uint2*)&sh.vt[buf][dim][vt_col(dim, 16 * sp + 4 * hh)];
         const uint2 hi = *(const uint2*)&sh.vt[buf][dim][vt_col(dim, 16 * sp + 8 + 4 * hh)];
-        const op_t va = __builtin_bit_cast(op_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        va[sp][d] = __builtin_bit_cast(op_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) o[d][qb] = M::run(va, pb[qb][sp], o[d][qb]);
+    for (int sp = 0; sp < 2; ++sp) {
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) o[d][qb] = M::run(va[sp][d], pb[qb][sp], o[d][qb]);
       }
     }
   };
