@@ -203,6 +203,34 @@ def dense_decode_fn(torch):
             ("flash+expanded_kv", make(SDPBackend.FLASH_ATTENTION, False))]
 
 
+# ----------------------------------------------------------------------------- block-sparse decode
+
+
+def block_sparse_leg(args, torch, np):
+    """The positional block-sparse arm (context 32768, 512 blocks of 64 with block-mean
+    centroids, top-33 blocks + a 128-token window + 64 sink tokens: 34 blocks a kv-head)
+    through the fused decode kernel, rotating 16 resident cache copies."""
+    from lsa_rocm_lab import workloads
+    from lsa_rocm_lab.port import pipeline
+
+    q, k, v = workloads.geometry(T_CTX, HQ, HKV, D, dtype=torch.bfloat16, seed=0, device="cuda")
+    config = workloads.BLOCK_SPARSE_32K
+    buckets = pipeline.position_buckets(k, config, centroid="mean")
+    pos = torch.tensor([T_CTX - 1], device="cuda", dtype=torch.int32)
+    base = DecodeCache(q[:, -1:].contiguous(), k, v, buckets, pos)
+    R = 16
+    caches = [base] + [copy_cache(base) for _ in range(R - 1)]
+    _, lengths, _ = decode_step(base, config)
+    torch.cuda.synchronize()
+    gathered = int(lengths.to(torch.int64).sum().item()) * D * 2 * 2
+    us = graph_launch_us(lambda i: decode_step(caches[i % R], config), R, max(1, args.kernel_launches // R), torch)
+    gbps = gathered / (us * 1e-6) / 1e9
+    log(f"block-sparse decode {us:.2f} us per step ({gbps:.0f} GB/s on {gathered} gathered bytes)")
+    return {"workload": "block_sparse_decode_32k", "blocks_per_kv_head": 34,
+            "tokens_read": lengths.cpu().numpy().tolist(), "us_per_step": round(us, 3),
+            "gathered_bytes": gathered, "gbps": round(gbps, 1), "roofline_frac": round(gbps / HBM_PEAK_GBS, 4)}
+
+
 # ----------------------------------------------------------------------------- tree decode
 
 
@@ -506,6 +534,9 @@ def main() -> int:
                    "speedup_vs_dense": None if dense_p is None else round(dense_p / p_ms, 3)}
         log(f"prefill {prefill}")
 
+    # ---- the positional block-sparse arm through the same fused kernel
+    block_sparse = block_sparse_leg(args, torch, np)
+
     # ---- batched tree decode (B=32 x 131k): the bandwidth-bound regime of the read
     tree = None
     if not args.no_tree:
@@ -595,6 +626,7 @@ def main() -> int:
         "dense": dense,
         "speedup_vs_dense": None if speedup is None else round(speedup, 3),
         "prefill": prefill,
+        "block_sparse_decode": block_sparse,
         "tree_decode": tree,
         "cpu_baseline": cpu,
         "parity": parity,

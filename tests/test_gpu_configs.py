@@ -101,6 +101,11 @@ def test_block_sparse_32k_bf16():
         assert len(blocks) == 34 and {0, 510, 511} <= blocks
     want = oracle.sparse_read(_np(q[:, -1:]), _np(k), _np(v), want_l[None, None], want_n[None, None])
     check_read(out, want)
+    # the same step through the fused decode kernel (window and sink tails, 34 parts a head)
+    pos = torch.tensor([T - 1], device=DEV, dtype=torch.int32)
+    out2, lists2, lengths2 = pipeline.flat_decode(q[:, -1:], k, v, pos, buckets, config)
+    assert np.array_equal(_np(lists2[0]), want_l) and np.array_equal(_np(lengths2[0]), want_n)
+    check_read(out2, want)
 
 
 def test_flat_decode_32k_clustered():
