@@ -107,6 +107,9 @@ __device__ __forceinline__ float group_sum(float x) {
 // accumulation of exact products (v_dot2c).
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 template <typename T>
 __device__ __forceinline__ float dot8(const uint32_t* q, const uint4& k) {
   const uint32_t kw[4] = {k.x, k.y, k.z, k.w};
@@ -143,17 +146,54 @@ struct ReadLds {
   int flag;
 };
 
+// Which instances score on the matrix cores: 16-bit rows of D = 128 (tiles of 64 slots,
+// 16 lanes a row) for up to 8 query heads a kv-head.
+template <typename T, int D, int GQ>
+struct ReadMfma {
+  static constexpr bool ON = sizeof(T) == 2 && D == 128 && GQ <= 8 && ReadShape<T, D, GQ>::NT == 64 &&
+                             ReadShape<T, D, GQ>::LPT == 16;
+};
+
+// 16x16x32 MFMA on 8 packed 16-bit elements a lane, fp32 accumulate.
+template <typename T> struct Mfma16;
+template <> struct Mfma16<bf16_t> {
+  static __device__ __forceinline__ f32x4_t run(const uint4& a, const uint4& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                   0, 0, 0);
+  }
+};
+template <> struct Mfma16<_Float16> {
+  static __device__ __forceinline__ f32x4_t run(const uint4& a, const uint4& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+  }
+};
+
 // The GQ query rows of one kv-head as this lane holds them: raw 16-byte words (16-bit
 // rows score with packed dot products on them, the scale applied to the fp32 sum) and, for
-// fp32 rows, floats pre-scaled by scale_log2. qrow points at the GQ contiguous rows.
+// fp32 rows, floats pre-scaled by scale_log2. qrow points at the GQ contiguous rows. For
+// the matrix-core score, qm is the B operand of S^T = K Q^T: lane (row = lane / 16,
+// col = lane % 16) holds dims 32 i + 8 row .. + 8 of query head col (zeros for col >= GQ)
+// for the i-th 32-dim quarter.
 template <typename T, int D, int GQ>
 struct QueryRegs {
   static constexpr bool PACKED = sizeof(T) == 2;
   uint32_t qw[GQ][4];
   float qf[GQ][ReadShape<T, D, GQ>::VEC];
+  uint4 qm[D / 32 > 0 ? D / 32 : 1];
 
   __device__ __forceinline__ void load(const T* qrow, float scale_log2) {
     using S = ReadShape<T, D, GQ>;
+    if constexpr (ReadMfma<T, D, GQ>::ON) {
+      const int lane = threadIdx.x & (LSA_WAVE - 1), row = lane >> 4, col = lane & 15;
+      const T* src = qrow + (int64_t)(col < GQ ? col : 0) * D + 8 * row;
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i) {
+        const uint4 x = *(const uint4*)(src + 32 * i);
+        qm[i] = col < GQ ? x : make_uint4(0u, 0u, 0u, 0u);
+      }
+      return;
+    }
     const int lp = (threadIdx.x & (LSA_WAVE - 1)) % S::LPT;
 #pragma unroll
     for (int h = 0; h < GQ; ++h) {
@@ -184,6 +224,142 @@ struct AttnState {
   }
 };
 
+// attend_tiles for the matrix-core instances (ReadMfma::ON). Wave w takes slots
+// [16 w, 16 w + 16) of each 64-slot tile. S^T (16 tokens x 16 query columns, GQ real) =
+// K Q^T is four 16x16x32 MFMAs, one a 32-dim quarter: lane (row, col) loads dims
+// 32 i + 8 row .. + 8 of token col's K row. In the accumulator, lane (row, col) holds
+// tokens 4 row + u (u < 4) of head col, so a head's tile maximum is a max over four
+// registers and two lane swaps. The running maximum moves only when a tile's exceeds it
+// by more than 2^8 (weights stay below 256, exact in fp32), and only then is the state
+// rescaled. Weights reach the V side through a 16 x GQ LDS block per wave: lane (row, lp)
+// holds V dims 8 lp .. + 8 of tokens 4 row + u, the tokens of its own accumulator row,
+// so a masked token's weight is already 0 there. The state leaves in the layout of the
+// other instances (m uniform, l and acc per token group).
+//
+// Spans of three tiles or more are software-pipelined: tile t + 1's K/V loads are issued
+// before tile t is computed, and each lane's slot id is fetched two tiles ahead, ahead of
+// the loads it does not feed (memory counters retire in order, so a wait for an id must
+// not also wait for the rows in flight). The V side's ids come from the K side's by lane
+// permutes. Past the span the slots read -1: those rows load token 0 (cache hits) and
+// weigh nothing.
+template <typename T, int D, int GQ>
+struct MfmaTile {
+  static constexpr int NM = D / 32;
+  uint4 k[NM], v[4];
+  bool ok[4];
+};
+
+template <typename T, int D, int GQ, typename IdOf>
+__device__ __forceinline__ void attend_tiles_mfma(const QueryRegs<T, D, GQ>& q, const T* kb, const T* vb,
+                                                  int64_t tstride, int64_t Tk, int lo, int hi, IdOf id_of,
+                                                  float scale_log2, AttnState<T, D, GQ>& st) {
+  constexpr int NM = D / 32, NT = ReadShape<T, D, GQ>::NT, VEC = ReadShape<T, D, GQ>::VEC;
+  constexpr float kLazy = 8.0f;  // log2 growth of a head's maximum that forces a rescale
+  __shared__ __attribute__((aligned(16))) float pw[LSA_WAVES][16][GQ];
+  const int lane = threadIdx.x & (LSA_WAVE - 1), w = threadIdx.x / LSA_WAVE;
+  const int row = lane >> 4, col = lane & 15;
+  const T* kq = kb + 8 * (row - col);  // kb points at this lane's V dims (8 col)
+  const int s0 = 16 * w + col;         // this lane's slot (K side) within a tile
+  float mrun = st.m[0], lrun = st.l[0];  // head col's running max; its sum over this row's tokens
+#pragma unroll
+  for (int h = 1; h < GQ; ++h) {
+    mrun = col == h ? st.m[h] : mrun;
+    lrun = col == h ? st.l[h] : lrun;
+  }
+
+  auto issue = [&](int32_t idk, MfmaTile<T, D, GQ>& t) {
+    const bool okk = idk >= 0 && idk < Tk;
+    const uint64_t koff = (uint64_t)(uint32_t)(okk ? idk : 0) * (uint32_t)tstride;
+#pragma unroll
+    for (int i = 0; i < NM; ++i) t.k[i] = *(const uint4*)(kq + koff + 32 * i);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int32_t idv = __shfl(idk, 4 * row + u, LSA_WAVE);  // token 4 row + u's id
+      const bool okv = idv >= 0 && idv < Tk;
+      t.ok[u] = okv && col < GQ;
+      t.v[u] = *(const uint4*)(vb + (uint64_t)(uint32_t)(okv ? idv : 0) * (uint32_t)tstride);
+    }
+  };
+  auto compute = [&](const MfmaTile<T, D, GQ>& t) {
+    f32x4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NM; ++i) c = Mfma16<T>::run(t.k[i], q.qm[i], c);
+    float s[4], mt = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      s[u] = t.ok[u] ? c[u] * scale_log2 : -INFINITY;
+      mt = fmaxf(mt, s[u]);
+    }
+    mt = fmaxf(mt, lane_xor(mt, 16));
+    mt = fmaxf(mt, lane_xor(mt, 32));
+    if (__ballot(mt > mrun + kLazy) != 0) {  // wave-uniform: some head's maximum moved
+      const float mnew = fmaxf(mrun, mt);
+      const float alpha = fast_exp2(mrun - mnew);
+      mrun = mnew;
+      lrun *= alpha;
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) {
+        const float ah = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), h));
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) st.acc[h][e] *= ah;
+      }
+    }
+    float p[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      p[u] = fast_exp2(s[u] - mrun);  // 0 for masked tokens and padded heads
+      lrun += p[u];
+    }
+    if (col < GQ) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) pw[w][4 * row + u][col] = p[u];
+    }
+    __builtin_amdgcn_wave_barrier();  // the wave's LDS writes before its reads
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float ph[GQ];
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) ph[h] = pw[w][4 * row + u][h];
+      float vf[VEC];
+      Row16<T>::cvt(t.v[u], vf);
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) st.acc[h][e] = fmaf(ph[h], vf[e], st.acc[h][e]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the reads before the next tile's writes
+  };
+
+  MfmaTile<T, D, GQ> cur;
+  if (hi - lo > 2 * NT) {  // pipelined
+    int32_t id1 = id_of(lo + s0);
+    int32_t id2 = id_of(lo + NT + s0);
+    issue(id1, cur);
+    id1 = id2;
+    for (int base = lo; base < hi; base += NT) {
+      id2 = id_of(base + 2 * NT + s0);  // ids two tiles ahead, before the rows they do not feed
+      MfmaTile<T, D, GQ> nxt;
+      issue(id1, nxt);
+      compute(cur);
+      cur = nxt;
+      id1 = id2;
+    }
+  } else {
+    int32_t id1 = id_of(lo + s0);
+    for (int base = lo; base < hi; base += NT) {
+      issue(id1, cur);
+      id1 = id_of(base + NT + s0);  // next tile's id while this one computes
+      compute(cur);
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < GQ; ++h) {
+    st.m[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mrun), h));
+    st.l[h] = __shfl(lrun, 16 * row + h, LSA_WAVE);
+  }
+}
+
 // Online-softmax attention over list slots [lo, hi), tile by tile: id_of(j) is the token of
 // slot j, or -1 (skipped); it must be cheap and unconditional (a clamped load or an LDS
 // read). kb / vb point at the kv-head's row 0 plus this lane's VEC-element offset. fresh:
@@ -192,6 +368,10 @@ template <typename T, int D, int GQ, typename IdOf>
 __device__ __forceinline__ void attend_tiles(const QueryRegs<T, D, GQ>& q, const T* kb, const T* vb, int64_t tstride,
                                              int64_t Tk, int lo, int hi, IdOf id_of, float scale_log2, bool fresh,
                                              AttnState<T, D, GQ>& st) {
+  if constexpr (ReadMfma<T, D, GQ>::ON) {
+    attend_tiles_mfma<T, D, GQ>(q, kb, vb, tstride, Tk, lo, hi, id_of, scale_log2, st);
+    return;
+  }
   using S = ReadShape<T, D, GQ>;
   constexpr int VEC = S::VEC, LPT = S::LPT, TPW = S::TPW, U = S::U, NT = S::NT;
   constexpr bool PACKED = QueryRegs<T, D, GQ>::PACKED;

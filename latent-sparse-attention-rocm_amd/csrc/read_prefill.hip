@@ -19,6 +19,8 @@
 // in the 16-bit operand and most tiles skip the 128-register rescale.
 #include <math.h>
 
+#include <type_traits>
+
 #include "lsa_abi_common.h"
 #include "lsa_read_dev.h"
 
@@ -31,9 +33,8 @@ constexpr int KPAD = 8;    // LDS row padding of the K tile (elements)
 constexpr int VPAD = 8;    // of the V^T tile
 constexpr float kRescale = 8.0f;  // log2 growth of a column max that forces a rescale
 constexpr int kRows = 256;       // query rows of a workgroup
+constexpr int kSimds = 4;        // SIMDs of a CU: waves w and w + 4 share one
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 template <typename T> struct Mfma;
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
   int64_t x = blockIdx.x;
   const int hg = (int)(x % a.n_hg); x /= a.n_hg;
   const int g = (int)(x % a.Hkv); x /= a.Hkv;
-  const int c = (int)(x % a.C);
+  const int c = a.C - 1 - (int)(x % a.C);  // later chunks see more buckets: longest first
   const int64_t b = x / a.C;
   const int gq = a.Hq / a.Hkv;
   const int64_t c0 = (int64_t)c * a.chunk;
@@ -147,49 +148,54 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
     }
   }
 
-  // tile loads: key kk = pass * KPP + tid / SEGS, segment seg = tid % SEGS. A tile's list
-  // ids are fetched one tile ahead of its K/V rows (an unconditional, clamped load), and
-  // its rows one tile ahead of their use.
+  // tile loads: key kk = pass * KPP + tid / SEGS, segment seg = tid % SEGS. Rows are
+  // gathered two tiles ahead of their store into LDS, so a gather has two iterations of
+  // math to land, into one of two register sets chosen by the tile's parity (the loop is
+  // unrolled by two, so no register is copied while its load is in flight). A tile's list
+  // ids are fetched an iteration before its gather and issued ahead of the gather they do
+  // not feed: the vector-memory counter retires in order, so a wait for an id must not
+  // also wait for rows in flight. Loads past the last tile are clamped (unconditional
+  // loads keep every wait exact) and their rows are never used.
   const int seg = tid % SEGS;
   const int32_t* lsrc = a.W > 0 ? list : a.lengths + li;  // always a valid address
-  // raw list ids: `lidq` of the next tile to gather, `lidn` of the one after, issued
-  // before that gather and handed over at the end of the iteration, so every wait for a
-  // load falls after the math that hides it (the vector-memory counter retires in order)
-  int32_t lidq[PASSES], lidn[PASSES];
   const bool loader = KPP <= TK || tid / SEGS < TK;  // threads with a key to load
-  auto fetch_ids = [&](int tile, int32_t (&dst)[PASSES]) {
+  int32_t lid[2][PASSES];
+  uint4 kreg[2][PASSES], vreg[2][PASSES];
+  int kinfo[2][PASSES];
+  auto fetch_ids = [&](auto set, int tile) {
+    constexpr int S = decltype(set)::value;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       const int j = tile * TK + p * KPP + (loader ? tid / SEGS : 0);
       const int jl = j < n_list ? j : (n_list > 0 ? n_list - 1 : 0);
-      dst[p] = lsrc[jl];
+      lid[S][p] = lsrc[jl];
     }
   };
-  uint4 kreg[PASSES], vreg[PASSES];
-  int kinfo[PASSES];
-  auto load_tile = [&](int tile) {
+  auto load_tile = [&](auto set, int tile) {
+    constexpr int S = decltype(set)::value;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       const int j = tile * TK + p * KPP + (loader ? tid / SEGS : 0);
-      const int32_t lid = lidq[p];
+      const int32_t l = lid[S][p];
       const int o = j - n_list;
       const bool in_list = j < n_list;
-      const int info = in_list ? (((lid >= 0) & (lid < a.Tk)) ? -1 : -2) : (j < n_tot ? o : -2);
-      const int32_t id = in_list ? lid : (int32_t)(c0 + o);
+      const int info = in_list ? (((l >= 0) & (l < a.Tk)) ? -1 : -2) : (j < n_tot ? o : -2);
+      const int32_t id = in_list ? l : (int32_t)(c0 + o);
       const uint64_t off = (uint64_t)(uint32_t)(info >= -1 ? id : 0) * (uint64_t)a.kv_st + seg * 8;
-      kreg[p] = *(const uint4*)(kb + off);
-      vreg[p] = *(const uint4*)(vb + off);
-      kinfo[p] = info;
+      kreg[S][p] = *(const uint4*)(kb + off);
+      vreg[S][p] = *(const uint4*)(vb + off);
+      kinfo[S][p] = info;
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](auto set, int buf) {
+    constexpr int S = decltype(set)::value;
     if (!loader) return;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       const int kk = p * KPP + tid / SEGS;
-      const bool ok = kinfo[p] >= -1;
-      const uint4 kr = ok ? kreg[p] : make_uint4(0, 0, 0, 0);
-      const uint4 vr = ok ? vreg[p] : make_uint4(0, 0, 0, 0);
+      const bool ok = kinfo[S][p] >= -1;
+      const uint4 kr = ok ? kreg[S][p] : make_uint4(0, 0, 0, 0);
+      const uint4 vr = ok ? vreg[S][p] : make_uint4(0, 0, 0, 0);
       *(uint4*)&sh.k[buf][kk][seg * 8] = kr;
       const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
 #pragma unroll
@@ -198,7 +204,7 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
         sh.vt[buf][d0][vt_col(d0, kk)] = (uint16_t)(vw[e] & 0xFFFFu);
         sh.vt[buf][d0 + 1][vt_col(d0 + 1, kk)] = (uint16_t)(vw[e] >> 16);
       }
-      if (seg == 0) sh.info[buf][kk] = kinfo[p];
+      if (seg == 0) sh.info[buf][kk] = kinfo[S][p];
     }
   };
 
@@ -336,37 +342,45 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
   };
 
   // Pipeline, one barrier per tile over three LDS buffers: iteration t stores tile t + 1
-  // (gathered an iteration earlier), issues the gather of tile t + 2 and the scores of
-  // tile t + 1, then runs tile t's softmax and P V. A buffer is rewritten two iterations
-  // after its last reader, which the intervening barrier has let finish.
-  f32x16_t st_cur[QB], st_next[QB];
-  fetch_ids(0, lidq);
-  load_tile(0);
-  fetch_ids(1, lidq);
-  store_tile(0);
-  __syncthreads();
-  if (n_tiles > 1) {
-    fetch_ids(2, lidn);
-    load_tile(1);
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) lidq[p] = lidn[p];
-  }
-  scores(0, st_cur);
-  for (int tile = 0; tile < n_tiles; ++tile) {
+  // (gathered two iterations earlier) and issues the ids of tile t + 4 and the gather of
+  // tile t + 3 before the barrier, then the scores of tile t + 1 and tile t's softmax and
+  // P V. A buffer is rewritten
+  // two iterations after its last reader, which the intervening barrier has let finish.
+  // The two waves of a SIMD (w and w + 4) take the matrix core and the VALU in turn: one
+  // runs the next tile's scores while the other runs this tile's softmax.
+  using Set0 = std::integral_constant<int, 0>;
+  using Set1 = std::integral_constant<int, 1>;
+  auto step = [&](auto x, auto y, int tile, f32x16_t (&cur)[QB], f32x16_t (&nxt)[QB]) {
     const bool more = tile + 1 < n_tiles;
-    if (more) store_tile((tile + 1) % 3);
+    if (more) store_tile(x, (tile + 1) % 3);
+    fetch_ids(y, tile + 4);  // issued before the barrier, into the set just stored
+    load_tile(x, tile + 3);
     __syncthreads();
-    if (tile + 2 < n_tiles) {  // in flight during this tile's math
-      fetch_ids(tile + 3, lidn);
-      load_tile(tile + 2);
+    if (w < kSimds) {
+      if (more) scores((tile + 1) % 3, nxt);
+      softmax_pv(tile % 3, cur);
+    } else {
+      softmax_pv(tile % 3, cur);
+      if (more) scores((tile + 1) % 3, nxt);
     }
-    if (more) scores((tile + 1) % 3, st_next);
-    softmax_pv(tile % 3, st_cur);
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) st_cur[qb] = st_next[qb];
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) lidq[p] = lidn[p];
+  };
+  f32x16_t st_a[QB], st_b[QB];
+  fetch_ids(Set0{}, 0);
+  fetch_ids(Set1{}, 1);
+  load_tile(Set0{}, 0);
+  fetch_ids(Set0{}, 2);
+  load_tile(Set1{}, 1);
+  fetch_ids(Set1{}, 3);
+  store_tile(Set0{}, 0);
+  __syncthreads();
+  load_tile(Set0{}, 2);
+  scores(0, st_a);
+  int tile = 0;
+  for (; tile + 1 < n_tiles; tile += 2) {
+    step(Set1{}, Set0{}, tile, st_a, st_b);
+    step(Set0{}, Set1{}, tile + 1, st_b, st_a);
   }
+  if (tile < n_tiles) step(Set1{}, Set0{}, tile, st_a, st_b);
 
   // normalise and store: lane (hh, q) holds dims 32 d + 8 (r / 4) + 4 hh + r % 4 of column q
 #pragma unroll
