@@ -30,7 +30,7 @@ namespace {
 
 constexpr int TK = 32;     // keys per tile
 constexpr int KPAD = 8;    // LDS row padding of the K tile (elements)
-constexpr int VPAD = 8;    // of the V^T tile
+constexpr int VPAD = 32;   // of the V tile: rows 16 dwords apart mod 64 banks (conflict-free transposed reads)
 constexpr float kRescale = 8.0f;  // log2 growth of a column max that forces a rescale
 constexpr int kRows = 256;       // query rows of a workgroup
 constexpr int kSimds = 4;        // SIMDs of a CU: waves w and w + 4 share one
@@ -66,14 +66,22 @@ template <> struct Mfma<_Float16> {
 template <int D>
 struct alignas(16) PrefillLds {
   uint16_t k[3][TK][D + KPAD];   // K rows, raw 16-bit elements (three tiles in flight)
-  uint16_t vt[3][D][TK + VPAD];  // V^T, swizzled (vt_col)
+  uint16_t v[3][TK][D + VPAD];   // V rows, raw 16-bit elements
   int info[3][TK];               // per key: -2 skipped, -1 list key (every row), o >= 0 local offset
 };
 
-// Column of key `key` in V^T row `dim`: groups of 4 keys (8 bytes) XOR-swizzled by the
-// row's eighth, so the transposed stores (16 dims apart per lane group) and the operand
-// reads spread over the LDS banks (2-way instead of 16-way on the stores).
-__device__ __forceinline__ int vt_col(int dim, int key) { return 4 * ((key >> 2) ^ ((dim >> 3) & 7)) + (key & 3); }
+// Four keys of one V column from the row-major V tile, for a V^T MFMA operand, by the
+// transposing LDS read (ds_read_b64_tr_b16): in each group of 16 lanes, lane j addresses
+// the 8 bytes at key0 + j / 4, dims dim0 + 4 (j % 4) .. + 3, and lane i receives keys
+// key0 .. key0 + 3 of dim dim0 + i.
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+template <int D>
+__device__ __forceinline__ uint2 v_column4(const uint16_t (&vtile)[TK][D + VPAD], int key0, int dim0, int lane16) {
+  const uint16_t* src = &vtile[key0 + lane16 / 4][dim0 + 4 * (lane16 % 4)];
+  typedef __attribute__((address_space(3))) v4i16_t lds_v4;
+  const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4*)(src));
+  return __builtin_bit_cast(uint2, r);
+}
 
 struct PrefillArgs {
   const void* q;
@@ -197,13 +205,7 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
       const uint4 kr = ok ? kreg[S][p] : make_uint4(0, 0, 0, 0);
       const uint4 vr = ok ? vreg[S][p] : make_uint4(0, 0, 0, 0);
       *(uint4*)&sh.k[buf][kk][seg * 8] = kr;
-      const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int d0 = seg * 8 + 2 * e;
-        sh.vt[buf][d0][vt_col(d0, kk)] = (uint16_t)(vw[e] & 0xFFFFu);
-        sh.vt[buf][d0 + 1][vt_col(d0 + 1, kk)] = (uint16_t)(vw[e] >> 16);
-      }
+      *(uint4*)&sh.v[buf][kk][seg * 8] = vr;
       if (seg == 0) sh.info[buf][kk] = kinfo[S][p];
     }
   };
@@ -317,16 +319,17 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
         pb[qb][sp] = __builtin_bit_cast(op_t, u);
       }
     }
-    // O^T += V^T P^T: A = V^T rows (dims) at the same key order, two 8-byte LDS reads,
-    // all in flight before the first MFMA
+    // O^T += V^T P^T: A = V^T rows (dims) at the same key order: lane (hh, ln) holds dim
+    // 32 d + ln at keys 16 sp + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}, two transposing
+    // 8-byte LDS reads, all in flight before the first MFMA
     op_t va[2][DB];
+    const int l16 = lane % 16, dhalf = 16 * (ln / 16);
 #pragma unroll
     for (int sp = 0; sp < 2; ++sp) {
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
-        const int dim = 32 * d + ln;
-        const uint2 lo = *(const uint2*)&sh.vt[buf][dim][vt_col(dim, 16 * sp + 4 * hh)];
-        const uint2 hi = *(const uint2*)&sh.vt[buf][dim][vt_col(dim, 16 * sp + 8 + 4 * hh)];
+        const uint2 lo = v_column4<D>(sh.v[buf], 16 * sp + 4 * hh, 32 * d + dhalf, l16);
+        const uint2 hi = v_column4<D>(sh.v[buf], 16 * sp + 8 + 4 * hh, 32 * d + dhalf, l16);
         va[sp][d] = __builtin_bit_cast(op_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
       }
     }
