@@ -74,12 +74,13 @@ struct alignas(16) PrefillLds {
 // transposing LDS read (ds_read_b64_tr_b16): in each group of 16 lanes, lane j addresses
 // the 8 bytes at key0 + j / 4, dims dim0 + 4 (j % 4) .. + 3, and lane i receives keys
 // key0 .. key0 + 3 of dim dim0 + i.
+// `lane_base` is this lane's part of the address (key j / 4, dims 4 (j % 4) of the tile);
+// the rest is a constant byte offset, which the read's immediate field takes.
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
-template <int D>
-__device__ __forceinline__ uint2 v_column4(const uint16_t (&vtile)[TK][D + VPAD], int key0, int dim0, int lane16) {
-  const uint16_t* src = &vtile[key0 + lane16 / 4][dim0 + 4 * (lane16 % 4)];
+typedef __attribute__((address_space(3))) char lds_char;
+__device__ __forceinline__ uint2 v_column4(const lds_char* lane_base, int offset) {
   typedef __attribute__((address_space(3))) v4i16_t lds_v4;
-  const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4*)(src));
+  const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4*)(lane_base + offset));
   return __builtin_bit_cast(uint2, r);
 }
 
@@ -113,6 +114,9 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
 
   const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
   const int hh = lane / 32, ln = lane % 32;
+  // this lane's byte offset in a V tile for the transposing reads: keys 4 hh + (lane % 16) / 4,
+  // dims 16 (ln / 16) + 4 (lane % 4)
+  const int vlane = 2 * ((4 * hh + (lane % 16) / 4) * (D + VPAD) + 16 * (ln / 16) + 4 * (lane % 4));
   int64_t x = blockIdx.x;
   const int hg = (int)(x % a.n_hg); x /= a.n_hg;
   const int g = (int)(x % a.Hkv); x /= a.Hkv;
@@ -323,13 +327,14 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
     // 32 d + ln at keys 16 sp + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}, two transposing
     // 8-byte LDS reads, all in flight before the first MFMA
     op_t va[2][DB];
-    const int l16 = lane % 16, dhalf = 16 * (ln / 16);
+    constexpr int VROW = 2 * (D + VPAD);  // bytes per V row
+    const lds_char* vbase = (const lds_char*)&sh.v[buf][0][0] + vlane;
 #pragma unroll
     for (int sp = 0; sp < 2; ++sp) {
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
-        const uint2 lo = v_column4<D>(sh.v[buf], 16 * sp + 4 * hh, 32 * d + dhalf, l16);
-        const uint2 hi = v_column4<D>(sh.v[buf], 16 * sp + 8 + 4 * hh, 32 * d + dhalf, l16);
+        const uint2 lo = v_column4(vbase, 16 * sp * VROW + 64 * d);
+        const uint2 hi = v_column4(vbase, (16 * sp + 8) * VROW + 64 * d);
         va[sp][d] = __builtin_bit_cast(op_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
       }
     }
