@@ -33,7 +33,6 @@ constexpr int KPAD = 8;    // LDS row padding of the K tile (elements)
 constexpr int VPAD = 32;   // of the V tile: rows 16 dwords apart mod 64 banks (conflict-free transposed reads)
 constexpr float kRescale = 8.0f;  // log2 growth of a column max that forces a rescale
 constexpr int kRows = 256;       // query rows of a workgroup
-constexpr int kSimds = 4;        // SIMDs of a CU: waves w and w + 4 share one
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
@@ -250,13 +249,20 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
       for (int qb = 0; qb < QB; ++qb) st[qb] = M::run(ka[s], qop[qb][s], st[qb]);
     }
   };
-  // online softmax of the tile in `buf` (raw scores st), then O^T += V^T P^T
-  auto softmax_pv = [&](int buf, f32x16_t (&st)[QB]) {
+  // One tile of math for a wave: the softmax of tile `cb` (raw scores cur) and O^T +=
+  // V^T P^T, with the scores of the next tile (LDS buffer `nb`) into nxt interleaved with
+  // the exponentials, so the matrix core runs while the VALU works. After the last tile
+  // the next-tile scores read a stale buffer and are never used.
+  auto tile_math = [&](int cb, int nb, f32x16_t (&cur)[QB], f32x16_t (&nxt)[QB]) {
+    // the next tile's K operands and this tile's key info, in flight together
+    op_t ka[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) ka[s] = __builtin_bit_cast(op_t, *(const uint4*)&sh.k[nb][ln][16 * s + 8 * hh]);
     // the lane's 16 keys: 8 (r / 4) + 4 hh + r % 4, four runs of four
     int kinf[16];
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
-      const int4 v4 = *(const int4*)&sh.info[buf][8 * r4 + 4 * hh];
+      const int4 v4 = *(const int4*)&sh.info[cb][8 * r4 + 4 * hh];
       kinf[4 * r4 + 0] = v4.x; kinf[4 * r4 + 1] = v4.y; kinf[4 * r4 + 2] = v4.z; kinf[4 * r4 + 3] = v4.w;
     }
     // the mask only where this wave sees a skipped or local key (a uniform branch: most
@@ -271,7 +277,7 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
         for (int r = 0; r < 16; ++r) {
           const int inf = kinf[r];
           const bool vis = (inf == -1) | ((unsigned)inf <= (unsigned)tok[qb]);
-          st[qb][r] = vis ? st[qb][r] : -INFINITY;
+          cur[qb][r] = vis ? cur[qb][r] : -INFINITY;
         }
       }
     }
@@ -279,9 +285,9 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
     float mt[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      float mx = st[qb][0];
+      float mx = cur[qb][0];
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, st[qb][r]);
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, cur[qb][r]);
       mt[qb] = fmaxf(mx, lane_xor(mx, 32)) * a.scale_log2;
     }
     // lazy rescale: only when some column's max grew by more than 2^kRescale
@@ -302,33 +308,41 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
         }
       }
     }
-    // P^T as the B operand: regs 8 s' .. 8 s' + 7 of the accumulator are keys
-    // 16 s' + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}; p = exp2(s * scale - m)
-    op_t pb[QB][2];
+    // next scores, one k-step at a time, each followed by its share of this tile's
+    // weights p = exp2(s * scale - m) (the accumulator regs 8 s' .. 8 s' + 7 are keys
+    // 16 s' + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}: the P^T B operand)
+    constexpr int EPS = 16 / KS;  // exponentials per k-step (even)
+    uint32_t pw[QB][8];           // the weights, packed in pairs as they are made
+    float ls[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      float pv[16];
+      ls[qb] = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        pv[r] = fast_exp2(fmaf(st[qb][r], a.scale_log2, -m_run[qb]));
-        l_run[qb] += pv[r];
-      }
-#pragma unroll
-      for (int sp = 0; sp < 2; ++sp) {
-        uint4 u;
-        u.x = M::pack2(pv[8 * sp + 0], pv[8 * sp + 1]);
-        u.y = M::pack2(pv[8 * sp + 2], pv[8 * sp + 3]);
-        u.z = M::pack2(pv[8 * sp + 4], pv[8 * sp + 5]);
-        u.w = M::pack2(pv[8 * sp + 6], pv[8 * sp + 7]);
-        pb[qb][sp] = __builtin_bit_cast(op_t, u);
-      }
+      for (int r = 0; r < 16; ++r) nxt[qb][r] = 0.0f;
     }
-    // O^T += V^T P^T: A = V^T rows (dims) at the same key order: lane (hh, ln) holds dim
-    // 32 d + ln at keys 16 sp + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}, two transposing
-    // 8-byte LDS reads, all in flight before the first MFMA
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) nxt[qb] = M::run(ka[s], qop[qb][s], nxt[qb]);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+        for (int e = 0; e < EPS; e += 2) {
+          const int r = EPS * s + e;
+          const float p0 = fast_exp2(fmaf(cur[qb][r], a.scale_log2, -m_run[qb]));
+          const float p1 = fast_exp2(fmaf(cur[qb][r + 1], a.scale_log2, -m_run[qb]));
+          ls[qb] += p0 + p1;
+          pw[qb][r / 2] = M::pack2(p0, p1);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);  // this k-step's MFMA, then its weights, in order
+    }
+    // V^T operands of this tile: lane (hh, ln) holds dim 32 d + ln at keys
+    // 16 sp + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}, two transposing 8-byte reads
+    // (issued after the score MFMAs have taken their K operands)
     op_t va[2][DB];
     constexpr int VROW = 2 * (D + VPAD);  // bytes per V row
-    const lds_char* vbase = (const lds_char*)&sh.v[buf][0][0] + vlane;
+    const lds_char* vbase = (const lds_char*)&sh.v[cb][0][0] + vlane;
 #pragma unroll
     for (int sp = 0; sp < 2; ++sp) {
 #pragma unroll
@@ -338,7 +352,15 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
         va[sp][d] = __builtin_bit_cast(op_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
       }
     }
-    __builtin_amdgcn_sched_barrier(0);
+    op_t pb[QB][2];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      l_run[qb] += ls[qb];
+#pragma unroll
+      for (int sp = 0; sp < 2; ++sp)
+        pb[qb][sp] = __builtin_bit_cast(op_t, make_uint4(pw[qb][4 * sp], pw[qb][4 * sp + 1], pw[qb][4 * sp + 2],
+                                                         pw[qb][4 * sp + 3]));
+    }
 #pragma unroll
     for (int sp = 0; sp < 2; ++sp) {
 #pragma unroll
@@ -351,11 +373,9 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
 
   // Pipeline, one barrier per tile over three LDS buffers: iteration t stores tile t + 1
   // (gathered two iterations earlier) and issues the ids of tile t + 4 and the gather of
-  // tile t + 3 before the barrier, then the scores of tile t + 1 and tile t's softmax and
-  // P V. A buffer is rewritten
-  // two iterations after its last reader, which the intervening barrier has let finish.
-  // The two waves of a SIMD (w and w + 4) take the matrix core and the VALU in turn: one
-  // runs the next tile's scores while the other runs this tile's softmax.
+  // tile t + 3 before the barrier, then tile t's math (with tile t + 1's scores folded
+  // in). A buffer is rewritten two iterations after its last reader, which the
+  // intervening barrier has let finish.
   using Set0 = std::integral_constant<int, 0>;
   using Set1 = std::integral_constant<int, 1>;
   auto step = [&](auto x, auto y, int tile, f32x16_t (&cur)[QB], f32x16_t (&nxt)[QB]) {
@@ -364,13 +384,7 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
     fetch_ids(y, tile + 4);  // issued before the barrier, into the set just stored
     load_tile(x, tile + 3);
     __syncthreads();
-    if (w < kSimds) {
-      if (more) scores((tile + 1) % 3, nxt);
-      softmax_pv(tile % 3, cur);
-    } else {
-      softmax_pv(tile % 3, cur);
-      if (more) scores((tile + 1) % 3, nxt);
-    }
+    tile_math(tile % 3, (tile + 1) % 3, cur, nxt);
   };
   f32x16_t st_a[QB], st_b[QB];
   fetch_ids(Set0{}, 0);
