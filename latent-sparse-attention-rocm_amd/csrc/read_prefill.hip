@@ -425,7 +425,7 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
   }
 }
 
-constexpr int kQB = 1;  // 8 waves of 32 query columns: two waves per SIMD hide each other's latency
+constexpr int kQB = 1;  // one block of 32 query columns per wave (two waves a SIMD)
 
 template <typename T>
 void launch_prefill(const PrefillArgs& a, int D, dim3 grid, hipStream_t s) {

@@ -306,24 +306,75 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
 
 // ------------------------------------------------------------------ index queries / centroids
 
-template <typename QT>
+// V consecutive elements of a row as floats (one 4 V-byte or 2 V-byte load).
+template <typename QT, int V> struct RowVec;
+template <typename QT> struct RowVec<QT, 1> {
+  static __device__ __forceinline__ void load(const QT* p, float* f) { f[0] = elem<QT>::load(p, 0); }
+};
+template <> struct RowVec<float, 4> {
+  static __device__ __forceinline__ void load(const float* p, float* f) {
+    const float4 x = *(const float4*)p;
+    f[0] = x.x; f[1] = x.y; f[2] = x.z; f[3] = x.w;
+  }
+};
+template <> struct RowVec<bf16_t, 4> {
+  static __device__ __forceinline__ void load(const bf16_t* p, float* f) {
+    const uint2 x = *(const uint2*)p;
+    f[0] = __uint_as_float(x.x << 16); f[1] = __uint_as_float(x.x & 0xFFFF0000u);
+    f[2] = __uint_as_float(x.y << 16); f[3] = __uint_as_float(x.y & 0xFFFF0000u);
+  }
+};
+template <> struct RowVec<_Float16, 4> {
+  static __device__ __forceinline__ void load(const _Float16* p, float* f) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 x = *(const h4*)p;
+    f[0] = (float)x[0]; f[1] = (float)x[1]; f[2] = (float)x[2]; f[3] = (float)x[3];
+  }
+};
+
+// One thread per V dims of an output row (b, chunk, kv-head): the fp32 sum over the
+// chunk's tokens and, within a token, the group's heads in order (the canonical order),
+// then one division. The (token, head) rows are walked in batches of 16 whose loads are
+// all in flight before the batch's adds.
+template <typename QT, int V>
 __global__ void index_queries_kernel(const QT* q, int64_t B, int64_t T, int Hq, int Hkv, int D, int chunk,
                                      float* out) {
   const int64_t C = T / chunk;
-  const int64_t n = B * C * Hkv * D;
+  const int DV = D / V;
+  const int64_t n = B * C * Hkv * DV;
   const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (idx >= n) return;
-  const int d = (int)(idx % D);
-  const int g = (int)((idx / D) % Hkv);
-  const int64_t c = (idx / ((int64_t)D * Hkv)) % C;
-  const int64_t b = idx / ((int64_t)D * Hkv * C);
+  const int dv = (int)(idx % DV);
+  const int g = (int)((idx / DV) % Hkv);
+  const int64_t c = (idx / ((int64_t)DV * Hkv)) % C;
+  const int64_t b = idx / ((int64_t)DV * Hkv * C);
   const int G = Hq / Hkv;
-  float acc = 0.0f;
-  for (int t = 0; t < chunk; ++t) {
-    const int64_t base = ((b * T + c * chunk + t) * Hq + (int64_t)g * G) * D + d;
-    for (int h = 0; h < G; ++h) acc += elem<QT>::load(q, base + (int64_t)h * D);
+  const QT* base = q + ((b * T + c * chunk) * Hq + (int64_t)g * G) * D + dv * V;
+  const int64_t tstride = (int64_t)Hq * D;
+  const int rows = chunk * G;  // (token, head) rows, token-major
+  constexpr int NB = 16;
+  float acc[V];
+#pragma unroll
+  for (int e = 0; e < V; ++e) acc[e] = 0.0f;
+  for (int k0 = 0; k0 < rows; k0 += NB) {
+    float x[NB][V];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int k = k0 + j < rows ? k0 + j : rows - 1;  // clamped: every load in bounds
+      const int t = k / G, h = k - t * G;
+      RowVec<QT, V>::load(base + t * tstride + (int64_t)h * D, x[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      if (k0 + j < rows) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) acc[e] += x[j][e];
+      }
+    }
   }
-  out[idx] = acc / (float)(chunk * G);
+  const float cnt = (float)(chunk * G);
+#pragma unroll
+  for (int e = 0; e < V; ++e) out[idx * V + e] = acc[e] / cnt;
 }
 
 template <typename KT>
@@ -656,8 +707,16 @@ extern "C" int lsa_index_queries(const void* q, int q_dtype, int64_t B, int64_t 
   const int64_t n = B * (T / chunk) * Hkv * D;
   if (n == 0) return LSA_OK;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)((n + 255) / 256));
-  LSA_DISPATCH_QT(q_dtype, { index_queries_kernel<QT><<<grid, 256, 0, s>>>((const QT*)q, B, T, Hq, Hkv, D, chunk, out); })
+  const int esize = q_dtype == LSA_F32 ? 4 : 2;
+  const bool vec = D % 4 == 0 && ((uintptr_t)q % (4 * esize)) == 0;  // 4 dims a thread
+  const dim3 grid((unsigned)((n / (vec ? 4 : 1) + 255) / 256));
+  if (vec) {
+    LSA_DISPATCH_QT(q_dtype,
+                    { index_queries_kernel<QT, 4><<<grid, 256, 0, s>>>((const QT*)q, B, T, Hq, Hkv, D, chunk, out); })
+  } else {
+    LSA_DISPATCH_QT(q_dtype,
+                    { index_queries_kernel<QT, 1><<<grid, 256, 0, s>>>((const QT*)q, B, T, Hq, Hkv, D, chunk, out); })
+  }
   LSA_LAUNCHED("lsa_index_queries");
   return LSA_OK;
 }
