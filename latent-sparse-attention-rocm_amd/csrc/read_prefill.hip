@@ -28,7 +28,8 @@ using namespace lsa;
 
 namespace {
 
-constexpr int TK = 32;     // keys per tile
+constexpr int TK = 64;     // keys per staged tile (one barrier)
+constexpr int TS = 32;     // keys per sub-tile (one 32 x 32 S^T block)
 constexpr int KPAD = 8;    // LDS row padding of the K tile (elements)
 constexpr int VPAD = 32;   // of the V tile: rows 16 dwords apart mod 64 banks (conflict-free transposed reads)
 constexpr float kRescale = 8.0f;  // log2 growth of a column max that forces a rescale
@@ -229,10 +230,10 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
     l_run[qb] = 0.0f;
   }
 
-  // S^T = K Q^T of the tile in LDS buffer `buf`: rows = its 32 keys, columns = this wave's
-  // query rows. Issued a tile ahead of its softmax, so the matrix core runs while the VALU
-  // does the previous tile's softmax.
-  auto scores = [&](int buf, f32x16_t (&st)[QB]) {
+  // S^T = K Q^T of sub-tile `half` of the tile in LDS buffer `buf`: rows = its 32 keys,
+  // columns = this wave's query rows (the first sub-tile's; later ones are folded into the
+  // previous sub-tile's math).
+  auto scores = [&](int buf, int half, f32x16_t (&st)[QB]) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
@@ -241,7 +242,8 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
     // every K operand in flight before the first MFMA (LDS latency paid once)
     op_t ka[KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) ka[s] = __builtin_bit_cast(op_t, *(const uint4*)&sh.k[buf][ln][16 * s + 8 * hh]);
+    for (int s = 0; s < KS; ++s)
+      ka[s] = __builtin_bit_cast(op_t, *(const uint4*)&sh.k[buf][TS * half + ln][16 * s + 8 * hh]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
@@ -249,20 +251,21 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
       for (int qb = 0; qb < QB; ++qb) st[qb] = M::run(ka[s], qop[qb][s], st[qb]);
     }
   };
-  // One tile of math for a wave: the softmax of tile `cb` (raw scores cur) and O^T +=
-  // V^T P^T, with the scores of the next tile (LDS buffer `nb`) into nxt interleaved with
-  // the exponentials, so the matrix core runs while the VALU works. After the last tile
-  // the next-tile scores read a stale buffer and are never used.
-  auto tile_math = [&](int cb, int nb, f32x16_t (&cur)[QB], f32x16_t (&nxt)[QB]) {
+  // One sub-tile of math for a wave: the softmax of sub-tile (cb, ch) (raw scores cur)
+  // and O^T += V^T P^T, with the scores of the next sub-tile (nb, nh) into nxt interleaved
+  // with the exponentials, so the matrix core runs while the VALU works. After the last
+  // sub-tile the next scores read a stale buffer and are never used.
+  auto tile_math = [&](int cb, int ch, int nb, int nh, f32x16_t (&cur)[QB], f32x16_t (&nxt)[QB]) {
     // the next tile's K operands and this tile's key info, in flight together
     op_t ka[KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) ka[s] = __builtin_bit_cast(op_t, *(const uint4*)&sh.k[nb][ln][16 * s + 8 * hh]);
+    for (int s = 0; s < KS; ++s)
+      ka[s] = __builtin_bit_cast(op_t, *(const uint4*)&sh.k[nb][TS * nh + ln][16 * s + 8 * hh]);
     // the lane's 16 keys: 8 (r / 4) + 4 hh + r % 4, four runs of four
     int kinf[16];
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
-      const int4 v4 = *(const int4*)&sh.info[cb][8 * r4 + 4 * hh];
+      const int4 v4 = *(const int4*)&sh.info[cb][TS * ch + 8 * r4 + 4 * hh];
       kinf[4 * r4 + 0] = v4.x; kinf[4 * r4 + 1] = v4.y; kinf[4 * r4 + 2] = v4.z; kinf[4 * r4 + 3] = v4.w;
     }
     // the mask only where this wave sees a skipped or local key (a uniform branch: most
@@ -342,7 +345,7 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
     // (issued after the score MFMAs have taken their K operands)
     op_t va[2][DB];
     constexpr int VROW = 2 * (D + VPAD);  // bytes per V row
-    const lds_char* vbase = (const lds_char*)&sh.v[cb][0][0] + vlane;
+    const lds_char* vbase = (const lds_char*)&sh.v[cb][TS * ch][0] + vlane;
 #pragma unroll
     for (int sp = 0; sp < 2; ++sp) {
 #pragma unroll
@@ -384,7 +387,8 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
     fetch_ids(y, tile + 4);  // issued before the barrier, into the set just stored
     load_tile(x, tile + 3);
     __syncthreads();
-    tile_math(tile % 3, (tile + 1) % 3, cur, nxt);
+    tile_math(tile % 3, 0, tile % 3, 1, cur, nxt);        // sub-tile 2t, scores of 2t + 1
+    tile_math(tile % 3, 1, (tile + 1) % 3, 0, nxt, cur);  // sub-tile 2t + 1, scores of 2t + 2
   };
   f32x16_t st_a[QB], st_b[QB];
   fetch_ids(Set0{}, 0);
@@ -396,11 +400,11 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
   store_tile(Set0{}, 0);
   __syncthreads();
   load_tile(Set0{}, 2);
-  scores(0, st_a);
+  scores(0, 0, st_a);
   int tile = 0;
   for (; tile + 1 < n_tiles; tile += 2) {
     step(Set1{}, Set0{}, tile, st_a, st_b);
-    step(Set0{}, Set1{}, tile + 1, st_b, st_a);
+    step(Set0{}, Set1{}, tile + 1, st_a, st_b);
   }
   if (tile < n_tiles) step(Set1{}, Set0{}, tile, st_a, st_b);
 
