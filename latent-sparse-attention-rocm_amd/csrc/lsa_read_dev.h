@@ -236,7 +236,7 @@ struct AttnState {
 // so a masked token's weight is already 0 there. The state leaves in the layout of the
 // other instances (m uniform, l and acc per token group).
 //
-// Spans of three tiles or more are software-pipelined: tile t + 1's K/V loads are issued
+// With PIPE, spans of three tiles or more are software-pipelined: tile t + 1's K/V loads are issued
 // before tile t is computed, and each lane's slot id is fetched two tiles ahead, ahead of
 // the loads it does not feed (memory counters retire in order, so a wait for an id must
 // not also wait for the rows in flight). The V side's ids come from the K side's by lane
@@ -249,7 +249,7 @@ struct MfmaTile {
   bool ok[4];
 };
 
-template <typename T, int D, int GQ, typename IdOf>
+template <typename T, int D, int GQ, bool PIPE, typename IdOf>
 __device__ __forceinline__ void attend_tiles_mfma(const QueryRegs<T, D, GQ>& q, const T* kb, const T* vb,
                                                   int64_t tstride, int64_t Tk, int lo, int hi, IdOf id_of,
                                                   float scale_log2, AttnState<T, D, GQ>& st) {
@@ -332,7 +332,7 @@ __device__ __forceinline__ void attend_tiles_mfma(const QueryRegs<T, D, GQ>& q, 
   };
 
   MfmaTile<T, D, GQ> cur;
-  if (hi - lo > 2 * NT) {  // pipelined
+  if (PIPE && hi - lo > 2 * NT) {  // pipelined
     int32_t id1 = id_of(lo + s0);
     int32_t id2 = id_of(lo + NT + s0);
     issue(id1, cur);
@@ -364,12 +364,12 @@ __device__ __forceinline__ void attend_tiles_mfma(const QueryRegs<T, D, GQ>& q, 
 // slot j, or -1 (skipped); it must be cheap and unconditional (a clamped load or an LDS
 // read). kb / vb point at the kv-head's row 0 plus this lane's VEC-element offset. fresh:
 // the state is empty, so the first tile needs no rescale.
-template <typename T, int D, int GQ, typename IdOf>
+template <typename T, int D, int GQ, bool PIPE = false, typename IdOf>
 __device__ __forceinline__ void attend_tiles(const QueryRegs<T, D, GQ>& q, const T* kb, const T* vb, int64_t tstride,
                                              int64_t Tk, int lo, int hi, IdOf id_of, float scale_log2, bool fresh,
                                              AttnState<T, D, GQ>& st) {
   if constexpr (ReadMfma<T, D, GQ>::ON) {
-    attend_tiles_mfma<T, D, GQ>(q, kb, vb, tstride, Tk, lo, hi, id_of, scale_log2, st);
+    attend_tiles_mfma<T, D, GQ, PIPE>(q, kb, vb, tstride, Tk, lo, hi, id_of, scale_log2, st);
     return;
   }
   using S = ReadShape<T, D, GQ>;
@@ -481,7 +481,7 @@ __device__ __forceinline__ void attend_span(const T* qrow, const T* kb, const T*
   QueryRegs<T, D, GQ> q;
   q.load(qrow, scale_log2);
   st.clear();
-  attend_tiles<T, D, GQ>(q, kb, vb, tstride, Tk, lo, hi, id_of, scale_log2, true, st);
+  attend_tiles<T, D, GQ, true>(q, kb, vb, tstride, Tk, lo, hi, id_of, scale_log2, true, st);
   merge_token_groups<T, D, GQ>(st);
 }
 
