@@ -93,7 +93,7 @@ def copy_cache(c: DecodeCache):
 
     b = c.buckets
     nb = Buckets(b.centroids.clone(), b.members.clone(), b.sizes.clone(), centroids_f32=None,
-                 ends=None if b.ends is None else b.ends.clone())
+                 ends=None if b.ends is None else b.ends.clone(), spans=b.spans)
     return DecodeCache(c.q.clone(), c.k.clone(), c.v.clone(), nb, c.pos.clone())
 
 

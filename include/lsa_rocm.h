@@ -185,14 +185,20 @@ int lsa_read_chunked_mfma_ok(int dtype, int32_t D, int32_t chunk);
  * stream-ordered. status (optional, int32) is set to 1 if a reader workgroup gave up
  * waiting for its unit's selection (not expected: readers wait only on lower-numbered
  * workgroups, which never wait); the counters must then be zeroed again.
+ * table_flags: 0, or LSA_TABLE_SPANS when every bucket row j holds exactly the consecutive
+ * ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0) in order, -1 after (the contiguous-segment
+ * tables): the kept members of a pick are then a range, counted and expanded without
+ * reading the member rows (the same lists). Requires ends.
  * Limits: top_p (capped at rows) <= 64; head dim {32,64,128,256}; group {1,2,4,8}. */
+#define LSA_TABLE_SPANS 1
 int64_t lsa_decode_flat_counters(int64_t R, int32_t Hkv, int32_t rows, int32_t top_p);
 size_t lsa_decode_flat_scratch_bytes(int dtype, int64_t R, int32_t Hq, int32_t Hkv, int32_t D, int32_t rows,
                                      int32_t top_p, int32_t window, int32_t sink, int32_t select_splits,
                                      int32_t readers);
 int lsa_decode_flat(const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk, int32_t Hq,
                     int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride, int64_t kv_head_stride,
-                    const void* centroids, const int32_t* members, const int32_t* ends, int32_t rows, int32_t cap,
+                    const void* centroids, const int32_t* members, const int32_t* ends, int32_t table_flags,
+                    int32_t rows, int32_t cap,
                     int64_t row_tables, int64_t group_tables, int score_mode, const int32_t* positions,
                     int32_t cluster_block_size, int32_t block_buckets, int32_t top_p, int32_t window, int32_t sink,
                     int32_t top_k, float scale, int32_t select_splits, int32_t readers, int32_t* counters,

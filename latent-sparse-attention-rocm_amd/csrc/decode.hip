@@ -124,7 +124,7 @@ extern "C" size_t lsa_decode_flat_scratch_bytes(int dtype, int64_t R, int32_t Hq
 extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk,
                                int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride,
                                int64_t kv_head_stride, const void* centroids, const int32_t* members,
-                               const int32_t* ends, int32_t rows, int32_t cap, int64_t row_tables,
+                               const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables,
                                int64_t group_tables, int score_mode, const int32_t* positions,
                                int32_t cluster_block_size, int32_t block_buckets, int32_t top_p, int32_t window,
                                int32_t sink, int32_t top_k, float scale, int32_t select_splits, int32_t readers,
@@ -149,6 +149,10 @@ extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int 
   LSA_REQUIRE(top_p >= 1 && window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE,
               "lsa_decode_flat: top_p >= 1, window/sink/top_k >= 0");
   LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "lsa_decode_flat: cluster_block_size must be >= 1");
+  LSA_REQUIRE((table_flags & ~LSA_TABLE_SPANS) == 0, LSA_ERR_SHAPE, "lsa_decode_flat: unknown table flags %d",
+              table_flags);
+  LSA_REQUIRE(!(table_flags & LSA_TABLE_SPANS) || ends, LSA_ERR_SHAPE,
+              "lsa_decode_flat: LSA_TABLE_SPANS needs the span ends");
   const int K = top_p < rows ? top_p : rows;
   LSA_REQUIRE(K <= kMaxPicks, LSA_ERR_SHAPE, "lsa_decode_flat: %d picks exceed %d", K, kMaxPicks);
   LSA_REQUIRE((int64_t)K * cap < 0x7FFFFFFF && (int64_t)top_k + window + sink <= 0x7FFFFFFF, LSA_ERR_SHAPE,
@@ -186,6 +190,7 @@ extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int 
   a.Tk = Tk; a.kv_sb = kv_batch_stride; a.kv_st = kv_token_stride; a.kv_sh = kv_head_stride;
   a.centroids = centroids; a.members = members; a.ends = ends; a.rows = rows; a.cap = cap;
   a.vec_rows = (cap % 4 == 0 && ((uintptr_t)members % 16) == 0) ? 1 : 0;
+  a.spans = (table_flags & LSA_TABLE_SPANS) ? 1 : 0;
   a.row_tables = row_tables; a.group_tables = group_tables; a.positions = positions;
   a.cluster_block = cluster_block_size; a.block_buckets = block_buckets;
   a.K = p.K; a.kp = p.kp; a.window = window; a.sink = sink; a.top_k = top_k; a.W = top_k + window + sink;

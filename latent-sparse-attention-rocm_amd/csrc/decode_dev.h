@@ -35,6 +35,7 @@ struct DecodeArgs {
   const int32_t* ends;
   int rows, cap;
   int vec_rows;        // cap % 4 == 0 and the member table 16-byte aligned
+  int spans;           // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0)
   int64_t row_tables, group_tables;
   const int32_t* positions;
   int cluster_block, block_buckets;
@@ -59,6 +60,7 @@ struct SelLds {
   TopkScratch tks;
   int pick[kMaxPicks];
   int cnt[kMaxPicks];
+  int first[kMaxPicks];  // span tables: the first kept id of each pick
   int rec[2 * kMaxPicks];
   int flag;
 };
@@ -158,13 +160,24 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
   __syncthreads();
   DECODE_MARK(4);
 
-  // kept members of every pick (sink <= id < window start): wave w counts picks w, w + 4,
-  // ... eight at a time; a member row streams through the wave in 16-byte lane loads (256
-  // slots per wave load; 64 four-byte loads without vec_rows), counted with ballots
+  // kept members of every pick (sink <= id < window start). Span tables: the range
+  // [ends[b - 1], ends[b]) clipped to [sink, window start), from two ends words. Otherwise
+  // wave w counts picks w, w + 4, ... eight at a time; a member row streams through the
+  // wave in 16-byte lane loads (256 slots per wave load; 64 four-byte loads without
+  // vec_rows), counted with ballots
   const int32_t* tab = a.members + t * (int64_t)a.rows * a.cap;
   const int64_t wstart = window_start_of(position, a.window);
   constexpr int MJ = 8;
-  for (int jb = 0; jb < a.K; jb += MJ * LSA_WAVES) {
+  if (a.spans) {
+    if (w == 0 && lane < a.K) {
+      const int b = sh.pick[lane];
+      const int64_t begin = b > 0 ? ends[b - 1] : 0, end = b >= 0 ? ends[b] : 0;
+      const int64_t lo = begin > a.sink ? begin : a.sink, hi = end < wstart ? end : wstart;
+      sh.cnt[lane] = b >= 0 && hi > lo ? (int)(hi - lo) : 0;
+      sh.first[lane] = (int)lo;
+    }
+  }
+  for (int jb = 0; jb < (a.spans ? 0 : a.K); jb += MJ * LSA_WAVES) {
     int cnt[MJ];
     int b[MJ];
 #pragma unroll
@@ -224,7 +237,7 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
     }
     const int end = incl < a.top_k ? incl : a.top_k;
     if (lane < a.K) {
-      sh.rec[lane] = sh.pick[lane] + 2;
+      sh.rec[lane] = (a.spans ? sh.first[lane] : sh.pick[lane]) + 2;  // pick, or its first kept id
       sh.rec[a.K + lane] = end + 1;
     }
     if (lane == a.K - 1) {
@@ -333,30 +346,39 @@ __device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int
       const int lo_rank = u * span;
       n = min(span, sh.n[j] - lo_rank);
       slot0 = sh.start[j] + lo_rank;
-      // ranks [lo_rank, lo_rank + n) of the pick's kept members, in table order
-      const int32_t* row = tab + (int64_t)sh.pick[j] * a.cap;
-      const uint64_t below = (1ull << lane) - 1ull;
-      for (int c0 = 0, run = 0; c0 < a.cap && run < lo_rank + n; c0 += LSA_BLOCK) {
-        const int e = c0 + tid;
-        const int32_t id = row[e < a.cap ? e : 0];
-        const bool keep = e < a.cap && id >= a.sink && (int64_t)id < wstart;
-        const uint64_t m = __ballot(keep);
-        if (lane == 0) sh.wcnt[w] = (int)__popcll(m);
+      if (a.spans) {  // the kept members are consecutive ids from the record's first one
+        const int32_t first = sh.pick[j] + lo_rank;
+        for (int k = tid; k < n; k += LSA_BLOCK) {
+          ids[k] = first + k;
+          lrow[slot0 + k] = first + k;
+        }
         __syncthreads();
-        int off = 0, tot = 0;
+      } else {
+        // ranks [lo_rank, lo_rank + n) of the pick's kept members, in table order
+        const int32_t* row = tab + (int64_t)sh.pick[j] * a.cap;
+        const uint64_t below = (1ull << lane) - 1ull;
+        for (int c0 = 0, run = 0; c0 < a.cap && run < lo_rank + n; c0 += LSA_BLOCK) {
+          const int e = c0 + tid;
+          const int32_t id = row[e < a.cap ? e : 0];
+          const bool keep = e < a.cap && id >= a.sink && (int64_t)id < wstart;
+          const uint64_t m = __ballot(keep);
+          if (lane == 0) sh.wcnt[w] = (int)__popcll(m);
+          __syncthreads();
+          int off = 0, tot = 0;
 #pragma unroll
-        for (int ww = 0; ww < LSA_WAVES; ++ww) {
-          const int c = sh.wcnt[ww];
-          off += ww < w ? c : 0;
-          tot += c;
+          for (int ww = 0; ww < LSA_WAVES; ++ww) {
+            const int c = sh.wcnt[ww];
+            off += ww < w ? c : 0;
+            tot += c;
+          }
+          const int rank = run + off + (int)__popcll(m & below) - lo_rank;
+          if (keep && rank >= 0 && rank < n) {
+            ids[rank] = id;
+            lrow[slot0 + rank] = id;
+          }
+          run += tot;
+          __syncthreads();  // wcnt is rewritten by the next chunk; ids are complete
         }
-        const int rank = run + off + (int)__popcll(m & below) - lo_rank;
-        if (keep && rank >= 0 && rank < n) {
-          ids[rank] = id;
-          lrow[slot0 + rank] = id;
-        }
-        run += tot;
-        __syncthreads();  // wcnt is rewritten by the next chunk; ids are complete
       }
     } else {
       const int t0 = (p - pparts) * span;

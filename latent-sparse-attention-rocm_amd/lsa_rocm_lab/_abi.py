@@ -21,6 +21,7 @@ LIB_PATH = pathlib.Path(os.environ.get("LSA_ROCM_LIB", pathlib.Path(__file__).pa
 LSA_F32, LSA_BF16, LSA_F16 = 0, 1, 2
 CHUNKED_AUTO, CHUNKED_GATHER, CHUNKED_MFMA = 0, 1, 2
 SCORE_BF16, SCORE_F32 = 0, 1
+TABLE_SPANS = 1  # LSA_TABLE_SPANS: every bucket row holds exactly its span of `ends`
 CENTROID_MEAN, CENTROID_NORMALIZED = 0, 1
 
 _ERRORS = {
@@ -67,7 +68,7 @@ SIGNATURES = {
     "lsa_read_chunked_mfma_ok": (_int, [_int, _i32, _i32]),
     "lsa_decode_flat_counters": (_i64, [_i64, _i32, _i32, _i32]),
     "lsa_decode_flat_scratch_bytes": (_sz, [_int, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
-    "lsa_decode_flat": (_int, [_p, _p, _p, _int, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _p, _i32,
+    "lsa_decode_flat": (_int, [_p, _p, _p, _int, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _p, _i32, _i32,
                                _i32, _i64, _i64, _int, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p,
                                _i64, _p, _sz, _p, _p, _p, _p, _p]),
 }

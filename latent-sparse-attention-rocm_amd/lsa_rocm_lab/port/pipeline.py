@@ -67,6 +67,10 @@ class Buckets:
     sizes: torch.Tensor  # [..., rows] int32
     centroids_f32: torch.Tensor | None = None  # [..., rows, index_dim] fp32 - fp32 scoring
     ends: torch.Tensor | None = None  # [..., rows] int32 exclusive span end, nondecreasing
+    # True when every row j holds exactly the ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0),
+    # in order (contiguous-segment tables): the fused decode then counts and expands a
+    # pick's kept members from the ends alone
+    spans: bool = False
 
     @property
     def rows(self) -> int:
@@ -451,6 +455,7 @@ def flat_decode(
     table, mode = _score_table(buckets, score_dtype)
     members = buckets.members.to(device=device, dtype=torch.int32).contiguous()
     ends = _ends(buckets)
+    flags = _abi.TABLE_SPANS if (buckets.spans and ends is not None) else 0
     pos = _positions32(positions, device)
     if pos.numel() != B:
         raise ValueError(f"a position a batch row: {B} rows, {pos.numel()} positions")
@@ -470,7 +475,7 @@ def flat_decode(
     ws = _abi.Workspace.get(device, "decode", nbytes)
     counters = _abi.Counters.get(device, max(n_counters, 1))
     _abi.call("lsa_decode_flat", q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, Tk, Hq, Hkv, D, sb, st, sh,
-              table.data_ptr(), members.data_ptr(), _abi.ptr(ends), rows, cap, layout.row_tables,
+              table.data_ptr(), members.data_ptr(), _abi.ptr(ends), flags, rows, cap, layout.row_tables,
               layout.group_tables, mode, pos.data_ptr(), config.cluster_block_size, config.block_bucket_count,
               config.top_p, config.window_size, config.sink_size, top_k, float(scale), splits, readers,
               counters.data_ptr(), counters.numel(), _abi.ptr(ws), nbytes, lists.data_ptr(), lengths.data_ptr(),

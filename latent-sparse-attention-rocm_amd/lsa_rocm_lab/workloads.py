@@ -202,7 +202,9 @@ def cluster_buckets(data: Clustered, target: int, cap: int = 256, max_size: int 
         starts = starts[0]
     members, sizes, ends = segment_tables(starts, cap, data.k.device)
     c32, c16 = bucket_centroids(data.k, members, "mean")
-    return Buckets(c16, members, sizes, centroids_f32=c32, ends=ends)
+    # rows are exactly their spans when the segments start at 0 and none exceeds the cap
+    spans = bool((starts[..., 0] == 0).all()) and int(sizes.max().item()) <= cap
+    return Buckets(c16, members, sizes, centroids_f32=c32, ends=ends, spans=spans)
 
 
 def node_tree(buckets: Buckets, node_size: int = 16) -> Hierarchy:

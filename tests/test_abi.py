@@ -79,7 +79,7 @@ def _decode_args(**kw):
     """lsa_decode_flat arguments for a flat 32k decode shape with fake (never dereferenced)
     pointers; kw overrides by name."""
     args = dict(q=16, k=16, v=16, dtype=_abi.LSA_BF16, R=1, Tk=32768, Hq=32, Hkv=8, D=128, sb=0, st=1024, sh=128,
-                cent=16, members=16, ends=None, rows=512, cap=256, row_tables=0, group_tables=1,
+                cent=16, members=16, ends=None, flags=0, rows=512, cap=256, row_tables=0, group_tables=1,
                 mode=_abi.SCORE_BF16, pos=16, cbs=64, bb=1, top_p=32, window=0, sink=0, top_k=8192, scale=0.088,
                 splits=16, readers=0, counters=16, n_counters=1 << 20, scratch=16, scratch_bytes=1 << 30, lists=16,
                 lengths=16, out=16, status=None, stream=None)
@@ -116,6 +116,10 @@ def test_decode_arguments_rejected_before_launch():
         _abi.call("lsa_decode_flat", *_decode_args(n_counters=10))
     with pytest.raises(_abi.LsaError, match="WORKSPACE"):
         _abi.call("lsa_decode_flat", *_decode_args(scratch_bytes=1024))
+    with pytest.raises(ValueError, match="table flags"):
+        _abi.call("lsa_decode_flat", *_decode_args(flags=2))
+    with pytest.raises(ValueError, match="span ends"):  # span tables need their ends
+        _abi.call("lsa_decode_flat", *_decode_args(flags=_abi.TABLE_SPANS))
 
 
 def test_chunked_read_paths():

@@ -163,3 +163,25 @@ def test_rejects_cpu_tensors_and_bad_shapes():
         pipeline.flat_decode(data.q[:, -1:].cpu(), data.k, data.v, pos, buckets, workloads.FLAT_32K)
     with pytest.raises(ValueError):
         pipeline.flat_decode(data.q[:, -2:], data.k, data.v, pos, buckets, workloads.FLAT_32K)
+
+
+@pytest.mark.parametrize("window,sink", [(0, 0), (100, 4)])
+def test_span_tables_match_member_tables(window, sink):
+    """Contiguous-segment tables decoded through their spans (LSA_TABLE_SPANS: counts and
+    ids from the ends, no member rows) and through their member rows give the same lists,
+    lengths and outputs, and both match the oracle; the window and sink clip some picks'
+    spans at both ends."""
+    import dataclasses
+
+    T, Hq, Hkv, D = 8192, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=128, seed=11, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    assert buckets.spans
+    config = dataclasses.replace(workloads.FLAT_32K, window_size=window, sink_size=sink)
+    for p in (T - 1, 3000):
+        pos = torch.tensor([p], dtype=torch.int32)
+        q = data.q[:, p:p + 1]
+        got = check_decode(q, data.k, data.v, pos, buckets, config, label=f"spans p={p}")
+        ref = check_decode(q, data.k, data.v, pos, dataclasses.replace(buckets, spans=False), config,
+                           label=f"members p={p}")
+        assert all(torch.equal(a, b) for a, b in zip(got, ref))
