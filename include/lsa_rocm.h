@@ -177,7 +177,7 @@ int lsa_read_chunked_mfma_ok(int dtype, int32_t D, int32_t chunk);
  * lists [R, Hkv, top_k + window + sink] and lengths [R, Hkv] (identical to
  * lsa_select_flat's) and out [R, Hq, D] (the read of those lists).
  *
- * readers: reader workgroups per (row, kv-head), 0 = default (2 * picks + the window/sink
+ * readers: reader workgroups per (row, kv-head), 0 = default (picks + the window/sink
  * parts), at most 256; each reads its share of the list in tiles of
  * lsa_read_tile_tokens() slots. counters: lsa_decode_flat_counters() int32 words, zero
  * before the first launch; every launch leaves them zero. scratch:

@@ -78,7 +78,7 @@ int64_t record_stride(int64_t units, int K) {
 // pick, plus the tail's parts), at most kMaxReaders.
 int default_readers(int K, int span, int window, int sink) {
   const int64_t tail = ((int64_t)window + sink + span - 1) / span;
-  const int64_t nr = 2 * (int64_t)K + tail;
+  const int64_t nr = (int64_t)K + tail;  // about one dense part a reader (buckets of ~one tile)
   return (int)(nr < kMaxReaders ? nr : kMaxReaders);
 }
 
