@@ -185,3 +185,24 @@ def test_span_tables_match_member_tables(window, sink):
         ref = check_decode(q, data.k, data.v, pos, dataclasses.replace(buckets, spans=False), config,
                            label=f"members p={p}")
         assert all(torch.equal(a, b) for a, b in zip(got, ref))
+
+
+def test_tied_scores_take_the_block_top_k():
+    """Every centroid equal: all scores tie, the one-wave histogram cut is not selective
+    (every key in one bin) and the block's radix top-k decides; ties go to the lower
+    bucket, so the picks are buckets 0..31 in order."""
+    T, Hq, Hkv, D = 8192, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=64, seed=12, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    import dataclasses
+
+    same = buckets.centroids[..., :1, :].expand_as(buckets.centroids).contiguous()
+    tied = dataclasses.replace(buckets, centroids=same, centroids_f32=same.float())
+    pos = torch.tensor([T - 1], dtype=torch.int32)
+    out, lists, lengths = check_decode(data.q[:, -1:], data.k, data.v, pos, tied, workloads.FLAT_32K,
+                                       label="tied scores")
+    ends = tied.ends.cpu()
+    for g in range(Hkv):
+        n = int(ends[g, 31])  # buckets 0..31 are the spans [0, ends[31])
+        assert int(lengths[0, g]) == n
+        assert torch.equal(lists[0, g, :n].cpu(), torch.arange(n, dtype=torch.int32))
