@@ -377,7 +377,8 @@ def main() -> int:
     gathered = int(n_tok.sum()) * D * 2 * 2          # K and V rows, bf16
     cand_bytes = HKV * N_BUCKETS * D * 2             # centroid scan, bf16
     cap = buckets.members.shape[-1]
-    ids_bytes = HKV * config.top_p * cap * 4         # member rows of the picked buckets
+    # the picks' member rows, or with span tables the two span ends a pick
+    ids_bytes = HKV * config.top_p * (8 if buckets.spans else cap * 4)
     list_bytes = lists0.numel() * 4 + lengths0.numel() * 4  # the lists handed back
     qo_bytes = 2 * HQ * D * 2
     total_bytes = gathered + cand_bytes + ids_bytes + list_bytes + qo_bytes
