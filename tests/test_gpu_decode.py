@@ -83,6 +83,20 @@ def test_clustered_decode_matches_oracle(splits):
                  label=f"clustered splits={splits}")
 
 
+@pytest.mark.parametrize("dtype,hq,hkv", [(torch.bfloat16, 8, 8), (torch.bfloat16, 8, 4), (torch.bfloat16, 16, 2),
+                                          (torch.float16, 8, 2), (torch.float16, 16, 2), (torch.float16, 4, 4)])
+def test_matrix_core_decode_group_sizes(dtype, hq, hkv):
+    """The fused decode on 16-bit rows of D = 128 reads on the matrix cores for 1, 2, 4 and
+    8 query heads a kv-head, in bf16 and fp16; lists bit-exact, outputs within the dtype's
+    bar."""
+    T, D = 8192, 128
+    data = workloads.clustered(T, hq, hkv, D, n_clusters=128, seed=hq + hkv, dtype=dtype, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    pos = torch.tensor([T - 1], dtype=torch.int32)
+    check_decode(data.q[:, -1:], data.k, data.v, pos, buckets, workloads.FLAT_32K,
+                 label=f"mfma decode {dtype} hq={hq} hkv={hkv}")
+
+
 def test_decode_32k_geometry_matches_unfused_path(monkeypatch):
     """The benchmark geometry: 32k context, Hq 32 / Hkv 8, 512 buckets per kv-head."""
     T, Hq, Hkv, D = 32768, 32, 8, 128

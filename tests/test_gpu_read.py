@@ -235,3 +235,33 @@ def test_kv_views_are_read_in_place():
     want = oracle.sparse_read(q[:, -1:, :4].float().numpy(), k[:, :, ::2].float().numpy(),
                               v[:, :, ::2].float().numpy(), ids.numpy(), lengths.numpy())
     check(got, want, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (8, 4), (16, 4), (16, 2)])
+def test_matrix_core_read_group_sizes(dtype, hq, hkv):
+    """16-bit rows of D = 128 score on the matrix cores for 1, 2, 4 and 8 query heads a
+    kv-head: a batch of per-token lists (one tile or two per row), then a decode row of
+    per-kv-head lists long enough that every split walks several tiles (the pipelined loop
+    with loads one tile ahead), at a fixed split count and at the planner's."""
+    T = 1024
+    q, k, v = geometry(dtype, T=T, Hq=hq, Hkv=hkv, D=128, seed=100 * hq + hkv)
+    g = torch.Generator().manual_seed(hq + 7 * hkv)
+    ids = torch.randint(-1, T, (1, 96, 160), generator=g, dtype=torch.int32)
+    lengths = torch.randint(0, 161, (1, 96), generator=g, dtype=torch.int32)
+    qs = q[:, -96:].contiguous()
+    print(f"case prefill rows {dtype} hq={hq} hkv={hkv}", flush=True)
+    check(run(sparse_read_auto, qs, k, v, ids, lengths), want_of(qs, k, v, ids, lengths), dtype)
+    ids = torch.randint(-1, T, (1, 1, hkv, 3000), generator=g, dtype=torch.int32)
+    lengths = torch.randint(2000, 3001, (1, 1, hkv), generator=g, dtype=torch.int32)
+    q1 = q[:, -1:].contiguous()
+    want = want_of(q1, k, v, ids, lengths)
+    for splits in ("4", None):
+        print(f"case decode row {dtype} hq={hq} hkv={hkv} splits={splits}", flush=True)
+        if splits:
+            os.environ["LSA_READ_SPLITS"] = splits
+        try:
+            got = run(sparse_read_auto, q1, k, v, ids, lengths)
+        finally:
+            os.environ.pop("LSA_READ_SPLITS", None)
+        check(got, want, dtype)
