@@ -4,19 +4,21 @@
 // slots) and then the chunk's own causal block [c*chunk, t] (the reference read of the
 // config-4 prefill: read_kernel_tiled.py:30-89 over these lists). Every row of a chunk
 // shares the list, so one workgroup serves (batch, chunk, kv-head, head group): the
-// chunk's rows of up to 256 / chunk query heads of the group - 256 query rows, 64 per
+// chunk's rows of up to 256 / chunk query heads of the group - 256 query rows, 32 per
 // wave - and every K/V row of the list is gathered once for all of them.
 //
-// Per 32-key tile: the K rows land in LDS row-major and the V rows transposed (V^T), double
-// buffered, the next tile's ids and rows in flight while this one computes. Each wave then
-// computes S^T = K Q^T (v_mfma_f32_32x32x16: the K rows are the A operand read straight
-// from LDS, Q^T the B operand held in registers for the whole kernel), masks invalid and
-// non-causal keys, runs the online softmax in the exp2 domain per query column, and
+// Per 64-key tile: the K and V rows land in LDS row-major (four tile buffers: two being
+// read, one being stored, one free), gathered a tile ahead of their store, from inside the
+// math of the tile before. Each wave computes S^T = K Q^T a 32-key sub-tile at a time
+// (v_mfma_f32_32x32x16: the K rows are the A operand read straight from LDS, Q^T the B
+// operand held in registers for the whole kernel), masks skipped and non-causal keys where
+// the sub-tile has any, runs the online softmax in the exp2 domain per query column, and
 // accumulates O^T += V^T P^T: the S^T accumulator layout is exactly the P^T B operand
 // (lane (h, q) holds keys 8(r/4) + 4h + r%4 of column q), so P needs no shuffle; the V^T
-// A operand pairs the same key order from LDS. The running max is rescaled lazily: only
-// when a column's max grows by more than 2^8 is the state rescaled, so P stays below 256
-// in the 16-bit operand and most tiles skip the 128-register rescale.
+// A operand comes from the row-major V tile through transposing LDS reads. The running
+// max is rescaled lazily: only when a column's max grows by more than 2^8 is the state
+// rescaled, so P stays below 256 in the 16-bit operand and most tiles skip the
+// 128-register rescale. The softmax normaliser sums the 16-bit weights the matrix ops use.
 #include <math.h>
 
 #include <type_traits>
@@ -34,6 +36,7 @@ constexpr int KPAD = 8;    // LDS row padding of the K tile (elements)
 constexpr int VPAD = 32;   // of the V tile: rows 16 dwords apart mod 64 banks (conflict-free transposed reads)
 constexpr float kRescale = 8.0f;  // log2 growth of a column max that forces a rescale
 constexpr int kRows = 256;       // query rows of a workgroup
+constexpr int NBUF = 4;          // LDS tile buffers (two read, one being stored, one free)
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
@@ -49,6 +52,11 @@ template <> struct Mfma<bf16_t> {
     const f2_t f = {lo, hi};
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2_t));
   }
+  // c + lo + hi of a packed pair (v_dot2_f32_bf16 against ones)
+  static __device__ __forceinline__ float sum2(uint32_t pair, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair), __builtin_bit_cast(bf16x2_t, 0x3F803F80u),
+                                           c, false);
+  }
 };
 template <> struct Mfma<_Float16> {
   typedef f16x8_t op_t;
@@ -61,13 +69,17 @@ template <> struct Mfma<_Float16> {
     const f2_t f = {lo, hi};
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2_t));
   }
+  static __device__ __forceinline__ float sum2(uint32_t pair, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, pair), __builtin_bit_cast(f16x2_t, 0x3C003C00u), c, false);
+  }
 };
 
 template <int D>
 struct alignas(16) PrefillLds {
-  uint16_t k[3][TK][D + KPAD];   // K rows, raw 16-bit elements (three tiles in flight)
-  uint16_t v[3][TK][D + VPAD];   // V rows, raw 16-bit elements
-  int info[3][TK];               // per key: -2 skipped, -1 list key (every row), o >= 0 local offset
+  uint16_t k[NBUF][TK][D + KPAD];   // K rows, raw 16-bit elements
+  uint16_t v[NBUF][TK][D + VPAD];   // V rows, raw 16-bit elements
+  int info[NBUF][TK];               // per key: -2 skipped, -1 list key (every row), o >= 0 local offset
+  int odd[NBUF][TK / TS];           // tile number whose sub-tile holds a key that is not a list key
 };
 
 // Four keys of one V column from the row-major V tile, for a V^T MFMA operand, by the
@@ -100,7 +112,7 @@ struct PrefillArgs {
 };
 
 // QB query blocks of 32 columns per wave; 8 / QB waves hold the workgroup's 256 rows.
-template <typename T, int D, int QB>
+template <typename T, int D, int QB, bool OFF32>
 __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs a) {
   using M = Mfma<T>;
   using op_t = typename M::op_t;
@@ -160,57 +172,83 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
     }
   }
 
-  // tile loads: key kk = pass * KPP + tid / SEGS, segment seg = tid % SEGS. Rows are
-  // gathered two tiles ahead of their store into LDS, so a gather has two iterations of
-  // math to land, into one of two register sets chosen by the tile's parity (the loop is
-  // unrolled by two, so no register is copied while its load is in flight). A tile's list
-  // ids are fetched an iteration before its gather and issued ahead of the gather they do
-  // not feed: the vector-memory counter retires in order, so a wait for an id must not
-  // also wait for rows in flight. Loads past the last tile are clamped (unconditional
-  // loads keep every wait exact) and their rows are never used.
+  // tile loads: key kk = pass * KPP + tid / SEGS, segment seg = tid % SEGS. A tile's rows are
+  // gathered one iteration before their store into LDS and its list ids one iteration
+  // before that; both are issued from inside the math (between matrix ops) rather than as a
+  // phase of their own, so the gathers and LDS writes overlap the matrix and vector work.
+  // Loads past the last tile are clamped (unconditional loads keep every wait exact) and
+  // their rows are never used.
   const int seg = tid % SEGS;
   const int32_t* lsrc = a.W > 0 ? list : a.lengths + li;  // always a valid address
   const bool loader = KPP <= TK || tid / SEGS < TK;  // threads with a key to load
-  int32_t lid[2][PASSES];
-  uint4 kreg[2][PASSES], vreg[2][PASSES];
-  int kinfo[2][PASSES];
-  auto fetch_ids = [&](auto set, int tile) {
-    constexpr int S = decltype(set)::value;
+  struct Rows {
+    int32_t id[PASSES];
+    uint4 k[PASSES], v[PASSES];
+    int info[PASSES];
+  };
+  Rows rows, rows_b;  // rows_b: the second tile of the prologue only
+  auto fetch_ids = [&](Rows& r, int tile) {
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       const int j = tile * TK + p * KPP + (loader ? tid / SEGS : 0);
       const int jl = j < n_list ? j : (n_list > 0 ? n_list - 1 : 0);
-      lid[S][p] = lsrc[jl];
+      r.id[p] = lsrc[jl];
     }
   };
-  auto load_tile = [&](auto set, int tile) {
-    constexpr int S = decltype(set)::value;
+  auto load_tile = [&](Rows& r, int tile) {
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       const int j = tile * TK + p * KPP + (loader ? tid / SEGS : 0);
-      const int32_t l = lid[S][p];
-      const int o = j - n_list;
+      const int32_t l = r.id[p];
       const bool in_list = j < n_list;
-      const int info = in_list ? (((l >= 0) & (l < a.Tk)) ? -1 : -2) : (j < n_tot ? o : -2);
-      const int32_t id = in_list ? l : (int32_t)(c0 + o);
-      const uint64_t off = (uint64_t)(uint32_t)(info >= -1 ? id : 0) * (uint64_t)a.kv_st + seg * 8;
-      kreg[S][p] = *(const uint4*)(kb + off);
-      vreg[S][p] = *(const uint4*)(vb + off);
-      kinfo[S][p] = info;
+      const bool valid = in_list ? (unsigned)l < (unsigned)a.Tk : j < n_tot;
+      const int32_t id = in_list ? l : (int32_t)c0 + (j - n_list);
+      r.info[p] = valid ? (in_list ? -1 : j - n_list) : -2;
+      const uint32_t row = valid ? (uint32_t)id : 0u;
+      if constexpr (OFF32) {
+        // byte offsets fit in 32 bits (checked on the host): base in SGPRs + one VGPR offset
+        const uint32_t off = (__umul24(row, (uint32_t)a.kv_st) + seg * 8) * (uint32_t)sizeof(T);
+        r.k[p] = *(const uint4*)((const char*)kb + off);
+        r.v[p] = *(const uint4*)((const char*)vb + off);
+      } else {
+        const uint64_t off = (uint64_t)row * (uint64_t)a.kv_st + seg * 8;
+        r.k[p] = *(const uint4*)(kb + off);
+        r.v[p] = *(const uint4*)(vb + off);
+      }
     }
   };
-  auto store_tile = [&](auto set, int buf) {
-    constexpr int S = decltype(set)::value;
+  // Skipped keys store zero rows (their weights are zero; a zero row keeps them so even when
+  // the clamped row holds non-finite values): a uniform branch, most tiles have none. A
+  // sub-tile holding a key that is not a list key is tagged with the tile number, so the
+  // math reads one word to learn whether it must mask.
+  auto store_tile = [&](const Rows& r, int buf, int tile) {
     if (!loader) return;
+    bool all_ok = true;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) all_ok &= r.info[p] >= -1;
+    if (__all(all_ok)) {
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) {
+        const int kk = p * KPP + tid / SEGS;
+        *(uint4*)&sh.k[buf][kk][seg * 8] = r.k[p];
+        *(uint4*)&sh.v[buf][kk][seg * 8] = r.v[p];
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) {
+        const int kk = p * KPP + tid / SEGS;
+        const bool ok = r.info[p] >= -1;
+        *(uint4*)&sh.k[buf][kk][seg * 8] = ok ? r.k[p] : make_uint4(0, 0, 0, 0);
+        *(uint4*)&sh.v[buf][kk][seg * 8] = ok ? r.v[p] : make_uint4(0, 0, 0, 0);
+      }
+    }
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       const int kk = p * KPP + tid / SEGS;
-      const bool ok = kinfo[S][p] >= -1;
-      const uint4 kr = ok ? kreg[S][p] : make_uint4(0, 0, 0, 0);
-      const uint4 vr = ok ? vreg[S][p] : make_uint4(0, 0, 0, 0);
-      *(uint4*)&sh.k[buf][kk][seg * 8] = kr;
-      *(uint4*)&sh.v[buf][kk][seg * 8] = vr;
-      if (seg == 0) sh.info[buf][kk] = kinfo[S][p];
+      if (seg == 0) {
+        sh.info[buf][kk] = r.info[p];
+        if (r.info[p] != -1) sh.odd[buf][kk / TS] = tile;
+      }
     }
   };
 
@@ -254,26 +292,25 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
   // One sub-tile of math for a wave: the softmax of sub-tile (cb, ch) (raw scores cur)
   // and O^T += V^T P^T, with the scores of the next sub-tile (nb, nh) into nxt interleaved
   // with the exponentials, so the matrix core runs while the VALU works. After the last
-  // sub-tile the next scores read a stale buffer and are never used.
-  auto tile_math = [&](int cb, int ch, int nb, int nh, f32x16_t (&cur)[QB], f32x16_t (&nxt)[QB]) {
-    // the next tile's K operands and this tile's key info, in flight together
+  // sub-tile the next scores read a stale buffer and are never used. hook(s) runs after
+  // k-step s (the loads and LDS stores of the pipeline, placed between matrix ops).
+  auto tile_math = [&](int cb, int ch, int ctile, int nb, int nh, f32x16_t (&cur)[QB], f32x16_t (&nxt)[QB],
+                       auto&& hook) {
+    // the next tile's K operands and this sub-tile's tag, in flight together
     op_t ka[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s)
       ka[s] = __builtin_bit_cast(op_t, *(const uint4*)&sh.k[nb][TS * nh + ln][16 * s + 8 * hh]);
-    // the lane's 16 keys: 8 (r / 4) + 4 hh + r % 4, four runs of four
-    int kinf[16];
+    // the mask only where the sub-tile holds a skipped or local key (a uniform branch: most
+    // sub-tiles are list keys every row sees)
+    if (__builtin_amdgcn_readfirstlane(sh.odd[cb][ch]) == ctile) {
+      // the lane's 16 keys: 8 (r / 4) + 4 hh + r % 4, four runs of four
+      int kinf[16];
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const int4 v4 = *(const int4*)&sh.info[cb][TS * ch + 8 * r4 + 4 * hh];
-      kinf[4 * r4 + 0] = v4.x; kinf[4 * r4 + 1] = v4.y; kinf[4 * r4 + 2] = v4.z; kinf[4 * r4 + 3] = v4.w;
-    }
-    // the mask only where this wave sees a skipped or local key (a uniform branch: most
-    // tiles are list keys every row sees)
-    int odd = 0;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) odd |= kinf[r] != -1;
-    if (__any(odd)) {
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int4 v4 = *(const int4*)&sh.info[cb][TS * ch + 8 * r4 + 4 * hh];
+        kinf[4 * r4 + 0] = v4.x; kinf[4 * r4 + 1] = v4.y; kinf[4 * r4 + 2] = v4.z; kinf[4 * r4 + 3] = v4.w;
+      }
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
@@ -316,13 +353,17 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
     // 16 s' + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}: the P^T B operand)
     constexpr int EPS = 16 / KS;  // exponentials per k-step (even)
     uint32_t pw[QB][8];           // the weights, packed in pairs as they are made
-    float ls[QB];
+    float ls[QB][2];              // their sum, in two chains
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      ls[qb] = 0.0f;
+      ls[qb][0] = ls[qb][1] = 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) nxt[qb][r] = 0.0f;
     }
+    // The two waves of a SIMD alternate between this matrix-heavy part and the vector-only
+    // part above; raising the wave's issue priority here lets its matrix ops issue first, so
+    // the other wave's max/rescale work fills the matrix ops' shadow.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
 #pragma unroll
@@ -334,11 +375,13 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
           const int r = EPS * s + e;
           const float p0 = fast_exp2(fmaf(cur[qb][r], a.scale_log2, -m_run[qb]));
           const float p1 = fast_exp2(fmaf(cur[qb][r + 1], a.scale_log2, -m_run[qb]));
-          ls[qb] += p0 + p1;
           pw[qb][r / 2] = M::pack2(p0, p1);
+          ls[qb][(r / 2) & 1] = M::sum2(pw[qb][r / 2], ls[qb][(r / 2) & 1]);  // the 16-bit weights the MFMA uses
         }
       }
       __builtin_amdgcn_sched_barrier(0);  // this k-step's MFMA, then its weights, in order
+      hook(s);
+      __builtin_amdgcn_sched_barrier(0);
     }
     // V^T operands of this tile: lane (hh, ln) holds dim 32 d + ln at keys
     // 16 sp + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}, two transposing 8-byte reads
@@ -358,7 +401,7 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
     op_t pb[QB][2];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      l_run[qb] += ls[qb];
+      l_run[qb] += ls[qb][0] + ls[qb][1];
 #pragma unroll
       for (int sp = 0; sp < 2; ++sp)
         pb[qb][sp] = __builtin_bit_cast(op_t, make_uint4(pw[qb][4 * sp], pw[qb][4 * sp + 1], pw[qb][4 * sp + 2],
@@ -372,41 +415,41 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
         for (int qb = 0; qb < QB; ++qb) o[d][qb] = M::run(va[sp][d], pb[qb][sp], o[d][qb]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
-  // Pipeline, one barrier per tile over three LDS buffers: iteration t stores tile t + 1
-  // (gathered two iterations earlier) and issues the ids of tile t + 4 and the gather of
-  // tile t + 3 before the barrier, then tile t's math (with tile t + 1's scores folded
-  // in). A buffer is rewritten two iterations after its last reader, which the
-  // intervening barrier has let finish.
-  using Set0 = std::integral_constant<int, 0>;
-  using Set1 = std::integral_constant<int, 1>;
-  auto step = [&](auto x, auto y, int tile, f32x16_t (&cur)[QB], f32x16_t (&nxt)[QB]) {
-    const bool more = tile + 1 < n_tiles;
-    if (more) store_tile(x, (tile + 1) % 3);
-    fetch_ids(y, tile + 4);  // issued before the barrier, into the set just stored
-    load_tile(x, tile + 3);
+  // Pipeline, one barrier per tile over NBUF = 4 LDS buffers. Iteration t computes tile t
+  // (its second sub-tile's math also takes the scores of tile t + 1's first sub-tile);
+  // inside the first sub-tile's math it stores tile t + 2 (gathered in iteration t - 1) and
+  // gathers tile t + 3 (ids fetched in iteration t - 1), inside the second it fetches the
+  // ids of tile t + 4. Buffer (t + 2) % 4 last held tile t - 2, whose readers finished
+  // before the barrier of iteration t - 1; tile t + 2 is first read after the barrier of
+  // iteration t + 1. The vector-memory counter retires in order, and every wait is for the
+  // oldest loads outstanding.
+  auto step = [&](int tile, f32x16_t (&cur)[QB], f32x16_t (&nxt)[QB]) {
     __syncthreads();
-    tile_math(tile % 3, 0, tile % 3, 1, cur, nxt);        // sub-tile 2t, scores of 2t + 1
-    tile_math(tile % 3, 1, (tile + 1) % 3, 0, nxt, cur);  // sub-tile 2t + 1, scores of 2t + 2
+    const bool store_next = tile + 2 < n_tiles;
+    tile_math(tile % NBUF, 0, tile, tile % NBUF, 1, cur, nxt, [&](int s) {
+      if (s == 1 && store_next) store_tile(rows, (tile + 2) % NBUF, tile + 2);
+      if (s == 3) load_tile(rows, tile + 3);
+    });
+    tile_math(tile % NBUF, 1, tile, (tile + 1) % NBUF, 0, nxt, cur, [&](int s) {
+      if (s == 1) fetch_ids(rows, tile + 4);
+    });
   };
   f32x16_t st_a[QB], st_b[QB];
-  fetch_ids(Set0{}, 0);
-  fetch_ids(Set1{}, 1);
-  load_tile(Set0{}, 0);
-  fetch_ids(Set0{}, 2);
-  load_tile(Set1{}, 1);
-  fetch_ids(Set1{}, 3);
-  store_tile(Set0{}, 0);
+  fetch_ids(rows, 0);
+  fetch_ids(rows_b, 1);
+  load_tile(rows, 0);
+  load_tile(rows_b, 1);
+  store_tile(rows, 0, 0);
+  fetch_ids(rows, 2);
+  store_tile(rows_b, 1, 1);
+  load_tile(rows, 2);
+  fetch_ids(rows, 3);
   __syncthreads();
-  load_tile(Set0{}, 2);
   scores(0, 0, st_a);
-  int tile = 0;
-  for (; tile + 1 < n_tiles; tile += 2) {
-    step(Set1{}, Set0{}, tile, st_a, st_b);
-    step(Set0{}, Set1{}, tile + 1, st_a, st_b);
-  }
-  if (tile < n_tiles) step(Set1{}, Set0{}, tile, st_a, st_b);
+  for (int tile = 0; tile < n_tiles; ++tile) step(tile, st_a, st_b);
 
   // normalise and store: lane (hh, q) holds dims 32 d + 8 (r / 4) + 4 hh + r % 4 of column q
 #pragma unroll
@@ -431,11 +474,11 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
 
 constexpr int kQB = 1;  // one block of 32 query columns per wave (two waves a SIMD)
 
-template <typename T>
+template <typename T, bool OFF32>
 void launch_prefill(const PrefillArgs& a, int D, dim3 grid, hipStream_t s) {
   constexpr int nth = 64 * (8 / kQB);
-  if (D == 64) prefill_mfma_kernel<T, 64, kQB><<<grid, nth, 0, s>>>(a);
-  else prefill_mfma_kernel<T, 128, kQB><<<grid, nth, 0, s>>>(a);
+  if (D == 64) prefill_mfma_kernel<T, 64, kQB, OFF32><<<grid, nth, 0, s>>>(a);
+  else prefill_mfma_kernel<T, 128, kQB, OFF32><<<grid, nth, 0, s>>>(a);
 }
 
 }  // namespace
@@ -469,8 +512,18 @@ int launch_read_chunked_mfma(const void* q, const void* k, const void* v, int dt
   const int64_t n = B * a.C * Hkv * a.n_hg;
   LSA_REQUIRE(n <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_read_chunked: too many workgroups");
   if (n == 0) return LSA_OK;
-  if (dtype == LSA_BF16) launch_prefill<bf16_t>(a, D, dim3((unsigned)n), s);
-  else launch_prefill<_Float16>(a, D, dim3((unsigned)n), s);
+  // 32-bit gather offsets when every row of one (batch, kv-head) view is within 4 GiB of its
+  // first and the row index and stride fit the 24-bit multiply
+  const uint64_t span = (uint64_t)(Tk > 0 ? Tk - 1 : 0) * (uint64_t)kv_st * 2u + (uint64_t)D * 2u;
+  const bool off32 = span < (1ull << 32) && Tk < (1 << 24) && kv_st < (1 << 24);
+  const dim3 grid((unsigned)n);
+  if (dtype == LSA_BF16) {
+    if (off32) launch_prefill<bf16_t, true>(a, D, grid, s);
+    else launch_prefill<bf16_t, false>(a, D, grid, s);
+  } else {
+    if (off32) launch_prefill<_Float16, true>(a, D, grid, s);
+    else launch_prefill<_Float16, false>(a, D, grid, s);
+  }
   LSA_LAUNCHED("lsa_read_chunked (mfma)");
   return LSA_OK;
 }

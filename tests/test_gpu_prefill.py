@@ -5,7 +5,8 @@ chunk's causal block [chunk start, t]. Cases: both 16-bit types, head dims 64 an
 chunks 16 / 32 / 64 / 128, groups 1 / 2 / 4 / 8 (several workgroups per kv-head when the
 group does not fit 256 rows), ragged and empty lists, -1 and out-of-range ids (skipped),
 duplicate ids (counted per occurrence), a partial last chunk, two batch rows, a long list
-with large score spreads (the lazy rescale), and agreement with the gather kernel.
+with large score spreads (the lazy rescale), K/V views whose rows lie more than 4 GiB
+apart (64-bit gather offsets), and agreement with the gather kernel.
 Tolerances (max-abs / mean-abs vs the fp64 oracle): bf16 2e-2 / 2e-3, fp16 5e-3 / 5e-4.
 """
 
@@ -52,7 +53,7 @@ def run_and_check(q, k, v, ids, lengths, chunk, path="mfma", label=""):
     got = sparse_read_chunked(q.to(DEV), k.to(DEV), v.to(DEV), ids.to(DEV), lengths.to(DEV), None, chunk, path=path)
     ids_np = ids.numpy().copy()
     ids_np[ids_np >= k.shape[1]] = -1  # the oracle indexes rows; out-of-range ids are skipped like -1
-    want = oracle.sparse_read_chunked(q.float().numpy(), k.float().numpy(), v.float().numpy(), ids_np,
+    want = oracle.sparse_read_chunked(q.float().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(), ids_np,
                                       lengths.numpy(), chunk)
     max_abs, mean_abs = TOL[q.dtype]
     err = np.abs(got.float().cpu().numpy() - want)
@@ -87,6 +88,22 @@ def test_mfma_prefill_duplicates_and_long_lists():
     q, k, v, ids, lengths = make_case(torch.bfloat16, T=1024, W=900, seed=9, scale=2.0)
     ids[..., 1::2] = ids[..., 0::2]  # every id twice
     run_and_check(q, k, v, ids, lengths, 64, label="long")
+
+
+def test_mfma_prefill_wide_token_stride():
+    """K/V rows 9.4 M elements apart (views into a 4.8 GB cache, read in place): byte
+    offsets past 4 GiB take the kernel's 64-bit gather addresses."""
+    q, k, v, ids, lengths = make_case(torch.bfloat16, T=256, Hq=8, Hkv=2, W=160, seed=21)
+    Tk, Hkv, D = k.shape[1], k.shape[2], k.shape[3]
+    stride = (1 << 23) + (1 << 20)
+    assert (Tk - 1) * stride * 2 >= 1 << 32
+    base = torch.empty(Tk, stride, dtype=torch.bfloat16, device=DEV)
+    kd = torch.as_strided(base, (1, Tk, Hkv, D), (Tk * stride, stride, D, 1))
+    vd = torch.as_strided(base, (1, Tk, Hkv, D), (Tk * stride, stride, D, 1), Hkv * D)
+    kd.copy_(k.to(DEV))
+    vd.copy_(v.to(DEV))
+    run_and_check(q, kd, vd, ids, lengths, 64, label="wide stride")
+    del kd, vd, base
 
 
 def test_mfma_and_gather_paths_agree():
