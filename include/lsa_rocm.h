@@ -131,6 +131,22 @@ int lsa_bucket_centroids(const void* keys, int k_dtype, int64_t tokens, int64_t 
                          int32_t kv_heads, int32_t D, const int32_t* members, int64_t n_tables, int32_t rows,
                          int32_t cap, int centroid_mode, float* out_f32, uint16_t* out_bf16, void* stream);
 
+/* Bucket-table build from the keys (the index build before the path; replaces the
+ * reference's build_buckets_gpu, pipeline.py:71-116, with contiguous segments): per table
+ * (batch b, kv-head g) the keys [T, D] at keys + b * kv_sb + g * kv_sh + t * kv_st + d are
+ * cut into pools of `pool` positions (fp64 sums), then the adjacent pair with the smallest
+ * Ward cost n_a n_b / (n_a + n_b) |mu_a - mu_b|^2 is merged (ties to the leftmost pair,
+ * merges past max_size positions skipped) until `target` segments remain. starts
+ * [B * Hkv, target + 1] int32 receives each table's segment start positions (last = T);
+ * status [B * Hkv] int32 receives 0, or 1 where no pair could merge before the target
+ * (that table's starts are then unset). scratch: lsa_ward_segments_scratch_bytes bytes of
+ * device memory. Limits: ceil(T / pool) <= 4096 pools, target <= pools, max_size >= pool,
+ * D <= 1024. */
+size_t lsa_ward_segments_scratch_bytes(int64_t tables, int64_t T, int32_t D, int32_t pool);
+int lsa_ward_segments(const void* keys, int k_dtype, int64_t B, int64_t T, int32_t kv_heads, int32_t D,
+                      int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int32_t pool, int32_t target, int32_t max_size,
+                      void* scratch, size_t scratch_bytes, int32_t* starts, int32_t* status, void* stream);
+
 /* Sparse gather read (reference read_kernel_tiled.py:30-156 sparse_read_auto / tiled,
  * read_kernel.py:26-120 v1): q [B, Tq, Hq, D] dense; k/v [B, Tk, Hkv, D] (dtype) with the
  * given element strides of batch, token and head (shared by K and V; rows of D contiguous

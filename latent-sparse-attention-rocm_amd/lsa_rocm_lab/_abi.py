@@ -59,6 +59,9 @@ SIGNATURES = {
                                _int, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
     "lsa_index_queries": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p]),
     "lsa_bucket_centroids": (_int, [_p, _int, _i64, _i64, _i64, _i32, _i32, _p, _i64, _i32, _i32, _int, _p, _p, _p]),
+    "lsa_ward_segments_scratch_bytes": (_sz, [_i64, _i64, _i32, _i32]),
+    "lsa_ward_segments": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _p, _sz, _p,
+                                 _p, _p]),
     "lsa_read_scratch_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "lsa_read_tile_tokens": (_i32, [_int, _i32, _i32]),
     "lsa_read": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _i32, _int,

@@ -536,6 +536,61 @@ def bucket_centroids(keys: torch.Tensor, members: torch.Tensor, centroid: str = 
     return out32, out16
 
 
+def segment_starts(keys: torch.Tensor, target: int, pool: int = 16, max_size: int = 256) -> torch.Tensor:
+    """Contiguous Ward-style segments of every (batch, kv-head) key table, built on the GPU
+    (the index build before the path; the reference's build_buckets_gpu, pipeline.py:71-116,
+    pools keys and merges them by the Ward cost - here the merges join adjacent segments
+    only, so every bucket is a run of consecutive positions).
+
+    keys [B, T, Hkv, D] (fp32 / bf16 / fp16, read in place when rows are contiguous): pools
+    of ``pool`` positions, then the adjacent pair with the smallest Ward cost
+    n_a n_b / (n_a + n_b) |mu_a - mu_b|^2 merges (ties to the leftmost pair, merges past
+    ``max_size`` positions skipped) until ``target`` segments remain. Returns the segment
+    start positions [B, Hkv, target + 1] int64 (last = T). Raises ValueError when a table
+    cannot reach ``target`` under ``max_size``."""
+    device = _on_device("segment_starts", keys)
+    if keys.dim() != 4:
+        raise ValueError(f"keys must be [B, T, Hkv, D], got {tuple(keys.shape)}")
+    if keys.stride(-1) != 1 or keys.data_ptr() % 16:
+        keys = keys.contiguous()
+    B, T, Hkv, D = keys.shape
+    tables = B * Hkv
+    nbytes = _abi.load().lsa_ward_segments_scratch_bytes(tables, T, D, pool)
+    scratch = torch.empty(max(int(nbytes), 8), dtype=torch.uint8, device=device)
+    starts = torch.empty(tables, target + 1, dtype=torch.int32, device=device)
+    status = torch.empty(tables, dtype=torch.int32, device=device)
+    _abi.call("lsa_ward_segments", keys.data_ptr(), _abi.dtype_code(keys.dtype), B, T, Hkv, D, keys.stride(0),
+              keys.stride(1), keys.stride(2), pool, target, max_size, scratch.data_ptr(), scratch.numel(),
+              starts.data_ptr(), status.data_ptr(), _abi.stream(device))
+    bad = int(status.max().item())
+    if bad:
+        raise ValueError(f"segment_starts: a table cannot reach {target} segments with max_size {max_size}")
+    return starts.view(B, Hkv, target + 1).long()
+
+
+def segment_buckets(keys: torch.Tensor, target: int, pool: int = 16, max_size: int = 256, cap: int | None = None,
+                    centroid: str = "mean") -> Buckets:
+    """Bucket tables of contiguous Ward-style segments built on the GPU from the keys
+    (``segment_starts``): member rows ids start .. end - 1 (-1 padded to ``cap``, default
+    ``max_size``), span ends, and centroids from the member keys (``bucket_centroids``).
+    Tables are [Hkv, rows, ...] for B == 1, else [B, Hkv, rows, ...], as the selects take
+    them; ``spans`` is set, so the fused decode expands picks from the ends."""
+    cap = max_size if cap is None else cap
+    if cap < max_size:
+        raise ValueError(f"cap {cap} below max_size {max_size}: segments would not fit their rows")
+    st = segment_starts(keys, target, pool, max_size)
+    if keys.shape[0] == 1:
+        st = st[0]
+    begin, end = st[..., :-1], st[..., 1:]
+    sizes = (end - begin).to(torch.int32)
+    slot = torch.arange(cap, device=st.device, dtype=torch.int64)
+    members = torch.where(slot < sizes[..., None], begin[..., None] + slot, torch.full_like(slot, -1))
+    members = members.to(torch.int32).contiguous()
+    c32, c16 = bucket_centroids(keys, members, centroid)
+    return Buckets(c16, members, sizes.contiguous(), centroids_f32=c32, ends=end.to(torch.int32).contiguous(),
+                   spans=True)
+
+
 def position_buckets(index_keys: torch.Tensor, config: PortConfig, centroid: str = "normalized") -> Buckets:
     """Positional block-sparse buckets - runs of ``bucket_size`` consecutive keys (reference
     pipeline.py:378-403). index_keys [T, d] gives one table; [B, T, Hkv, D] one table per

@@ -25,6 +25,10 @@ Pinning (what each function is checked against in tests/test_oracle.py):
   sparse_read                    torch SDPA on full causal lists (textbook), duplicate ->
                                  V row, empty -> 0 / NaN
   tree_select_row                brute-force sort of every candidate on tiny trees
+  ward_pair_cost                 exact rational arithmetic (fractions) and math.fsum
+  ward_segments_keys             brute force (every adjacent cost recomputed from the
+                                 segments each step, no links), two-cluster closed form,
+                                 invariants (contiguous cover, target count, max_size)
   window/sink tail order         PARITY UNPINNED (upstream _append_window_and_sink is not
                                  available); the tail SET is pinned by causality and the
                                  read output is order-invariant.
@@ -302,6 +306,96 @@ def position_members(blocks: int, cluster_block_size: int, bucket_size: int, buc
     members = np.full((rows, bucket_cap), -1, dtype=np.int32)
     members[:, :bucket_size] = np.arange(rows * bucket_size, dtype=np.int32).reshape(rows, bucket_size)
     return members
+
+
+WARD_LANES = 64  # partials of a segment-pair cost (one per lane of a 64-wide wave)
+
+
+def ward_pool_sums(keys: np.ndarray, pool: int) -> tuple[np.ndarray, np.ndarray]:
+    """Pools of ``pool`` consecutive positions (the last one shorter): fp64 key sums, the
+    positions of a pool added in order, and the pool sizes. keys [T, D] -> ([P, D], [P]).
+
+    The first step of the contiguous bucket build (the index build the reference runs as
+    build_buckets_gpu, pipeline.py:71-116, which also pools keys before merging, :91-93)."""
+    keys = np.asarray(keys, dtype=np.float32)
+    T, D = keys.shape
+    npool = -(-T // pool)
+    sums = np.zeros((npool, D), dtype=np.float64)
+    sizes = np.array([min(pool, T - i * pool) for i in range(npool)], dtype=np.int64)
+    for j in range(pool):
+        rows = np.arange(npool) * pool + j
+        ok = rows < T
+        sums[ok] = sums[ok] + keys[rows[ok]].astype(np.float64)
+    return sums, sizes
+
+
+def ward_pair_cost(sa: np.ndarray, sb: np.ndarray, na: int, nb: int, max_size: int) -> float:
+    """Ward cost of merging adjacent segments with key sums ``sa``/``sb`` and sizes
+    ``na``/``nb``: n_a n_b / (n_a + n_b) * |sa / n_a - sb / n_b|^2 (the merge criterion
+    the reference's bucket build uses, pipeline.py:95-96), +inf past ``max_size``.
+
+    Canonical fp64 order, no fused multiply-add: squared differences fold into 64
+    partials (partial l = sum_k sq[l + 64 k], k ascending), then halve 32, 16, .., 1."""
+    if na + nb > max_size:
+        return float("inf")
+    fa, fb = float(na), float(nb)
+    diff = np.asarray(sa, dtype=np.float64) / fa - np.asarray(sb, dtype=np.float64) / fb
+    sq = diff * diff
+    part = np.zeros(WARD_LANES, dtype=np.float64)
+    for k in range(0, sq.shape[0], WARD_LANES):
+        chunk = sq[k:k + WARD_LANES]
+        part[:chunk.shape[0]] = part[:chunk.shape[0]] + chunk
+    h = WARD_LANES // 2
+    while h >= 1:
+        part[:h] = part[:h] + part[h:2 * h]
+        h //= 2
+    w = (fa * fb) / (fa + fb)
+    return float(w * part[0])
+
+
+def ward_segments_keys(keys: np.ndarray, pool: int, target: int, max_size: int) -> np.ndarray:
+    """Contiguous Ward-style buckets from the keys of one table: pools of ``pool``
+    positions, then the adjacent pair with the smallest ``ward_pair_cost`` merged (ties to
+    the leftmost pair; pairs past ``max_size`` never merge) until ``target`` segments
+    remain. keys [T, D] -> segment start positions [target + 1] (last = T).
+
+    Raises ValueError when no pair can merge before ``target`` is reached."""
+    sums, sizes = ward_pool_sums(keys, pool)
+    npool = sums.shape[0]
+    if target > npool:
+        raise ValueError(f"target {target} exceeds the {npool} pools")
+    size = sizes.copy()
+    nxt = np.arange(1, npool + 1)
+    nxt[-1] = -1
+    prv = np.arange(-1, npool - 1)
+    cost = np.full(npool, np.inf)
+    for i in range(npool - 1):
+        cost[i] = ward_pair_cost(sums[i], sums[i + 1], int(size[i]), int(size[i + 1]), max_size)
+    alive = npool
+    while alive > target:
+        i = int(np.argmin(cost))  # first minimum: the leftmost pair
+        if not cost[i] < np.inf:
+            raise ValueError(f"no pair merges under max_size {max_size} with {alive} segments left")
+        j = int(nxt[i])
+        sums[i] = sums[i] + sums[j]
+        size[i] += size[j]
+        nxt[i] = nxt[j]
+        if nxt[j] >= 0:
+            prv[nxt[j]] = i
+        cost[j] = np.inf
+        if prv[i] >= 0:
+            a = int(prv[i])
+            cost[a] = ward_pair_cost(sums[a], sums[i], int(size[a]), int(size[i]), max_size)
+        cost[i] = (ward_pair_cost(sums[i], sums[nxt[i]], int(size[i]), int(size[nxt[i]]), max_size)
+                   if nxt[i] >= 0 else np.inf)
+        alive -= 1
+    starts = np.empty(target + 1, dtype=np.int64)
+    p = 0
+    for r in range(target):
+        starts[r] = p * pool
+        p = int(nxt[p])
+    starts[target] = keys.shape[0]
+    return starts
 
 
 # --------------------------------------------------------------------------- selection

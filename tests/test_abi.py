@@ -136,6 +136,32 @@ def test_chunked_read_paths():
         _abi.call("lsa_read_chunked", *base, 7, 16, None)
 
 
+def test_segment_build_arguments_rejected_before_launch():
+    lib = _abi.load()
+    assert lib.lsa_ward_segments_scratch_bytes(8, 32768, 128, 16) == 8 * 2048 * 128 * 8
+    assert lib.lsa_ward_segments_scratch_bytes(1, 100, 64, 16) == 7 * 64 * 8  # a shorter last pool
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below fails its checks first
+
+    def call(**kw):
+        a = dict(B=1, T=32768, H=8, D=128, pool=16, target=512, max_size=256, scratch_bytes=1 << 30)
+        a.update(kw)
+        _abi.call("lsa_ward_segments", p, _abi.LSA_BF16, a["B"], a["T"], a["H"], a["D"], a["T"] * a["H"] * a["D"],
+                  a["H"] * a["D"], a["D"], a["pool"], a["target"], a["max_size"], p, a["scratch_bytes"], p, p, None)
+
+    with pytest.raises(ValueError, match="NULL"):
+        _abi.call("lsa_ward_segments", None, _abi.LSA_BF16, 1, 64, 1, 64, 0, 64, 0, 16, 2, 64, p, 1 << 20, p, p, None)
+    with pytest.raises(ValueError, match="pools exceed"):
+        call(pool=4)  # 8192 pools
+    with pytest.raises(ValueError, match="target"):
+        call(T=1024, target=65)
+    with pytest.raises(ValueError, match="max_size"):
+        call(max_size=8)
+    with pytest.raises(ValueError, match="scratch"):
+        call(scratch_bytes=1024)
+    with pytest.raises(ValueError, match="dtype"):
+        _abi.call("lsa_ward_segments", p, 9, 1, 64, 1, 64, 0, 64, 0, 16, 2, 64, p, 1 << 20, p, p, None)
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_abi, "_lib", None)
     monkeypatch.setattr(_abi, "LIB_PATH", tmp_path / "absent.so")

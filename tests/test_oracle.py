@@ -273,3 +273,68 @@ def test_tree_select_row_equals_brute_force():
     want = sorted(cand, key=lambda c: (-bs[c], c))[:5]
     assert picks.tolist() == want
     assert lst[:n].tolist() == [int(m) for b in want for m in members[b]]
+
+
+# --------------------------------------------------------------------------- segment build
+
+
+def test_ward_pair_cost_exact_rationals_and_fsum():
+    """The canonical-order fp64 cost agrees with the exact rational value on dyadic sums
+    (every operation exact), and with an fsum of exact squares to 1e-14 on random sums."""
+    rng = np.random.default_rng(3)
+    sa = rng.integers(-64, 64, 128).astype(np.float64)
+    sb = rng.integers(-64, 64, 128).astype(np.float64)
+    na, nb = 4, 8  # power-of-two sizes: the means are exact
+    got = oracle.ward_pair_cost(sa, sb, na, nb, 64)
+    want = Fraction(na * nb, na + nb) * sum((Fraction(int(a), na) - Fraction(int(b), nb)) ** 2 for a, b in zip(sa, sb))
+    assert got == float(want)
+    import math
+    sa, sb = rng.standard_normal(96) * 10, rng.standard_normal(96) * 10
+    got = oracle.ward_pair_cost(sa, sb, 17, 23, 64)
+    want = 17 * 23 / 40 * math.fsum((a / 17 - b / 23) ** 2 for a, b in zip(sa, sb))
+    assert abs(got - want) <= 1e-14 * want
+    assert oracle.ward_pair_cost(sa, sb, 40, 30, 64) == float("inf")
+    assert oracle.ward_pair_cost(sa, sa, 5, 5, 64) == 0.0
+
+
+def _ward_brute(keys, pool, target, max_size):
+    """Greedy adjacent merge with no links: every step recomputes every adjacent cost from
+    the current segment list and merges the first minimum."""
+    sums, sizes = oracle.ward_pool_sums(keys, pool)
+    segs = [(i * pool, int(sizes[i]), sums[i].copy()) for i in range(len(sizes))]
+    while len(segs) > target:
+        costs = [oracle.ward_pair_cost(segs[k][2], segs[k + 1][2], segs[k][1], segs[k + 1][1], max_size)
+                 for k in range(len(segs) - 1)]
+        k = int(np.argmin(costs))
+        assert costs[k] < np.inf
+        a, b = segs[k], segs[k + 1]
+        segs[k:k + 2] = [(a[0], a[1] + b[1], a[2] + b[2])]
+    return np.array([s[0] for s in segs] + [keys.shape[0]])
+
+
+@pytest.mark.parametrize("T,D,pool,target,max_size", [(200, 8, 8, 6, 64), (333, 16, 4, 20, 48), (512, 64, 16, 5, 512)])
+def test_ward_segments_equal_brute_force(T, D, pool, target, max_size):
+    rng = np.random.default_rng(T + D)
+    centers = rng.standard_normal((6, D)).astype(np.float32)
+    labels = np.repeat(rng.integers(0, 6, T // 10 + 1), 10)[:T]
+    keys = centers[labels] + 0.3 * rng.standard_normal((T, D)).astype(np.float32)
+    got = oracle.ward_segments_keys(keys, pool, target, max_size)
+    assert np.array_equal(got, _ward_brute(keys, pool, target, max_size))
+    sizes = np.diff(got)
+    assert got[0] == 0 and got[-1] == T and len(got) == target + 1
+    assert (sizes > 0).all() and (sizes <= max(max_size, pool)).all()
+    assert (got[:-1] % pool == 0).all()
+
+
+def test_ward_segments_two_clusters_split_at_the_boundary():
+    """Two well-separated halves merge into exactly the two halves; ties (identical keys)
+    merge leftmost first."""
+    rng = np.random.default_rng(5)
+    keys = np.concatenate([np.full((1024, 32), 3.0), np.full((1024, 32), -3.0)]).astype(np.float32)
+    keys += 0.01 * rng.standard_normal(keys.shape).astype(np.float32)
+    assert oracle.ward_segments_keys(keys, 16, 2, 4096).tolist() == [0, 1024, 2048]
+    same = np.ones((64, 8), dtype=np.float32)
+    # every cost ties at 0: the leftmost pair merges each step, so the first segment grows
+    assert oracle.ward_segments_keys(same, 8, 3, 64).tolist() == [0, 48, 56, 64]
+    with pytest.raises(ValueError, match="max_size"):
+        oracle.ward_segments_keys(same, 8, 3, 8)
