@@ -591,6 +591,82 @@ def segment_buckets(keys: torch.Tensor, target: int, pool: int = 16, max_size: i
                    spans=True)
 
 
+def build_buckets(keys: torch.Tensor, config: PortConfig, pool: int | None = None, max_size: int | None = None,
+                  centroid: str = "normalized", spans: bool = False, first_block: int = 0) -> Buckets:
+    """Bucket tables of the closed cluster blocks, built on the GPU (reference
+    build_buckets_gpu, pipeline.py:71-116: every closed block of ``cluster_block_size``
+    keys pooled by ``pool_size`` and merged by the Ward cost into ``block_bucket_count``
+    buckets of at most ``bucket_cap`` keys, rows block after block, centroids the
+    normalized member-key sum). The merges here join adjacent segments only
+    (``segment_starts`` per block), so every bucket is a run of consecutive positions.
+
+    keys [T, d] (one index-space table) or [B, T, Hkv, D] (per-kv-head tables: [Hkv, rows,
+    ...] for B == 1, else [B, Hkv, rows, ...]). Blocks ``first_block`` .. T // block - 1 are
+    built (``extend_buckets`` appends newly closed blocks). ``spans``: also set the span
+    ends (span tables: the decode expands picks from the ends, and a bucket is visible once
+    its span has ended); without them the reference's rule applies - a query sees the
+    buckets of the closed blocks before its own."""
+    device = _on_device("build_buckets", keys)
+    block, bpb, cap = config.cluster_block_size, config.block_bucket_count, config.bucket_cap
+    pool = config.pool_size if pool is None else pool
+    max_size = cap if max_size is None else max_size
+    if max_size > cap:
+        raise ValueError(f"max_size {max_size} exceeds the bucket cap {cap}")
+    flat = keys.dim() == 2
+    k4 = keys.view(1, keys.shape[0], 1, keys.shape[1]) if flat else keys
+    if k4.stride(-1) != 1 or k4.data_ptr() % 16:
+        k4 = k4.contiguous()
+    B, T, Hkv, D = k4.shape
+    blocks = T // block - first_block
+    if blocks <= 0:
+        raise ValueError(f"no closed block past block {first_block} in {T} keys (block {block})")
+    per_b = []
+    for b in range(B):
+        # the closed blocks as a batch of tables: batch stride = one block of positions
+        st = k4.stride(1)
+        view = torch.as_strided(k4, (blocks, block, Hkv, D), (block * st, st, k4.stride(2), 1),
+                                k4.storage_offset() + b * k4.stride(0) + first_block * block * st)
+        starts = segment_starts(view, bpb, pool, max_size)  # [blocks, Hkv, bpb + 1], block-local
+        base = (first_block + torch.arange(blocks, device=device, dtype=torch.int64)) * block
+        starts = starts + base[:, None, None]
+        begin = starts[..., :-1].permute(1, 0, 2).reshape(Hkv, blocks * bpb)
+        end = starts[..., 1:].permute(1, 0, 2).reshape(Hkv, blocks * bpb)
+        per_b.append((begin, end))
+    begin = torch.stack([x[0] for x in per_b])  # [B, Hkv, rows]
+    end = torch.stack([x[1] for x in per_b])
+    sizes = (end - begin).to(torch.int32)
+    slot = torch.arange(cap, device=device, dtype=torch.int64)
+    members = torch.where(slot < sizes[..., None], begin[..., None] + slot, torch.full_like(slot, -1)).to(torch.int32)
+    end = end.to(torch.int32)
+    if flat:  # one table: [rows, ...]
+        members, sizes, end = members[0, 0], sizes[0, 0], end[0, 0]
+    elif B == 1:  # per-kv-head tables of one sequence: [Hkv, rows, ...]
+        members, sizes, end = members[0], sizes[0], end[0]
+    members = members.contiguous()
+    c32, c16 = bucket_centroids(keys if flat else k4, members, centroid)
+    return Buckets(c16, members, sizes.contiguous(), centroids_f32=c32, ends=end.contiguous() if spans else None,
+                   spans=spans)
+
+
+def extend_buckets(buckets: Buckets, keys: torch.Tensor, config: PortConfig, **build_kw) -> Buckets:
+    """The tables with the blocks closed since they were built appended (a decode cache
+    grows one token a step; a block's buckets are built once, when it closes): the rows of
+    blocks rows // block_bucket_count .. T // cluster_block_size - 1, built as
+    ``build_buckets`` builds them, concatenated after the existing rows."""
+    bpb = config.block_bucket_count
+    have = buckets.rows // bpb
+    T = keys.shape[0] if keys.dim() == 2 else keys.shape[1]
+    if T // config.cluster_block_size <= have:
+        return buckets
+    spans = buckets.ends is not None
+    new = build_buckets(keys, config, first_block=have, spans=spans, **build_kw)
+    return Buckets(torch.cat([buckets.centroids, new.centroids], dim=-2),
+                   torch.cat([buckets.members, new.members], dim=-2),
+                   torch.cat([buckets.sizes, new.sizes], dim=-1),
+                   centroids_f32=torch.cat([buckets.centroids_f32, new.centroids_f32], dim=-2),
+                   ends=torch.cat([buckets.ends, new.ends], dim=-1) if spans else None, spans=spans)
+
+
 def position_buckets(index_keys: torch.Tensor, config: PortConfig, centroid: str = "normalized") -> Buckets:
     """Positional block-sparse buckets - runs of ``bucket_size`` consecutive keys (reference
     pipeline.py:378-403). index_keys [T, d] gives one table; [B, T, Hkv, D] one table per

@@ -6,7 +6,10 @@ costs). Cases: fp32 / bf16 / fp16 keys, head dims 32 / 64 / 128, pool sizes 4 / 
 shorter last pool, several (batch, kv-head) tables with strided cache views, the 32k
 table of the benchmark geometry, ties (identical keys merge leftmost first), a target no
 merge can reach under max_size (ValueError), and the tables feeding the fused decode
-(lists equal the oracle's flat select over the same tables).
+(lists equal the oracle's flat select over the same tables). The block-structured build
+(the reference's closed cluster blocks, 64 buckets of at most 16 keys a 512-key block)
+matches the oracle per block and drives the flat select; a cache extended block by block
+as it grows equals one built once.
 """
 
 import numpy as np
@@ -89,3 +92,62 @@ def test_built_tables_drive_the_fused_decode():
         assert np.abs(buckets.centroids_f32[g].cpu().numpy() - want).max() <= 1e-5
     pos = torch.tensor([T - 1], dtype=torch.int32)
     check_decode(data.q[:, -1:], data.k, data.v, pos, buckets, workloads.FLAT_32K, label="built tables")
+
+
+def oracle_block_tables(keys_2d, config, pool, max_size):
+    """Per closed block: the oracle's segments, made absolute, rows block after block."""
+    block, bpb = config.cluster_block_size, config.block_bucket_count
+    starts = []
+    for blk in range(keys_2d.shape[0] // block):
+        st = oracle.ward_segments_keys(keys_2d[blk * block:(blk + 1) * block], pool, bpb, max_size)
+        starts.append(st[:-1] + blk * block)
+        last = st[-1] + blk * block
+    begin = np.concatenate(starts)
+    end = np.concatenate([begin[1:], [last]])
+    members = np.full((begin.shape[0], config.bucket_cap), -1, dtype=np.int32)
+    for r, (a, b) in enumerate(zip(begin, end)):
+        members[r, :b - a] = np.arange(a, b)
+    return members, end
+
+
+def test_build_buckets_reference_blocks_and_select():
+    """The reference's block structure (512-key blocks, 64 buckets of at most 16 keys from
+    pools of 4, normalized-sum centroids) on one index-space table: members equal the
+    oracle's per-block segments, centroids the oracle's, and the flat select over the
+    tables (closed blocks before the query's own visible) equals the oracle's."""
+    config = pipeline.PortConfig(top_p=16, top_k=256, window_size=64, sink_size=4)
+    T, d = 2048 + 100, 64
+    keys = clustered_keys(1, T, 1, d, torch.float32, seed=31)[0, :, 0]
+    buckets = pipeline.build_buckets(keys.to(DEV), config)
+    want_members, _ = oracle_block_tables(keys.numpy(), config, config.pool_size, config.bucket_cap)
+    assert buckets.ends is None and not buckets.spans
+    assert np.array_equal(buckets.members.cpu().numpy(), want_members)
+    cent = oracle.bucket_centroids(keys.numpy(), want_members, "normalized")
+    assert np.abs(buckets.centroids_f32.cpu().numpy() - cent).max() <= 1e-6
+    q = torch.randn(5, d, generator=torch.Generator().manual_seed(2))
+    pos = torch.tensor([600, 1100, 1535, 1536, T - 1], dtype=torch.int32)
+    lists, lengths = pipeline.flat_select(q.to(DEV), pos.to(DEV), buckets, config)
+    wl, wn = oracle.flat_select(q.numpy(), pos.numpy(), buckets.centroids.float().cpu().numpy(), want_members,
+                                cluster_block_size=config.cluster_block_size, block_buckets=config.block_bucket_count,
+                                top_p=config.top_p, top_k=config.top_k, window=config.window_size,
+                                sink=config.sink_size, mode="bf16")
+    assert np.array_equal(lengths.cpu().numpy(), wn) and np.array_equal(lists.cpu().numpy(), wl)
+
+
+def test_extend_buckets_equals_a_full_build():
+    """A cache built at 3 closed blocks and extended as it grows to 5 (one block at a time,
+    and with no new block) equals the tables built once at 5 blocks, field for field."""
+    config = pipeline.PortConfig(cluster_block_size=256, bucket_size=16, bucket_cap=32, pool_size=8)
+    keys = clustered_keys(1, 5 * 256 + 40, 2, 64, torch.bfloat16, seed=41).to(DEV)
+    for spans in (False, True):
+        grown = pipeline.build_buckets(keys[:, :3 * 256 + 10], config, spans=spans)
+        for T in (3 * 256 + 200, 4 * 256, 5 * 256 + 40):
+            grown = pipeline.extend_buckets(grown, keys[:, :T], config)
+        full = pipeline.build_buckets(keys, config, spans=spans)
+        for f in ("centroids", "members", "sizes", "centroids_f32", "ends"):
+            a, b = getattr(grown, f), getattr(full, f)
+            assert (a is None and b is None) or torch.equal(a, b), f
+        assert grown.spans == spans
+    members, end = oracle_block_tables(keys[0, :, 1].float().cpu().numpy(), config, 8, 32)
+    assert np.array_equal(full.members[1].cpu().numpy(), members)
+    assert np.array_equal(full.ends[1].cpu().numpy(), end)
