@@ -2,6 +2,7 @@
 reference's error types, and no CPU fallback anywhere on the path."""
 
 import os
+import pathlib
 
 import pytest
 import torch
@@ -82,3 +83,22 @@ def test_config_defaults_match_the_reference():
             c.sink_size, c.node_bucket_size, c.top_level, c.node_cluster_block_size, c.beam_width,
             c.start_nodes) == (512, 4, 8, 16, 1024, 4096, 512, 4, 4, 3, 64, 64, None)
     assert c.block_bucket_count == 64
+
+
+def test_bucket_build_rejects_cpu_tensors():
+    """The bucket build is a GPU kernel too: host tensors raise, nothing falls back."""
+    keys = torch.zeros(1, 1024, 2, 64)
+    with pytest.raises(ValueError, match="ROCm kernel"):
+        pipeline.segment_starts(keys, 8)
+    with pytest.raises(ValueError, match="ROCm kernel"):
+        pipeline.build_buckets(keys[0, :, 0], pipeline.PortConfig())
+
+
+def test_bench_refuses_more_than_one_gpu():
+    import subprocess
+    import sys
+
+    root = pathlib.Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode != 0 and "one GPU" in r.stdout + r.stderr
