@@ -95,10 +95,13 @@ int lsa_expand(const void* picks, int picks_are_keys, int64_t R, int32_t G, int3
  * N columns of a (row, group) are split over `splits` workgroups whose sorted partial
  * top-k lists the last one to arrive merges (splits == 1: counters and scratch unused).
  * counters: R * G int32 that read zero at launch; every launch leaves them zero again.
- * scratch: lsa_select_flat_scratch_bytes(), no initialisation. Out as lsa_expand. */
+ * scratch: lsa_select_flat_scratch_bytes(), no initialisation. table_flags: 0 or
+ * LSA_TABLE_SPANS (span tables: the expansion takes each pick's kept ids from the span ends,
+ * with no member-row loads; the lists are the ones the member rows give). Out as lsa_expand. */
 size_t lsa_select_flat_scratch_bytes(int64_t R, int32_t G, int32_t top_p, int32_t N, int32_t splits);
 int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D, const void* centroids,
-                    const int32_t* members, const int32_t* ends, int32_t rows, int32_t cap, int64_t row_tables,
+                    const int32_t* members, const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap,
+                    int64_t row_tables,
                     int64_t group_tables, int score_mode, const int32_t* positions, int32_t cluster_block_size,
                     int32_t block_buckets, int32_t top_p, int32_t window, int32_t sink, int32_t top_k,
                     int32_t splits, int32_t* counters, void* scratch, size_t scratch_bytes, int32_t* lists,

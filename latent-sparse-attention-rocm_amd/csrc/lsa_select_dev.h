@@ -309,6 +309,47 @@ __device__ __forceinline__ int32_t tail_id(int64_t i, int64_t window_start, int6
   return i < n_win ? (int32_t)(window_start + i) : (i < n_win + n_sink ? (int32_t)(i - n_win) : -1);
 }
 
+// Rank-order expansion of one row over span tables (bucket row b holds exactly the ids
+// ends[b - 1] .. ends[b] - 1, ends[-1] = 0, in order): pick b keeps the consecutive ids
+// [max(begin_b, sink), min(ends[b], window_start)), so the kept list is a concatenation of
+// ranges, stored in rank order until top_k, then the window and sink tail, then -1 to
+// `width`. The same list expand_walk builds from the member rows, with no member loads.
+// n_picks <= 64; lds: 129 ints. Every thread of the block calls it; returns the length.
+__device__ __forceinline__ int expand_spans(const int32_t* picks, int n_picks, const int32_t* ends, int rows,
+                                            int64_t position, int window, int sink, int top_k, int32_t* out,
+                                            int width, int* lds) {
+  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
+  const int64_t ws = position + 1 - window;
+  const int64_t window_start = ws > 0 ? ws : 0;
+  if (w == 0) {
+    int lo = 0, c = 0;
+    const int b = lane < n_picks ? picks[lane] : -1;
+    if (b >= 0 && b < rows) {
+      const int64_t begin = b > 0 ? ends[b - 1] : 0, end = ends[b];
+      const int64_t l = begin > sink ? begin : sink, h = end < window_start ? end : window_start;
+      lo = (int)l;
+      c = h > l ? (int)(h - l) : 0;
+    }
+    const int incl = wave_inclusive_sum(c);
+    lds[lane] = lo;
+    lds[LSA_WAVE + lane] = incl - c;  // first slot of pick `lane`
+    if (lane == LSA_WAVE - 1) lds[2 * LSA_WAVE] = incl;
+  }
+  __syncthreads();
+  const int total = lds[2 * LSA_WAVE];
+  const int kept = total < top_k ? total : top_k;
+  for (int j = w; j < n_picks; j += LSA_WAVES) {  // wave w stores picks w, w + 4, ...
+    const int lo = lds[j], p0 = lds[LSA_WAVE + j];
+    const int p1 = j + 1 < LSA_WAVE ? lds[LSA_WAVE + j + 1] : total;
+    const int e = p1 < kept ? p1 : kept;
+    for (int x = p0 + lane; x < e; x += LSA_WAVE) out[x] = lo + (x - p0);
+  }
+  const int64_t n_win = position + 1 - window_start > 0 ? position + 1 - window_start : 0;
+  const int64_t n_sink = sink < window_start ? sink : window_start;
+  for (int x = kept + tid; x < width; x += LSA_BLOCK) out[x] = tail_id(x - kept, window_start, n_win, n_sink);
+  return kept + (int)n_win + (int)n_sink;
+}
+
 // Rank-order expansion of one row (reference select_fused.py:172-214): picks in rank
 // order, member slots in table order, keep ids with sink <= id < window_start until
 // top_k are stored; then the window [window_start, position] and the sinks

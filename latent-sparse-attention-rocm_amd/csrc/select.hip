@@ -145,6 +145,7 @@ struct FlatArgs {
   int window, sink, top_k;
   int S, cs;          // splits and columns per split
   int stage;          // 1: the list row is assembled in LDS after keys and picks
+  int spans;          // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0)
   uint64_t* ws_keys;  // [R*G, rows] every column's key (S > 1)
   int* ws_count;      // [R*G] arrival counters (S > 1)
   int32_t* lists;
@@ -210,10 +211,17 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_flat_kernel(const QT* q, boo
   for (int j = threadIdx.x; j < a.K; j += LSA_BLOCK) pk[j] = key_column(u_to_key(best[j]));
   __syncthreads();
   const int width = a.top_k + a.window + a.sink;
-  const int32_t* tab = a.members + t * a.rows * (int64_t)a.cap;
-  int32_t* stage = a.stage ? (int32_t*)(smem + ((a.rows + a.kp + 1) & ~1)) : nullptr;  // 16-byte aligned
-  const int len = expand_walk(pk, a.K, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k,
-                              a.lists + i * width, width, scan, stage);
+  int len;
+  if (a.spans) {  // span tables: kept ids from the picks' span ends, no member rows
+    __shared__ int span_lds[2 * LSA_WAVE + 1];
+    len = expand_spans(pk, a.K, ends, a.rows, position, a.window, a.sink, a.top_k, a.lists + i * width, width,
+                       span_lds);
+  } else {
+    const int32_t* tab = a.members + t * a.rows * (int64_t)a.cap;
+    int32_t* stage = a.stage ? (int32_t*)(smem + ((a.rows + a.kp + 1) & ~1)) : nullptr;  // 16-byte aligned
+    len = expand_walk(pk, a.K, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k, a.lists + i * width, width,
+                      scan, stage);
+  }
   if (threadIdx.x == 0) a.lengths[i] = len;
 }
 
@@ -589,7 +597,8 @@ extern "C" size_t lsa_select_flat_scratch_bytes(int64_t R, int32_t G, int32_t to
 }
 
 extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D,
-                               const void* centroids, const int32_t* members, const int32_t* ends, int32_t rows,
+                               const void* centroids, const int32_t* members, const int32_t* ends,
+                               int32_t table_flags, int32_t rows,
                                int32_t cap, int64_t row_tables, int64_t group_tables, int score_mode,
                                const int32_t* positions, int32_t cluster_block_size, int32_t block_buckets,
                                int32_t top_p, int32_t window, int32_t sink, int32_t top_k, int32_t splits,
@@ -607,6 +616,10 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
   LSA_REQUIRE(top_p >= 1 && window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE,
               "lsa_select_flat: top_p >= 1, window/sink/top_k >= 0");
   LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "lsa_select_flat: cluster_block_size must be >= 1");
+  LSA_REQUIRE((table_flags & ~LSA_TABLE_SPANS) == 0, LSA_ERR_SHAPE, "lsa_select_flat: unknown table flags %d",
+              table_flags);
+  LSA_REQUIRE(!(table_flags & LSA_TABLE_SPANS) || ends, LSA_ERR_SHAPE,
+              "lsa_select_flat: LSA_TABLE_SPANS needs the span ends");
   LSA_REQUIRE(splits >= 1 && splits <= 256 && splits <= rows, LSA_ERR_SHAPE,
               "lsa_select_flat: splits in [1, min(256, rows)], got %d", splits);
   const int K = flat_picks(top_p, rows);
@@ -627,11 +640,12 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
   a.ws_count = counters;
   a.ws_keys = need ? (uint64_t*)scratch : nullptr;
   a.lists = lists; a.lengths = lengths;
+  a.spans = (table_flags & LSA_TABLE_SPANS) ? 1 : 0;
   // the list row is staged in LDS when it fits beside the keys (coalesced row stores)
   const int width = top_k + window + sink;
   const size_t base_lds = sizeof(uint64_t) * (((size_t)rows + kp + 1) & ~(size_t)1);
   const size_t stage_lds = sizeof(int32_t) * ((size_t)width + 4);
-  a.stage = (width % 4 == 0 && ((uintptr_t)lists % 16) == 0 && base_lds + stage_lds <= kMaxDynLds) ? 1 : 0;
+  a.stage = (!a.spans && width % 4 == 0 && ((uintptr_t)lists % 16) == 0 && base_lds + stage_lds <= kMaxDynLds) ? 1 : 0;
   const size_t shmem = base_lds + (a.stage ? stage_lds : 0);
   const dim3 grid((unsigned)(R * G), (unsigned)splits);
   const bool bf16 = score_mode == LSA_SCORE_BF16;

@@ -309,7 +309,8 @@ def _fused_select(index_queries, positions, buckets, config, top_k, score_dtype)
     ws = _abi.Workspace.get(device, "select", nbytes)
     counters = _abi.Counters.get(device, layout.R * layout.G) if nbytes else None
     _abi.call("lsa_select_flat", q.data_ptr(), _abi.dtype_code(q.dtype), layout.R, layout.G, layout.D,
-              table.data_ptr(), members.data_ptr(), _abi.ptr(ends), layout.rows, members.shape[-1],
+              table.data_ptr(), members.data_ptr(), _abi.ptr(ends),
+              _abi.TABLE_SPANS if (buckets.spans and ends is not None) else 0, layout.rows, members.shape[-1],
               layout.row_tables, layout.group_tables, mode, pos.data_ptr(), config.cluster_block_size,
               config.block_bucket_count, config.top_p, config.window_size, config.sink_size, top_k, splits,
               _abi.ptr(counters), _abi.ptr(ws), nbytes, lists.data_ptr(), lengths.data_ptr(), _abi.stream(device))

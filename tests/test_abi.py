@@ -38,7 +38,7 @@ def test_null_pointers_rejected_before_launch():
         _abi.call("lsa_read", None, None, None, 1, 1, 1, 8, 8, 2, 64, 1024, 128, 64, None, None, 4, 0, 0.1, 0, 1, None,
                   None, 0, None, None)
     with pytest.raises(ValueError, match="NULL"):
-        _abi.call("lsa_select_flat", None, 1, 1, 8, 128, None, None, None, 512, 256, 0, 1, 0, None, 64, 1, 32, 0, 0,
+        _abi.call("lsa_select_flat", None, 1, 1, 8, 128, None, None, None, 0, 512, 256, 0, 1, 0, None, 64, 1, 32, 0, 0,
                   8192, 8, None, None, 0, None, None, None)
 
 
@@ -71,7 +71,7 @@ def test_workspace_required_for_split_reads():
 def test_select_limits_rejected():
     # 8192 columns in one split exceed the LDS key budget
     with pytest.raises(ValueError, match="exceed"):
-        _abi.call("lsa_select_flat", 16, 1, 1, 1, 128, 16, 16, None, 8192, 16, 0, 0, 0, 16, 512, 64, 32, 0, 0, 64, 1,
+        _abi.call("lsa_select_flat", 16, 1, 1, 1, 128, 16, 16, None, 0, 8192, 16, 0, 0, 0, 16, 512, 64, 32, 0, 0, 64, 1,
                   None, None, 0, 16, 16, None)
 
 

@@ -366,3 +366,28 @@ def test_fused_all_tied_scores_break_to_lower_bucket(rows_visible):
         assert np.array_equal(_np(got_l[:, g]), want_l) and np.array_equal(_np(got_n[:, g]), want_n)
         first = min(32, rows_visible - 1)  # a position sees the closed blocks before its own
         assert np.array_equal(want_l[0][: first * cap], np.arange(first * cap))
+
+
+@pytest.mark.parametrize("window,sink,top_k", [(0, 0, 8192), (100, 4, 8192), (300, 16, 700)])
+def test_fused_select_span_tables_match_member_rows(window, sink, top_k):
+    """Span tables (contiguous segments) expanded from their ends (no member-row loads)
+    give the lists the member rows give, and both equal the oracle's; the window and sink
+    clip picks at both ends, and top_k cuts a pick short."""
+    import dataclasses
+
+    T, Hq, Hkv, D = 8192, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=128, seed=17, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    assert buckets.spans
+    config = dataclasses.replace(workloads.FLAT_32K, window_size=window, sink_size=sink, top_k=top_k)
+    idx = pipeline.index_queries(data.q[:, -3:], Hkv)[0]  # [3, Hkv, D]
+    positions = torch.tensor([T - 1, 5000, 700], dtype=torch.int32, device=DEV)
+    got = _switched("fused", idx, positions, buckets, config)
+    ref = _switched("fused", idx, positions, dataclasses.replace(buckets, spans=False), config)
+    assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1])
+    for g in range(Hkv):
+        cent = buckets.centroids[g].float().cpu().numpy()
+        want_l, want_n = oracle.flat_select(_np(idx[:, g]), _np(positions), cent, _np(buckets.members[g]),
+                                            cluster_block_size=64, block_buckets=1, top_p=32, top_k=top_k,
+                                            window=window, sink=sink, mode="bf16", ends=_np(buckets.ends[g]))
+        assert np.array_equal(_np(got[0][:, g]), want_l) and np.array_equal(_np(got[1][:, g]), want_n)
