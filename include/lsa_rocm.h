@@ -96,8 +96,9 @@ int lsa_expand(const void* picks, int picks_are_keys, int64_t R, int32_t G, int3
  * top-k lists the last one to arrive merges (splits == 1: counters and scratch unused).
  * counters: R * G int32 that read zero at launch; every launch leaves them zero again.
  * scratch: lsa_select_flat_scratch_bytes(), no initialisation. table_flags: 0 or
- * LSA_TABLE_SPANS (span tables: the expansion takes each pick's kept ids from the span ends,
- * with no member-row loads; the lists are the ones the member rows give). Out as lsa_expand. */
+ * LSA_TABLE_SPANS (span tables: with at most 64 picks the expansion takes each pick's kept
+ * ids from the span ends, with no member-row loads; the lists are the ones the member rows
+ * give). Out as lsa_expand. */
 size_t lsa_select_flat_scratch_bytes(int64_t R, int32_t G, int32_t top_p, int32_t N, int32_t splits);
 int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D, const void* centroids,
                     const int32_t* members, const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap,
@@ -111,10 +112,10 @@ int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int32_t G, int3
  * _beam_pick_rows with one node level): the best `beam_width` of the n_nodes node
  * centroids, then the best top_p of their children plus the uncovered visible buckets
  * [covered, visible), then the flat expansion. node_centroids [tables, n_nodes, D],
- * children [tables, n_nodes, node_size] int32 bucket ids. */
+ * children [tables, n_nodes, node_size] int32 bucket ids. table_flags as lsa_select_flat. */
 int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D, const void* node_centroids,
                     const int32_t* children, int32_t n_nodes, int32_t node_size, const void* centroids,
-                    const int32_t* members, const int32_t* ends, int32_t rows, int32_t cap, int64_t row_tables,
+                    const int32_t* members, const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables,
                     int64_t group_tables, int score_mode, const int32_t* positions, int32_t cluster_block_size,
                     int32_t block_buckets, int32_t covered, int32_t beam_width, int32_t top_p, int32_t window,
                     int32_t sink, int32_t top_k, int32_t* lists, int32_t* lengths, void* stream);

@@ -243,6 +243,7 @@ struct TreeArgs {
   int covered, beam, top_p;
   int nodes_pow2, beam_pow2, cand_cap, cand_pow2, top_pow2;
   int window, sink, top_k;
+  int spans;  // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0)
   int32_t* lists;
   int32_t* lengths;
 };
@@ -306,9 +307,16 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
   for (int j = threadIdx.x; j < a.top_p; j += LSA_BLOCK) cand[j] = j < k ? key_column(u_to_key(best[j])) : -1;
   __syncthreads();
   const int width = a.top_k + a.window + a.sink;
-  const int32_t* tab = a.members + t * (int64_t)a.rows * a.cap;
-  const int len = expand_walk(cand, a.top_p, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k,
-                              a.lists + i * width, width, scan, nullptr);
+  int len;
+  if (a.spans) {  // span tables: kept ids from the picks' span ends, no member rows
+    __shared__ int span_lds[2 * LSA_WAVE + 1];
+    len = expand_spans(cand, a.top_p, a.ends + t * a.rows, a.rows, position, a.window, a.sink, a.top_k,
+                       a.lists + i * width, width, span_lds);
+  } else {
+    const int32_t* tab = a.members + t * (int64_t)a.rows * a.cap;
+    len = expand_walk(cand, a.top_p, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k, a.lists + i * width,
+                      width, scan, nullptr);
+  }
   if (threadIdx.x == 0) a.lengths[i] = len;
 }
 
@@ -640,7 +648,7 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
   a.ws_count = counters;
   a.ws_keys = need ? (uint64_t*)scratch : nullptr;
   a.lists = lists; a.lengths = lengths;
-  a.spans = (table_flags & LSA_TABLE_SPANS) ? 1 : 0;
+  a.spans = (table_flags & LSA_TABLE_SPANS) && K <= LSA_WAVE ? 1 : 0;  // more picks: the member rows
   // the list row is staged in LDS when it fits beside the keys (coalesced row stores)
   const int width = top_k + window + sink;
   const size_t base_lds = sizeof(uint64_t) * (((size_t)rows + kp + 1) & ~(size_t)1);
@@ -661,7 +669,7 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
 extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D,
                                const void* node_centroids, const int32_t* children, int32_t n_nodes,
                                int32_t node_size, const void* centroids, const int32_t* members, const int32_t* ends,
-                               int32_t rows, int32_t cap, int64_t row_tables, int64_t group_tables, int score_mode,
+                               int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables, int64_t group_tables, int score_mode,
                                const int32_t* positions, int32_t cluster_block_size, int32_t block_buckets,
                                int32_t covered, int32_t beam_width, int32_t top_p, int32_t window, int32_t sink,
                                int32_t top_k, int32_t* lists, int32_t* lengths, void* stream) {
@@ -679,6 +687,10 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
               "lsa_select_tree: n_nodes, node_size, beam_width, top_p >= 1");
   LSA_REQUIRE(window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE, "lsa_select_tree: window/sink/top_k >= 0");
   LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "lsa_select_tree: cluster_block_size must be >= 1");
+  LSA_REQUIRE((table_flags & ~LSA_TABLE_SPANS) == 0, LSA_ERR_SHAPE, "lsa_select_tree: unknown table flags %d",
+              table_flags);
+  LSA_REQUIRE(!(table_flags & LSA_TABLE_SPANS) || ends, LSA_ERR_SHAPE,
+              "lsa_select_tree: LSA_TABLE_SPANS needs the span ends");
   const int beam = beam_width < n_nodes ? beam_width : n_nodes;
   const int64_t max_fresh = rows - covered > 0 ? rows - covered : 0;
   const int64_t cand_cap = (int64_t)beam * node_size + max_fresh;
@@ -694,6 +706,7 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
   a.nodes_pow2 = next_pow2(n_nodes); a.beam_pow2 = next_pow2(beam); a.cand_cap = (int)cand_cap;
   a.cand_pow2 = next_pow2((int)(cand_cap > 0 ? cand_cap : 1)); a.top_pow2 = next_pow2(top_p);
   a.window = window; a.sink = sink; a.top_k = top_k; a.lists = lists; a.lengths = lengths;
+  a.spans = (table_flags & LSA_TABLE_SPANS) && top_p <= LSA_WAVE ? 1 : 0;  // else the member rows
   const int keys_slots = a.nodes_pow2 > a.cand_pow2 ? a.nodes_pow2 : a.cand_pow2;
   const int best_slots = a.beam_pow2 > a.top_pow2 ? a.beam_pow2 : a.top_pow2;
   const int cand_slots = a.cand_pow2 > top_p ? a.cand_pow2 : top_p;

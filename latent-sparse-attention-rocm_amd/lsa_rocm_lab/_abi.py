@@ -55,7 +55,7 @@ SIGNATURES = {
     "lsa_select_flat_scratch_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "lsa_select_flat": (_int, [_p, _int, _i64, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i64, _i64, _int, _p, _i32, _i32,
                                _i32, _i32, _i32, _i32, _i32, _p, _p, _sz, _p, _p, _p]),
-    "lsa_select_tree": (_int, [_p, _int, _i64, _i32, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i32, _i32, _i64, _i64,
+    "lsa_select_tree": (_int, [_p, _int, _i64, _i32, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i64, _i64,
                                _int, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
     "lsa_index_queries": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p]),
     "lsa_bucket_centroids": (_int, [_p, _int, _i64, _i64, _i64, _i32, _i32, _p, _i64, _i32, _i32, _int, _p, _p, _p]),

@@ -82,7 +82,8 @@ def tree_select_batched(
     lengths = torch.empty(layout.out_shape(), dtype=torch.int32, device=device)
     _abi.call("lsa_select_tree", q.data_ptr(), _abi.dtype_code(q.dtype), layout.R, layout.G, layout.D,
               ncent.data_ptr(), children.data_ptr(), n_nodes, node_size, bcent.data_ptr(), members.data_ptr(),
-              _abi.ptr(ends), layout.rows, members.shape[-1], layout.row_tables, layout.group_tables, mode,
+              _abi.ptr(ends), _abi.TABLE_SPANS if (buckets.spans and ends is not None) else 0, layout.rows,
+              members.shape[-1], layout.row_tables, layout.group_tables, mode,
               pos.data_ptr(), config.cluster_block_size, config.block_bucket_count, n_nodes * node_size,
               config.beam_width, config.top_p, config.window_size, config.sink_size, top_k, lists.data_ptr(),
               lengths.data_ptr(), _abi.stream(device))

@@ -184,6 +184,15 @@ def test_tree_decode_batched_reduced():
                     window=0, sink=0, mode=score_dtype)
                 assert np.array_equal(_np(lists[b, g]), l), (score_dtype, b, g)
                 assert int(lengths[b, g]) == n
+    # span tables expand from their ends: the member rows give the same lists, also with a
+    # window and sinks clipping the picks
+    import dataclasses
+
+    members_only = dataclasses.replace(buckets, spans=False)
+    for cfg in (config, dataclasses.replace(config, window_size=200, sink_size=4)):
+        a = pipeline.tree_select(idx, pos, buckets, tree, cfg)
+        b = pipeline.tree_select(idx, pos, members_only, tree, cfg)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
     # the read over per-(sequence, kv-head) lists
     out = pipeline.lsa_read(data.q[:, -1:], data.k, data.v, lists.unsqueeze(1), lengths.unsqueeze(1), D ** -0.5)
     want = oracle.sparse_read(_np(data.q[:, -1:]), _np(data.k), _np(data.v), _np(lists)[:, None],
