@@ -227,6 +227,8 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_flat_kernel(const QT* q, boo
 
 // ------------------------------------------------------------------ two-level tree select
 
+constexpr int kSeenBits = 8192;  // buckets a tree table may hold for the LDS dedup bitmap
+
 struct TreeArgs {
   int64_t R;
   int G;
@@ -282,7 +284,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
   const int n_kids = beam * a.node_size;
   const int n_cand = n_kids + n_fresh;
   const int32_t* kids = a.children + t * (int64_t)a.n_nodes * a.node_size;
-  for (int j = threadIdx.x; j < a.cand_pow2; j += LSA_BLOCK) {
+  auto candidate = [&](int j) -> int32_t {
     int32_t c = -1;
     if (j < n_kids) {
       const int node = key_column(u_to_key(best[j / a.node_size]));
@@ -290,13 +292,29 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
     } else if (j < n_cand) {
       c = a.covered + (j - n_kids);
     }
-    keys[j] = (c >= 0 && c < a.rows) ? (uint64_t)c + 1 : 0;  // id + 1, 0 = none
-  }
-  __syncthreads();
-  bitonic_sort_desc(keys, a.cand_pow2);  // equal ids adjacent: keep the first
-  for (int j = threadIdx.x; j < a.cand_pow2; j += LSA_BLOCK) {
-    const uint64_t v = keys[j];
-    cand[j] = (v != 0 && (j == 0 || keys[j - 1] != v)) ? (int32_t)(v - 1) : -1;
+    return (c >= 0 && c < a.rows) ? c : -1;
+  };
+  // every candidate bucket once (the order does not matter: a key carries its column)
+  if (a.rows <= kSeenBits) {  // an LDS bitmap over bucket ids: the first lane to set a bit keeps it
+    __shared__ uint32_t seen[kSeenBits / 32];
+    for (int x = threadIdx.x; x < (a.rows + 31) / 32; x += LSA_BLOCK) seen[x] = 0;
+    __syncthreads();
+    for (int j = threadIdx.x; j < a.cand_pow2; j += LSA_BLOCK) {
+      const int32_t c = candidate(j);
+      const uint32_t bit = 1u << (c & 31);
+      cand[j] = (c >= 0 && !(atomicOr(&seen[c >> 5], bit) & bit)) ? c : -1;
+    }
+  } else {  // sort the ids: equal ids adjacent, keep the first
+    for (int j = threadIdx.x; j < a.cand_pow2; j += LSA_BLOCK) {
+      const int32_t c = candidate(j);
+      keys[j] = c >= 0 ? (uint64_t)c + 1 : 0;  // id + 1, 0 = none
+    }
+    __syncthreads();
+    bitonic_sort_desc(keys, a.cand_pow2);
+    for (int j = threadIdx.x; j < a.cand_pow2; j += LSA_BLOCK) {
+      const uint64_t v = keys[j];
+      cand[j] = (v != 0 && (j == 0 || keys[j - 1] != v)) ? (int32_t)(v - 1) : -1;
+    }
   }
   __syncthreads();
   const CT* bcent = (const CT*)a.centroids + t * (int64_t)a.rows * D;

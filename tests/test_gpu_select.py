@@ -391,3 +391,40 @@ def test_fused_select_span_tables_match_member_rows(window, sink, top_k):
                                             cluster_block_size=64, block_buckets=1, top_p=32, top_k=top_k,
                                             window=window, sink=sink, mode="bf16", ends=_np(buckets.ends[g]))
         assert np.array_equal(_np(got[0][:, g]), want_l) and np.array_equal(_np(got[1][:, g]), want_n)
+
+
+@pytest.mark.parametrize("spans", [True, False])
+def test_tree_select_fresh_buckets_and_shared_children(spans):
+    """Nodes covering only the first 48 of 64 buckets (the rest join as fresh candidates
+    once visible) and two nodes sharing children (each bucket must be a candidate once):
+    lists equal the oracle's two-level beam, with span tables expanded from their ends or
+    the member rows walked."""
+    import dataclasses
+
+    from lsa_rocm_lab.port.pipeline import Hierarchy, NodeLevel
+
+    T, Hq, Hkv, D = 4096, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=32, seed=23, device=DEV)
+    buckets = dataclasses.replace(workloads.cluster_buckets(data, target=64), spans=spans)
+    children = torch.arange(48, dtype=torch.int32).view(3, 16).clone()
+    children[2, :8] = children[1, :8]  # node 2 shares half its children with node 1
+    children = children.expand(Hkv, 3, 16).contiguous().to(DEV)
+    ncent = buckets.centroids_f32[:, children[0].long()].mean(dim=2).contiguous()  # [Hkv, 3, D]
+    tree = Hierarchy(levels=[NodeLevel(ncent, children, centroids_bf16=ncent.to(torch.bfloat16))])
+    config = dataclasses.replace(workloads.TREE_131K, beam_width=2, top_p=24, window_size=64, sink_size=4)
+    idx = pipeline.index_queries(data.q[:, -2:], Hkv)[0]  # [2, Hkv, D]
+    pos = torch.tensor([T - 1, 2500], dtype=torch.int32, device=DEV)
+    for score_dtype in ("fp32", "bf16"):
+        lists, lengths = pipeline.tree_select(idx, pos, buckets, tree, config, score_dtype=score_dtype)
+        ends = _np(buckets.ends)
+        for r in range(2):
+            for g in range(Hkv):
+                nc = (ncent if score_dtype == "fp32" else tree.levels[0].centroids_bf16.float())[g]
+                bc = (buckets.centroids_f32 if score_dtype == "fp32" else buckets.centroids.float())[g]
+                visible = int((ends[g] <= int(pos[r]) + 1).sum())
+                want_l, want_n, _ = oracle.tree_select_row(
+                    _np(idx[r, g]), _np(nc), _np(children[g]), _np(bc), _np(buckets.members[g]), int(pos[r]),
+                    visible=visible, covered=48, beam_width=2, top_p=24, top_k=config.top_k, window=64, sink=4,
+                    mode=score_dtype)
+                assert np.array_equal(_np(lists[r, g]), want_l), (score_dtype, r, g)
+                assert int(lengths[r, g]) == want_n
