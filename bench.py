@@ -21,7 +21,7 @@ launch duration (which includes the dispatch gap, so it is an upper bound on the
 kernel's own duration, which rocprofv3's kernel trace reports).
 
 Comparators in the same run: dense SDPA decode on the same GPU (same rotation), the
-chunked prefill (configs' prefill row) as tok/s beside dense causal SDPA, and the CPU
+32k chunked prefill as tok/s beside dense causal SDPA, and the CPU
 oracle on the host cores (a bounded sample of decode steps; its lists are also checked
 bit-exact against the GPU's, and its output within the bf16 bar).
 
@@ -345,7 +345,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: the select+read path shards by kv-head with no exchange "
-              "inside the step, and this build runs on a single MI355X; use --gpus 1.", file=sys.stderr)
+              "inside the step, and this benchmark runs on a single MI355X; use --gpus 1.", file=sys.stderr)
         return 2
 
     import numpy as np

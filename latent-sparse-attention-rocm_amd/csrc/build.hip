@@ -2,7 +2,7 @@
 //
 // The index build that precedes the select+read path (the reference builds its bucket tables
 // with build_buckets_gpu, pipeline.py:71-116: pooled keys merged by the Ward cost into
-// buckets, centroids from the member keys). This build keeps the buckets contiguous - every
+// buckets, centroids from the member keys). Here the buckets stay contiguous - every
 // bucket is a run of consecutive positions, so a table is its span ends and the decode
 // expands a pick from them - and merges adjacent segments only:
 //

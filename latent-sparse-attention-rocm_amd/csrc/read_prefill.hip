@@ -2,7 +2,7 @@
 //
 // Query row t of chunk c = t / chunk reads chunk c's per-kv-head list (its first lengths
 // slots) and then the chunk's own causal block [c*chunk, t] (the reference read of the
-// config-4 prefill: read_kernel_tiled.py:30-89 over these lists). Every row of a chunk
+// chunked prefill: read_kernel_tiled.py:30-89 over these lists). Every row of a chunk
 // shares the list, so one workgroup serves (batch, chunk, kv-head, head group): the
 // chunk's rows of up to 256 / chunk query heads of the group - 256 query rows, 32 per
 // wave - and every K/V row of the list is gathered once for all of them.

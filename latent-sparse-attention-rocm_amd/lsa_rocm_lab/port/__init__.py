@@ -1,7 +1,7 @@
 """The select+read port surface on MI355X (reference src/lsa_rocm_lab/port/__init__.py).
 
 The reference bootstraps an upstream checkout and re-exports its Triton modules
-(port/__init__.py:39-56). This build has no upstream or Triton dependency: the
+(port/__init__.py:39-56). This package has no upstream or Triton dependency: the
 package only locates the HIP library, loaded lazily on the first kernel call.
 """
 

@@ -1,6 +1,6 @@
 """CPU oracle: a numpy restatement of the reference's select+read path.
 
-TEST INFRASTRUCTURE. This module is the checker the HIP path is compared
+TEST INFRASTRUCTURE. This module is what the HIP path is compared
 against. Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
 leg of ``bench.py`` may import it; the product package never does.
 
@@ -209,10 +209,10 @@ def visible_counts(positions: np.ndarray, rows: int, cluster_block_size: int, bl
 
 
 def canonical_scores(queries: np.ndarray, centroids: np.ndarray, mode: str = "bf16") -> np.ndarray:
-    """``queries @ centroids.T`` in the build's canonical arithmetic, fp32 out.
+    """``queries @ centroids.T`` in a fixed canonical arithmetic, fp32 out.
 
     Reference pipeline.py:217-232 (``torch.mm`` bf16 x bf16 -> fp32, or fp32 x fp32 on
-    ``centroids_f32``). The reference's summation order is rocBLAS's; this build fixes
+    ``centroids_f32``). The reference's summation order is rocBLAS's; the oracle fixes
     one: operands rounded to the mode's type (bf16 RNE, or fp32), products and sums in
     fp64, 16 partial sums each over a contiguous D/16 slice accumulated in order, the
     16 partials combined by the tree (p, p+8), (p, p+4), (p, p+2), (p, p+1), then one
@@ -250,7 +250,7 @@ def index_queries(q: np.ndarray, heads_kv: int, chunk: int = 1) -> np.ndarray:
     """GQA-collapsed index queries: the mean over each kv-head's query group and over
     ``chunk`` consecutive tokens, fp32.
 
-    Reference gates.py:50-59 collapses GQA through upstream ``regroup``; the BASELINE
+    Reference gates.py:50-59 collapses GQA through upstream ``regroup``; the benchmark
     geometry instead specifies the per-kv-head mean over the group (and the chunk mean
     for chunked prefill). Canonical order: fp32 sum over tokens of the chunk, within a
     token over the group's heads in order, then one fp32 division by the count.
@@ -271,7 +271,7 @@ def index_queries(q: np.ndarray, heads_kv: int, chunk: int = 1) -> np.ndarray:
 def bucket_centroids(keys: np.ndarray, members: np.ndarray, mode: str = "mean") -> np.ndarray:
     """Bucket centroids from member keys, fp32.
 
-    ``mean``: the bucket-mean key. ``normalized``: the L2-normalized
+    ``mean``: the bucket-mean key (the benchmark workloads). ``normalized``: the L2-normalized
     sum (reference pipeline.py:108-115, :396-403, F.normalize eps 1e-12). Canonical
     order: fp32 sum over member slots in table order; the norm is
     ``fp32(sqrt(sum_d fp64(s_d)^2))`` with the fp64 squares summed in dim order.

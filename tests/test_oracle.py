@@ -1,4 +1,4 @@
-"""Pins the CPU oracle before it is trusted as the checker (CPU only, no GPU).
+"""Pins the CPU oracle before it is trusted to check the GPU (CPU only, no GPU).
 
 Every oracle function is checked against something that does not share its code: a
 library routine (torch sort / SDPA / bf16 conversion / normalize), exact fp64 or rational
