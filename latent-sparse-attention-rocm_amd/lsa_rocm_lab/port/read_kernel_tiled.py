@@ -27,13 +27,16 @@ MAX_SPLITS = 256
 
 
 def _read_splits(units: int, width: int, tile: int) -> int:
-    """Spans per (row, kv-head): with few rows (decode) a list is cut into spans of one
-    tile so ~every CU gets a workgroup; with many rows each list stays whole or nearly."""
+    """Spans per (row, kv-head), aiming at about 512 workgroups: with few rows (B=1
+    decode: 8 units) a list is cut into spans of one tile so ~every CU gets a workgroup;
+    with many rows each list stays whole or nearly, and a workgroup streams its span with
+    the next tile's loads in flight (B=32 x 131k tree read: 2 spans a list, 58 us; 16
+    spans took 62.7 us, the partials and their combine costing more than the spread)."""
     env = os.environ.get("LSA_READ_SPLITS")
     if env:
         return max(1, min(int(env), MAX_SPLITS))
     tiles = max(1, math.ceil(width / tile))
-    return max(1, min(tiles, max(1, 4096 // max(units, 1)), MAX_SPLITS))
+    return max(1, min(tiles, max(1, 512 // max(units, 1)), MAX_SPLITS))
 
 
 def _kv_layout(k: torch.Tensor, v: torch.Tensor):
