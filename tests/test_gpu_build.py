@@ -151,3 +151,24 @@ def test_extend_buckets_equals_a_full_build():
     members, end = oracle_block_tables(keys[0, :, 1].float().cpu().numpy(), config, 8, 32)
     assert np.array_equal(full.members[1].cpu().numpy(), members)
     assert np.array_equal(full.ends[1].cpu().numpy(), end)
+
+
+def test_tables_saved_and_loaded_select_alike(tmp_path):
+    """Span tables built on the GPU, written to disk and loaded back onto the GPU, give
+    the same fused-select lists as the tables in memory (and equal them field for field)."""
+    from lsa_rocm_lab.port import tables
+
+    T, Hq, Hkv, D = 8192, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=128, seed=5, device=DEV)
+    built = pipeline.segment_buckets(data.k, T // 64, 16, 256)
+    tables.save_buckets(tmp_path / "idx.safetensors", built)
+    loaded = tables.load_buckets(tmp_path / "idx.safetensors", DEV)
+    for f in ("centroids", "members", "sizes", "centroids_f32", "ends"):
+        a, b = getattr(built, f), getattr(loaded, f)
+        assert (a is None and b is None) or torch.equal(a, b), f
+    assert loaded.spans
+    idx = pipeline.index_queries(data.q[:, -1:], Hkv)[0]
+    pos = torch.full((idx.shape[0],), T - 1, dtype=torch.int32, device=DEV)
+    la, na = pipeline.flat_select(idx, pos, built, workloads.FLAT_32K)
+    lb, nb = pipeline.flat_select(idx, pos, loaded, workloads.FLAT_32K)
+    assert torch.equal(na, nb) and torch.equal(la, lb)
