@@ -69,6 +69,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-tree", action="store_true", help="skip the B=32 x 131k tree decode leg")
     ap.add_argument("--tree-steps", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-build", action="store_true", help="skip the bucket-table build leg")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run 3 plain device copies of this many MiB (calibrates HBM byte counters)")
     return ap.parse_args()
@@ -340,6 +341,32 @@ def tree_decode_leg(args, torch, np):
 # ----------------------------------------------------------------------------- main
 
 
+def bucket_build_leg(args, torch):
+    """The index build before the path: contiguous Ward-style segments of the 32k cache's
+    keys (8 kv-heads, pools of 16 -> 512 buckets of at most 256 positions each), the pool
+    sums and the greedy merge on the GPU (build.hip). One workgroup per table runs the
+    1536 dependent merges, so the leg is latency-bound; it reports time per merge step."""
+    from lsa_rocm_lab import workloads
+    from lsa_rocm_lab.port import pipeline
+
+    T, POOL, TARGET, CAP = 32768, 16, 512, 256
+    data = workloads.clustered(T, HQ, HKV, D, n_clusters=512, seed=1, device="cuda")
+    first = pipeline.segment_starts(data.k, TARGET, POOL, CAP)
+    times = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        again = pipeline.segment_starts(data.k, TARGET, POOL, CAP)
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    ms = sorted(times)[len(times) // 2]
+    merges = T // POOL - TARGET
+    return {"workload": "segment_starts_32k", "tables": HKV, "positions": T, "pool": POOL, "buckets": TARGET,
+            "max_size": CAP, "ms": round(ms, 3), "merges_per_table": merges,
+            "us_per_merge": round(ms * 1e3 / merges, 3), "deterministic": bool(torch.equal(first, again))}
+
+
 def main() -> int:
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -544,6 +571,12 @@ def main() -> int:
         tree = tree_decode_leg(args, torch, np)
         log(f"tree {tree}")
 
+    # ---- the bucket-table build (the index build before the path)
+    build = None
+    if not args.no_build:
+        build = bucket_build_leg(args, torch)
+        log(f"bucket build {build}")
+
     # ---- CPU baseline: the oracle on the host, bounded sample; doubles as the parity check
     cpu = None
     parity = None
@@ -629,6 +662,7 @@ def main() -> int:
         "prefill": prefill,
         "block_sparse_decode": block_sparse,
         "tree_decode": tree,
+        "bucket_build": build,
         "cpu_baseline": cpu,
         "parity": parity,
     }
