@@ -20,10 +20,13 @@ replays on the stream it runs on; algorithmic bytes (gathered K and V rows) / av
 launch duration (which includes the dispatch gap, so it is an upper bound on the
 kernel's own duration, which rocprofv3's kernel trace reports).
 
-Comparators in the same run: dense SDPA decode on the same GPU (same rotation), the
-32k chunked prefill as tok/s beside dense causal SDPA, and the CPU
-oracle on the host cores (a bounded sample of decode steps; its lists are also checked
-bit-exact against the GPU's, and its output within the bf16 bar).
+Comparators in the same run: dense decode on the same GPU and the same rotation (every
+SDPA backend that runs, and this library's split-K read over the whole causal list; the
+fastest is the comparator), the 32k chunked prefill as tok/s beside dense causal SDPA, a
+plain device copy (achievable HBM bandwidth), and the torch CPU restatement of the step
+(oracle/cpu_step.py) on every host core and on one, for the 32k decode and the 2k fp32
+decode (a bounded sample; its lists are checked bit-exact against the GPU's). The numpy
+oracle checks the timed step's lists (bit-exact) and read (bf16 bar).
 
 One GPU only: ``--gpus N`` with N > 1 exits with a message.
 """
@@ -93,7 +96,8 @@ def copy_cache(c: DecodeCache):
     from lsa_rocm_lab.port.pipeline import Buckets
 
     b = c.buckets
-    nb = Buckets(b.centroids.clone(), b.members.clone(), b.sizes.clone(), centroids_f32=None,
+    nb = Buckets(b.centroids.clone(), b.members.clone(), b.sizes.clone(),
+                 centroids_f32=None if b.centroids_f32 is None else b.centroids_f32.clone(),
                  ends=None if b.ends is None else b.ends.clone(), spans=b.spans)
     return DecodeCache(c.q.clone(), c.k.clone(), c.v.clone(), nb, c.pos.clone())
 
@@ -182,8 +186,9 @@ def graph_launch_us(fn, n: int, replays: int, torch) -> float:
     return e0.elapsed_time(e1) * 1e3 / (n * replays)
 
 
-def dense_decode_fn(torch):
-    """Dense SDPA decode over the whole cache, restricted to fused kernels (no math path)."""
+def dense_decode_fns(torch):
+    """Dense SDPA decode over the whole cache, one per fused backend torch offers here (the
+    math path is left out: it materializes the scores and is no attention kernel)."""
     import torch.nn.functional as F
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
@@ -199,9 +204,72 @@ def dense_decode_fn(torch):
                 return F.scaled_dot_product_attention(qq, kk, vv, scale=D ** -0.5, enable_gqa=gqa)
         return fn
 
-    return [("flash+gqa", make(SDPBackend.FLASH_ATTENTION, True)),
-            ("efficient+gqa", make(SDPBackend.EFFICIENT_ATTENTION, True)),
-            ("flash+expanded_kv", make(SDPBackend.FLASH_ATTENTION, False))]
+    return [("sdpa_flash+gqa", make(SDPBackend.FLASH_ATTENTION, True)),
+            ("sdpa_efficient+gqa", make(SDPBackend.EFFICIENT_ATTENTION, True)),
+            ("sdpa_flash+expanded_kv", make(SDPBackend.FLASH_ATTENTION, False)),
+            ("sdpa_efficient+expanded_kv", make(SDPBackend.EFFICIENT_ATTENTION, False))]
+
+
+def dense_leg(caches, R, us_step, torch):
+    """Dense decode comparators on the same rotation: every SDPA backend that runs, and
+    this library's own split-K read over the whole causal list (ids 0..T-1 per kv-head,
+    the dense attention this GPU can do with the same kernel). Each is a HIP graph of R
+    steps over the resident copies, wall-clock timed; the fastest is the comparator."""
+    from lsa_rocm_lab.port.read_kernel_tiled import sparse_read_auto
+
+    rows = {}
+    for name, fn in dense_decode_fns(torch):
+        try:
+            fn(caches[0].q, caches[0].k, caches[0].v)
+            torch.cuda.synchronize()
+        except RuntimeError as exc:
+            log(f"dense {name} unavailable: {str(exc).splitlines()[0][:120]}")
+            continue
+        rows[name] = lambda i, fn=fn: fn(caches[i % R].q, caches[i % R].k, caches[i % R].v)
+    ids = torch.arange(T_CTX, device="cuda", dtype=torch.int32).view(1, 1, T_CTX)
+    full = torch.full((1, 1), T_CTX, device="cuda", dtype=torch.int32)
+    rows["lsa_read_dense"] = lambda i: sparse_read_auto(caches[i % R].q, caches[i % R].k, caches[i % R].v, ids,
+                                                        full, D ** -0.5)
+    out = {}
+    for name, dfn in rows.items():
+        event_launch_times(dfn, 8, torch)
+        try:
+            g = capture(dfn, R, torch)
+            n_rep = max(1, 256 // R)
+            g.replay()
+            torch.cuda.synchronize()
+            w0 = time.perf_counter()
+            for _ in range(n_rep):
+                g.replay()
+            torch.cuda.synchronize()
+            us = (time.perf_counter() - w0) / (n_rep * R) * 1e6
+            how = "graph"
+        except RuntimeError as exc:
+            log(f"dense {name}: graph capture failed ({str(exc).splitlines()[0][:80]}); event-timed launches")
+            us = statistics.mean(event_launch_times(dfn, 128, torch)) * 1e3
+            how = "events"
+        out[name] = {"us_per_step": round(us, 3), "timing": how,
+                     "gbps": round(2 * T_CTX * HKV * D * 2 / (us * 1e-6) / 1e9, 1)}
+    best = min(out, key=lambda n: out[n]["us_per_step"])
+    log(f"dense decode: {out}")
+    return {"backends": out, "fastest": best, "us_per_step": out[best]["us_per_step"],
+            "kv_bytes": 2 * T_CTX * HKV * D * 2,
+            "speedup_vs_fastest": round(out[best]["us_per_step"] / us_step, 3),
+            "meets_3x": bool(out[best]["us_per_step"] / us_step >= 3.0)}
+
+
+def copy_leg(torch, mib: int = 1024):
+    """Achievable HBM bandwidth on this box: a device-to-device copy of `mib` MiB (read +
+    write bytes / time), median of event-timed copies."""
+    src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    times = event_launch_times(lambda i: dst.copy_(src), 9, torch)
+    ms = statistics.median(times)
+    del src, dst
+    return {"bytes_moved": 2 * (mib << 20), "ms": round(ms, 4), "gbps": round(2 * (mib << 20) / (ms * 1e-3) / 1e9, 1)}
 
 
 # ----------------------------------------------------------------------------- block-sparse decode
@@ -318,7 +386,8 @@ def tree_decode_leg(args, torch, np):
         l, n, _ = oracle.tree_select_row(
             idx0[b, gg].float().cpu().numpy(), lvl.centroids_bf16[b, gg].float().cpu().numpy(),
             lvl.children[b, gg].cpu().numpy(), buckets.centroids[b, gg].float().cpu().numpy(),
-            buckets.members[b, gg].cpu().numpy(), T - 1, visible=buckets.rows, covered=buckets.rows,
+            buckets.members[b, gg].cpu().numpy(), T - 1, visible=buckets.rows,
+            node_block=config.node_cluster_block_size,
             beam_width=config.beam_width, top_p=config.top_p, top_k=config.top_k, window=0, sink=0, mode="bf16")
         exact &= bool(np.array_equal(lists0[b, gg].cpu().numpy(), l)) and int(lengths0[b, gg]) == n
     k0, v0 = data.k[:1].float().cpu().numpy(), data.v[:1].float().cpu().numpy()
@@ -336,6 +405,141 @@ def tree_decode_leg(args, torch, np):
             "speedup_vs_dense": None if dense_us is None else round(dense_us / us, 2),
             "parity": {"lists_bit_exact_sampled": exact, "read_max_abs": float(err.max()),
                        "read_mean_abs": float(err.mean())}}
+
+
+# ----------------------------------------------------------------------------- config 1 and the CPU
+
+
+def decode_2k_leg(args, torch, np):
+    """The CPU-runnable decode config on the GPU: B=1, context 2048, Hq 8 / Hkv 2, D 64, fp32,
+    q/k/v ~ N(0, 1) seed 0, positional blocks of 64 with block-mean centroids, top-7 blocks
+    + the last block as the window + block 0 as the sinks (8 blocks, 512 tokens a kv-head).
+    One fused decode launch a step, graph-replayed over 16 resident copies; lists checked
+    bit-exact and the read within the fp32 bar (1e-4) against the numpy oracle."""
+    import oracle
+    from lsa_rocm_lab import workloads
+    from lsa_rocm_lab.port import pipeline
+
+    T, Hq, Hkv, Dh = 2048, 8, 2, 64
+    q, k, v = workloads.geometry(T, Hq, Hkv, Dh, dtype=torch.float32, seed=0, device="cuda")
+    config = workloads.DECODE_2K
+    buckets = pipeline.position_buckets(k, config, centroid="mean")
+    pos = torch.tensor([T - 1], device="cuda", dtype=torch.int32)
+    base = DecodeCache(q[:, -1:].contiguous(), k, v, buckets, pos)
+    R = 16
+    caches = [base] + [copy_cache(base) for _ in range(R - 1)]
+
+    def step(i):
+        c = caches[i % R]
+        out, lists, lengths = pipeline.flat_decode(c.q, c.k, c.v, c.pos, c.buckets, config, scale=Dh ** -0.5,
+                                                   score_dtype="fp32")
+        return lists, lengths, out
+
+    lists, lengths, out = step(0)
+    torch.cuda.synchronize()
+    us = graph_launch_us(step, R, max(1, args.kernel_launches // R), torch)
+    q_np, k_np, v_np = base.q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy()
+    idx = oracle.index_queries(q_np, Hkv)[0, 0]
+    cents, mem = buckets.centroids_f32.cpu().numpy(), buckets.members.cpu().numpy()
+    ls, ns = [], []
+    for g in range(Hkv):
+        l, n = oracle.flat_select(idx[g][None], np.array([T - 1]), cents[g], mem[g],
+                                  cluster_block_size=config.cluster_block_size, block_buckets=config.block_bucket_count,
+                                  top_p=config.top_p, top_k=config.top_k, window=config.window_size,
+                                  sink=config.sink_size, mode="fp32")
+        ls.append(l[0])
+        ns.append(n[0])
+    ls, ns = np.stack(ls), np.array(ns)
+    want = oracle.sparse_read(q_np, k_np, v_np, ls[None, None], ns[None, None], Dh ** -0.5)
+    err = np.abs(out.cpu().numpy() - want)
+    return {"workload": "decode_2k_fp32", "context": T, "heads_q": Hq, "heads_kv": Hkv, "head_dim": Dh,
+            "dtype": "fp32", "tokens_read": lengths.cpu().numpy().tolist(), "gpu_us_per_step": round(us, 3),
+            "parity": {"lists_bit_exact": bool(np.array_equal(lists[0].cpu().numpy(), ls)),
+                       "lengths_bit_exact": bool(np.array_equal(lengths[0].cpu().numpy(), ns)),
+                       "read_max_abs": float(err.max()), "read_mean_abs": float(err.mean())},
+            "_inputs": (base, config)}
+
+
+def cpu_model() -> str:
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return "unknown"
+
+
+def time_cpu(fn, budget_s: float, min_reps: int = 3, warmup: int = 1) -> tuple[float, float, int]:
+    """(p50, p95) seconds and the count of fn() calls that fit in budget_s, after warmup."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < min_reps:
+        c0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - c0)
+    times.sort()
+    return times[len(times) // 2], times[min(len(times) - 1, int(0.95 * len(times)))], len(times)
+
+
+def cpu_leg(args, torch, base, data, buckets, config, lists0, lengths0, c1):
+    """The pure-torch CPU restatement of the decode step (oracle/cpu_step.py: index queries,
+    canonical scores, top-k, rank-order expansion, gather attention, whole-tensor ops) on
+    the host: every core the process may use (torch.set_num_threads), then one thread, for
+    the 32k flat decode and the 2k fp32 decode. Its lists are checked bit-exact against the
+    GPU's. A bounded sample: about args.cpu_seconds of CPU work in all."""
+    import os
+
+    from oracle import cpu_step
+
+    cores = len(os.sched_getaffinity(0))
+    budget = args.cpu_seconds / 4.0
+    k_cpu, v_cpu = data.k.cpu(), data.v.cpu()
+    q_cpu = base.q[:, 0].cpu()
+    cent, mem, ends = buckets.centroids.cpu(), buckets.members.cpu(), buckets.ends.cpu()
+    pos = torch.tensor([T_CTX - 1])
+
+    def flat():
+        return cpu_step.decode_step(q_cpu, k_cpu, v_cpu, cent, mem, ends, pos,
+                                    cluster_block_size=config.cluster_block_size,
+                                    block_buckets=config.block_bucket_count, top_p=config.top_p, top_k=config.top_k,
+                                    window=config.window_size, sink=config.sink_size, scale=D ** -0.5, mode="bf16")
+
+    b1, cfg1 = c1["_inputs"]
+    q1, k1, v1 = b1.q[:, 0].cpu(), b1.k.cpu(), b1.v.cpu()
+    cent1, mem1 = b1.buckets.centroids_f32.cpu(), b1.buckets.members.cpu()
+    pos1 = torch.tensor([b1.k.shape[1] - 1])
+
+    def small():
+        return cpu_step.decode_step(q1, k1, v1, cent1, mem1, None, pos1, cluster_block_size=cfg1.cluster_block_size,
+                                    block_buckets=cfg1.block_bucket_count, top_p=cfg1.top_p, top_k=cfg1.top_k,
+                                    window=cfg1.window_size, sink=cfg1.sink_size, scale=64 ** -0.5, mode="fp32")
+
+    prev = torch.get_num_threads()
+    res = {}
+    try:
+        for threads in (cores, 1):
+            torch.set_num_threads(threads)
+            res[threads] = (time_cpu(flat, budget), time_cpu(small, budget))
+    finally:
+        torch.set_num_threads(prev)
+    ls, ns, _ = flat()
+    same = bool(torch.equal(ls[0], lists0[0].cpu()) and torch.equal(ns[0], lengths0[0].cpu()))
+    (f50, f95, fn), (s50, s95, sn) = res[cores]
+    (f50_1, _, _), (s50_1, _, _) = res[1]
+    c1["cpu_us_per_step"] = round(s50 * 1e6, 1)
+    c1["cpu_cores"] = cores
+    return {"value": round(f50 * 1e6, 1), "unit": "us/step", "cores": cores, "kind": "port",
+            "model": cpu_model(), "p95_us": round(f95 * 1e6, 1), "one_thread_us": round(f50_1 * 1e6, 1),
+            "lists_bit_exact_vs_gpu": same,
+            "decode_2k_fp32": {"us_per_step": round(s50 * 1e6, 1), "p95_us": round(s95 * 1e6, 1),
+                               "one_thread_us": round(s50_1 * 1e6, 1), "steps": sn},
+            "sample": f"{fn} flat_decode_32k steps and {sn} decode_2k_fp32 steps of the torch CPU restatement "
+                      f"(oracle/cpu_step.py) at {cores} threads, the same at 1 thread; median (p50)"}
 
 
 # ----------------------------------------------------------------------------- main
@@ -471,36 +675,11 @@ def main() -> int:
         f"unfused step {unfused_us:.2f} us (select {sel_us:.2f} + read {read_us:.2f} + index queries); "
         f"unfused lists identical: {unfused_same}")
 
-    # ---- dense SDPA comparator on the same rotation
-    dense = {"backend": None}
-    for name, fn in dense_decode_fn(torch):
-        try:
-            fn(caches[0].q, caches[0].k, caches[0].v)
-            torch.cuda.synchronize()
-        except RuntimeError as exc:
-            log(f"dense {name} unavailable: {str(exc).splitlines()[0][:120]}")
-            continue
-        dfn = lambda i, fn=fn: fn(caches[i % R].q, caches[i % R].k, caches[i % R].v)
-        event_launch_times(dfn, 16, torch)
-        try:
-            dgraph = capture(dfn, R, torch)
-            torch.cuda.synchronize()
-            w0 = time.perf_counter()
-            n_rep = max(1, 256 // R)
-            for _ in range(n_rep):
-                dgraph.replay()
-            torch.cuda.synchronize()
-            dense_us = (time.perf_counter() - w0) / (n_rep * R) * 1e6
-            how = "graph"
-        except RuntimeError as exc:
-            log(f"dense graph capture failed ({str(exc).splitlines()[0][:80]}); event-timed launches instead")
-            dense_us = statistics.mean(event_launch_times(dfn, 256, torch)) * 1e3
-            how = "events"
-        dense = {"backend": name, "us_per_step": round(dense_us, 3), "timing": how,
-                 "kv_bytes": 2 * T_CTX * HKV * D * 2}
-        break
-    speedup = dense["us_per_step"] / us_step if dense.get("us_per_step") else None
-    log(f"dense decode {dense}")
+    # ---- dense comparators on the same rotation
+    dense = dense_leg(caches, R, us_step, torch)
+    speedup = dense["speedup_vs_fastest"]
+    copy = copy_leg(torch)
+    log(f"copy {copy}")
 
     # ---- prefill (chunked, shared selection per 64-token chunk)
     prefill = None
@@ -577,49 +756,42 @@ def main() -> int:
         build = bucket_build_leg(args, torch)
         log(f"bucket build {build}")
 
-    # ---- CPU baseline: the oracle on the host, bounded sample; doubles as the parity check
-    cpu = None
+    # ---- parity of the timed step against the numpy oracle (lists bit-exact, read in the bar)
     parity = None
     if not args.no_cpu:
         import oracle
-        from threadpoolctl import threadpool_limits
 
         q_np = base.q.float().cpu().numpy()
-        k_np, v_np = data.k.float().cpu().numpy(), data.v.float().cpu().numpy()
         cents = buckets.centroids.float().cpu().numpy()
-        members = buckets.members.cpu().numpy()
-        ends = buckets.ends.cpu().numpy()
-
-        def cpu_step():
-            idx = oracle.index_queries(q_np, HKV)[0, 0]
-            ls, ns = [], []
-            for g in range(HKV):
-                lst, n = oracle.flat_select(idx[g][None], np.array([T_CTX - 1]), cents[g], members[g],
-                                            cluster_block_size=config.cluster_block_size,
-                                            block_buckets=config.block_bucket_count, top_p=config.top_p,
-                                            top_k=config.top_k, window=config.window_size,
-                                            sink=config.sink_size, mode="bf16", ends=ends[g])
-                ls.append(lst[0])
-                ns.append(n[0])
-            ls, ns = np.stack(ls), np.array(ns)
-            out = oracle.sparse_read(q_np, k_np, v_np, ls[None, None], ns[None, None], D ** -0.5)
-            return ls, ns, out
-
-        times = []
-        with threadpool_limits(limits=1):
-            t_end = time.perf_counter() + args.cpu_seconds
-            while time.perf_counter() < t_end or len(times) < 2:
-                c0 = time.perf_counter()
-                ls, ns, out_cpu = cpu_step()
-                times.append(time.perf_counter() - c0)
-        cpu = {"value": round(statistics.median(times) * 1e6, 1), "unit": "us/step", "cores": 1, "kind": "port",
-               "sample": f"{len(times)} full flat_decode_32k steps (index queries, select, read) of the numpy "
-                         f"oracle, one BLAS thread, median"}
-        err = np.abs(out0.float().cpu().numpy() - out_cpu)
+        members_np, ends_np = buckets.members.cpu().numpy(), buckets.ends.cpu().numpy()
+        idx_np = oracle.index_queries(q_np, HKV)[0, 0]
+        ls, ns = [], []
+        for g in range(HKV):
+            lst, n = oracle.flat_select(idx_np[g][None], np.array([T_CTX - 1]), cents[g], members_np[g],
+                                        cluster_block_size=config.cluster_block_size,
+                                        block_buckets=config.block_bucket_count, top_p=config.top_p,
+                                        top_k=config.top_k, window=config.window_size, sink=config.sink_size,
+                                        mode="bf16", ends=ends_np[g])
+            ls.append(lst[0])
+            ns.append(n[0])
+        ls, ns = np.stack(ls), np.array(ns)
+        want = oracle.sparse_read(q_np, data.k.float().cpu().numpy(), data.v.float().cpu().numpy(),
+                                  ls[None, None], ns[None, None], D ** -0.5)
+        err = np.abs(out0.float().cpu().numpy() - want)
         parity = {"lists_bit_exact": bool(np.array_equal(lists0[0].cpu().numpy(), ls)),
                   "lengths_bit_exact": bool(np.array_equal(lengths0[0].cpu().numpy(), ns)),
                   "read_max_abs": float(err.max()), "read_mean_abs": float(err.mean())}
-        log(f"cpu {cpu} parity {parity}")
+        log(f"parity {parity}")
+
+    # ---- the 2k fp32 decode (CPU-runnable config): GPU step and parity
+    c1 = decode_2k_leg(args, torch, np)
+    log(f"decode_2k_fp32 {c1}")
+
+    # ---- CPU baseline: the torch CPU restatement of the same step on the host cores
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_leg(args, torch, base, data, buckets, config, lists0, lengths0, c1)
+        log(f"cpu {cpu}")
 
     if args.copy_mib:  # a plain copy of known size, for scaling FETCH_SIZE / WRITE_SIZE counters
         src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
@@ -659,6 +831,8 @@ def main() -> int:
                      "all_bytes_per_launch": total_bytes},
         "dense": dense,
         "speedup_vs_dense": None if speedup is None else round(speedup, 3),
+        "hbm_copy": copy,
+        "decode_2k_fp32": {k: v for k, v in c1.items() if not k.startswith("_")},
         "prefill": prefill,
         "block_sparse_decode": block_sparse,
         "tree_decode": tree,

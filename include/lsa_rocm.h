@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define LSA_ABI_VERSION 1
+#define LSA_ABI_VERSION 2
 
 enum lsa_status {
   LSA_OK = 0,
@@ -108,16 +108,21 @@ int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int32_t G, int3
                     int32_t splits, int32_t* counters, void* scratch, size_t scratch_bytes, int32_t* lists,
                     int32_t* lengths, void* stream);
 
-/* Two-level tree select (reference pipeline.py:319-337 tree_select, _tree.py:438-493
- * _beam_pick_rows with one node level): the best `beam_width` of the n_nodes node
- * centroids, then the best top_p of their children plus the uncovered visible buckets
- * [covered, visible), then the flat expansion. node_centroids [tables, n_nodes, D],
- * children [tables, n_nodes, node_size] int32 bucket ids. table_flags as lsa_select_flat. */
+/* Two-level tree select (reference pipeline.py:319-337 tree_select, _tree.py:318-373
+ * _beam_pick_rows with one node level, _tree.py:100-142 _growth_replay): per (row, group)
+ * with V visible buckets, node growth covers the first C = min(floor(V / node_block) *
+ * node_block, n_nodes * node_size) buckets (node_block = the reference's
+ * node_cluster_block_size), so the made nodes are [0, C / node_size). The best
+ * `beam_width` made nodes (a tie to the lower node), then the best top_p of their visible
+ * children plus the fresh buckets [C, V), each bucket once (a tie to the lower bucket),
+ * then the flat expansion. node_centroids [tables, n_nodes, D], children [tables,
+ * n_nodes, node_size] int32 bucket ids (node n's children lie in [0, (n + 1) * node_size),
+ * as growth makes them). table_flags as lsa_select_flat. */
 int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D, const void* node_centroids,
                     const int32_t* children, int32_t n_nodes, int32_t node_size, const void* centroids,
                     const int32_t* members, const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables,
                     int64_t group_tables, int score_mode, const int32_t* positions, int32_t cluster_block_size,
-                    int32_t block_buckets, int32_t covered, int32_t beam_width, int32_t top_p, int32_t window,
+                    int32_t block_buckets, int32_t node_block, int32_t beam_width, int32_t top_p, int32_t window,
                     int32_t sink, int32_t top_k, int32_t* lists, int32_t* lengths, void* stream);
 
 /* GQA-collapsed index queries (reference gates.py:50-59 make_index_space, per-kv-head
@@ -202,9 +207,12 @@ int lsa_read_chunked_mfma_ok(int dtype, int32_t D, int32_t chunk);
  * lsa_read_tile_tokens() slots. counters: lsa_decode_flat_counters() int32 words, zero
  * before the first launch; every launch leaves them zero. scratch:
  * lsa_decode_flat_scratch_bytes(), 16-byte aligned. Launches sharing counters must be
- * stream-ordered. status (optional, int32) is set to 1 if a reader workgroup gave up
- * waiting for its unit's selection (not expected: readers wait only on lower-numbered
- * workgroups, which never wait); the counters must then be zeroed again.
+ * stream-ordered. status (optional, int32 in device or pinned host memory; written with a
+ * system-scope store) is set to 1 if a reader workgroup gave up waiting for its unit's
+ * selection (not expected: readers wait only on lower-numbered workgroups, which never
+ * wait). Such a reader writes nothing and still arrives, so the arrival counters reset,
+ * but that launch's outputs are invalid and a record published after the give-up can
+ * outlive it: the caller zeroes the counters before the next launch.
  * table_flags: 0, or LSA_TABLE_SPANS when every bucket row j holds exactly the consecutive
  * ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0) in order, -1 after (the contiguous-segment
  * tables): the kept members of a pick are then a range, counted and expanded without
@@ -224,6 +232,13 @@ int lsa_decode_flat(const void* q, const void* k, const void* v, int dtype, int6
                     int32_t top_k, float scale, int32_t select_splits, int32_t readers, int32_t* counters,
                     int64_t n_counters, void* scratch, size_t scratch_bytes, int32_t* lists, int32_t* lengths,
                     void* out, int32_t* status, void* stream);
+
+/* Test hook (thread-local, this thread's later lsa_decode_flat calls): skip_publish != 0
+ * makes the select workgroups skip publishing the record, and spin_limit > 0 replaces the
+ * readers' poll limit, so a test can make the bounded wait give up with every workgroup
+ * still exiting normally. lsa_debug_decode(0, 0) restores the defaults. No counterpart in
+ * the reference (its decode has no cross-workgroup wait). */
+void lsa_debug_decode(int32_t skip_publish, int32_t spin_limit);
 
 #ifdef __cplusplus
 }

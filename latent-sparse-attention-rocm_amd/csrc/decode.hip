@@ -197,7 +197,9 @@ extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int 
   a.S = select_splits; a.cs = (rows + select_splits - 1) / select_splits;
   a.span = p.span; a.NR = p.NR;
   a.scale_log2 = scale * kLog2e;
-  a.spin_limit = 1 << 22;  // polls of about a microsecond each: seconds
+  a.spin_limit = decode_debug().spin_limit > 0 ? decode_debug().spin_limit
+                                              : 1 << 22;  // polls of about a microsecond each: seconds
+  a.skip_publish = decode_debug().skip_publish;
   a.sel_count = counters;
   a.rd_count = counters + units;
   a.record = counters + 2 * units;

@@ -44,6 +44,7 @@ struct DecodeArgs {
   int span, NR;        // slots per read part, readers per unit
   float scale_log2;
   int spin_limit;
+  int skip_publish;    // test hook: select workgroups never publish the record (readers give up)
   int* sel_count;      // [units] select arrivals
   int* rd_count;       // [units] reader arrivals
   int32_t* record;     // kRecordCopies copies, `cstride` words apart: [units][2K] words A then B
@@ -52,7 +53,8 @@ struct DecodeArgs {
   float* ws_part;      // [units][NR][GQ*(D+2)] (NR > 1)
   int32_t* lists;      // [units][W]
   int32_t* lengths;    // [units]
-  int32_t* status;     // optional: set to 1 by a reader whose wait timed out
+  int32_t* status;     // optional: set to 1 by a reader whose wait timed out (system scope:
+                       // the word may live in pinned host memory)
 };
 
 struct SelLds {
@@ -247,6 +249,7 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
     }
   }
   __syncthreads();
+  if (a.skip_publish) return;
   // every copy of the record, write-through
   const int words = 2 * a.K;
   for (int x = tid; x < kRecordCopies * words; x += LSA_BLOCK) {
@@ -317,12 +320,22 @@ __device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int
       sh.filled = filled;
       sh.pparts = pparts;
       sh.bad = bad;
-      if (bad && a.status) coherent_store_i32(a.status, 1);
+      if (bad && a.status) __hip_atomic_store(a.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
   }
   __syncthreads();
   DECODE_MARK(1);
-  if (sh.bad) return;  // the unit's state is unusable; the caller zeroes the counters again
+  if (sh.bad) {
+    // no record: this reader writes nothing but still arrives, so the unit's counter
+    // resets; *status tells the caller the unit's outputs are invalid
+    if (arrive_last(&a.rd_count[i], a.NR, &sh.rd.flag)) {
+      for (int x = tid; x < kRecordCopies * words; x += LSA_BLOCK) {
+        const int c = x / words, k = x - c * words;
+        coherent_store_i32(a.record + c * a.cstride + i * words + k, 0);
+      }
+    }
+    return;
+  }
 
   const int filled = sh.filled, pparts = sh.pparts;
   const int n_act = pparts + (n_tail + span - 1) / span;  // dense parts: picks' then the tail's

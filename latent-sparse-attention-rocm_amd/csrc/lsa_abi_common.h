@@ -15,6 +15,13 @@ namespace lsa {
 int fail(int code, const char* fmt, ...);
 void clear_error();
 
+// Test hooks of the fused decode (thread-local, set by lsa_debug_decode).
+struct DecodeDebug {
+  int skip_publish;  // select workgroups never publish the record
+  int spin_limit;    // polls before a reader gives up; 0 = the default
+};
+const DecodeDebug& decode_debug();
+
 inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 inline int next_pow2(int x) {
   int p = 1;

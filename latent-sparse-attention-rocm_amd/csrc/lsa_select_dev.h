@@ -43,6 +43,28 @@ __device__ __forceinline__ int visible_count(int64_t position, int rows, int clu
 }
 
 
+// visible_count for span ends, by the whole block in two rounds of parallel loads instead
+// of a serial binary search (one dependent round trip per halving): thread t samples the
+// end of stride-sized run t, the count of samples <= position + 1 names the run holding
+// the boundary, and that run's ends are loaded and counted. `lds` holds 2 * LSA_WAVES
+// ints. Every thread calls it; every thread gets the count.
+__device__ __forceinline__ int visible_count_block(int64_t position, int rows, const int32_t* ends, int* lds) {
+  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
+  const int64_t lim = position + 1;
+  const int step = (rows + LSA_BLOCK - 1) / LSA_BLOCK;  // ends per run (rows <= 256 * step)
+  const int runs = (rows + step - 1) / step;
+  const int s = min(rows - 1, (tid + 1) * step - 1);
+  const bool le = tid < runs && (int64_t)ends[s] <= lim;  // run tid lies wholly at or below lim
+  if (lane == 0) lds[w] = (int)__popcll(__ballot(le));
+  __syncthreads();
+  const int full = lds[0] + lds[1] + lds[2] + lds[3];  // runs wholly visible (ends are nondecreasing)
+  const int base = min(full * step, rows);  // the last run may be short
+  const int j = base + tid;
+  const bool v2 = tid < step && j < rows && (int64_t)ends[j < rows ? j : rows - 1] <= lim;
+  if (lane == 0) lds[LSA_WAVES + w] = (int)__popcll(__ballot(v2));
+  __syncthreads();
+  return base + lds[LSA_WAVES] + lds[LSA_WAVES + 1] + lds[LSA_WAVES + 2] + lds[LSA_WAVES + 3];
+}
 
 // fp64 partial over the lane's slice, then the 16-lane tree: the canonical score.
 template <typename CT, int SPAN>

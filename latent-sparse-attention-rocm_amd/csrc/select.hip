@@ -4,7 +4,8 @@
 //
 // Reference behaviour restated: pipeline.py:184-316 (visible_counts, best_first_keys,
 // _production_scores, flat_select[_reference]), select_fused.py:52-280
-// (select_topk_scores, expand_in_order_from_keys), _tree.py:438-493 (_beam_pick_rows).
+// (select_topk_scores, expand_in_order_from_keys), _tree.py:318-373 (_beam_pick_rows) with
+// _tree.py:100-142 (_growth_replay) for one node level.
 #include "lsa_abi_common.h"
 #include "lsa_select_dev.h"
 
@@ -246,7 +247,7 @@ struct TreeArgs {
   int64_t row_tables, group_tables;
   const int32_t* positions;
   int cluster_block, block_buckets;
-  int covered, beam, top_p;
+  int node_block, beam, top_p;
   int nodes_pow2, beam_pow2, cand_cap, cand_pow2, top_pow2;
   int window, sink, top_k;
   int spans;  // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0)
@@ -272,19 +273,25 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
   float qs[SPAN];
   load_query_slice<QT, SPAN>(q + i * D, p, bf16_mode, qs);
 
-  // level 1: every node, the best `beam` (a tie to the lower node)
+  // the row's growth (reference _tree.py:100-142 with one level, page = the row's visible
+  // count): nodes are made from whole blocks of node_block visible buckets, so the first
+  // `covered` buckets lie under the made nodes [0, made) and [covered, visible) are fresh
+  __shared__ int vis_lds[2 * LSA_WAVES];
+  const int visible = max(0, a.ends ? visible_count_block(position, a.rows, a.ends + t * a.rows, vis_lds)
+                                    : visible_count(position, a.rows, a.cluster_block, a.block_buckets, nullptr));
+  const int covered = min(visible / a.node_block * a.node_block, a.n_nodes * a.node_size);
+  const int made = covered / a.node_size;
+
+  // level 1: the made nodes, the best `beam` (a tie to the lower node); the rest are EMPTY
   const CT* ncent = (const CT*)a.node_centroids + t * (int64_t)a.n_nodes * D;
-  score_slice_keys<CT, SPAN>(qs, ncent, D, 0, a.n_nodes, a.n_nodes, keys);
+  score_slice_keys<CT, SPAN>(qs, ncent, D, 0, a.n_nodes, made, keys);
   __syncthreads();
   const int beam = min(a.beam, a.n_nodes);
   block_topk_sorted(keys, a.n_nodes, beam, a.beam_pow2, best, &tks, &st);
 
-  // level 0 candidates: the kept nodes' children, then the uncovered visible buckets (none
-  // when the nodes cover every bucket, which needs no visibility count)
-  const int visible = a.covered >= a.rows ? a.rows
-                                          : visible_count(position, a.rows, a.cluster_block, a.block_buckets,
-                                                          a.ends ? a.ends + t * a.rows : nullptr);
-  const int n_fresh = max(0, visible - a.covered);
+  // level 0 candidates: the kept nodes' children (only visible buckets), then the fresh
+  // buckets [covered, visible)
+  const int n_fresh = max(0, visible - covered);
   const int n_kids = beam * a.node_size;
   const int n_cand = n_kids + n_fresh;
   const int32_t* kids = a.children + t * (int64_t)a.n_nodes * a.node_size;
@@ -294,9 +301,9 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
       const int node = key_column(u_to_key(best[j / a.node_size]));
       if (node >= 0) c = kids[(int64_t)node * a.node_size + j % a.node_size];
     } else if (j < n_cand) {
-      c = a.covered + (j - n_kids);
+      c = covered + (j - n_kids);
     }
-    return (c >= 0 && c < a.rows) ? c : -1;
+    return (c >= 0 && c < visible) ? c : -1;
   };
   // every candidate bucket once (the order does not matter: a key carries its column)
   if (a.rows <= kSeenBits) {  // an LDS bitmap over bucket ids: the first lane to set a bit keeps it
@@ -693,7 +700,7 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
                                int32_t node_size, const void* centroids, const int32_t* members, const int32_t* ends,
                                int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables, int64_t group_tables, int score_mode,
                                const int32_t* positions, int32_t cluster_block_size, int32_t block_buckets,
-                               int32_t covered, int32_t beam_width, int32_t top_p, int32_t window, int32_t sink,
+                               int32_t node_block, int32_t beam_width, int32_t top_p, int32_t window, int32_t sink,
                                int32_t top_k, int32_t* lists, int32_t* lengths, void* stream) {
   LSA_REQUIRE(queries && node_centroids && children && centroids && members && positions && lists && lengths,
               LSA_ERR_NULL, "lsa_select_tree: NULL pointer");
@@ -705,8 +712,8 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
   LSA_TRY(check_aligned(node_centroids, D, score_mode, nullptr, cap));
   LSA_TRY(check_query_aligned(queries, q_dtype, D));
   LSA_REQUIRE(R >= 0 && G >= 1 && R * G <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_select_tree: bad sizes");
-  LSA_REQUIRE(n_nodes >= 1 && node_size >= 1 && beam_width >= 1 && top_p >= 1 && covered >= 0, LSA_ERR_SHAPE,
-              "lsa_select_tree: n_nodes, node_size, beam_width, top_p >= 1");
+  LSA_REQUIRE(n_nodes >= 1 && node_size >= 1 && beam_width >= 1 && top_p >= 1 && node_block >= 1, LSA_ERR_SHAPE,
+              "lsa_select_tree: n_nodes, node_size, node_block, beam_width, top_p >= 1");
   LSA_REQUIRE(window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE, "lsa_select_tree: window/sink/top_k >= 0");
   LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "lsa_select_tree: cluster_block_size must be >= 1");
   LSA_REQUIRE((table_flags & ~LSA_TABLE_SPANS) == 0, LSA_ERR_SHAPE, "lsa_select_tree: unknown table flags %d",
@@ -714,8 +721,11 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
   LSA_REQUIRE(!(table_flags & LSA_TABLE_SPANS) || ends, LSA_ERR_SHAPE,
               "lsa_select_tree: LSA_TABLE_SPANS needs the span ends");
   const int beam = beam_width < n_nodes ? beam_width : n_nodes;
-  const int64_t max_fresh = rows - covered > 0 ? rows - covered : 0;
-  const int64_t cand_cap = (int64_t)beam * node_size + max_fresh;
+  // fresh buckets [covered, visible): fewer than node_block past the made nodes, or every
+  // bucket past the nodes' reach
+  const int64_t reach = (int64_t)n_nodes * node_size;
+  const int64_t max_fresh = rows - reach > (int64_t)node_block - 1 ? rows - reach : node_block - 1;
+  const int64_t cand_cap = (int64_t)beam * node_size + (max_fresh < rows ? max_fresh : rows);
   LSA_REQUIRE(n_nodes <= kMaxLdsKeys && cand_cap <= kMaxLdsKeys && top_p <= kMaxLdsKeys, LSA_ERR_SHAPE,
               "lsa_select_tree: %d nodes / %lld candidates exceed %d", n_nodes, (long long)cand_cap, kMaxLdsKeys);
   if (R * G == 0) return LSA_OK;
@@ -723,7 +733,7 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
   a.R = R; a.G = G; a.node_centroids = node_centroids; a.children = children; a.n_nodes = n_nodes;
   a.node_size = node_size; a.centroids = centroids; a.members = members; a.ends = ends; a.rows = rows; a.cap = cap;
   a.row_tables = row_tables; a.group_tables = group_tables; a.positions = positions;
-  a.cluster_block = cluster_block_size; a.block_buckets = block_buckets; a.covered = covered;
+  a.cluster_block = cluster_block_size; a.block_buckets = block_buckets; a.node_block = node_block;
   a.beam = beam_width; a.top_p = top_p;
   a.nodes_pow2 = next_pow2(n_nodes); a.beam_pow2 = next_pow2(beam); a.cand_cap = (int)cand_cap;
   a.cand_pow2 = next_pow2((int)(cand_cap > 0 ? cand_cap : 1)); a.top_pow2 = next_pow2(top_p);

@@ -45,6 +45,7 @@ _sz = ctypes.c_size_t
 SIGNATURES = {
     "lsa_abi_version": (_int, []),
     "lsa_last_error": (ctypes.c_char_p, []),
+    "lsa_debug_decode": (None, [_i32, _i32]),
     "lsa_visible_counts": (_int, [_p, _i64, _i32, _i32, _i32, _i32, _p, _i64, _i64, _p, _p]),
     "lsa_score_rows": (_int, [_p, _int, _i64, _i32, _i32, _p, _i32, _i64, _i64, _int, _p, _p]),
     "lsa_pack_listing": (_int, [_p, _p, _i64, _i32, _p, _p]),
@@ -139,6 +140,16 @@ def stream(device: torch.device | None = None) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def device_index(device: torch.device | int | str | None) -> int:
+    """The ordinal of a CUDA device (``cuda`` alone is the current device)."""
+    if device is None:
+        return torch.cuda.current_device()
+    if isinstance(device, int):
+        return device
+    device = torch.device(device)
+    return torch.cuda.current_device() if device.index is None else device.index
+
+
 def dtype_code(dtype: torch.dtype) -> int:
     if dtype == torch.float32:
         return LSA_F32
@@ -151,17 +162,22 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 class Workspace:
     """Scratch per (device, stream, purpose), grown on demand; kernels fully write the
-    part they read, so it needs no initialisation. Calls sharing it are stream-ordered."""
+    part they read, so it needs no initialisation. Calls sharing it are stream-ordered.
+    A buffer that is outgrown is retired, never freed: a HIP graph captured earlier may
+    still replay against it."""
 
     _buffers: dict[tuple, torch.Tensor] = {}
+    _retired: list[torch.Tensor] = []
 
     @classmethod
     def get(cls, device: torch.device, purpose: str, nbytes: int) -> torch.Tensor | None:
         if nbytes <= 0:
             return None
-        key = (device.index, stream(device), purpose)
+        key = (device_index(device), stream(device), purpose)
         buf = cls._buffers.get(key)
         if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                cls._retired.append(buf)
             buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
             cls._buffers[key] = buf
         return buf
@@ -169,15 +185,43 @@ class Workspace:
 
 class Counters:
     """Split-arrival counters per (device, stream): int32 that every kernel finds zero at
-    launch and leaves zero, so the buffer is zero-filled only when it is (re)allocated."""
+    launch and leaves zero, so the buffer is zero-filled only when it is (re)allocated.
+    Outgrown buffers are retired, never freed (a captured graph may hold them)."""
 
     _buffers: dict[tuple, torch.Tensor] = {}
+    _retired: list[torch.Tensor] = []
 
     @classmethod
     def get(cls, device: torch.device, n: int) -> torch.Tensor:
-        key = (device.index, stream(device))
+        key = (device_index(device), stream(device))
         buf = cls._buffers.get(key)
         if buf is None or buf.numel() < n:
+            if buf is not None:
+                cls._retired.append(buf)
             buf = torch.zeros(max(n, 4096), dtype=torch.int32, device=device)
             cls._buffers[key] = buf
         return buf
+
+    @classmethod
+    def reset(cls, device: torch.device) -> None:
+        """Zeroes every counter buffer of the device (after a decode gave up waiting)."""
+        index = device_index(device)
+        for (dev, _), buf in cls._buffers.items():
+            if dev == index:
+                buf.zero_()
+
+
+class StatusWord:
+    """One int32 per device in pinned host memory that the fused decode sets (system-scope
+    store) when a reader gives up waiting; the host reads it without a device sync."""
+
+    _words: dict[int, torch.Tensor] = {}
+
+    @classmethod
+    def get(cls, device: torch.device) -> torch.Tensor:
+        index = device_index(device)
+        word = cls._words.get(index)
+        if word is None:
+            word = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+            cls._words[index] = word
+        return word

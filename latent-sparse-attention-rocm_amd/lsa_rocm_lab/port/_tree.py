@@ -1,13 +1,14 @@
 """The tree beam on the GPU (reference src/lsa_rocm_lab/port/_tree.py), one HIP kernel.
 
-Scope: a node tree of ONE level over the buckets (every bucket under a node, e.g.
-128 nodes of 16 buckets). Per (query row, kv-head) one workgroup scores every node,
-keeps the best ``beam_width`` (a tie to the lower node), gathers their children plus
-the uncovered visible buckets ``[covered, visible)``, removes duplicates, keeps the
-best ``top_p`` (a tie to the lower bucket), and expands them in rank order - the
-semantics of the reference's ``_beam_pick_rows`` (:438-493) with one level, where the
-top level's candidates are all of its nodes. Invalid candidates are never picked
-(the list tail is -1). The multi-level walk with growth replay is not built here.
+Scope: a node tree of ONE level over the buckets (e.g. 128 nodes of 16 buckets). Per
+(query row, kv-head) one workgroup replays the row's growth (reference :100-142 with one
+level: nodes are made over whole ``node_cluster_block_size`` blocks of the row's visible
+buckets), scores the made nodes, keeps the best ``beam_width`` (a tie to the lower
+node), gathers their visible children plus the fresh buckets ``[covered, visible)``,
+removes duplicates, keeps the best ``top_p`` (a tie to the lower bucket), and expands
+them in rank order - the semantics of the reference's ``_beam_pick_rows`` (:318-373)
+with one level, whose start level is taken whole. Invalid candidates are never picked
+(the list tail is -1).
 """
 
 from __future__ import annotations
@@ -40,7 +41,7 @@ def tree_select_batched(
 ):
     """Select by the one-level beam, expand in rank order - see ``pipeline.tree_select``.
 
-    ``LSA_TREE_IMPL`` (reference _tree.py:173) is read for compatibility; ``per_page``
+    ``LSA_TREE_IMPL`` (reference _tree.py:53) is read for compatibility; ``per_page``
     and ``batched`` name the same kernel here.
     """
     os.environ.get("LSA_TREE_IMPL", "per_page")
@@ -84,12 +85,12 @@ def tree_select_batched(
               ncent.data_ptr(), children.data_ptr(), n_nodes, node_size, bcent.data_ptr(), members.data_ptr(),
               _abi.ptr(ends), _abi.TABLE_SPANS if (buckets.spans and ends is not None) else 0, layout.rows,
               members.shape[-1], layout.row_tables, layout.group_tables, mode,
-              pos.data_ptr(), config.cluster_block_size, config.block_bucket_count, n_nodes * node_size,
+              pos.data_ptr(), config.cluster_block_size, config.block_bucket_count, config.node_cluster_block_size,
               config.beam_width, config.top_p, config.window_size, config.sink_size, top_k, lists.data_ptr(),
               lengths.data_ptr(), _abi.stream(device))
     return lists, lengths
 
 
 def tree_select_per_page(index_queries, positions, buckets, hierarchy, config, top_k=None, score_dtype="fp32"):
-    """Reference _tree.py:183-205 entry name; the same kernel as ``tree_select_batched``."""
+    """Reference _tree.py:63-85 entry name; the same kernel as ``tree_select_batched``."""
     return tree_select_batched(index_queries, positions, buckets, hierarchy, config, top_k, score_dtype)

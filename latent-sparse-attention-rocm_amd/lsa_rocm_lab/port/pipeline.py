@@ -71,6 +71,9 @@ class Buckets:
     # in order (contiguous-segment tables): the fused decode then counts and expands a
     # pick's kept members from the ends alone
     spans: bool = False
+    # how the centroids were made ("mean" or "normalized"), when a builder here made them;
+    # extend_buckets builds appended rows the same way
+    centroid: str | None = None
 
     @property
     def rows(self) -> int:
@@ -434,8 +437,11 @@ def flat_decode(
     byte-identical to ``flat_select(index_queries(q, Hkv)[:, 0], ...)``'s. ``splits``: select
     workgroups per (row, kv-head) (default as ``flat_select``); ``readers``: reader
     workgroups per (row, kv-head) (default: ``LSA_DECODE_READERS`` or the library's
-    choice); ``status`` (optional int32 [1] on the device) is set to 1 if a reader gave up
-    waiting.
+    choice). ``status``: an int32 [1] tensor (device or pinned host) that a launch sets to
+    1 when a reader gives up waiting for its unit's selection; by default the library's
+    pinned word, checked at the start of every call without a device sync: if an earlier
+    launch gave up, the arrival counters are zeroed again and ``LsaError`` is raised
+    (``check_decode`` makes the same check after a sync).
     """
     from lsa_rocm_lab.port.read_kernel_tiled import _kv_layout
 
@@ -473,6 +479,10 @@ def flat_decode(
     n_counters = _abi.size("lsa_decode_flat_counters", B, Hkv, rows, config.top_p)
     nbytes = _abi.size("lsa_decode_flat_scratch_bytes", dt, B, Hq, Hkv, D, rows, config.top_p,
                        config.window_size, config.sink_size, splits, readers)
+    if status is None:
+        status = _abi.StatusWord.get(device)
+        if int(status[0]) != 0:
+            _decode_gave_up(device, status)
     ws = _abi.Workspace.get(device, "decode", nbytes)
     counters = _abi.Counters.get(device, max(n_counters, 1))
     _abi.call("lsa_decode_flat", q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, Tk, Hq, Hkv, D, sb, st, sh,
@@ -482,6 +492,30 @@ def flat_decode(
               counters.data_ptr(), counters.numel(), _abi.ptr(ws), nbytes, lists.data_ptr(), lengths.data_ptr(),
               out.data_ptr(), _abi.ptr(status), _abi.stream(device))
     return out, lists, lengths
+
+
+def _decode_gave_up(device: torch.device, status: torch.Tensor) -> None:
+    """A fused decode launch gave up waiting: its outputs were invalid and a late record
+    may sit in the counters. Zero them (outside graph capture) and raise."""
+    if torch.cuda.is_current_stream_capturing():
+        raise _abi.LsaError(-6, "flat_decode: an earlier launch gave up waiting for its selection; "
+                                "the counters need a reset outside graph capture")
+    torch.cuda.synchronize(device)
+    _abi.Counters.reset(device)
+    torch.cuda.synchronize(device)
+    status.zero_()
+    raise _abi.LsaError(-6, "flat_decode: an earlier launch gave up waiting for its selection and its "
+                            "outputs are invalid; the arrival counters were zeroed")
+
+
+def check_decode(device: torch.device | int | None = None) -> None:
+    """Synchronizes the device and raises ``LsaError`` (after zeroing the counters) if a
+    fused decode launch on it gave up waiting since the last check."""
+    device = torch.device("cuda", _abi.device_index(device))
+    torch.cuda.synchronize(device)
+    status = _abi.StatusWord.get(device)
+    if int(status[0]) != 0:
+        _decode_gave_up(device, status)
 
 
 def lsa_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale, chunk_size: int = 64):
@@ -589,7 +623,7 @@ def segment_buckets(keys: torch.Tensor, target: int, pool: int = 16, max_size: i
     members = members.to(torch.int32).contiguous()
     c32, c16 = bucket_centroids(keys, members, centroid)
     return Buckets(c16, members, sizes.contiguous(), centroids_f32=c32, ends=end.to(torch.int32).contiguous(),
-                   spans=True)
+                   spans=True, centroid=centroid)
 
 
 def build_buckets(keys: torch.Tensor, config: PortConfig, pool: int | None = None, max_size: int | None = None,
@@ -646,26 +680,34 @@ def build_buckets(keys: torch.Tensor, config: PortConfig, pool: int | None = Non
     members = members.contiguous()
     c32, c16 = bucket_centroids(keys if flat else k4, members, centroid)
     return Buckets(c16, members, sizes.contiguous(), centroids_f32=c32, ends=end.contiguous() if spans else None,
-                   spans=spans)
+                   spans=spans, centroid=centroid)
 
 
 def extend_buckets(buckets: Buckets, keys: torch.Tensor, config: PortConfig, **build_kw) -> Buckets:
     """The tables with the blocks closed since they were built appended (a decode cache
     grows one token a step; a block's buckets are built once, when it closes): the rows of
     blocks rows // block_bucket_count .. T // cluster_block_size - 1, built as
-    ``build_buckets`` builds them, concatenated after the existing rows."""
+    ``build_buckets`` builds them, concatenated after the existing rows. The new rows keep
+    the tables' centroid kind (``buckets.centroid``, else ``build_kw["centroid"]``), span
+    flag and optional tensors: a table without ``centroids_f32`` or ``ends`` gets none."""
     bpb = config.block_bucket_count
     have = buckets.rows // bpb
     T = keys.shape[0] if keys.dim() == 2 else keys.shape[1]
     if T // config.cluster_block_size <= have:
         return buckets
-    spans = buckets.ends is not None
-    new = build_buckets(keys, config, first_block=have, spans=spans, **build_kw)
+    kind = buckets.centroid or build_kw.pop("centroid", "normalized")
+    build_kw.pop("centroid", None)
+    has_ends = buckets.ends is not None
+    if buckets.spans and not has_ends:
+        raise ValueError("extend_buckets: span tables need their ends")
+    new = build_buckets(keys, config, first_block=have, spans=has_ends, centroid=kind, **build_kw)
     return Buckets(torch.cat([buckets.centroids, new.centroids], dim=-2),
                    torch.cat([buckets.members, new.members], dim=-2),
                    torch.cat([buckets.sizes, new.sizes], dim=-1),
-                   centroids_f32=torch.cat([buckets.centroids_f32, new.centroids_f32], dim=-2),
-                   ends=torch.cat([buckets.ends, new.ends], dim=-1) if spans else None, spans=spans)
+                   centroids_f32=(None if buckets.centroids_f32 is None
+                                  else torch.cat([buckets.centroids_f32, new.centroids_f32], dim=-2)),
+                   ends=torch.cat([buckets.ends, new.ends], dim=-1) if has_ends else None,
+                   spans=buckets.spans, centroid=kind)
 
 
 def position_buckets(index_keys: torch.Tensor, config: PortConfig, centroid: str = "normalized") -> Buckets:
@@ -686,4 +728,4 @@ def position_buckets(index_keys: torch.Tensor, config: PortConfig, centroid: str
         members = members.expand(*lead, rows, cap).contiguous()
     sizes = (members >= 0).sum(-1, dtype=torch.int32)
     c32, c16 = bucket_centroids(index_keys, members, centroid)
-    return Buckets(c16, members, sizes, centroids_f32=c32)
+    return Buckets(c16, members, sizes, centroids_f32=c32, centroid=centroid)

@@ -35,10 +35,13 @@ def select_topk_scores(scores: torch.Tensor, lengths: torch.Tensor, top_p: int) 
         top_p: Best keys per row.
 
     Returns:
-        Ordered packed keys [R, K2] int64, K2 = next_pow2(min(top_p, N)), EMPTY-padded.
+        Ordered packed keys [R, K2] int64, K2 = next_pow2(min(top_p, N)), EMPTY-padded;
+        on the sampled-listing path (N > 4 * top_p, reference :97-117) [R, min(top_p, N)],
+        the width ``torch.topk`` gives there.
     """
     rows, columns = scores.shape
-    if columns > WHOLE_FACTOR * top_p:
+    sampled = columns > WHOLE_FACTOR * top_p
+    if sampled:
         warnings.warn(
             f"select_topk_scores: {columns} columns > {WHOLE_FACTOR} * top_p {top_p} "
             "- sampled listing contract, using the length-respecting pack+topk "
@@ -53,12 +56,12 @@ def select_topk_scores(scores: torch.Tensor, lengths: torch.Tensor, top_p: int) 
     k2 = _next_pow2(keep)
     out = torch.empty(rows, k2, device=scores.device, dtype=torch.int64)
     if rows == 0:
-        return out
+        return out[:, :keep] if sampled else out
     scores = scores.contiguous()
     lengths = lengths.to(device=scores.device, dtype=torch.int32).reshape(rows).contiguous()
     _abi.call("lsa_select_topk_scores", scores.data_ptr(), lengths.data_ptr(), rows, columns, top_p,
               out.data_ptr(), _abi.stream(scores.device))
-    return out
+    return out[:, :keep].contiguous() if sampled and keep != k2 else out
 
 
 def _expand(picks, picks_are_keys, bucket_members, positions, window_size, sink_size, top_k):

@@ -14,8 +14,9 @@ stores the member lists in CSR form, every row of every table in order:
 n_rows is the product of the table shape (*lead, rows). The metadata holds the format tag
 ("lsa-bucket-tables/1"), the member row width (bucket_cap) and the span flag. Loading
 checks every invariant the select kernels rely on (offsets start at 0 and never decrease,
-no row wider than bucket_cap, shapes agree, span tables hold exactly their span) and raises
-ValueError otherwise; safetensors executes nothing from the file.
+no row wider than bucket_cap, member ids >= 0, shapes agree, ends nondecreasing along each
+table's rows, span tables hold exactly their span) and raises ValueError otherwise;
+safetensors executes nothing from the file.
 """
 
 from __future__ import annotations
@@ -43,6 +44,8 @@ def save_buckets(path: str | os.PathLike, buckets: Buckets) -> None:
         raise ValueError("save_buckets: a row size lies outside [0, bucket_cap]")
     rows2d = members.reshape(-1, cap)
     keep = torch.arange(cap)[None, :] < flat_sizes[:, None]
+    if bool(((rows2d >= 0) != keep).any()) or bool((rows2d < -1).any()):
+        raise ValueError("save_buckets: every row must hold its `sizes` real ids (>= 0) first, then -1 padding")
     offsets = torch.zeros(flat_sizes.numel() + 1, dtype=torch.int64)
     torch.cumsum(flat_sizes, 0, out=offsets[1:])
     tensors = {
@@ -90,6 +93,8 @@ def load_buckets(path: str | os.PathLike, device: str | torch.device = "cpu") ->
         raise ValueError("load_buckets: a row's offsets decrease or exceed bucket_cap")
     if int(offsets[-1]) != ids.numel() or ids.dim() != 1:
         raise ValueError(f"load_buckets: {ids.numel()} member ids for offsets ending at {int(offsets[-1])}")
+    if bool((ids < 0).any()):
+        raise ValueError("load_buckets: member ids must be >= 0 (-1 only pads a row past its size)")
     members = torch.full((n_rows, cap), -1, dtype=torch.int32)
     keep = torch.arange(cap)[None, :] < sizes[:, None]
     members[keep] = ids
@@ -103,6 +108,10 @@ def load_buckets(path: str | os.PathLike, device: str | torch.device = "cpu") ->
     ends = t.get("ends")
     if ends is not None and ends.dtype != torch.int32:
         raise ValueError("load_buckets: ends must be int32")
+    if ends is not None and shape[-1] > 1:
+        e2 = ends.reshape(-1, shape[-1])
+        if bool((e2[:, 1:] < e2[:, :-1]).any()):
+            raise ValueError("load_buckets: ends decrease along a table's rows")
     if spans:
         if ends is None:
             raise ValueError("load_buckets: a span table needs its ends")

@@ -24,7 +24,9 @@ Pinning (what each function is checked against in tests/test_oracle.py):
   bucket_centroids               fp64 closed form
   sparse_read                    torch SDPA on full causal lists (textbook), duplicate ->
                                  V row, empty -> 0 / NaN
-  tree_select_row                brute-force sort of every candidate on tiny trees
+  tree_select_row / tree_growth  brute-force sort of every candidate on tiny trees; the
+                                 growth replay of _tree.py:100-142 restated literally
+                                 (page ends, block counts) on small tables
   ward_pair_cost                 exact rational arithmetic (fractions) and math.fsum
   ward_segments_keys             brute force (every adjacent cost recomputed from the
                                  segments each step, no links), two-cluster closed form,
@@ -121,14 +123,17 @@ def unpack_ids(keys: np.ndarray) -> np.ndarray:
 def select_topk_scores(scores: np.ndarray, lengths: np.ndarray, top_p: int) -> np.ndarray:
     """Fused pack + best-first top-k (reference select_fused.py:83-137, kernel :52-80).
 
-    Output [R, K2], K2 = next_pow2(min(top_p, N)); EMPTY pads the tail. Also the
-    length-respecting wide-row fallback (:97-117), which computes the same thing.
+    Output [R, K2], K2 = next_pow2(min(top_p, N)); EMPTY pads the tail. Rows wider than
+    4 * top_p take the length-respecting fallback (:97-117): the same keys, at the width
+    ``torch.topk(k=min(top_p, N))`` returns, [R, min(top_p, N)].
     """
     scores = np.asarray(scores, dtype=np.float32)
     rows, cols = scores.shape
     keep = min(int(top_p), cols)
     k2 = next_pow2(keep)
     best = best_first_keys(pack_keys(scores, lengths), keep)
+    if cols > 4 * int(top_p):
+        return best
     out = np.full((rows, k2), EMPTY, dtype=np.int64)
     out[:, :keep] = best
     return out
@@ -424,23 +429,41 @@ def flat_select(index_queries: np.ndarray, positions: np.ndarray, centroids: np.
     return expand_in_order(unpack_ids(ordered), members, positions, window, sink, top_k)
 
 
+def tree_growth(visible: int, node_block: int, n_nodes: int, node_size: int) -> tuple[int, int]:
+    """(covered buckets, made nodes) of a one-level tree for a row seeing ``visible``
+    buckets (reference _tree.py:100-142 ``_growth_replay`` with top_level 1: every page end
+    covers the whole ``node_cluster_block_size`` blocks of closed buckets not yet covered
+    and makes ``block / node_bucket_size`` nodes of each; the page's end is the row's
+    visible count, _tree.py:76-80). Capped by the nodes the table holds."""
+    covered = min(max(visible, 0) // node_block * node_block, n_nodes * node_size)
+    return covered, covered // node_size
+
+
 def tree_select_row(query: np.ndarray, node_centroids: np.ndarray, children: np.ndarray,
                     bucket_centroids_: np.ndarray, members: np.ndarray, position: int, visible: int,
-                    covered: int, beam_width: int, top_p: int, top_k: int, window: int, sink: int,
+                    node_block: int, beam_width: int, top_p: int, top_k: int, window: int, sink: int,
                     mode: str = "fp32") -> tuple[np.ndarray, int, np.ndarray]:
-    """Two-level beam for one (row, table) (reference _tree.py:318-373 with one node level).
+    """Two-level beam for one (row, table) (reference _tree.py:318-373 ``_beam_pick_rows``
+    with one node level, the growth of ``tree_growth``).
 
-    Level 1: every node is a candidate; keep the best ``beam_width`` by score, a tie to
-    the lower node. Level 0: the kept nodes' children plus the uncovered visible buckets
-    ``[covered, visible)``, deduplicated, the best ``top_p`` by score (tie -> lower
-    bucket), -1 padded; then the flat expansion. Returns (list, length, picks).
+    Level 1: the made nodes [0, made) are the candidates (the start level whole,
+    _tree.py:344-346); keep the best ``beam_width`` by score, a tie to the lower node
+    (the stable descending argsort over ascending candidates, :350-351). Level 0: the
+    kept nodes' children plus the fresh buckets ``[covered, visible)`` (:359-361), each
+    bucket once (first-occurrence dedup, :306-315), children at or past ``visible``
+    dropped (growth only makes nodes over closed buckets), the best ``top_p`` by score
+    (tie -> lower bucket), -1 padded; then the flat expansion. Returns (list, length,
+    picks).
     """
+    n_nodes = node_centroids.shape[0]
+    visible = max(int(visible), 0)
+    covered, made = tree_growth(visible, node_block, n_nodes, children.shape[1])
     node_scores = canonical_scores(query[None, :], node_centroids, mode)
-    nodes = unpack_ids(best_first_keys(pack_keys(node_scores, np.array([node_centroids.shape[0]])),
-                                       beam_width))[0]
+    nodes = unpack_ids(best_first_keys(pack_keys(node_scores, np.array([made])), beam_width))[0]
     kids = children[nodes[nodes >= 0]].reshape(-1)
     fresh = np.arange(covered, max(covered, visible))
-    cand = np.unique(np.concatenate([kids[kids >= 0], fresh]).astype(np.int64))
+    kids = kids[(kids >= 0) & (kids < visible)]
+    cand = np.unique(np.concatenate([kids, fresh]).astype(np.int64))
     picks = np.full(top_p, -1, dtype=np.int32)
     if cand.size:
         scores = canonical_scores(query[None, :], bucket_centroids_[cand], mode)[0]

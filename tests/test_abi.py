@@ -29,7 +29,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_version_and_error_string():
     lib = _abi.load()
-    assert lib.lsa_abi_version() == 1
+    assert lib.lsa_abi_version() == 2
     assert isinstance(lib.lsa_last_error(), bytes)
 
 

@@ -153,6 +153,27 @@ def test_extend_buckets_equals_a_full_build():
     assert np.array_equal(full.ends[1].cpu().numpy(), end)
 
 
+def test_extend_buckets_keeps_centroid_kind_and_optional_fields():
+    """Extension builds the new rows as the tables were built: bucket-mean centroids stay
+    means without repeating the kind, member-row tables get no span ends, and tables that
+    carry no fp32 centroids (as a file may load them) get none appended."""
+    import dataclasses
+
+    config = pipeline.PortConfig(cluster_block_size=256, bucket_size=16, bucket_cap=32, pool_size=8)
+    keys = clustered_keys(1, 5 * 256 + 40, 2, 64, torch.bfloat16, seed=43).to(DEV)
+    for spans in (False, True):
+        full = pipeline.build_buckets(keys, config, spans=spans, centroid="mean")
+        part = pipeline.build_buckets(keys[:, :3 * 256 + 10], config, spans=spans, centroid="mean")
+        grown = pipeline.extend_buckets(part, keys, config)
+        assert grown.centroid == "mean" and grown.spans == spans and (grown.ends is None) == (not spans)
+        for f in ("centroids", "members", "sizes", "centroids_f32", "ends"):
+            a, b = getattr(grown, f), getattr(full, f)
+            assert (a is None and b is None) or torch.equal(a, b), (spans, f)
+        bare = dataclasses.replace(part, centroids_f32=None, centroid=None)
+        grown = pipeline.extend_buckets(bare, keys, config, centroid="mean")
+        assert grown.centroids_f32 is None and torch.equal(grown.centroids, full.centroids)
+
+
 def test_tables_saved_and_loaded_select_alike(tmp_path):
     """Span tables built on the GPU, written to disk and loaded back onto the GPU, give
     the same fused-select lists as the tables in memory (and equal them field for field)."""

@@ -180,7 +180,8 @@ def test_tree_decode_batched_reduced():
                 bcent = (buckets.centroids_f32 if score_dtype == "fp32" else buckets.centroids.float())[b, g]
                 l, n, _ = oracle.tree_select_row(
                     _np(idx[b, g]), _np(ncent), _np(lvl.children[b, g]), _np(bcent), _np(buckets.members[b, g]),
-                    T - 1, visible=buckets.rows, covered=buckets.rows, beam_width=4, top_p=16, top_k=8192,
+                    T - 1, visible=buckets.rows, node_block=config.node_cluster_block_size, beam_width=4, top_p=16,
+                    top_k=8192,
                     window=0, sink=0, mode=score_dtype)
                 assert np.array_equal(_np(lists[b, g]), l), (score_dtype, b, g)
                 assert int(lengths[b, g]) == n
@@ -198,3 +199,71 @@ def test_tree_decode_batched_reduced():
     want = oracle.sparse_read(_np(data.q[:, -1:]), _np(data.k), _np(data.v), _np(lists)[:, None],
                               _np(lengths)[:, None])
     check_read(out, want)
+
+
+def test_tree_decode_ragged_positions_follow_growth():
+    """Rows early in the cache: each (sequence, kv-head) sees only the buckets whose span
+    has ended, node growth covers whole 64-bucket blocks of them, and the rest are fresh
+    candidates - lists bit-exact against the oracle's growth replay."""
+    B, T, Hq, Hkv, D = 3, 16384, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=256, seed=5, B=B, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    tree = workloads.node_tree(buckets, node_size=16)
+    config = pipeline.PortConfig(**{**workloads.TREE_131K.__dict__, "beam_width": 4, "top_p": 16,
+                                    "window_size": 128, "sink_size": 4})
+    pos = torch.tensor([T - 1, 9000, 2500], device=DEV, dtype=torch.int32)
+    idx = pipeline.index_queries(data.q[:, -1:], Hkv)[:, 0]
+    ends = _np(buckets.ends)
+    lvl = tree.levels[0]
+    for score_dtype in ("fp32", "bf16"):
+        lists, lengths = pipeline.tree_select(idx, pos, buckets, tree, config, score_dtype=score_dtype)
+        for b in range(B):
+            for g in range(Hkv):
+                visible = int((ends[b, g] <= int(pos[b]) + 1).sum())
+                ncent = (lvl.centroids if score_dtype == "fp32" else lvl.centroids_bf16.float())[b, g]
+                bcent = (buckets.centroids_f32 if score_dtype == "fp32" else buckets.centroids.float())[b, g]
+                l, n, picks = oracle.tree_select_row(
+                    _np(idx[b, g]), _np(ncent), _np(lvl.children[b, g]), _np(bcent), _np(buckets.members[b, g]),
+                    int(pos[b]), visible=visible, node_block=config.node_cluster_block_size, beam_width=4, top_p=16,
+                    top_k=config.top_k, window=128, sink=4, mode=score_dtype)
+                assert np.array_equal(_np(lists[b, g]), l), (score_dtype, b, g)
+                assert int(lengths[b, g]) == n
+                assert (picks[picks >= 0] < visible).all()
+
+
+def test_tree_decode_configured_geometry():
+    """The batched tree decode at its configured size: B=32 sequences x 131072 tokens,
+    Hq 32 / Hkv 8, D 128 bf16, 2048 buckets = 128 nodes x 16 per (sequence, kv-head), top-8
+    nodes then top-32 buckets. All 256 selections bit-exact against the oracle; the split
+    read of 4 sequences within the bf16 bar (max-abs 2e-2, mean-abs 2e-3)."""
+    B, T, Hq, Hkv, D = 32, 131072, 32, 8, 128
+    print("tree 131k x 32: building the workload", flush=True)
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=2048, seed=0, B=B, device=DEV, gen_device=DEV,
+                               q_tokens=1)
+    buckets = workloads.cluster_buckets(data, target=2048, workers=16)
+    tree = workloads.node_tree(buckets, node_size=16)
+    config = workloads.TREE_131K
+    assert buckets.rows == 2048 and tree.levels[0].children.shape[-2:] == (128, 16)
+    pos = torch.full((B,), T - 1, device=DEV, dtype=torch.int32)
+    idx = pipeline.index_queries(data.q, Hkv)[:, 0]  # [B, Hkv, D]
+    lists, lengths = pipeline.tree_select(idx, pos, buckets, tree, config, score_dtype="bf16")
+    out = pipeline.lsa_read(data.q, data.k, data.v, lists.unsqueeze(1), lengths.unsqueeze(1), D ** -0.5)
+    torch.cuda.synchronize()
+    print("tree 131k x 32: checking 256 selections", flush=True)
+    lvl = tree.levels[0]
+    idx_np, nc_np = _np(idx), _np(lvl.centroids_bf16)
+    kids_np, bc_np, mem_np = _np(lvl.children), _np(buckets.centroids), _np(buckets.members)
+    lists_np, lengths_np = _np(lists), _np(lengths)
+    for b in range(B):
+        for g in range(Hkv):
+            l, n, _ = oracle.tree_select_row(idx_np[b, g], nc_np[b, g], kids_np[b, g], bc_np[b, g], mem_np[b, g],
+                                             T - 1, visible=2048, node_block=config.node_cluster_block_size,
+                                             beam_width=8, top_p=32, top_k=config.top_k, window=0, sink=0,
+                                             mode="bf16")
+            assert np.array_equal(lists_np[b, g], l), (b, g)
+            assert int(lengths_np[b, g]) == n, (b, g)
+    print("tree 131k x 32: checking the read of 4 sequences", flush=True)
+    for b in (0, 11, 22, 31):
+        want = oracle.sparse_read(_np(data.q[b:b + 1]), _np(data.k[b:b + 1]), _np(data.v[b:b + 1]),
+                                  lists_np[b:b + 1, None], lengths_np[b:b + 1, None], D ** -0.5)
+        check_read(out[b:b + 1], want)

@@ -220,3 +220,40 @@ def test_tied_scores_take_the_block_top_k():
         n = int(ends[g, 31])  # buckets 0..31 are the spans [0, ends[31])
         assert int(lengths[0, g]) == n
         assert torch.equal(lists[0, g, :n].cpu(), torch.arange(n, dtype=torch.int32))
+
+
+def test_give_up_is_reported_and_the_next_launch_is_clean():
+    """The host makes every reader's bounded wait give up (select workgroups skip
+    publishing, a 64-poll limit): all workgroups exit normally, the status word reads 1,
+    the next flat_decode call zeroes the counters and raises, and the launch after it is
+    bit-identical to one before the failure."""
+    from lsa_rocm_lab import _abi
+
+    T, Hq, Hkv, D = 4096, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=64, seed=31, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    config = PortConfig(cluster_block_size=64, bucket_size=64, bucket_cap=256, top_p=16, top_k=4096,
+                        window_size=64, sink_size=4)
+    q = data.q[:, -1:].contiguous()
+    pos = torch.tensor([T - 1], dtype=torch.int32, device=DEV)
+    good = pipeline.flat_decode(q, data.k, data.v, pos, buckets, config)
+    torch.cuda.synchronize()
+    word = _abi.StatusWord.get(torch.device(DEV))
+    assert int(word[0]) == 0
+    lib = _abi.load()
+    print("case give-up: skip_publish=1 spin_limit=64", flush=True)
+    lib.lsa_debug_decode(1, 64)
+    try:
+        pipeline.flat_decode(q, data.k, data.v, pos, buckets, config)
+        torch.cuda.synchronize()
+    finally:
+        lib.lsa_debug_decode(0, 0)
+    assert int(word[0]) == 1
+    with pytest.raises(_abi.LsaError, match="gave up"):
+        pipeline.flat_decode(q, data.k, data.v, pos, buckets, config)
+    assert int(word[0]) == 0
+    again = pipeline.flat_decode(q, data.k, data.v, pos, buckets, config)
+    torch.cuda.synchronize()
+    for a, b in zip(good, again):
+        assert torch.equal(a, b)
+    pipeline.check_decode()  # nothing pending

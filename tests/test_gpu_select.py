@@ -118,6 +118,18 @@ def test_wide_rows_warn_and_stay_length_respecting():
     assert np.array_equal(_np(got), want)
 
 
+def test_sampled_listing_width_is_top_p():
+    """Rows wider than 4 * top_p: the reference returns torch.topk(k=min(top_p, N))
+    (select_fused.py:117), so a non-power-of-two top_p gives that width."""
+    g = torch.Generator().manual_seed(TIME + 1)
+    scores = torch.randn(8, 512, generator=g)
+    lengths = torch.tensor([512, 300, 100, 99, 7, 1, 0, 512], dtype=torch.int32)
+    with pytest.warns(UserWarning, match="sampled listing"):
+        got = select_fused.select_topk_scores(scores.to(DEV), lengths.to(DEV), 100)
+    assert tuple(got.shape) == (8, 100)
+    assert np.array_equal(_np(got), oracle.select_topk_scores(scores.numpy(), lengths.numpy(), 100))
+
+
 def _members(rows, cap, seed=TIME + 3, holes=0.15, top=997):
     g = torch.Generator().manual_seed(seed)
     m = (torch.rand(rows * cap, generator=g) * top).long().reshape(rows, cap)
@@ -396,9 +408,10 @@ def test_fused_select_span_tables_match_member_rows(window, sink, top_k):
 @pytest.mark.parametrize("spans", [True, False])
 def test_tree_select_fresh_buckets_and_shared_children(spans):
     """Nodes covering only the first 48 of 64 buckets (the rest join as fresh candidates
-    once visible) and two nodes sharing children (each bucket must be a candidate once):
-    lists equal the oracle's two-level beam, with span tables expanded from their ends or
-    the member rows walked."""
+    once visible), a row early in the cache (growth has made 2 of the 3 nodes; its other
+    visible buckets are fresh) and two nodes sharing children (each bucket must be a
+    candidate once): lists equal the oracle's two-level beam, with span tables expanded
+    from their ends or the member rows walked."""
     import dataclasses
 
     from lsa_rocm_lab.port.pipeline import Hierarchy, NodeLevel
@@ -411,7 +424,8 @@ def test_tree_select_fresh_buckets_and_shared_children(spans):
     children = children.expand(Hkv, 3, 16).contiguous().to(DEV)
     ncent = buckets.centroids_f32[:, children[0].long()].mean(dim=2).contiguous()  # [Hkv, 3, D]
     tree = Hierarchy(levels=[NodeLevel(ncent, children, centroids_bf16=ncent.to(torch.bfloat16))])
-    config = dataclasses.replace(workloads.TREE_131K, beam_width=2, top_p=24, window_size=64, sink_size=4)
+    config = dataclasses.replace(workloads.TREE_131K, beam_width=2, top_p=24, window_size=64, sink_size=4,
+                                 node_cluster_block_size=16)
     idx = pipeline.index_queries(data.q[:, -2:], Hkv)[0]  # [2, Hkv, D]
     pos = torch.tensor([T - 1, 2500], dtype=torch.int32, device=DEV)
     for score_dtype in ("fp32", "bf16"):
@@ -424,7 +438,7 @@ def test_tree_select_fresh_buckets_and_shared_children(spans):
                 visible = int((ends[g] <= int(pos[r]) + 1).sum())
                 want_l, want_n, _ = oracle.tree_select_row(
                     _np(idx[r, g]), _np(nc), _np(children[g]), _np(bc), _np(buckets.members[g]), int(pos[r]),
-                    visible=visible, covered=48, beam_width=2, top_p=24, top_k=config.top_k, window=64, sink=4,
+                    visible=visible, node_block=16, beam_width=2, top_p=24, top_k=config.top_k, window=64, sink=4,
                     mode=score_dtype)
                 assert np.array_equal(_np(lists[r, g]), want_l), (score_dtype, r, g)
                 assert int(lengths[r, g]) == want_n

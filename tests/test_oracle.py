@@ -55,6 +55,19 @@ def test_select_topk_scores_equals_brute_force(rows, cols, top_p):
         assert (got[r, len(want):] == oracle.EMPTY).all()
 
 
+def test_select_topk_scores_sampled_path_width():
+    """Rows wider than 4 * top_p take the reference's fallback (select_fused.py:97-117):
+    torch.topk(k=min(top_p, N)) over the length-masked packed keys, so the width is
+    min(top_p, N), not its next power of two."""
+    scores = RNG.standard_normal((8, 512)).astype(np.float32)
+    lengths = np.array([512, 300, 100, 99, 7, 1, 0, 512])
+    got = oracle.select_topk_scores(scores, lengths, 100)
+    assert got.shape == (8, 100)
+    keys = torch.from_numpy(oracle.pack_keys(scores, lengths))
+    want = torch.topk(keys, k=100, dim=1, sorted=True).values.numpy()
+    assert np.array_equal(got, want)
+
+
 def test_all_tied_scores_pick_ids_in_ascending_order():
     got = oracle.unpack_ids(oracle.select_topk_scores(np.zeros((2, 300), np.float32), np.array([300, 7]), 64))
     assert got[0].tolist() == list(range(64))
@@ -256,23 +269,63 @@ def test_flat_select_equals_brute_force():
         assert lists[r].tolist() == want and int(lengths[r]) == n
 
 
+def _growth_replay_literal(visible, page_buckets, node_block, size):
+    """The reference's growth replay (_tree.py:100-142) for a one-level tree, stepped
+    page end by page end exactly as written there, up to the page whose end is the
+    row's visible count; returns (covered, made[0])."""
+    covered, made = 0, 0
+    for end in range(page_buckets, visible + 1, page_buckets):
+        blocks = (end - covered) // node_block
+        if blocks < max(1, page_buckets // node_block):
+            continue
+        covered += blocks * node_block
+        made += blocks * node_block // size
+    return covered, made
+
+
+@pytest.mark.parametrize("page_buckets,node_block,size", [(8, 64, 4), (64, 64, 4), (128, 64, 16), (16, 16, 16)])
+def test_tree_growth_is_the_reference_replay(page_buckets, node_block, size):
+    n_nodes = 10_000
+    for pages in range(0, 70):
+        visible = pages * page_buckets
+        assert oracle.tree_growth(visible, node_block, n_nodes, size) == \
+            _growth_replay_literal(visible, page_buckets, node_block, size), (pages,)
+    # the table's nodes cap the growth; negative counts see nothing
+    assert oracle.tree_growth(640, 64, 3, 16) == (48, 3)
+    assert oracle.tree_growth(-5, 64, 3, 16) == (0, 0)
+
+
+def _tree_brute(q, ncent, children, bcent, visible, node_block, beam, top_p):
+    """The one-level beam by plain sorting: made nodes of whole node_block blocks, the best
+    `beam` of them (ties -> lower node), their visible children plus the fresh buckets,
+    each once, the best top_p (ties -> lower bucket)."""
+    size = children.shape[1]
+    covered = min(visible // node_block * node_block, ncent.shape[0] * size)
+    made = covered // size
+    ns = ncent.astype(np.float64) @ q.astype(np.float64)
+    kept = sorted(range(made), key=lambda j: (-ns[j], j))[:beam]
+    cand = {int(c) for j in kept for c in children[j] if 0 <= c < visible}
+    cand |= set(range(covered, visible))
+    bs = bcent.astype(np.float64) @ q.astype(np.float64)
+    return sorted(cand, key=lambda c: (-bs[c], c))[:top_p]
+
+
 def test_tree_select_row_equals_brute_force():
     D, n_nodes, size = 16, 6, 4
     q = RNG.standard_normal(D).astype(np.float32)
-    bcent = RNG.standard_normal((n_nodes * size, D)).astype(np.float32)
+    bcent = RNG.standard_normal((n_nodes * size + 5, D)).astype(np.float32)
     children = np.arange(n_nodes * size, dtype=np.int32).reshape(n_nodes, size)
-    ncent = bcent.reshape(n_nodes, size, D).mean(1)
-    members = np.arange(n_nodes * size * 3, dtype=np.int32).reshape(n_nodes * size, 3)
-    lst, n, picks = oracle.tree_select_row(q, ncent, children, bcent, members, position=10_000,
-                                           visible=n_nodes * size, covered=n_nodes * size, beam_width=2, top_p=5,
-                                           top_k=100, window=0, sink=0, mode="fp32")
-    ns = ncent.astype(np.float64) @ q.astype(np.float64)
-    beam = sorted(range(n_nodes), key=lambda j: (-ns[j], j))[:2]
-    cand = sorted(children[beam].ravel().tolist())
-    bs = bcent.astype(np.float64) @ q.astype(np.float64)
-    want = sorted(cand, key=lambda c: (-bs[c], c))[:5]
-    assert picks.tolist() == want
-    assert lst[:n].tolist() == [int(m) for b in want for m in members[b]]
+    ncent = bcent[: n_nodes * size].reshape(n_nodes, size, D).mean(1)
+    members = np.arange(bcent.shape[0] * 3, dtype=np.int32).reshape(bcent.shape[0], 3)
+    # every visible count, incl. partial node blocks and buckets past the nodes' reach
+    for visible in range(0, bcent.shape[0] + 1):
+        for node_block in (4, 8):
+            lst, n, picks = oracle.tree_select_row(q, ncent, children, bcent, members, position=10_000,
+                                                   visible=visible, node_block=node_block, beam_width=2,
+                                                   top_p=5, top_k=100, window=0, sink=0, mode="fp32")
+            want = _tree_brute(q, ncent, children, bcent, visible, node_block, 2, 5)
+            assert picks[: len(want)].tolist() == want and (picks[len(want):] == -1).all(), (visible, node_block)
+            assert lst[:n].tolist() == [int(m) for b in want for m in members[b]]
 
 
 # --------------------------------------------------------------------------- segment build

@@ -2,6 +2,8 @@
 rejection of malformed files. CPU only; the GPU tests drive the fused select from a loaded
 table."""
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -62,6 +64,18 @@ def test_span_tables_round_trip(tmp_path):
     assert got.spans
 
 
+def test_save_rejects_holes_and_bad_ids(tmp_path):
+    b = member_table((2,), 6, 8, 16, seed=4)
+    holed = b.members.clone()
+    holed[0, 0, 0] = -1  # a hole before real ids of the row
+    with pytest.raises(ValueError, match="real ids"):
+        tables.save_buckets(tmp_path / "h.safetensors", dataclasses.replace(b, members=holed))
+    low = b.members.clone()
+    low[1, 2, -1] = -5  # below the padding value
+    with pytest.raises(ValueError, match="real ids"):
+        tables.save_buckets(tmp_path / "l.safetensors", dataclasses.replace(b, members=low))
+
+
 def _write(path, tensors, meta):
     save_file(tensors, str(path), metadata=meta)
 
@@ -82,6 +96,8 @@ def test_malformed_files_raise(tmp_path):
         "int64": ({"offsets": good["offsets"].int()}, meta),
         "ends": ({"ends": torch.zeros(2, 5, dtype=torch.int32)}, meta),
         "needs its ends": ({}, {**meta, "spans": "1"}),
+        "must be >= 0": ({"member_ids": torch.cat([good["member_ids"][:1] * 0 - 1, good["member_ids"][1:]])}, meta),
+        "ends decrease": ({"ends": torch.tensor([[5, 4, 6, 7, 8, 9], [1, 2, 3, 4, 5, 6]], dtype=torch.int32)}, meta),
     }
     for i, (match, (change, m)) in enumerate(cases.items()):
         p = tmp_path / f"bad{i}.safetensors"
