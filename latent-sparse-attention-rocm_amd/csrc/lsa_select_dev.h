@@ -55,13 +55,15 @@ __device__ __forceinline__ int visible_count_block(int64_t position, int rows, c
   const int runs = (rows + step - 1) / step;
   const int s = min(rows - 1, (tid + 1) * step - 1);
   const bool le = tid < runs && (int64_t)ends[s] <= lim;  // run tid lies wholly at or below lim
-  if (lane == 0) lds[w] = (int)__popcll(__ballot(le));
+  const int c1 = (int)__popcll(__ballot(le));  // every lane votes
+  if (lane == 0) lds[w] = c1;
   __syncthreads();
   const int full = lds[0] + lds[1] + lds[2] + lds[3];  // runs wholly visible (ends are nondecreasing)
   const int base = min(full * step, rows);  // the last run may be short
   const int j = base + tid;
   const bool v2 = tid < step && j < rows && (int64_t)ends[j < rows ? j : rows - 1] <= lim;
-  if (lane == 0) lds[LSA_WAVES + w] = (int)__popcll(__ballot(v2));
+  const int c2 = (int)__popcll(__ballot(v2));
+  if (lane == 0) lds[LSA_WAVES + w] = c2;
   __syncthreads();
   return base + lds[LSA_WAVES] + lds[LSA_WAVES + 1] + lds[LSA_WAVES + 2] + lds[LSA_WAVES + 3];
 }
