@@ -233,6 +233,25 @@ int lsa_decode_flat(const void* q, const void* k, const void* v, int dtype, int6
                     int64_t n_counters, void* scratch, size_t scratch_bytes, int32_t* lists, int32_t* lengths,
                     void* out, int32_t* status, void* stream);
 
+/* lsa_decode_flat without caller buffers, for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart
+ * in the reference. The counters and scratch live in a 16 MiB file-scope device array per
+ * GPU (1 MiB of counters, 15 MiB of scratch); a call needing more returns
+ * LSA_ERR_WORKSPACE. The library never allocates on this path. The first call on a device
+ * clears the counters with a fill kernel on `stream`; every launch leaves them zero.
+ * Calls share the device's array and keep its last contents: calls that overlap on one
+ * GPU race and must not. reset_counters != 0 clears the counters first (after a launch
+ * that set *status). Arguments and outputs otherwise as lsa_decode_flat. */
+int lsa_decode_flat_noalloc(const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk,
+                            int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride,
+                            int64_t kv_head_stride, const void* centroids, const int32_t* members,
+                            const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables,
+                            int64_t group_tables, int score_mode, const int32_t* positions,
+                            int32_t cluster_block_size, int32_t block_buckets, int32_t top_p, int32_t window,
+                            int32_t sink, int32_t top_k, float scale, int32_t select_splits, int32_t readers,
+                            int32_t reset_counters, int32_t* lists, int32_t* lengths, void* out, int32_t* status,
+                            void* stream);
+
 /* Test hook (thread-local, this thread's later lsa_decode_flat calls): skip_publish != 0
  * makes the select workgroups skip publishing the record, and spin_limit > 0 replaces the
  * readers' poll limit, so a test can make the bounded wait give up with every workgroup
