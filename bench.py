@@ -300,6 +300,47 @@ def block_sparse_leg(args, torch, np):
             "gathered_bytes": gathered, "gbps": round(gbps, 1), "roofline_frac": round(gbps / HBM_PEAK_GBS, 4)}
 
 
+# ----------------------------------------------------------------------------- batched flat decode
+
+
+def batched_flat_leg(args, torch, np):
+    """The fused decode kernel in its bandwidth regime: B=32 sequences x 32768 tokens, Hq 32
+    / Hkv 8, D 128 bf16, 512 clustered Ward buckets per (sequence, kv-head), top-32 buckets:
+    one launch a step, rotating over 4 query tokens (the 4.3 GB cache is far beyond the MALL).
+    Reports gathered bytes / launch time against the 8 TB/s peak; lists checked bit-exact
+    against the unfused select on every (sequence, kv-head)."""
+    from lsa_rocm_lab import workloads
+    from lsa_rocm_lab.port import pipeline
+
+    B, T, NQ = 32, 32768, 4
+    data = workloads.clustered(T, HQ, HKV, D, n_clusters=512, seed=3, B=B, device="cuda", gen_device="cuda",
+                               q_tokens=NQ)
+    buckets = workloads.cluster_buckets(data, target=N_BUCKETS, workers=16)
+    config = workloads.FLAT_32K
+    pos = torch.full((B,), T - 1, device="cuda", dtype=torch.int32)
+    qs = [data.q[:, i:i + 1].contiguous() for i in range(NQ)]
+
+    def step(i):
+        out, lists, lengths = pipeline.flat_decode(qs[i % NQ], data.k, data.v, pos, buckets, config, scale=D ** -0.5)
+        return lists, lengths, out
+
+    res = [step(i) for i in range(NQ)]
+    torch.cuda.synchronize()
+    toks = [int(r[1].to(torch.int64).sum().item()) for r in res]
+    gathered = statistics.mean(toks) * D * 2 * 2
+    us = graph_launch_us(step, NQ, max(1, args.tree_steps // NQ), torch)
+    gbps = gathered / (us * 1e-6) / 1e9
+    idx = pipeline.index_queries(qs[0], HKV)[:, 0]
+    os.environ["LSA_SELECT_IMPL"] = "fused"
+    l2, n2 = pipeline.flat_select(idx, pos, buckets, config)
+    same = bool(torch.equal(l2, res[0][0]) and torch.equal(n2, res[0][1]))
+    log(f"batched flat decode B={B}: {us:.1f} us/step, {gbps:.0f} GB/s on {gathered / 1e6:.1f} MB gathered")
+    del data
+    return {"workload": "flat_decode_32k_b32", "batch": B, "context": T, "us_per_step": round(us, 2),
+            "gathered_bytes": int(gathered), "gbps": round(gbps, 1), "roofline_frac": round(gbps / HBM_PEAK_GBS, 4),
+            "lists_equal_unfused_select": same}
+
+
 # ----------------------------------------------------------------------------- tree decode
 
 
@@ -744,6 +785,9 @@ def main() -> int:
     # ---- the positional block-sparse arm through the same fused kernel
     block_sparse = block_sparse_leg(args, torch, np)
 
+    # ---- batched flat decode (B=32 x 32k): the fused kernel's bandwidth regime
+    batched = None if args.no_tree else batched_flat_leg(args, torch, np)
+
     # ---- batched tree decode (B=32 x 131k): the bandwidth-bound regime of the read
     tree = None
     if not args.no_tree:
@@ -835,6 +879,7 @@ def main() -> int:
         "decode_2k_fp32": {k: v for k, v in c1.items() if not k.startswith("_")},
         "prefill": prefill,
         "block_sparse_decode": block_sparse,
+        "batched_flat_decode": batched,
         "tree_decode": tree,
         "bucket_build": build,
         "cpu_baseline": cpu,

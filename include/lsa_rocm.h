@@ -202,6 +202,14 @@ int lsa_read_chunked_mfma_ok(int dtype, int32_t D, int32_t chunk);
  * lists [R, Hkv, top_k + window + sink] and lengths [R, Hkv] (identical to
  * lsa_select_flat's) and out [R, Hq, D] (the read of those lists).
  *
+ * select_splits: select workgroups per (row, kv-head), 1..min(256, rows) (the exchange
+ * form: the splits score slices of the table and the last to arrive publishes the picks
+ * to the readers), or 0: the replicated form, with no select workgroups - every reader
+ * workgroup scores its unit's whole table (a matrix-core screen with a proven error
+ * bound, then the exact canonical score of the few rows near the cut), so no workgroup
+ * waits on another before the gather; the picks and lists are the same. The replicated
+ * form needs LSA_TABLE_SPANS, bf16 scoring, head dim <= 128, at most 1024 buckets and 64
+ * picks (lsa_decode_flat_rep_ok).
  * readers: reader workgroups per (row, kv-head), 0 = default (picks + the window/sink
  * parts), at most 256; each reads its share of the list in tiles of
  * lsa_read_tile_tokens() slots. counters: lsa_decode_flat_counters() int32 words, zero
@@ -220,6 +228,9 @@ int lsa_read_chunked_mfma_ok(int dtype, int32_t D, int32_t chunk);
  * Limits: top_p (capped at rows) <= 64; head dim {32,64,128,256}; group {1,2,4,8}. */
 #define LSA_TABLE_SPANS 1
 int64_t lsa_decode_flat_counters(int64_t R, int32_t Hkv, int32_t rows, int32_t top_p);
+/* 1 when lsa_decode_flat's replicated form (select_splits 0) serves this shape. */
+int lsa_decode_flat_rep_ok(int dtype, int32_t D, int32_t group, int32_t rows, int32_t top_p, int score_mode,
+                           int32_t table_flags);
 size_t lsa_decode_flat_scratch_bytes(int dtype, int64_t R, int32_t Hq, int32_t Hkv, int32_t D, int32_t rows,
                                      int32_t top_p, int32_t window, int32_t sink, int32_t select_splits,
                                      int32_t readers);

@@ -38,6 +38,7 @@ namespace {
 // ------------------------------------------------------------------ host
 
 struct Plan {
+  bool rep;         // replicated select: every workgroup is a reader that selects for itself
   int K, kp, span, NR;
   int64_t cstride;  // words between record copies
   size_t keys_bytes, part_bytes, shmem;
@@ -67,6 +68,38 @@ size_t reader_lds_d(int D, int gq, int span) {
   }
 }
 
+template <int D>
+size_t rep_lds_gq(int gq, int span) {
+  switch (gq) {
+    case 1: return rep_ids_offset<D, 1>() + sizeof(int32_t) * (size_t)span;
+    case 2: return rep_ids_offset<D, 2>() + sizeof(int32_t) * (size_t)span;
+    case 4: return rep_ids_offset<D, 4>() + sizeof(int32_t) * (size_t)span;
+    default: return rep_ids_offset<D, 8>() + sizeof(int32_t) * (size_t)span;
+  }
+}
+
+// LDS of a replicated-select workgroup; 0 where that kernel does not exist (D = 256).
+size_t rep_lds_d(int D, int gq, int span) {
+  switch (D) {
+    case 32: return rep_lds_gq<32>(gq, span);
+    case 64: return rep_lds_gq<64>(gq, span);
+    case 128: return rep_lds_gq<128>(gq, span);
+    default: return 0;
+  }
+}
+
+// Why the replicated select cannot serve a shape (nullptr: it can).
+const char* rep_unfit(int dtype, int D, int gq, int rows, int top_p, int score_mode, int table_flags) {
+  if (!(table_flags & LSA_TABLE_SPANS)) return "it needs span tables (LSA_TABLE_SPANS)";
+  if (score_mode != LSA_SCORE_BF16) return "it scores bf16 centroids only";
+  if (D > 128) return "head dim above 128";
+  if (rows > kRepMaxRows) return "more buckets than it holds in LDS";
+  if ((top_p < rows ? top_p : rows) > kMaxPicks) return "more than 64 picks";
+  const int span = lsa_read_tile_tokens(dtype, D, gq);
+  if (span <= 0 || rep_lds_d(D, gq, span) + 4096 > kMaxLds) return "its LDS exceeds 64 KiB";
+  return nullptr;
+}
+
 // Record copies sit one 4 KiB page plus 256 bytes apart, so readers polling different
 // copies load from different memory channels.
 int64_t record_stride(int64_t units, int K) {
@@ -84,6 +117,7 @@ int default_readers(int K, int span, int window, int sink) {
 
 int plan_decode(int dtype, int D, int gq, int64_t units, int rows, int top_p, int window, int sink, int splits,
                 int readers, Plan* p) {
+  p->rep = splits == 0;
   p->K = top_p < rows ? top_p : rows;
   p->kp = next_pow2(p->K);
   p->span = lsa_read_tile_tokens(dtype, D, gq);
@@ -94,6 +128,11 @@ int plan_decode(int dtype, int D, int gq, int64_t units, int rows, int top_p, in
   p->cstride = record_stride(units, p->K);
   p->keys_bytes = splits > 1 ? (size_t)units * rows * sizeof(uint64_t) : 0;
   p->part_bytes = p->NR > 1 ? (size_t)units * p->NR * (size_t)(gq * (D + 2)) * sizeof(float) : 0;
+  if (p->rep) {
+    p->keys_bytes = 0;
+    p->shmem = rep_lds_d(D, gq, p->span);
+    return LSA_OK;
+  }
   const size_t sel = sel_keys_offset() + sizeof(uint64_t) * ((size_t)rows + p->kp);
   const size_t rd = reader_lds_d(D, gq, p->span);
   p->shmem = sel > rd ? sel : rd;
@@ -101,6 +140,13 @@ int plan_decode(int dtype, int D, int gq, int64_t units, int rows, int top_p, in
 }
 
 }  // namespace
+
+extern "C" int lsa_decode_flat_rep_ok(int dtype, int32_t D, int32_t group, int32_t rows, int32_t top_p,
+                                      int score_mode, int32_t table_flags) {
+  if (!(D == 32 || D == 64 || D == 128) || !(group == 1 || group == 2 || group == 4 || group == 8)) return 0;
+  if (rows < 1 || top_p < 1) return 0;
+  return rep_unfit(dtype, D, group, rows, top_p, score_mode, table_flags) == nullptr ? 1 : 0;
+}
 
 extern "C" int64_t lsa_decode_flat_counters(int64_t R, int32_t Hkv, int32_t rows, int32_t top_p) {
   if (R <= 0 || Hkv <= 0 || rows <= 0 || top_p <= 0) return 0;
@@ -157,8 +203,13 @@ extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int 
   LSA_REQUIRE(K <= kMaxPicks, LSA_ERR_SHAPE, "lsa_decode_flat: %d picks exceed %d", K, kMaxPicks);
   LSA_REQUIRE((int64_t)K * cap < 0x7FFFFFFF && (int64_t)top_k + window + sink <= 0x7FFFFFFF, LSA_ERR_SHAPE,
               "lsa_decode_flat: list too wide");
-  LSA_REQUIRE(select_splits >= 1 && select_splits <= 256 && select_splits <= rows, LSA_ERR_SHAPE,
-              "lsa_decode_flat: select splits in [1, min(256, rows)], got %d", select_splits);
+  LSA_REQUIRE(select_splits >= 0 && select_splits <= 256 && select_splits <= rows, LSA_ERR_SHAPE,
+              "lsa_decode_flat: select splits in [0, min(256, rows)], got %d", select_splits);
+  if (select_splits == 0) {
+    const char* why = rep_unfit(dtype, D, gq, rows, top_p, score_mode, table_flags);
+    LSA_REQUIRE(why == nullptr, LSA_ERR_SHAPE, "lsa_decode_flat: the replicated select (splits 0) does not apply: %s",
+                why ? why : "");
+  }
   const uintptr_t mis = ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)centroids) & 15;
   LSA_REQUIRE(mis == 0, LSA_ERR_ALIGN, "lsa_decode_flat: q/k/v/centroids must be 16-byte aligned");
   const int64_t esize = dtype == LSA_F32 ? 4 : 2;
@@ -170,8 +221,8 @@ extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int 
   if (units == 0) return LSA_OK;
   Plan p;
   LSA_TRY(plan_decode(dtype, D, gq, units, rows, top_p, window, sink, select_splits, readers, &p));
-  LSA_REQUIRE(p.kp + rows <= 6144, LSA_ERR_SHAPE, "lsa_decode_flat: %d columns + %d picks exceed 6144 LDS keys", rows,
-              p.kp);
+  LSA_REQUIRE(p.rep || p.kp + rows <= 6144, LSA_ERR_SHAPE,
+              "lsa_decode_flat: %d columns + %d picks exceed 6144 LDS keys", rows, p.kp);
   LSA_REQUIRE(p.shmem <= kMaxLds, LSA_ERR_SHAPE, "lsa_decode_flat: %zu bytes of LDS exceed %zu", p.shmem, kMaxLds);
   const int64_t grid = units * (select_splits + p.NR);
   LSA_REQUIRE(grid <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_decode_flat: too many workgroups");
@@ -194,7 +245,7 @@ extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int 
   a.row_tables = row_tables; a.group_tables = group_tables; a.positions = positions;
   a.cluster_block = cluster_block_size; a.block_buckets = block_buckets;
   a.K = p.K; a.kp = p.kp; a.window = window; a.sink = sink; a.top_k = top_k; a.W = top_k + window + sink;
-  a.S = select_splits; a.cs = (rows + select_splits - 1) / select_splits;
+  a.S = select_splits; a.cs = select_splits > 0 ? (rows + select_splits - 1) / select_splits : rows;
   a.span = p.span; a.NR = p.NR;
   a.scale_log2 = scale * kLog2e;
   a.spin_limit = decode_debug().spin_limit > 0 ? decode_debug().spin_limit
@@ -210,9 +261,9 @@ extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int 
   const dim3 g3((unsigned)grid);
   hipStream_t s = (hipStream_t)stream;
   const bool bf16 = score_mode == LSA_SCORE_BF16;
-  if (dtype == LSA_BF16) decode::launch_bf16(a, bf16, D, gq, g3, p.shmem, s);
-  else if (dtype == LSA_F16) decode::launch_f16(a, bf16, D, gq, g3, p.shmem, s);
-  else decode::launch_f32(a, bf16, D, gq, g3, p.shmem, s);
+  if (dtype == LSA_BF16) decode::launch_bf16(a, p.rep, bf16, D, gq, g3, p.shmem, s);
+  else if (dtype == LSA_F16) decode::launch_f16(a, p.rep, bf16, D, gq, g3, p.shmem, s);
+  else decode::launch_f32(a, p.rep, bf16, D, gq, g3, p.shmem, s);
   LSA_LAUNCHED("lsa_decode_flat");
   return LSA_OK;
 }

@@ -17,9 +17,12 @@ constexpr int kMaxReaders = 256;     // readers per unit (split partials of the 
 constexpr int kRecordCopies = 8;     // copies of every record, polled by different readers
 constexpr size_t kMaxLds = 64 * 1024;
 
-// Phase hooks: no-ops unless a build defines DECODE_MARK(k) (timestamps for profiling).
+// Phase hooks: no-ops unless a build defines DECODE_MARK(k) (timestamps for profiling; k < 16:
+// 0-6 the exchange form's select and reader phases, 8-11 the replicated select's).
 #ifndef DECODE_MARK
 #define DECODE_MARK(k) ((void)0)
+#define DECODE_TRACE_BEGIN() ((void)0)
+#define DECODE_TRACE_END() ((void)0)
 #endif
 
 struct DecodeArgs {
@@ -112,8 +115,8 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
   uint64_t* keys = (uint64_t*)(smem + sel_keys_offset());  // [rows]
   uint64_t* best = keys + a.rows;                           // [kp]
   const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
-  const int64_t r = i / a.G;
-  const int g = (int)(i % a.G);
+  const int64_t r = (uint32_t)i / (uint32_t)a.G;  // units < 2^31 (checked on the host): 32-bit division
+  const int g = (int)((uint32_t)i % (uint32_t)a.G);
   const int64_t position = a.positions[r];
   const int64_t t = r * a.row_tables + g * a.group_tables;
   const CT* cent = (const CT*)a.centroids + t * a.rows * (int64_t)D;
@@ -126,10 +129,50 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
   DECODE_MARK(0);
 
   float qs[SPAN];
-  group_mean_slice<T, SPAN, GQ>((const T*)a.q + (r * a.Hq + (int64_t)g * GQ) * D, tid & 15, BF16_MODE, qs);
-  score_keys<CT, SPAN>(
-      qs, cent, D, n_local, [&](int j) { return c0 + j; },
-      [&](int j) { return ends ? (int64_t)ends[c0 + j] <= lim : c0 + j < vis; }, keys + c0);
+  const T* qrow = (const T*)a.q + (r * a.Hq + (int64_t)g * GQ) * D;
+  constexpr int GROUPS = LSA_BLOCK / 16;
+  if (n_local <= 2 * GROUPS) {
+    // one memory round trip: the group's query rows, the (at most) two centroid rows each
+    // 16-lane group scores and their span ends are all in flight before the index query
+    // is formed (group_mean_slice's arithmetic) and the rows are scored (score_keys')
+    const int grp = tid >> 4, p = tid & 15;
+    SpanRaw<T, SPAN> qraw[GQ];
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) qraw[h].load(qrow + (int64_t)h * D + p * SPAN);
+    SpanRaw<CT, SPAN> craw[2];
+    int col[2];
+    int32_t e[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int j = k * GROUPS + grp;
+      col[k] = j < n_local ? c0 + j : -1;
+      const int cc = col[k] >= 0 ? col[k] : c0;
+      craw[k].load(cent + (int64_t)cc * D + p * SPAN);
+      e[k] = ends ? ends[cc] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < SPAN; ++j) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) acc += qraw[h].at(j);
+      const float x = acc / (float)GQ;
+      qs[j] = BF16_MODE ? bf16_round(x) : x;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      double acc = 0.0;
+#pragma unroll
+      for (int x = 0; x < SPAN; ++x) acc = fma((double)qs[x], (double)craw[k].at(x), acc);
+      const float sc = score_tree16(acc);
+      const bool keep = col[k] >= 0 && (ends ? (int64_t)e[k] <= lim : col[k] < vis);
+      if (p == 0 && col[k] >= 0) keys[col[k]] = keep ? key_to_u(pack_key(sc, col[k])) : 0;
+    }
+  } else {
+    group_mean_slice<T, SPAN, GQ>(qrow, tid & 15, BF16_MODE, qs);
+    score_keys<CT, SPAN>(
+        qs, cent, D, n_local, [&](int j) { return c0 + j; },
+        [&](int j) { return ends ? (int64_t)ends[c0 + j] <= lim : c0 + j < vis; }, keys + c0);
+  }
   DECODE_MARK(1);
 
   if (a.S > 1) {
@@ -259,84 +302,26 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
   DECODE_MARK(6);
 }
 
+// The reader's work once it holds its unit's picks (sh.pick: a pick's bucket, or its first
+// kept id for span tables; sh.start / sh.n / sh.abase: its list slots, kept count and first
+// dense part; sh.filled, sh.pparts): expand each of its parts into `ids` and the list,
+// attend them, write its share of the list padding, publish its split partial and arrive;
+// the last reader of the unit combines the partials (and, with clear_record, zeroes the
+// unit's record copies for the next launch).
 template <typename T, int D, int GQ>
-__device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int64_t i, int role) {
+__device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh, int32_t* ids, int64_t i, int role,
+                                           const QueryRegs<T, D, GQ>& qr, int64_t position, bool clear_record) {
   using S = ReadShape<T, D, GQ>;
   constexpr int VEC = S::VEC, LPT = S::LPT;
   constexpr int PSTRIDE = GQ * (D + 2);
-  RdLds<D, GQ>& sh = *(RdLds<D, GQ>*)smem;
-  int32_t* ids = (int32_t*)(smem + rd_ids_offset<D, GQ>());  // [span]
   const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
   const int K = a.K, span = a.span, words = 2 * K;
-  const int64_t r = i / a.G;
-  const int g = (int)(i % a.G);
-  const int64_t position = a.positions[r];
+  const int64_t r = (uint32_t)i / (uint32_t)a.G;  // units < 2^31 (checked on the host): 32-bit division
+  const int g = (int)((uint32_t)i % (uint32_t)a.G);
   const int64_t wstart = window_start_of(position, a.window);
   const int64_t n_win = position + 1 - wstart > 0 ? position + 1 - wstart : 0;
   const int64_t n_sink = a.sink < wstart ? a.sink : wstart;
   const int n_tail = (int)(n_win + n_sink);
-  const int32_t* mine = a.record + (role % kRecordCopies) * a.cstride + i * words;
-  DECODE_MARK(0);
-
-  // the query rows go out before the wait
-  const T* qrow = (const T*)a.q + (r * a.Hq + (int64_t)g * GQ) * D;
-  QueryRegs<T, D, GQ> qr;
-  qr.load(qrow, a.scale_log2);
-
-  // wait for the unit's record; wave 0 polls its copy and decodes it
-  if (w == 0) {
-    int32_t wa = 1, wb = 1;
-    int bad = 0;
-    for (int it = 0;; ++it) {
-      wa = lane < K ? coherent_load_i32(mine + lane) : 1;
-      wb = lane < K ? coherent_load_i32(mine + K + lane) : 1;
-      if (__all(wa != 0 && wb != 0)) break;
-      if (it >= a.spin_limit) {
-        bad = 1;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-    }
-    const int end = wb - 1;
-    int prev = __shfl_up(end, 1, LSA_WAVE);
-    if (lane == 0) prev = 0;
-    const int n = lane < K ? end - prev : 0;
-    const int parts = (n + span - 1) / span;
-    int incl = parts;
-#pragma unroll
-    for (int d = 1; d < LSA_WAVE; d <<= 1) {
-      const int y = __shfl_up(incl, d, LSA_WAVE);
-      if (lane >= d) incl += y;
-    }
-    if (lane < K) {
-      sh.pick[lane] = wa - 2;
-      sh.start[lane] = prev;
-      sh.n[lane] = n;
-      sh.abase[lane] = incl - parts;
-    }
-    const int filled = __shfl(end, K - 1, LSA_WAVE);
-    const int pparts = __shfl(incl, K - 1, LSA_WAVE);
-    if (lane == 0) {
-      sh.filled = filled;
-      sh.pparts = pparts;
-      sh.bad = bad;
-      if (bad && a.status) __hip_atomic_store(a.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
-  }
-  __syncthreads();
-  DECODE_MARK(1);
-  if (sh.bad) {
-    // no record: this reader writes nothing but still arrives, so the unit's counter
-    // resets; *status tells the caller the unit's outputs are invalid
-    if (arrive_last(&a.rd_count[i], a.NR, &sh.rd.flag)) {
-      for (int x = tid; x < kRecordCopies * words; x += LSA_BLOCK) {
-        const int c = x / words, k = x - c * words;
-        coherent_store_i32(a.record + c * a.cstride + i * words + k, 0);
-      }
-    }
-    return;
-  }
-
   const int filled = sh.filled, pparts = sh.pparts;
   const int n_act = pparts + (n_tail + span - 1) / span;  // dense parts: picks' then the tail's
   const int n_part = n_act < a.NR ? n_act : a.NR;        // readers with work (one partial each)
@@ -433,65 +418,471 @@ __device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int
   }
   DECODE_MARK(4);
   if (!arrive_last(&a.rd_count[i], a.NR, &sh.rd.flag)) return;
+  (void)w;
   DECODE_MARK(5);
   if (n_part > 1) {
     combine_partials<T, D, GQ>(sh.rd, parts, n_part, outp, 0);
   } else if (n_part == 0) {  // nothing to read: zeros
     for (int k = tid; k < GQ * D; k += LSA_BLOCK) store_out<T>(outp + k, 0.0f);
   }
-  for (int x = tid; x < kRecordCopies * words; x += LSA_BLOCK) {
-    const int c = x / words, k = x - c * words;
-    coherent_store_i32(a.record + c * a.cstride + i * words + k, 0);
+  if (clear_record) {
+    for (int x = tid; x < kRecordCopies * words; x += LSA_BLOCK) {
+      const int c = x / words, k = x - c * words;
+      coherent_store_i32(a.record + c * a.cstride + i * words + k, 0);
+    }
   }
   DECODE_MARK(6);
+}
+
+template <typename T, int D, int GQ>
+__device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int64_t i, int role) {
+  using S = ReadShape<T, D, GQ>;
+  constexpr int VEC = S::VEC, LPT = S::LPT;
+  constexpr int PSTRIDE = GQ * (D + 2);
+  RdLds<D, GQ>& sh = *(RdLds<D, GQ>*)smem;
+  int32_t* ids = (int32_t*)(smem + rd_ids_offset<D, GQ>());  // [span]
+  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
+  const int K = a.K, span = a.span, words = 2 * K;
+  const int64_t r = (uint32_t)i / (uint32_t)a.G;  // units < 2^31 (checked on the host): 32-bit division
+  const int g = (int)((uint32_t)i % (uint32_t)a.G);
+  const int64_t position = a.positions[r];
+  const int64_t wstart = window_start_of(position, a.window);
+  const int64_t n_win = position + 1 - wstart > 0 ? position + 1 - wstart : 0;
+  const int64_t n_sink = a.sink < wstart ? a.sink : wstart;
+  const int n_tail = (int)(n_win + n_sink);
+  const int32_t* mine = a.record + (role % kRecordCopies) * a.cstride + i * words;
+  DECODE_MARK(0);
+
+  // the query rows go out before the wait
+  const T* qrow = (const T*)a.q + (r * a.Hq + (int64_t)g * GQ) * D;
+  QueryRegs<T, D, GQ> qr;
+  qr.load(qrow, a.scale_log2);
+
+  // wait for the unit's record; wave 0 polls its copy and decodes it
+  if (w == 0) {
+    int32_t wa = 1, wb = 1;
+    int bad = 0;
+    for (int it = 0;; ++it) {
+      wa = lane < K ? coherent_load_i32(mine + lane) : 1;
+      wb = lane < K ? coherent_load_i32(mine + K + lane) : 1;
+      if (__all(wa != 0 && wb != 0)) break;
+      if (it >= a.spin_limit) {
+        bad = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    const int end = wb - 1;
+    int prev = __shfl_up(end, 1, LSA_WAVE);
+    if (lane == 0) prev = 0;
+    const int n = lane < K ? end - prev : 0;
+    const int parts = (n + span - 1) / span;
+    int incl = parts;
+#pragma unroll
+    for (int d = 1; d < LSA_WAVE; d <<= 1) {
+      const int y = __shfl_up(incl, d, LSA_WAVE);
+      if (lane >= d) incl += y;
+    }
+    if (lane < K) {
+      sh.pick[lane] = wa - 2;
+      sh.start[lane] = prev;
+      sh.n[lane] = n;
+      sh.abase[lane] = incl - parts;
+    }
+    const int filled = __shfl(end, K - 1, LSA_WAVE);
+    const int pparts = __shfl(incl, K - 1, LSA_WAVE);
+    if (lane == 0) {
+      sh.filled = filled;
+      sh.pparts = pparts;
+      sh.bad = bad;
+      if (bad && a.status) __hip_atomic_store(a.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  }
+  __syncthreads();
+  DECODE_MARK(1);
+  if (sh.bad) {
+    // no record: this reader writes nothing but still arrives, so the unit's counter
+    // resets; *status tells the caller the unit's outputs are invalid
+    if (arrive_last(&a.rd_count[i], a.NR, &sh.rd.flag)) {
+      for (int x = tid; x < kRecordCopies * words; x += LSA_BLOCK) {
+        const int c = x / words, k = x - c * words;
+        coherent_store_i32(a.record + c * a.cstride + i * words + k, 0);
+      }
+    }
+    return;
+  }
+
+  read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, true);
+}
+
+// ------------------------------------------------------------------ replicated select
+
+// Every reader workgroup selects for itself (no select workgroups, no cross-workgroup wait
+// before the gather). The canonical top-K of a unit is found exactly in three steps:
+//  1. screen: all visible rows are scored on the matrix cores (bf16 16x16x32 MFMAs, fp32
+//     sums) together with S_r = sum_d |q_d| |c_rd| (the same MFMA on the absolute values).
+//     The products of bf16 operands are exact in fp32, so any fp32 summation order of the
+//     D products is within 127 * 2^-23 * S_r < 2^-16 S_r of the exact dot product, and the
+//     canonical score (fp64 sums, one fp32 rounding) within 2^-24 |exact| + 2^-48 S_r <=
+//     2^-23 S_r of it: |screen - canonical| < 2^-15 S_r. Each row gets the interval
+//     [lo, hi] = screen -/+ (2^-14 S_r + 2^-90), which holds its canonical score.
+//  2. threshold: at least K rows have lo >= L for any L up to the K-th largest lo, so the
+//     canonical K-th best score is >= L and every row of the canonical top-K has hi >= L.
+//     L is the lower edge of a 256-bin histogram of lo: the candidates are the rows whose
+//     hi falls in that bin or above (a superset of hi >= L, as the bin map is monotone).
+//  3. the candidates (usually K plus a few) are re-scored exactly (the canonical fp64
+//     order) and sorted by packed key; the best K are the canonical top-K, ties to the
+//     lower bucket.
+// Non-finite scores or more than 64 candidates take the exact path for every row (the
+// same scoring and top-K as the select workgroups of decode_flat_kernel). Every reader of
+// a unit computes the same picks (identical inputs and instruction sequence). Span tables,
+// bf16 scoring, head dim 32/64/128, at most kRepMaxRows buckets and 64 picks.
+constexpr int kRepMaxRows = 1024;
+constexpr int kRepMaxCand = LSA_WAVE;
+
+struct RepLds {
+  float lo[kRepMaxRows];      // screen - bound (-inf: not visible); the exact path's u64 keys
+  float hi[kRepMaxRows];      // screen + bound
+  int32_t ends[kRepMaxRows];  // the table's span ends
+  int hist[256];
+  TopkScratch tks;
+  RadixState st;
+  uint64_t ckey[kRepMaxCand];  // candidates' exact keys; the exact path's sorted best
+  int cand[kRepMaxCand];
+  float wmin[LSA_WAVES], wmax[LSA_WAVES];
+  int wcnt[LSA_WAVES], wbad[LSA_WAVES];
+  int ncand, cut;
+};
+
+template <int D, int GQ>
+constexpr size_t rep_extra_offset() {
+  return (sizeof(RdLds<D, GQ>) + 15) & ~(size_t)15;
+}
+template <int D, int GQ>
+constexpr size_t rep_ids_offset() {
+  return (rep_extra_offset<D, GQ>() + sizeof(RepLds) + 15) & ~(size_t)15;
+}
+
+template <typename T, int D, int GQ>
+__device__ __forceinline__ void rep_role(const DecodeArgs& a, char* smem, int64_t i, int role) {
+  constexpr int NM = D / 32;    // 32-dim chunks of a centroid row (MFMA K)
+  constexpr int SPAN = D / 16;  // dims a lane holds in the 16-lane canonical layout
+  constexpr float kBound = 6.103515625e-05f;  // 2^-14
+  constexpr float kTiny = 8.077935669463161e-28f;  // 2^-90
+  RdLds<D, GQ>& sh = *(RdLds<D, GQ>*)smem;
+  RepLds& ex = *(RepLds*)(smem + rep_extra_offset<D, GQ>());
+  int32_t* ids = (int32_t*)(smem + rep_ids_offset<D, GQ>());
+  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
+  const int row4 = lane >> 4, col = lane & 15;
+  const int K = a.K, rows = a.rows;
+  const int64_t r = (uint32_t)i / (uint32_t)a.G;  // units < 2^31 (checked on the host): 32-bit division
+  const int g = (int)((uint32_t)i % (uint32_t)a.G);
+  const int64_t position = a.positions[r];
+  const int64_t t = r * a.row_tables + g * a.group_tables;
+  const bf16_t* cent = (const bf16_t*)a.centroids + t * (int64_t)rows * D;
+  const int32_t* ends = a.ends + t * rows;
+  const int64_t lim = position + 1;
+  const int64_t wstart = window_start_of(position, a.window);
+  const T* qrow = (const T*)a.q + (r * a.Hq + (int64_t)g * GQ) * D;
+  DECODE_MARK(8);
+
+  // the span ends into LDS, the query rows for the read, the index query (the group mean,
+  // bf16-rounded, in the 16-lane layout: lane p holds dims SPAN p .. SPAN p + SPAN)
+  for (int m = tid; m < rows; m += LSA_BLOCK) ex.ends[m] = ends[m];
+  QueryRegs<T, D, GQ> qr;
+  qr.load(qrow, a.scale_log2);
+  float qs[SPAN];
+  group_mean_slice<T, SPAN, GQ>(qrow, tid & 15, true, qs);
+  // the screen's B operand: lane (row4, col) holds dims 32 c + 8 row4 .. + 8 of column col;
+  // column 0 = the index query, column 1 = its absolute values, the rest zero
+  uint32_t qpk[SPAN / 2];
+#pragma unroll
+  for (int k = 0; k < SPAN / 2; ++k)
+    qpk[k] = (uint32_t)f32_to_bf16(qs[2 * k]) | ((uint32_t)f32_to_bf16(qs[2 * k + 1]) << 16);
+  uint4 bq[NM];
+#pragma unroll
+  for (int c = 0; c < NM; ++c) {
+    uint32_t v4[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int d = 32 * c + 8 * row4 + 2 * k;  // first of the two dims of word k
+      const uint32_t x = (uint32_t)__shfl((int)qpk[(2 * k % SPAN) / 2], d / SPAN, LSA_WAVE);
+      v4[k] = col == 0 ? x : (col == 1 ? (x & 0x7FFF7FFFu) : 0u);
+    }
+    bq[c] = make_uint4(v4[0], v4[1], v4[2], v4[3]);
+  }
+  if (tid < 256) ex.hist[tid] = 0;
+  if (tid == 0) ex.ncand = 0;
+
+  // 1. screen: wave w takes 16-row groups w, w + 4, ...; two groups' rows in flight at once
+  int bad = 0;
+  const int ngrp = (rows + 15) / 16;
+  constexpr int GB = 2;
+  for (int gb = w; gb < ngrp; gb += LSA_WAVES * GB) {
+    uint4 A[GB][NM];
+    int e4[GB][4];
+#pragma unroll
+    for (int gi = 0; gi < GB; ++gi) {
+      const int grp = gb + LSA_WAVES * gi;
+      const int m = min(16 * grp + col, rows - 1);
+#pragma unroll
+      for (int c = 0; c < NM; ++c) A[gi][c] = *(const uint4*)(cent + (int64_t)m * D + 32 * c + 8 * row4);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) e4[gi][u] = ends[min(16 * grp + 4 * row4 + u, rows - 1)];
+    }
+#pragma unroll
+    for (int gi = 0; gi < GB; ++gi) {
+      const int grp = gb + LSA_WAVES * gi;
+      if (grp >= ngrp) break;  // wave-uniform
+      f32x4_t cs = {0.0f, 0.0f, 0.0f, 0.0f}, cb = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < NM; ++c) {
+        cs = Mfma16<bf16_t>::run(A[gi][c], bq[c], cs);
+        const uint4 ab = make_uint4(A[gi][c].x & 0x7FFF7FFFu, A[gi][c].y & 0x7FFF7FFFu, A[gi][c].z & 0x7FFF7FFFu,
+                                    A[gi][c].w & 0x7FFF7FFFu);
+        cb = Mfma16<bf16_t>::run(ab, bq[c], cb);
+      }
+      // lane (row4, 0) holds the screens of rows 16 grp + 4 row4 + u, lane (row4, 1) their S
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float sabs = __shfl(cb[u], (lane + 1) & (LSA_WAVE - 1), LSA_WAVE);
+        const int m = 16 * grp + 4 * row4 + u;
+        if (col == 0 && m < rows) {
+          const float s = cs[u];
+          const float bnd = sabs * kBound + kTiny;
+          const bool fin = (s - s == 0.0f) && (bnd - bnd == 0.0f);
+          const bool vis = (int64_t)e4[gi][u] <= lim;
+          bad |= (vis && !fin) ? 1 : 0;
+          ex.lo[m] = vis ? s - bnd : -INFINITY;
+          ex.hi[m] = vis ? s + bnd : -INFINITY;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  DECODE_MARK(9);
+
+  // 2. visible count, range of lo, histogram cut
+  float mn = INFINITY, mx = -INFINITY;
+  int cnt = 0;
+  for (int m = tid; m < rows; m += LSA_BLOCK) {
+    const float x = ex.lo[m];
+    const bool live = x != -INFINITY;
+    mn = live ? fminf(mn, x) : mn;
+    mx = live ? fmaxf(mx, x) : mx;
+    cnt += live ? 1 : 0;
+  }
+#pragma unroll
+  for (int x = LSA_WAVE / 2; x >= 1; x >>= 1) {
+    mn = fminf(mn, __shfl_xor(mn, x, LSA_WAVE));
+    mx = fmaxf(mx, __shfl_xor(mx, x, LSA_WAVE));
+    cnt += __shfl_xor(cnt, x, LSA_WAVE);
+    bad |= __shfl_xor(bad, x, LSA_WAVE);
+  }
+  if (lane == 0) { ex.wmin[w] = mn; ex.wmax[w] = mx; ex.wcnt[w] = cnt; ex.wbad[w] = bad; }
+  __syncthreads();
+  mn = fminf(fminf(ex.wmin[0], ex.wmin[1]), fminf(ex.wmin[2], ex.wmin[3]));
+  mx = fmaxf(fmaxf(ex.wmax[0], ex.wmax[1]), fmaxf(ex.wmax[2], ex.wmax[3]));
+  cnt = ex.wcnt[0] + ex.wcnt[1] + ex.wcnt[2] + ex.wcnt[3];
+  bool slow = (ex.wbad[0] | ex.wbad[1] | ex.wbad[2] | ex.wbad[3]) != 0;  // uniform
+  const float scale = mx > mn ? 256.0f / (mx - mn) : 0.0f;
+  auto bin_of = [&](float x) {
+    const float b = (x - mn) * scale;
+    return b < 0.0f ? 0 : (b >= 255.0f ? 255 : (int)b);
+  };
+  int cut = 0;  // cnt <= K: every visible row is a candidate
+  if (!slow && cnt > K) {
+    for (int m = tid; m < rows; m += LSA_BLOCK) {
+      const float x = ex.lo[m];
+      if (x != -INFINITY) atomicAdd(&ex.hist[bin_of(x)], 1);
+    }
+    __syncthreads();
+    if (w == 0) {
+      // lane l owns bins 255 - 4l .. 252 - 4l; the highest bin whose suffix count reaches K
+      const int c0 = ex.hist[255 - 4 * lane], c1 = ex.hist[254 - 4 * lane];
+      const int c2 = ex.hist[253 - 4 * lane], c3 = ex.hist[252 - 4 * lane];
+      const int mine = c0 + c1 + c2 + c3;
+      const int inc = wave_inclusive_sum(mine);
+      const int above = inc - mine;
+      const bool here = above < K && K <= inc;
+      const int d = above + c0 >= K ? 255 - 4 * lane
+                  : (above + c0 + c1 >= K ? 254 - 4 * lane : (above + c0 + c1 + c2 >= K ? 253 - 4 * lane
+                                                                                         : 252 - 4 * lane));
+      const uint64_t hm = __ballot(here);
+      const int cutv = __shfl(d, hm ? __ffsll((long long)hm) - 1 : 0, LSA_WAVE);
+      if (lane == 0) ex.cut = cutv;
+    }
+    __syncthreads();
+    cut = ex.cut;
+  }
+  if (!slow) {
+    for (int m = tid; m < rows; m += LSA_BLOCK) {
+      const float x = ex.hi[m];
+      if (x != -INFINITY && (cnt <= K || bin_of(x) >= cut)) {
+        const int slot = atomicAdd(&ex.ncand, 1);
+        if (slot < kRepMaxCand) ex.cand[slot] = m;
+      }
+    }
+    __syncthreads();
+    slow = ex.ncand > kRepMaxCand;
+  }
+  DECODE_MARK(10);
+
+  const int kp = a.kp;
+  if (!slow) {
+    // 3. exact scores of the candidates (16 lanes a row, 16 rows a pass), then one wave
+    // sorts their keys
+    const int nc = ex.ncand;
+    for (int jb = 0; jb < nc; jb += LSA_BLOCK / 16) {
+      const int j = jb + (tid >> 4);
+      const int m = ex.cand[j < nc ? j : 0];
+      SpanRaw<bf16_t, SPAN> raw;
+      raw.load(cent + (int64_t)m * D + (tid & 15) * SPAN);
+      double acc = 0.0;
+#pragma unroll
+      for (int e = 0; e < SPAN; ++e) acc = fma((double)qs[e], (double)raw.at(e), acc);
+      const float sc = score_tree16(acc);
+      if ((tid & 15) == 0 && j < nc) ex.ckey[j] = key_to_u(pack_key(sc, m));
+    }
+    __syncthreads();
+    if (w == 0) {
+      uint64_t v = lane < nc ? ex.ckey[lane] : 0;
+      v = wave_sort64_desc(v);
+      const int32_t b = key_column(u_to_key(v));
+      sh.pick[lane] = (lane < K && b >= 0 && b < rows) ? b : -1;
+    }
+  } else {
+    // exact canonical scores of every visible row, then the block top-K
+    uint64_t* keys = (uint64_t*)ex.lo;  // lo and hi: kRepMaxRows u64
+    score_keys<bf16_t, SPAN>(
+        qs, cent, D, rows, [&](int j) { return j; }, [&](int j) { return (int64_t)ex.ends[j] <= lim; }, keys);
+    __syncthreads();
+    block_topk_sorted(keys, rows, K, kp, ex.ckey, &ex.tks, &ex.st);
+    if (w == 0) {
+      const uint64_t v = lane < kp ? ex.ckey[lane] : 0;
+      const int32_t b = key_column(u_to_key(v));
+      sh.pick[lane] = (lane < K && b >= 0 && b < rows) ? b : -1;
+    }
+  }
+  __syncthreads();
+  DECODE_MARK(11);
+
+  // each pick's kept range [max(begin, sink), min(end, window start)), its list slots and
+  // its dense parts (as the record of the exchange form gives them)
+  if (w == 0) {
+    const int b = lane < K ? sh.pick[lane] : -1;
+    int cntk = 0, first = 0;
+    if (b >= 0) {
+      const int64_t begin = b > 0 ? ex.ends[b - 1] : 0, end = ex.ends[b];
+      const int64_t lo = begin > a.sink ? begin : a.sink, hi = end < wstart ? end : wstart;
+      cntk = hi > lo ? (int)(hi - lo) : 0;
+      first = (int)lo;
+    }
+    const int incl = wave_inclusive_sum(cntk);
+    const int end = incl < a.top_k ? incl : a.top_k;
+    int prev = __shfl_up(end, 1, LSA_WAVE);
+    if (lane == 0) prev = 0;
+    const int n = lane < K ? end - prev : 0;
+    const int parts = (n + a.span - 1) / a.span;
+    const int pincl = wave_inclusive_sum(parts);
+    if (lane < K) {
+      sh.pick[lane] = first;
+      sh.start[lane] = prev;
+      sh.n[lane] = n;
+      sh.abase[lane] = pincl - parts;
+    }
+    const int filled = __shfl(end, K - 1, LSA_WAVE);
+    const int pparts = __shfl(pincl, K - 1, LSA_WAVE);  // every lane takes part in the shuffles
+    if (lane == 0) {
+      sh.filled = filled;
+      sh.pparts = pparts;
+      if (role == 0) {
+        const int64_t n_win = position + 1 - wstart > 0 ? position + 1 - wstart : 0;
+        const int64_t n_sink = a.sink < wstart ? a.sink : wstart;
+        a.lengths[i] = filled + (int)n_win + (int)n_sink;
+      }
+    }
+  }
+  __syncthreads();
+  read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, false);
+}
+
+// One workgroup per (unit, reader), unit fastest: every workgroup is a reader that
+// selects for itself (rep_role).
+template <typename T, int D, int GQ>
+__global__ __launch_bounds__(LSA_BLOCK) void decode_rep_kernel(DecodeArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  const uint32_t units = (uint32_t)(a.R * a.G);  // the grid is < 2^31 workgroups (checked on the host)
+  const uint32_t id = blockIdx.x;
+  DECODE_TRACE_BEGIN();
+  rep_role<T, D, GQ>(a, smem, id % units, (int)(id / units));
+  DECODE_TRACE_END();
 }
 
 template <typename T, typename CT, int D, int GQ>
 __global__ __launch_bounds__(LSA_BLOCK) void decode_flat_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) char smem[];
-  const int64_t units = a.R * a.G;
-  const int64_t id = blockIdx.x;
-  const int64_t nsel = units * a.S;
+  const uint32_t units = (uint32_t)(a.R * a.G);  // the grid is < 2^31 workgroups (checked on the host)
+  const uint32_t id = blockIdx.x;
+  const uint32_t nsel = units * (uint32_t)a.S;
+  DECODE_TRACE_BEGIN();
   if (id < nsel) {
     select_role<T, CT, D, GQ>(a, smem, id % units, (int)(id / units));
   } else {
-    const int64_t rid = id - nsel;  // readers: unit fastest, then role (low roles have work)
+    const uint32_t rid = id - nsel;  // readers: unit fastest, then role (low roles have work)
     reader_role<T, D, GQ>(a, smem, rid % units, (int)(rid / units));
   }
+  DECODE_TRACE_END();
 }
 
 // ------------------------------------------------------------------ launch
 
+template <typename T, typename CT, int D, int GQ>
+void launch_one(const DecodeArgs& a, bool rep, dim3 grid, size_t shmem, hipStream_t s) {
+  if constexpr (D <= 128 && __is_same(CT, bf16_t)) {
+    if (rep) {
+      decode_rep_kernel<T, D, GQ><<<grid, LSA_BLOCK, shmem, s>>>(a);
+      return;
+    }
+  }
+  decode_flat_kernel<T, CT, D, GQ><<<grid, LSA_BLOCK, shmem, s>>>(a);
+}
+
 template <typename T, typename CT, int D>
-void launch_gq(const DecodeArgs& a, int gq, dim3 grid, size_t shmem, hipStream_t s) {
+void launch_gq(const DecodeArgs& a, bool rep, int gq, dim3 grid, size_t shmem, hipStream_t s) {
   switch (gq) {
-    case 1: decode_flat_kernel<T, CT, D, 1><<<grid, LSA_BLOCK, shmem, s>>>(a); break;
-    case 2: decode_flat_kernel<T, CT, D, 2><<<grid, LSA_BLOCK, shmem, s>>>(a); break;
-    case 4: decode_flat_kernel<T, CT, D, 4><<<grid, LSA_BLOCK, shmem, s>>>(a); break;
-    default: decode_flat_kernel<T, CT, D, 8><<<grid, LSA_BLOCK, shmem, s>>>(a); break;
+    case 1: launch_one<T, CT, D, 1>(a, rep, grid, shmem, s); break;
+    case 2: launch_one<T, CT, D, 2>(a, rep, grid, shmem, s); break;
+    case 4: launch_one<T, CT, D, 4>(a, rep, grid, shmem, s); break;
+    default: launch_one<T, CT, D, 8>(a, rep, grid, shmem, s); break;
   }
 }
 
 template <typename T, typename CT>
-void launch_d(const DecodeArgs& a, int D, int gq, dim3 grid, size_t shmem, hipStream_t s) {
+void launch_d(const DecodeArgs& a, bool rep, int D, int gq, dim3 grid, size_t shmem, hipStream_t s) {
   switch (D) {
-    case 32: launch_gq<T, CT, 32>(a, gq, grid, shmem, s); break;
-    case 64: launch_gq<T, CT, 64>(a, gq, grid, shmem, s); break;
-    case 128: launch_gq<T, CT, 128>(a, gq, grid, shmem, s); break;
-    default: launch_gq<T, CT, 256>(a, gq, grid, shmem, s); break;
+    case 32: launch_gq<T, CT, 32>(a, rep, gq, grid, shmem, s); break;
+    case 64: launch_gq<T, CT, 64>(a, rep, gq, grid, shmem, s); break;
+    case 128: launch_gq<T, CT, 128>(a, rep, gq, grid, shmem, s); break;
+    default: launch_gq<T, CT, 256>(a, rep, gq, grid, shmem, s); break;
   }
 }
 
+// rep: the replicated-select kernel (bf16 tables, D <= 128); else the exchange kernel.
 template <typename T>
-void launch_type(const DecodeArgs& a, bool bf16_table, int D, int gq, dim3 grid, size_t shmem, hipStream_t s) {
-  if (bf16_table) launch_d<T, bf16_t>(a, D, gq, grid, shmem, s);
-  else launch_d<T, float>(a, D, gq, grid, shmem, s);
+void launch_type(const DecodeArgs& a, bool rep, bool bf16_table, int D, int gq, dim3 grid, size_t shmem,
+                 hipStream_t s) {
+  if (bf16_table) launch_d<T, bf16_t>(a, rep, D, gq, grid, shmem, s);
+  else launch_d<T, float>(a, false, D, gq, grid, shmem, s);
 }
 
 // Defined by decode_bf16.hip, decode_f16.hip and decode_f32.hip.
-void launch_bf16(const DecodeArgs& a, bool bf16_table, int D, int gq, dim3 grid, size_t shmem, hipStream_t s);
-void launch_f16(const DecodeArgs& a, bool bf16_table, int D, int gq, dim3 grid, size_t shmem, hipStream_t s);
-void launch_f32(const DecodeArgs& a, bool bf16_table, int D, int gq, dim3 grid, size_t shmem, hipStream_t s);
+void launch_bf16(const DecodeArgs& a, bool rep, bool bf16_table, int D, int gq, dim3 grid, size_t shmem,
+                 hipStream_t s);
+void launch_f16(const DecodeArgs& a, bool rep, bool bf16_table, int D, int gq, dim3 grid, size_t shmem,
+                hipStream_t s);
+void launch_f32(const DecodeArgs& a, bool rep, bool bf16_table, int D, int gq, dim3 grid, size_t shmem,
+                hipStream_t s);
 
 }  // namespace decode
 }  // namespace lsa

@@ -4,8 +4,9 @@
 namespace lsa {
 namespace decode {
 
-void launch_f32(const DecodeArgs& a, bool bf16_table, int D, int gq, dim3 grid, size_t shmem, hipStream_t s) {
-  launch_type<float>(a, bf16_table, D, gq, grid, shmem, s);
+void launch_f32(const DecodeArgs& a, bool rep, bool bf16_table, int D, int gq, dim3 grid, size_t shmem,
+                hipStream_t s) {
+  launch_type<float>(a, rep, bf16_table, D, gq, grid, shmem, s);
 }
 
 }  // namespace decode

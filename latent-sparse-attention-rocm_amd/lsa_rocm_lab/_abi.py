@@ -71,6 +71,7 @@ SIGNATURES = {
                                 _i32, _f32, _i32, _p, _p]),
     "lsa_read_chunked_mfma_ok": (_int, [_int, _i32, _i32]),
     "lsa_decode_flat_counters": (_i64, [_i64, _i32, _i32, _i32]),
+    "lsa_decode_flat_rep_ok": (_int, [_int, _i32, _i32, _i32, _i32, _int, _i32]),
     "lsa_decode_flat_scratch_bytes": (_sz, [_int, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "lsa_decode_flat": (_int, [_p, _p, _p, _int, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _p, _i32, _i32,
                                _i32, _i64, _i64, _int, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p,

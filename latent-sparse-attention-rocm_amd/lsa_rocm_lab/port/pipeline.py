@@ -292,6 +292,29 @@ def _select_splits(R: int, G: int, rows: int, top_p: int) -> int:
     return max(1, min(math.ceil(rows / 32), cap, max(1, 2048 // max(units, 1))))
 
 
+def _decode_splits(dtype, D: int, group: int, units: int, rows: int, top_p: int, score_mode: int,
+                   table_flags: int) -> int:
+    """Select workgroups per (row, kv-head) of the fused decode: the exchange form's splits,
+    or 0 - the replicated form, where every reader selects for itself - when
+    ``LSA_DECODE_MODE=rep`` asks for it (or ``auto`` with at most ``LSA_DECODE_REP_UNITS``
+    (row, kv-head) units; 0 by default: at the 32k decode the replicated form's 128 KiB
+    centroid scan per reader costs more round trips than the exchange saves)."""
+    mode = os.environ.get("LSA_DECODE_MODE", "auto")
+    if mode not in ("auto", "rep", "exchange"):
+        raise ValueError(f"LSA_DECODE_MODE must be auto|rep|exchange, got {mode!r}")
+    ok = bool(_abi.load().lsa_decode_flat_rep_ok(_abi.dtype_code(dtype), D, group, rows, top_p, score_mode,
+                                                 table_flags))
+    if mode == "rep" and not ok:
+        raise ValueError("LSA_DECODE_MODE=rep: the replicated select does not apply to this shape")
+    if ok and (mode == "rep" or (mode == "auto" and units <= _REP_MAX_UNITS)):
+        return 0
+    return _select_splits(units, 1, rows, top_p)
+
+
+# (row, kv-head) units up to which the fused decode selects in every reader
+_REP_MAX_UNITS = int(os.environ.get("LSA_DECODE_REP_UNITS", "0"))
+
+
 def _fused_select(index_queries, positions, buckets, config, top_k, score_dtype):
     device = _on_device("flat_select", index_queries, buckets.centroids, buckets.members)
     if positions.shape[0] != index_queries.shape[0]:
@@ -468,7 +491,8 @@ def flat_decode(
         raise ValueError(f"a position a batch row: {B} rows, {pos.numel()} positions")
     top_k = config.top_k if top_k is None else top_k
     scale = D ** -0.5 if scale is None else scale
-    splits = _select_splits(B, Hkv, layout.rows, config.top_p) if splits is None else splits
+    if splits is None:
+        splits = _decode_splits(q.dtype, D, Hq // Hkv, B * Hkv, layout.rows, config.top_p, mode, flags)
     rows, cap = layout.rows, members.shape[-1]
     width = top_k + config.window_size + config.sink_size
     lists = torch.empty(B, Hkv, width, dtype=torch.int32, device=device)

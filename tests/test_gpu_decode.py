@@ -236,7 +236,8 @@ def test_give_up_is_reported_and_the_next_launch_is_clean():
                         window_size=64, sink_size=4)
     q = data.q[:, -1:].contiguous()
     pos = torch.tensor([T - 1], dtype=torch.int32, device=DEV)
-    good = pipeline.flat_decode(q, data.k, data.v, pos, buckets, config)
+    run = lambda: pipeline.flat_decode(q, data.k, data.v, pos, buckets, config, splits=2)  # the exchange form
+    good = run()
     torch.cuda.synchronize()
     word = _abi.StatusWord.get(torch.device(DEV))
     assert int(word[0]) == 0
@@ -244,16 +245,69 @@ def test_give_up_is_reported_and_the_next_launch_is_clean():
     print("case give-up: skip_publish=1 spin_limit=64", flush=True)
     lib.lsa_debug_decode(1, 64)
     try:
-        pipeline.flat_decode(q, data.k, data.v, pos, buckets, config)
+        run()
         torch.cuda.synchronize()
     finally:
         lib.lsa_debug_decode(0, 0)
     assert int(word[0]) == 1
     with pytest.raises(_abi.LsaError, match="gave up"):
-        pipeline.flat_decode(q, data.k, data.v, pos, buckets, config)
+        run()
     assert int(word[0]) == 0
-    again = pipeline.flat_decode(q, data.k, data.v, pos, buckets, config)
+    again = run()
     torch.cuda.synchronize()
     for a, b in zip(good, again):
         assert torch.equal(a, b)
     pipeline.check_decode()  # nothing pending
+
+
+REP_CASES = {
+    # label: (T, Hq, Hkv, D, dtype, B, positions, window, sink, top_p)
+    "8k bf16 hq8 hkv2": (8192, 8, 2, 128, torch.bfloat16, 1, [8191], 0, 0, 32),
+    "32k bf16 hq32 hkv8": (32768, 32, 8, 128, torch.bfloat16, 1, [32767], 0, 0, 32),
+    "8k fp16 hq16 hkv2": (8192, 16, 2, 128, torch.float16, 1, [8191], 0, 0, 32),
+    "4k fp32 hq8 hkv2": (4096, 8, 2, 128, torch.float32, 1, [4095], 0, 0, 32),
+    "4k bf16 d64 hq8 hkv8": (4096, 8, 8, 64, torch.bfloat16, 1, [4095], 0, 0, 16),
+    "8k bf16 window sink": (8192, 8, 2, 128, torch.bfloat16, 1, [8191], 300, 4, 32),
+    "8k bf16 ragged rows": (8192, 8, 2, 128, torch.bfloat16, 3, [8191, 3000, 40], 64, 4, 48),
+    "8k bf16 one pick": (8192, 8, 2, 128, torch.bfloat16, 1, [8191], 0, 0, 1),
+}
+
+
+@pytest.mark.parametrize("label", list(REP_CASES))
+def test_replicated_select_equals_exchange_and_oracle(label):
+    """The replicated form (every reader selects for itself: matrix-core screen, exact
+    re-score of the rows near the cut) against the oracle, and bit-identical to the
+    exchange form (select workgroups publishing the picks): lists, lengths and outputs."""
+    import dataclasses
+
+    T, Hq, Hkv, D, dtype, B, positions, window, sink, top_p = REP_CASES[label]
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=T // 64, seed=13, dtype=dtype, B=B, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    assert buckets.spans
+    config = dataclasses.replace(workloads.FLAT_32K, window_size=window, sink_size=sink, top_p=top_p)
+    pos = torch.tensor(positions, dtype=torch.int32)
+    q = torch.stack([data.q[b, p] for b, p in enumerate(positions)])[:, None]  # [B, 1, Hq, D]
+    rep = check_decode(q, data.k, data.v, pos, buckets, config, splits=0, label=f"rep {label}")
+    exch = pipeline.flat_decode(q, data.k, data.v, pos.to(DEV), buckets, config, splits=2)
+    for a, b in zip(rep, exch):
+        assert torch.equal(a, b), label
+
+
+def test_replicated_select_non_finite_takes_the_exact_path():
+    """A centroid holding +inf: its screen and bound are not finite, so the readers score
+    every row exactly (the bucket lands first or last by the sign of its score); lists
+    equal the oracle's and the exchange form's."""
+    import dataclasses
+
+    T, Hq, Hkv, D = 8192, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=128, seed=14, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    cent = buckets.centroids.clone()
+    cent[0, 5, 3] = float("inf")
+    cent[1, 9, 7] = float("inf")
+    odd = dataclasses.replace(buckets, centroids=cent, centroids_f32=cent.float())
+    pos = torch.tensor([T - 1], dtype=torch.int32)
+    rep = check_decode(data.q[:, -1:], data.k, data.v, pos, odd, workloads.FLAT_32K, splits=0, label="rep inf")
+    exch = pipeline.flat_decode(data.q[:, -1:], data.k, data.v, pos.to(DEV), odd, workloads.FLAT_32K, splits=2)
+    for a, b in zip(rep, exch):
+        assert torch.equal(a, b)
