@@ -46,7 +46,7 @@ struct Plan {
 
 template <int D, int GQ>
 size_t reader_lds(int span) {
-  return rd_ids_offset<D, GQ>() + sizeof(int32_t) * (size_t)span;
+  return rd_ids_offset<D, GQ>() + sizeof(int32_t) * (size_t)kChunkTiles * span;
 }
 
 template <int D>
@@ -71,10 +71,10 @@ size_t reader_lds_d(int D, int gq, int span) {
 template <int D>
 size_t rep_lds_gq(int gq, int span) {
   switch (gq) {
-    case 1: return rep_ids_offset<D, 1>() + sizeof(int32_t) * (size_t)span;
-    case 2: return rep_ids_offset<D, 2>() + sizeof(int32_t) * (size_t)span;
-    case 4: return rep_ids_offset<D, 4>() + sizeof(int32_t) * (size_t)span;
-    default: return rep_ids_offset<D, 8>() + sizeof(int32_t) * (size_t)span;
+    case 1: return rep_ids_offset<D, 1>() + sizeof(int32_t) * (size_t)kChunkTiles * span;
+    case 2: return rep_ids_offset<D, 2>() + sizeof(int32_t) * (size_t)kChunkTiles * span;
+    case 4: return rep_ids_offset<D, 4>() + sizeof(int32_t) * (size_t)kChunkTiles * span;
+    default: return rep_ids_offset<D, 8>() + sizeof(int32_t) * (size_t)kChunkTiles * span;
   }
 }
 
@@ -107,11 +107,16 @@ int64_t record_stride(int64_t units, int K) {
   return ((words + 1023) / 1024) * 1024 + 64;
 }
 
-// Readers per unit: enough that each typically reads one part of `span` slots (two per
-// pick, plus the tail's parts), at most kMaxReaders.
-int default_readers(int K, int span, int window, int sink) {
+// Readers per unit: with few units, about one tile of the list a reader (picks are buckets
+// of ~one tile, plus the tail's tiles), so the gather spreads over as many CUs as it can
+// use; with many units, enough readers for ~1024 workgroups in all, each streaming a run
+// of tiles through the pipelined gather (fewer partials to combine). At most kMaxReaders.
+int default_readers(int64_t units, int K, int span, int window, int sink) {
   const int64_t tail = ((int64_t)window + sink + span - 1) / span;
-  const int64_t nr = (int64_t)K + tail;  // about one dense part a reader (buckets of ~one tile)
+  int64_t nr = (int64_t)K + tail;
+  const int64_t spread = (1024 + units - 1) / units;
+  if (spread < nr) nr = spread;
+  if (nr < 1) nr = 1;
   return (int)(nr < kMaxReaders ? nr : kMaxReaders);
 }
 
@@ -124,7 +129,7 @@ int plan_decode(int dtype, int D, int gq, int64_t units, int rows, int top_p, in
   LSA_REQUIRE(p->span > 0, LSA_ERR_SHAPE, "lsa_decode_flat: no read tile for D=%d group=%d", D, gq);
   LSA_REQUIRE(readers >= 0 && readers <= kMaxReaders, LSA_ERR_SHAPE, "lsa_decode_flat: readers in [0, %d], got %d",
               kMaxReaders, readers);
-  p->NR = readers > 0 ? readers : default_readers(p->K, p->span, window, sink);
+  p->NR = readers > 0 ? readers : default_readers(units, p->K, p->span, window, sink);
   p->cstride = record_stride(units, p->K);
   p->keys_bytes = splits > 1 ? (size_t)units * rows * sizeof(uint64_t) : 0;
   p->part_bytes = p->NR > 1 ? (size_t)units * p->NR * (size_t)(gq * (D + 2)) * sizeof(float) : 0;
@@ -133,7 +138,9 @@ int plan_decode(int dtype, int D, int gq, int64_t units, int rows, int top_p, in
     p->shmem = rep_lds_d(D, gq, p->span);
     return LSA_OK;
   }
-  const size_t sel = sel_keys_offset() + sizeof(uint64_t) * ((size_t)rows + p->kp);
+  size_t sel = sel_keys_offset() + sizeof(uint64_t) * ((size_t)rows + p->kp);
+  const size_t scr = sel_keys_offset() + sizeof(ScreenLds) + sizeof(uint64_t) * (size_t)p->kp;
+  if (splits == 1 && scr > sel) sel = scr;  // a lone split may screen its table (screen_topk)
   const size_t rd = reader_lds_d(D, gq, p->span);
   p->shmem = sel > rd ? sel : rd;
   return LSA_OK;
@@ -246,6 +253,7 @@ extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int 
   a.cluster_block = cluster_block_size; a.block_buckets = block_buckets;
   a.K = p.K; a.kp = p.kp; a.window = window; a.sink = sink; a.top_k = top_k; a.W = top_k + window + sink;
   a.S = select_splits; a.cs = select_splits > 0 ? (rows + select_splits - 1) / select_splits : rows;
+  a.screen = select_splits == 1 && score_mode == LSA_SCORE_BF16 && screen_fits(D, rows, p.K) ? 1 : 0;
   a.span = p.span; a.NR = p.NR;
   a.scale_log2 = scale * kLog2e;
   a.spin_limit = decode_debug().spin_limit > 0 ? decode_debug().spin_limit

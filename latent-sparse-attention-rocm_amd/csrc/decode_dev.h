@@ -7,6 +7,7 @@
 
 #include "lsa_abi_common.h"
 #include "lsa_read_dev.h"
+#include "lsa_screen_dev.h"
 #include "lsa_select_dev.h"
 
 namespace lsa {
@@ -44,6 +45,7 @@ struct DecodeArgs {
   int cluster_block, block_buckets;
   int K, kp, window, sink, top_k, W;
   int S, cs;           // select splits and columns per split
+  int screen;          // S == 1 with bf16 tables that fit screen_topk: the select screens its table
   int span, NR;        // slots per read part, readers per unit
   float scale_log2;
   int spin_limit;
@@ -73,9 +75,9 @@ struct SelLds {
 template <int D, int GQ>
 struct RdLds {
   ReadLds<D, GQ, kMaxReaders> rd;
-  int pick[kMaxPicks], start[kMaxPicks], n[kMaxPicks], abase[kMaxPicks];
+  int pick[kMaxPicks], start[kMaxPicks], n[kMaxPicks];
   int wcnt[LSA_WAVES];
-  int filled, pparts, bad;
+  int filled, bad;
 };
 
 constexpr size_t sel_keys_offset() { return (sizeof(SelLds) + 15) & ~(size_t)15; }
@@ -131,7 +133,26 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
   float qs[SPAN];
   const T* qrow = (const T*)a.q + (r * a.Hq + (int64_t)g * GQ) * D;
   constexpr int GROUPS = LSA_BLOCK / 16;
-  if (n_local <= 2 * GROUPS) {
+  bool picked = false;
+  if constexpr (__is_same(CT, bf16_t) && D >= 32 && D <= 128) {
+    if (a.screen) {  // one split scores the whole table: on the matrix cores, exact (screen_topk)
+      group_mean_slice<T, SPAN, GQ>(qrow, tid & 15, true, qs);
+      ScreenLds& scr = *(ScreenLds*)(smem + sel_keys_offset());  // in place of the keys
+      uint64_t* sbest = (uint64_t*)(smem + sel_keys_offset() + sizeof(ScreenLds));
+      screen_topk<D, 4>(
+          qs, cent, a.rows, [](int j) { return j; },
+          [&](int j) { return ends ? (int64_t)ends[j] <= lim : j < vis; }, a.K, a.kp, sbest, scr);
+      for (int j = tid; j < a.K; j += LSA_BLOCK) {
+        const int32_t b = key_column(u_to_key(sbest[j]));
+        sh.pick[j] = (b >= 0 && b < a.rows) ? b : -1;
+      }
+      __syncthreads();
+      picked = true;
+    }
+  }
+  if (picked) {
+    DECODE_MARK(4);
+  } else if (n_local <= 2 * GROUPS) {
     // one memory round trip: the group's query rows, the (at most) two centroid rows each
     // 16-lane group scores and their span ends are all in flight before the index query
     // is formed (group_mean_slice's arithmetic) and the rows are scored (score_keys')
@@ -173,37 +194,39 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
         qs, cent, D, n_local, [&](int j) { return c0 + j; },
         [&](int j) { return ends ? (int64_t)ends[c0 + j] <= lim : c0 + j < vis; }, keys + c0);
   }
-  DECODE_MARK(1);
+  if (!picked) {
+    DECODE_MARK(1);
 
-  if (a.S > 1) {
-    __syncthreads();
-    uint64_t* mine = a.ws_keys + i * (int64_t)a.rows;
-    for (int j = tid; j < n_local; j += LSA_BLOCK) coherent_store_u64(mine + c0 + j, keys[c0 + j]);
-    if (!arrive_last(&a.sel_count[i], a.S, &sh.flag)) return;
-    DECODE_MARK(2);
-    for (int jb = 0; jb < a.rows; jb += 4 * LSA_BLOCK) {
-      uint64_t x[4];
+    if (a.S > 1) {
+      __syncthreads();
+      uint64_t* mine = a.ws_keys + i * (int64_t)a.rows;
+      for (int j = tid; j < n_local; j += LSA_BLOCK) coherent_store_u64(mine + c0 + j, keys[c0 + j]);
+      if (!arrive_last(&a.sel_count[i], a.S, &sh.flag)) return;
+      DECODE_MARK(2);
+      for (int jb = 0; jb < a.rows; jb += 4 * LSA_BLOCK) {
+        uint64_t x[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int j = jb + u * LSA_BLOCK + tid;
-        x[u] = coherent_load_u64(mine + (j < a.rows ? j : 0));
-      }
+        for (int u = 0; u < 4; ++u) {
+          const int j = jb + u * LSA_BLOCK + tid;
+          x[u] = coherent_load_u64(mine + (j < a.rows ? j : 0));
+        }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int j = jb + u * LSA_BLOCK + tid;
-        if (j < a.rows) keys[j] = x[u];
+        for (int u = 0; u < 4; ++u) {
+          const int j = jb + u * LSA_BLOCK + tid;
+          if (j < a.rows) keys[j] = x[u];
+        }
       }
     }
+    __syncthreads();
+    DECODE_MARK(3);
+    block_topk_sorted(keys, a.rows, a.K, a.kp, best, &sh.tks, &sh.st);
+    for (int j = tid; j < a.K; j += LSA_BLOCK) {
+      const int32_t b = key_column(u_to_key(best[j]));
+      sh.pick[j] = (b >= 0 && b < a.rows) ? b : -1;
+    }
+    __syncthreads();
+    DECODE_MARK(4);
   }
-  __syncthreads();
-  DECODE_MARK(3);
-  block_topk_sorted(keys, a.rows, a.K, a.kp, best, &sh.tks, &sh.st);
-  for (int j = tid; j < a.K; j += LSA_BLOCK) {
-    const int32_t b = key_column(u_to_key(best[j]));
-    sh.pick[j] = (b >= 0 && b < a.rows) ? b : -1;
-  }
-  __syncthreads();
-  DECODE_MARK(4);
 
   // kept members of every pick (sink <= id < window start). Span tables: the range
   // [ends[b - 1], ends[b]) clipped to [sink, window start), from two ends words. Otherwise
@@ -303,11 +326,16 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
 }
 
 // The reader's work once it holds its unit's picks (sh.pick: a pick's bucket, or its first
-// kept id for span tables; sh.start / sh.n / sh.abase: its list slots, kept count and first
-// dense part; sh.filled, sh.pparts): expand each of its parts into `ids` and the list,
-// attend them, write its share of the list padding, publish its split partial and arrive;
-// the last reader of the unit combines the partials (and, with clear_record, zeroes the
-// unit's record copies for the next launch).
+// kept id for span tables; sh.start / sh.n: its first list slot and kept count; sh.filled):
+// the unit's list of L = filled + tail slots is cut into tiles of `span` slots, and reader
+// `role` takes a contiguous run of them (the first TT % NR readers one tile more), so only
+// the last tile of a list is partial. The run is expanded into `ids` (and the list) in
+// chunks of up to kChunkTiles tiles and read with the software-pipelined tile loop; then
+// the reader writes its share of the list padding, publishes its split partial and
+// arrives. The last reader of the unit combines the partials (and, with clear_record,
+// zeroes the unit's record copies for the next launch).
+constexpr int kChunkTiles = 8;
+
 template <typename T, int D, int GQ>
 __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh, int32_t* ids, int64_t i, int role,
                                            const QueryRegs<T, D, GQ>& qr, int64_t position, bool clear_record) {
@@ -316,47 +344,72 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
   constexpr int PSTRIDE = GQ * (D + 2);
   const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
   const int K = a.K, span = a.span, words = 2 * K;
-  const int64_t r = (uint32_t)i / (uint32_t)a.G;  // units < 2^31 (checked on the host): 32-bit division
+  const int64_t r = (uint32_t)i / (uint32_t)a.G;
   const int g = (int)((uint32_t)i % (uint32_t)a.G);
   const int64_t wstart = window_start_of(position, a.window);
   const int64_t n_win = position + 1 - wstart > 0 ? position + 1 - wstart : 0;
   const int64_t n_sink = a.sink < wstart ? a.sink : wstart;
-  const int n_tail = (int)(n_win + n_sink);
-  const int filled = sh.filled, pparts = sh.pparts;
-  const int n_act = pparts + (n_tail + span - 1) / span;  // dense parts: picks' then the tail's
-  const int n_part = n_act < a.NR ? n_act : a.NR;        // readers with work (one partial each)
+  const int filled = sh.filled;
+  const int length = filled + (int)(n_win + n_sink);
+  const int TT = (length + span - 1) / span;  // tiles of the list
+  const int NR = a.NR;
+  const int q_t = TT / NR, rem = TT % NR;
+  const int t_lo = role * q_t + (role < rem ? role : rem);
+  const int t_hi = t_lo + q_t + (role < rem ? 1 : 0);
+  const int lo = t_lo * span, hi = min(length, t_hi * span);
+  const int n_part = TT < NR ? TT : NR;  // readers with a tile: roles [0, n_part)
   int32_t* lrow = a.lists + i * (int64_t)a.W;
   const int32_t* tab = a.members + (r * a.row_tables + g * a.group_tables) * (int64_t)a.rows * a.cap;
   const int lp = lane % LPT;
   const T* kb = (const T*)a.k + r * a.kv_sb + g * a.kv_sh + lp * VEC;
   const T* vb = (const T*)a.v + r * a.kv_sb + g * a.kv_sh + lp * VEC;
+  // the last pick whose first slot is <= s (picks without slots share the next one's start)
+  auto pick_of = [&](int s_) {
+    int a_ = 0, b_ = K;
+    while (b_ - a_ > 1) {
+      const int m_ = (a_ + b_) >> 1;
+      if (sh.start[m_] <= s_) a_ = m_; else b_ = m_;
+    }
+    return a_;
+  };
   AttnState<T, D, GQ> st;
   st.clear();
   bool fresh = true;
-  for (int p = role; p < n_act; p += a.NR) {
-    int n, slot0;
-    if (p < pparts) {
-      // pick j holds dense parts [abase[j], abase[j] + parts_j): the last pick whose base
-      // is <= p (bases are nondecreasing; picks without parts share the next one's base)
-      const uint64_t le = __ballot(lane < K && sh.abase[lane < K ? lane : 0] <= p);
-      const int j = (int)__popcll(le) - 1;
-      const int u = p - sh.abase[j];
-      const int lo_rank = u * span;
-      n = min(span, sh.n[j] - lo_rank);
-      slot0 = sh.start[j] + lo_rank;
-      if (a.spans) {  // the kept members are consecutive ids from the record's first one
-        const int32_t first = sh.pick[j] + lo_rank;
-        for (int k = tid; k < n; k += LSA_BLOCK) {
-          ids[k] = first + k;
-          lrow[slot0 + k] = first + k;
+  for (int c_lo = lo; c_lo < hi; c_lo += kChunkTiles * span) {
+    const int c_hi = min(hi, c_lo + kChunkTiles * span);
+    const int n = c_hi - c_lo;
+    if (a.spans) {  // a pick's kept members are consecutive ids from the record's first one
+      for (int k = tid; k < n; k += LSA_BLOCK) {
+        const int s_ = c_lo + k;
+        int32_t id;
+        if (s_ < filled) {
+          const int j = pick_of(s_);
+          id = sh.pick[j] + (s_ - sh.start[j]);
+        } else {
+          id = tail_id(s_ - filled, wstart, n_win, n_sink);
         }
-        __syncthreads();
-      } else {
-        // ranks [lo_rank, lo_rank + n) of the pick's kept members, in table order
+        ids[k] = id;
+        lrow[s_] = id;
+      }
+    } else {
+      for (int k = tid; k < n; k += LSA_BLOCK) {
+        const int s_ = c_lo + k;
+        if (s_ >= filled) {
+          const int32_t id = tail_id(s_ - filled, wstart, n_win, n_sink);
+          ids[k] = id;
+          lrow[s_] = id;
+        }
+      }
+      // the picks overlapping [c_lo, min(c_hi, filled)): ranks of each one's kept members in
+      // table order, by a block ballot scan over its member row
+      const uint64_t below = (1ull << lane) - 1ull;
+      for (int s0 = c_lo; s0 < min(c_hi, filled);) {  // uniform over the block
+        const int j = pick_of(s0);
+        const int lo_rank = s0 - sh.start[j];
+        const int nn = min(sh.start[j] + sh.n[j], c_hi) - s0;
         const int32_t* row = tab + (int64_t)sh.pick[j] * a.cap;
-        const uint64_t below = (1ull << lane) - 1ull;
-        for (int c0 = 0, run = 0; c0 < a.cap && run < lo_rank + n; c0 += LSA_BLOCK) {
-          const int e = c0 + tid;
+        for (int e0 = 0, run = 0; e0 < a.cap && run < lo_rank + nn; e0 += LSA_BLOCK) {
+          const int e = e0 + tid;
           const int32_t id = row[e < a.cap ? e : 0];
           const bool keep = e < a.cap && id >= a.sink && (int64_t)id < wstart;
           const uint64_t m = __ballot(keep);
@@ -370,27 +423,19 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
             tot += c;
           }
           const int rank = run + off + (int)__popcll(m & below) - lo_rank;
-          if (keep && rank >= 0 && rank < n) {
-            ids[rank] = id;
-            lrow[slot0 + rank] = id;
+          if (keep && rank >= 0 && rank < nn) {
+            ids[s0 - c_lo + rank] = id;
+            lrow[s0 + rank] = id;
           }
           run += tot;
-          __syncthreads();  // wcnt is rewritten by the next chunk; ids are complete
+          __syncthreads();  // wcnt is rewritten by the next chunk of the row
         }
+        s0 += nn;
       }
-    } else {
-      const int t0 = (p - pparts) * span;
-      n = min(span, n_tail - t0);
-      slot0 = filled + t0;
-      for (int k = tid; k < n; k += LSA_BLOCK) {
-        const int32_t id = tail_id(t0 + k, wstart, n_win, n_sink);
-        ids[k] = id;
-        lrow[slot0 + k] = id;
-      }
-      __syncthreads();
     }
+    __syncthreads();
     DECODE_MARK(2);
-    attend_tiles<T, D, GQ>(
+    attend_tiles<T, D, GQ, true>(
         qr, kb, vb, a.kv_st, a.Tk, 0, n,
         [&](int jj) {
           const int32_t x = ids[jj < n ? jj : 0];
@@ -398,16 +443,8 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
         },
         a.scale_log2, fresh, st);
     fresh = false;
-    __syncthreads();  // ids are rewritten by the next part
+    __syncthreads();  // ids are rewritten by the next chunk
     DECODE_MARK(3);
-  }
-  // the list's padding [length, W) is shared out over the unit's readers
-  {
-    const int length = filled + n_tail;
-    const int per = (a.W - length + a.NR - 1) / a.NR;
-    const int p0 = length + role * per;
-    const int p1 = min(p0 + per, a.W);
-    for (int k = p0 + tid; k < p1; k += LSA_BLOCK) lrow[k] = -1;
   }
 
   T* outp = (T*)a.out + (r * a.Hq + (int64_t)g * GQ) * D;
@@ -416,9 +453,15 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
     merge_token_groups<T, D, GQ>(st);
     finish_span<T, D, GQ>(sh.rd, st, n_part == 1, outp, n_part > 1 ? parts + (int64_t)role * PSTRIDE : nullptr, 0);
   }
+  // the list's padding [length, W) is shared out over the unit's readers
+  {
+    const int per = (a.W - length + NR - 1) / NR;
+    const int p0 = length + role * per;
+    const int p1 = min(p0 + per, a.W);
+    for (int k = p0 + tid; k < p1; k += LSA_BLOCK) lrow[k] = -1;
+  }
   DECODE_MARK(4);
-  if (!arrive_last(&a.rd_count[i], a.NR, &sh.rd.flag)) return;
-  (void)w;
+  if (!arrive_last(&a.rd_count[i], NR, &sh.rd.flag)) return;
   DECODE_MARK(5);
   if (n_part > 1) {
     combine_partials<T, D, GQ>(sh.rd, parts, n_part, outp, 0);
@@ -476,24 +519,14 @@ __device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int
     int prev = __shfl_up(end, 1, LSA_WAVE);
     if (lane == 0) prev = 0;
     const int n = lane < K ? end - prev : 0;
-    const int parts = (n + span - 1) / span;
-    int incl = parts;
-#pragma unroll
-    for (int d = 1; d < LSA_WAVE; d <<= 1) {
-      const int y = __shfl_up(incl, d, LSA_WAVE);
-      if (lane >= d) incl += y;
-    }
     if (lane < K) {
       sh.pick[lane] = wa - 2;
       sh.start[lane] = prev;
       sh.n[lane] = n;
-      sh.abase[lane] = incl - parts;
     }
     const int filled = __shfl(end, K - 1, LSA_WAVE);
-    const int pparts = __shfl(incl, K - 1, LSA_WAVE);
     if (lane == 0) {
       sh.filled = filled;
-      sh.pparts = pparts;
       sh.bad = bad;
       if (bad && a.status) __hip_atomic_store(a.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
@@ -518,40 +551,17 @@ __device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int
 // ------------------------------------------------------------------ replicated select
 
 // Every reader workgroup selects for itself (no select workgroups, no cross-workgroup wait
-// before the gather). The canonical top-K of a unit is found exactly in three steps:
-//  1. screen: all visible rows are scored on the matrix cores (bf16 16x16x32 MFMAs, fp32
-//     sums) together with S_r = sum_d |q_d| |c_rd| (the same MFMA on the absolute values).
-//     The products of bf16 operands are exact in fp32, so any fp32 summation order of the
-//     D products is within 127 * 2^-23 * S_r < 2^-16 S_r of the exact dot product, and the
-//     canonical score (fp64 sums, one fp32 rounding) within 2^-24 |exact| + 2^-48 S_r <=
-//     2^-23 S_r of it: |screen - canonical| < 2^-15 S_r. Each row gets the interval
-//     [lo, hi] = screen -/+ (2^-14 S_r + 2^-90), which holds its canonical score.
-//  2. threshold: at least K rows have lo >= L for any L up to the K-th largest lo, so the
-//     canonical K-th best score is >= L and every row of the canonical top-K has hi >= L.
-//     L is the lower edge of a 256-bin histogram of lo: the candidates are the rows whose
-//     hi falls in that bin or above (a superset of hi >= L, as the bin map is monotone).
-//  3. the candidates (usually K plus a few) are re-scored exactly (the canonical fp64
-//     order) and sorted by packed key; the best K are the canonical top-K, ties to the
-//     lower bucket.
-// Non-finite scores or more than 64 candidates take the exact path for every row (the
-// same scoring and top-K as the select workgroups of decode_flat_kernel). Every reader of
-// a unit computes the same picks (identical inputs and instruction sequence). Span tables,
-// bf16 scoring, head dim 32/64/128, at most kRepMaxRows buckets and 64 picks.
-constexpr int kRepMaxRows = 1024;
-constexpr int kRepMaxCand = LSA_WAVE;
+// before the gather): it screens its unit's whole table on the matrix cores and re-scores
+// the rows near the cut exactly (screen_topk: the canonical top-K, ties to the lower
+// bucket). Every reader of a unit computes the same picks (identical inputs and
+// instruction sequence). Span tables, bf16 scoring, head dim 32/64/128, at most
+// kScreenMaxRows buckets and 64 picks.
+constexpr int kRepMaxRows = kScreenMaxRows;
 
 struct RepLds {
-  float lo[kRepMaxRows];      // screen - bound (-inf: not visible); the exact path's u64 keys
-  float hi[kRepMaxRows];      // screen + bound
+  ScreenLds scr;
   int32_t ends[kRepMaxRows];  // the table's span ends
-  int hist[256];
-  TopkScratch tks;
-  RadixState st;
-  uint64_t ckey[kRepMaxCand];  // candidates' exact keys; the exact path's sorted best
-  int cand[kRepMaxCand];
-  float wmin[LSA_WAVES], wmax[LSA_WAVES];
-  int wcnt[LSA_WAVES], wbad[LSA_WAVES];
-  int ncand, cut;
+  uint64_t best[kMaxPicks];
 };
 
 template <int D, int GQ>
@@ -565,17 +575,13 @@ constexpr size_t rep_ids_offset() {
 
 template <typename T, int D, int GQ>
 __device__ __forceinline__ void rep_role(const DecodeArgs& a, char* smem, int64_t i, int role) {
-  constexpr int NM = D / 32;    // 32-dim chunks of a centroid row (MFMA K)
-  constexpr int SPAN = D / 16;  // dims a lane holds in the 16-lane canonical layout
-  constexpr float kBound = 6.103515625e-05f;  // 2^-14
-  constexpr float kTiny = 8.077935669463161e-28f;  // 2^-90
+  constexpr int SPAN = D / 16;
   RdLds<D, GQ>& sh = *(RdLds<D, GQ>*)smem;
   RepLds& ex = *(RepLds*)(smem + rep_extra_offset<D, GQ>());
   int32_t* ids = (int32_t*)(smem + rep_ids_offset<D, GQ>());
   const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
-  const int row4 = lane >> 4, col = lane & 15;
   const int K = a.K, rows = a.rows;
-  const int64_t r = (uint32_t)i / (uint32_t)a.G;  // units < 2^31 (checked on the host): 32-bit division
+  const int64_t r = (uint32_t)i / (uint32_t)a.G;
   const int g = (int)((uint32_t)i % (uint32_t)a.G);
   const int64_t position = a.positions[r];
   const int64_t t = r * a.row_tables + g * a.group_tables;
@@ -587,188 +593,25 @@ __device__ __forceinline__ void rep_role(const DecodeArgs& a, char* smem, int64_
   DECODE_MARK(8);
 
   // the span ends into LDS, the query rows for the read, the index query (the group mean,
-  // bf16-rounded, in the 16-lane layout: lane p holds dims SPAN p .. SPAN p + SPAN)
+  // bf16-rounded, in the 16-lane layout)
   for (int m = tid; m < rows; m += LSA_BLOCK) ex.ends[m] = ends[m];
   QueryRegs<T, D, GQ> qr;
   qr.load(qrow, a.scale_log2);
   float qs[SPAN];
   group_mean_slice<T, SPAN, GQ>(qrow, tid & 15, true, qs);
-  // the screen's B operand: lane (row4, col) holds dims 32 c + 8 row4 .. + 8 of column col;
-  // column 0 = the index query, column 1 = its absolute values, the rest zero
-  uint32_t qpk[SPAN / 2];
-#pragma unroll
-  for (int k = 0; k < SPAN / 2; ++k)
-    qpk[k] = (uint32_t)f32_to_bf16(qs[2 * k]) | ((uint32_t)f32_to_bf16(qs[2 * k + 1]) << 16);
-  uint4 bq[NM];
-#pragma unroll
-  for (int c = 0; c < NM; ++c) {
-    uint32_t v4[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int d = 32 * c + 8 * row4 + 2 * k;  // first of the two dims of word k
-      const uint32_t x = (uint32_t)__shfl((int)qpk[(2 * k % SPAN) / 2], d / SPAN, LSA_WAVE);
-      v4[k] = col == 0 ? x : (col == 1 ? (x & 0x7FFF7FFFu) : 0u);
-    }
-    bq[c] = make_uint4(v4[0], v4[1], v4[2], v4[3]);
-  }
-  if (tid < 256) ex.hist[tid] = 0;
-  if (tid == 0) ex.ncand = 0;
-
-  // 1. screen: wave w takes 16-row groups w, w + 4, ...; two groups' rows in flight at once
-  int bad = 0;
-  const int ngrp = (rows + 15) / 16;
-  constexpr int GB = 2;
-  for (int gb = w; gb < ngrp; gb += LSA_WAVES * GB) {
-    uint4 A[GB][NM];
-    int e4[GB][4];
-#pragma unroll
-    for (int gi = 0; gi < GB; ++gi) {
-      const int grp = gb + LSA_WAVES * gi;
-      const int m = min(16 * grp + col, rows - 1);
-#pragma unroll
-      for (int c = 0; c < NM; ++c) A[gi][c] = *(const uint4*)(cent + (int64_t)m * D + 32 * c + 8 * row4);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) e4[gi][u] = ends[min(16 * grp + 4 * row4 + u, rows - 1)];
-    }
-#pragma unroll
-    for (int gi = 0; gi < GB; ++gi) {
-      const int grp = gb + LSA_WAVES * gi;
-      if (grp >= ngrp) break;  // wave-uniform
-      f32x4_t cs = {0.0f, 0.0f, 0.0f, 0.0f}, cb = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int c = 0; c < NM; ++c) {
-        cs = Mfma16<bf16_t>::run(A[gi][c], bq[c], cs);
-        const uint4 ab = make_uint4(A[gi][c].x & 0x7FFF7FFFu, A[gi][c].y & 0x7FFF7FFFu, A[gi][c].z & 0x7FFF7FFFu,
-                                    A[gi][c].w & 0x7FFF7FFFu);
-        cb = Mfma16<bf16_t>::run(ab, bq[c], cb);
-      }
-      // lane (row4, 0) holds the screens of rows 16 grp + 4 row4 + u, lane (row4, 1) their S
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float sabs = __shfl(cb[u], (lane + 1) & (LSA_WAVE - 1), LSA_WAVE);
-        const int m = 16 * grp + 4 * row4 + u;
-        if (col == 0 && m < rows) {
-          const float s = cs[u];
-          const float bnd = sabs * kBound + kTiny;
-          const bool fin = (s - s == 0.0f) && (bnd - bnd == 0.0f);
-          const bool vis = (int64_t)e4[gi][u] <= lim;
-          bad |= (vis && !fin) ? 1 : 0;
-          ex.lo[m] = vis ? s - bnd : -INFINITY;
-          ex.hi[m] = vis ? s + bnd : -INFINITY;
-        }
-      }
-    }
-  }
-  __syncthreads();
-  DECODE_MARK(9);
-
-  // 2. visible count, range of lo, histogram cut
-  float mn = INFINITY, mx = -INFINITY;
-  int cnt = 0;
-  for (int m = tid; m < rows; m += LSA_BLOCK) {
-    const float x = ex.lo[m];
-    const bool live = x != -INFINITY;
-    mn = live ? fminf(mn, x) : mn;
-    mx = live ? fmaxf(mx, x) : mx;
-    cnt += live ? 1 : 0;
-  }
-#pragma unroll
-  for (int x = LSA_WAVE / 2; x >= 1; x >>= 1) {
-    mn = fminf(mn, __shfl_xor(mn, x, LSA_WAVE));
-    mx = fmaxf(mx, __shfl_xor(mx, x, LSA_WAVE));
-    cnt += __shfl_xor(cnt, x, LSA_WAVE);
-    bad |= __shfl_xor(bad, x, LSA_WAVE);
-  }
-  if (lane == 0) { ex.wmin[w] = mn; ex.wmax[w] = mx; ex.wcnt[w] = cnt; ex.wbad[w] = bad; }
-  __syncthreads();
-  mn = fminf(fminf(ex.wmin[0], ex.wmin[1]), fminf(ex.wmin[2], ex.wmin[3]));
-  mx = fmaxf(fmaxf(ex.wmax[0], ex.wmax[1]), fmaxf(ex.wmax[2], ex.wmax[3]));
-  cnt = ex.wcnt[0] + ex.wcnt[1] + ex.wcnt[2] + ex.wcnt[3];
-  bool slow = (ex.wbad[0] | ex.wbad[1] | ex.wbad[2] | ex.wbad[3]) != 0;  // uniform
-  const float scale = mx > mn ? 256.0f / (mx - mn) : 0.0f;
-  auto bin_of = [&](float x) {
-    const float b = (x - mn) * scale;
-    return b < 0.0f ? 0 : (b >= 255.0f ? 255 : (int)b);
-  };
-  int cut = 0;  // cnt <= K: every visible row is a candidate
-  if (!slow && cnt > K) {
-    for (int m = tid; m < rows; m += LSA_BLOCK) {
-      const float x = ex.lo[m];
-      if (x != -INFINITY) atomicAdd(&ex.hist[bin_of(x)], 1);
-    }
-    __syncthreads();
-    if (w == 0) {
-      // lane l owns bins 255 - 4l .. 252 - 4l; the highest bin whose suffix count reaches K
-      const int c0 = ex.hist[255 - 4 * lane], c1 = ex.hist[254 - 4 * lane];
-      const int c2 = ex.hist[253 - 4 * lane], c3 = ex.hist[252 - 4 * lane];
-      const int mine = c0 + c1 + c2 + c3;
-      const int inc = wave_inclusive_sum(mine);
-      const int above = inc - mine;
-      const bool here = above < K && K <= inc;
-      const int d = above + c0 >= K ? 255 - 4 * lane
-                  : (above + c0 + c1 >= K ? 254 - 4 * lane : (above + c0 + c1 + c2 >= K ? 253 - 4 * lane
-                                                                                         : 252 - 4 * lane));
-      const uint64_t hm = __ballot(here);
-      const int cutv = __shfl(d, hm ? __ffsll((long long)hm) - 1 : 0, LSA_WAVE);
-      if (lane == 0) ex.cut = cutv;
-    }
-    __syncthreads();
-    cut = ex.cut;
-  }
-  if (!slow) {
-    for (int m = tid; m < rows; m += LSA_BLOCK) {
-      const float x = ex.hi[m];
-      if (x != -INFINITY && (cnt <= K || bin_of(x) >= cut)) {
-        const int slot = atomicAdd(&ex.ncand, 1);
-        if (slot < kRepMaxCand) ex.cand[slot] = m;
-      }
-    }
-    __syncthreads();
-    slow = ex.ncand > kRepMaxCand;
-  }
-  DECODE_MARK(10);
-
-  const int kp = a.kp;
-  if (!slow) {
-    // 3. exact scores of the candidates (16 lanes a row, 16 rows a pass), then one wave
-    // sorts their keys
-    const int nc = ex.ncand;
-    for (int jb = 0; jb < nc; jb += LSA_BLOCK / 16) {
-      const int j = jb + (tid >> 4);
-      const int m = ex.cand[j < nc ? j : 0];
-      SpanRaw<bf16_t, SPAN> raw;
-      raw.load(cent + (int64_t)m * D + (tid & 15) * SPAN);
-      double acc = 0.0;
-#pragma unroll
-      for (int e = 0; e < SPAN; ++e) acc = fma((double)qs[e], (double)raw.at(e), acc);
-      const float sc = score_tree16(acc);
-      if ((tid & 15) == 0 && j < nc) ex.ckey[j] = key_to_u(pack_key(sc, m));
-    }
-    __syncthreads();
-    if (w == 0) {
-      uint64_t v = lane < nc ? ex.ckey[lane] : 0;
-      v = wave_sort64_desc(v);
-      const int32_t b = key_column(u_to_key(v));
-      sh.pick[lane] = (lane < K && b >= 0 && b < rows) ? b : -1;
-    }
-  } else {
-    // exact canonical scores of every visible row, then the block top-K
-    uint64_t* keys = (uint64_t*)ex.lo;  // lo and hi: kRepMaxRows u64
-    score_keys<bf16_t, SPAN>(
-        qs, cent, D, rows, [&](int j) { return j; }, [&](int j) { return (int64_t)ex.ends[j] <= lim; }, keys);
-    __syncthreads();
-    block_topk_sorted(keys, rows, K, kp, ex.ckey, &ex.tks, &ex.st);
-    if (w == 0) {
-      const uint64_t v = lane < kp ? ex.ckey[lane] : 0;
-      const int32_t b = key_column(u_to_key(v));
-      sh.pick[lane] = (lane < K && b >= 0 && b < rows) ? b : -1;
-    }
-  }
-  __syncthreads();
+  screen_topk<D, 2>(
+      qs, cent, rows, [](int j) { return j; }, [&](int j) { return (int64_t)ends[j] <= lim; }, K, a.kp, ex.best,
+      ex.scr);
   DECODE_MARK(11);
+  if (w == 0) {
+    const uint64_t v = lane < a.kp ? ex.best[lane] : 0;
+    const int32_t b = key_column(u_to_key(v));
+    sh.pick[lane] = (lane < K && b >= 0 && b < rows) ? b : -1;
+  }
+  __syncthreads();
 
-  // each pick's kept range [max(begin, sink), min(end, window start)), its list slots and
-  // its dense parts (as the record of the exchange form gives them)
+  // each pick's kept range [max(begin, sink), min(end, window start)) and its list slots
+  // (as the record of the exchange form gives them)
   if (w == 0) {
     const int b = lane < K ? sh.pick[lane] : -1;
     int cntk = 0, first = 0;
@@ -783,19 +626,14 @@ __device__ __forceinline__ void rep_role(const DecodeArgs& a, char* smem, int64_
     int prev = __shfl_up(end, 1, LSA_WAVE);
     if (lane == 0) prev = 0;
     const int n = lane < K ? end - prev : 0;
-    const int parts = (n + a.span - 1) / a.span;
-    const int pincl = wave_inclusive_sum(parts);
     if (lane < K) {
       sh.pick[lane] = first;
       sh.start[lane] = prev;
       sh.n[lane] = n;
-      sh.abase[lane] = pincl - parts;
     }
-    const int filled = __shfl(end, K - 1, LSA_WAVE);
-    const int pparts = __shfl(pincl, K - 1, LSA_WAVE);  // every lane takes part in the shuffles
+    const int filled = __shfl(end, K - 1, LSA_WAVE);  // every lane takes part in the shuffle
     if (lane == 0) {
       sh.filled = filled;
-      sh.pparts = pparts;
       if (role == 0) {
         const int64_t n_win = position + 1 - wstart > 0 ? position + 1 - wstart : 0;
         const int64_t n_sink = a.sink < wstart ? a.sink : wstart;

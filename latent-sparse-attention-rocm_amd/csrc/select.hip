@@ -7,6 +7,7 @@
 // (select_topk_scores, expand_in_order_from_keys), _tree.py:318-373 (_beam_pick_rows) with
 // _tree.py:100-142 (_growth_replay) for one node level.
 #include "lsa_abi_common.h"
+#include "lsa_screen_dev.h"
 #include "lsa_select_dev.h"
 
 using namespace lsa;
@@ -146,12 +147,34 @@ struct FlatArgs {
   int window, sink, top_k;
   int S, cs;          // splits and columns per split
   int stage;          // 1: the list row is assembled in LDS after keys and picks
+  int screen;         // one split, bf16 tables that fit screen_topk: matrix-core screen + exact re-score
   int spans;          // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0)
   uint64_t* ws_keys;  // [R*G, rows] every column's key (S > 1)
   int* ws_count;      // [R*G] arrival counters (S > 1)
   int32_t* lists;
   int32_t* lengths;
 };
+
+// The rank-order expansion of one row's picks pk[0..K) (in LDS) into its read list and
+// length: span tables from the picks' span ends, member tables by the walk over member
+// rows (staged in LDS after the keys when a.stage). Every thread calls it.
+__device__ __forceinline__ void expand_row(const FlatArgs& a, const int32_t* pk, int64_t t, const int32_t* ends,
+                                           int64_t position, int64_t i, int* scan) {
+  extern __shared__ uint64_t smem[];
+  const int width = a.top_k + a.window + a.sink;
+  int len;
+  if (a.spans) {  // span tables: kept ids from the picks' span ends, no member rows
+    __shared__ int span_lds[2 * LSA_WAVE + 1];
+    len = expand_spans(pk, a.K, ends, a.rows, position, a.window, a.sink, a.top_k, a.lists + i * width, width,
+                       span_lds);
+  } else {
+    const int32_t* tab = a.members + t * a.rows * (int64_t)a.cap;
+    int32_t* stage = a.stage ? (int32_t*)(smem + ((a.rows + a.kp + 1) & ~1)) : nullptr;  // 16-byte aligned
+    len = expand_walk(pk, a.K, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k, a.lists + i * width, width,
+                      scan, stage);
+  }
+  if (threadIdx.x == 0) a.lengths[i] = len;
+}
 
 // grid (R*G, S). Split s scores columns [s*cs, (s+1)*cs) of its table in one batch of
 // loads (query slice, centroid rows and the columns' span ends together); with S > 1 it
@@ -187,6 +210,20 @@ __global__ __launch_bounds__(LSA_BLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)
 
   float qs[SPAN];
   load_query_slice<QT, SPAN>(q + i * D, threadIdx.x & 15, bf16_mode, qs);
+  int32_t* pk = (int32_t*)keys;
+  if constexpr (__is_same(CT, bf16_t) && SPAN >= 2 && SPAN <= 8) {
+    if (a.screen) {  // the whole table on the matrix cores, exact (screen_topk)
+      ScreenLds& scr = *(ScreenLds*)smem;
+      uint64_t* sbest = (uint64_t*)((char*)smem + sizeof(ScreenLds));
+      screen_topk<D, 2>(
+          qs, cent, a.rows, [](int j) { return j; },
+          [&](int j) { return ends ? (int64_t)ends[j] <= lim : j < vis; }, a.K, a.kp, sbest, scr);
+      for (int j = threadIdx.x; j < a.K; j += LSA_BLOCK) pk[j] = key_column(u_to_key(sbest[j]));
+      __syncthreads();
+      expand_row(a, pk, t, ends, position, i, scan);
+      return;
+    }
+  }
   score_keys<CT, SPAN>(
       qs, cent, D, n_local, [&](int j) { return c0 + j; },
       [&](int j) { return ends ? (int64_t)ends[c0 + j] <= lim : c0 + j < vis; }, keys + c0);
@@ -212,22 +249,9 @@ __global__ __launch_bounds__(LSA_BLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)
   }
   __syncthreads();
   block_topk_sorted(keys, a.rows, a.K, a.kp, best, &tks, &st);
-  int32_t* pk = (int32_t*)keys;
   for (int j = threadIdx.x; j < a.K; j += LSA_BLOCK) pk[j] = key_column(u_to_key(best[j]));
   __syncthreads();
-  const int width = a.top_k + a.window + a.sink;
-  int len;
-  if (a.spans) {  // span tables: kept ids from the picks' span ends, no member rows
-    __shared__ int span_lds[2 * LSA_WAVE + 1];
-    len = expand_spans(pk, a.K, ends, a.rows, position, a.window, a.sink, a.top_k, a.lists + i * width, width,
-                       span_lds);
-  } else {
-    const int32_t* tab = a.members + t * a.rows * (int64_t)a.cap;
-    int32_t* stage = a.stage ? (int32_t*)(smem + ((a.rows + a.kp + 1) & ~1)) : nullptr;  // 16-byte aligned
-    len = expand_walk(pk, a.K, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k, a.lists + i * width, width,
-                      scan, stage);
-  }
-  if (threadIdx.x == 0) a.lengths[i] = len;
+  expand_row(a, pk, t, ends, position, i, scan);
 }
 
 // ------------------------------------------------------------------ two-level tree select
@@ -251,6 +275,7 @@ struct TreeArgs {
   int nodes_pow2, beam_pow2, cand_cap, cand_pow2, top_pow2;
   int window, sink, top_k;
   int spans;  // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0)
+  int screen1, screen0;  // bf16 tables that fit screen_topk: node / bucket level on the matrix cores
   int32_t* lists;
   int32_t* lengths;
 };
@@ -262,6 +287,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
   __shared__ RadixState st;
   __shared__ TopkScratch tks;
   __shared__ int scan[LSA_WAVES];
+  __shared__ ScreenLds scr;
   uint64_t* keys = smem;                    // [max(nodes_pow2, cand_pow2)]
   uint64_t* best = keys + max(a.nodes_pow2, a.cand_pow2);  // [max(beam_pow2, top_pow2)]
   int32_t* cand = (int32_t*)(best + max(a.beam_pow2, a.top_pow2));  // [cand_cap]
@@ -284,10 +310,21 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
 
   // level 1: the made nodes, the best `beam` (a tie to the lower node); the rest are EMPTY
   const CT* ncent = (const CT*)a.node_centroids + t * (int64_t)a.n_nodes * D;
-  score_slice_keys<CT, SPAN>(qs, ncent, D, 0, a.n_nodes, made, keys);
-  __syncthreads();
   const int beam = min(a.beam, a.n_nodes);
-  block_topk_sorted(keys, a.n_nodes, beam, a.beam_pow2, best, &tks, &st);
+  bool done1 = false;
+  if constexpr (__is_same(CT, bf16_t) && SPAN >= 2 && SPAN <= 8) {
+    if (a.screen1) {
+      screen_topk<D, 2>(
+          qs, ncent, a.n_nodes, [](int j) { return j; }, [&](int j) { return j < made; }, beam, a.beam_pow2, best,
+          scr);
+      done1 = true;
+    }
+  }
+  if (!done1) {
+    score_slice_keys<CT, SPAN>(qs, ncent, D, 0, a.n_nodes, made, keys);
+    __syncthreads();
+    block_topk_sorted(keys, a.n_nodes, beam, a.beam_pow2, best, &tks, &st);
+  }
 
   // level 0 candidates: the kept nodes' children (only visible buckets), then the fresh
   // buckets [covered, visible)
@@ -329,10 +366,21 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
   }
   __syncthreads();
   const CT* bcent = (const CT*)a.centroids + t * (int64_t)a.rows * D;
-  score_keys<CT, SPAN>(qs, bcent, D, a.cand_pow2, [&](int j) { return cand[j]; }, keys);
-  __syncthreads();
   const int k = min(a.top_p, a.cand_pow2);
-  block_topk_sorted(keys, a.cand_pow2, k, a.top_pow2, best, &tks, &st);
+  bool done0 = false;
+  if constexpr (__is_same(CT, bf16_t) && SPAN >= 2 && SPAN <= 8) {
+    if (a.screen0) {
+      screen_topk<D, 2>(
+          qs, bcent, a.cand_pow2, [&](int j) { return cand[j]; }, [](int) { return true; }, k, a.top_pow2, best,
+          scr);
+      done0 = true;
+    }
+  }
+  if (!done0) {
+    score_keys<CT, SPAN>(qs, bcent, D, a.cand_pow2, [&](int j) { return cand[j]; }, keys);
+    __syncthreads();
+    block_topk_sorted(keys, a.cand_pow2, k, a.top_pow2, best, &tks, &st);
+  }
   for (int j = threadIdx.x; j < a.top_p; j += LSA_BLOCK) cand[j] = j < k ? key_column(u_to_key(best[j])) : -1;
   __syncthreads();
   const int width = a.top_k + a.window + a.sink;
@@ -683,7 +731,10 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
   const size_t base_lds = sizeof(uint64_t) * (((size_t)rows + kp + 1) & ~(size_t)1);
   const size_t stage_lds = sizeof(int32_t) * ((size_t)width + 4);
   a.stage = (!a.spans && width % 4 == 0 && ((uintptr_t)lists % 16) == 0 && base_lds + stage_lds <= kMaxDynLds) ? 1 : 0;
-  const size_t shmem = base_lds + (a.stage ? stage_lds : 0);
+  a.screen = splits == 1 && score_mode == LSA_SCORE_BF16 && screen_fits(D, rows, K) ? 1 : 0;
+  size_t shmem = base_lds + (a.stage ? stage_lds : 0);
+  const size_t screen_lds = sizeof(ScreenLds) + sizeof(uint64_t) * (size_t)kp;
+  if (a.screen && screen_lds > shmem) shmem = screen_lds;
   const dim3 grid((unsigned)(R * G), (unsigned)splits);
   const bool bf16 = score_mode == LSA_SCORE_BF16;
   hipStream_t s = (hipStream_t)stream;
@@ -739,6 +790,9 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
   a.cand_pow2 = next_pow2((int)(cand_cap > 0 ? cand_cap : 1)); a.top_pow2 = next_pow2(top_p);
   a.window = window; a.sink = sink; a.top_k = top_k; a.lists = lists; a.lengths = lengths;
   a.spans = (table_flags & LSA_TABLE_SPANS) && top_p <= LSA_WAVE ? 1 : 0;  // else the member rows
+  a.screen1 = score_mode == LSA_SCORE_BF16 && screen_fits(D, n_nodes, beam) ? 1 : 0;
+  a.screen0 = score_mode == LSA_SCORE_BF16 && screen_fits(D, a.cand_pow2, top_p < a.cand_pow2 ? top_p : a.cand_pow2)
+                  ? 1 : 0;
   const int keys_slots = a.nodes_pow2 > a.cand_pow2 ? a.nodes_pow2 : a.cand_pow2;
   const int best_slots = a.beam_pow2 > a.top_pow2 ? a.beam_pow2 : a.top_pow2;
   const int cand_slots = a.cand_pow2 > top_p ? a.cand_pow2 : top_p;

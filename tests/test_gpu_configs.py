@@ -240,7 +240,7 @@ def test_tree_decode_configured_geometry():
     print("tree 131k x 32: building the workload", flush=True)
     data = workloads.clustered(T, Hq, Hkv, D, n_clusters=2048, seed=0, B=B, device=DEV, gen_device=DEV,
                                q_tokens=1)
-    buckets = workloads.cluster_buckets(data, target=2048, workers=16)
+    buckets = workloads.cluster_buckets(data, target=2048, workers=8)
     tree = workloads.node_tree(buckets, node_size=16)
     config = workloads.TREE_131K
     assert buckets.rows == 2048 and tree.levels[0].children.shape[-2:] == (128, 16)

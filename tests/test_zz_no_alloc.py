@@ -70,12 +70,12 @@ def test_noalloc_equals_workspace_decode_twice_then_smaller():
 
 
 def test_noalloc_rejects_sizes_beyond_its_array():
-    """Partials for 4096 (row, kv-head) units exceed the 15 MiB of scratch: a clear error
-    before any launch."""
+    """Partials of 32 readers for 4096 (row, kv-head) units exceed the 15 MiB of scratch
+    (and their counters the 1 MiB): a clear error before any launch."""
     lib = _abi.load()
-    need = lib.lsa_decode_flat_scratch_bytes(_abi.LSA_BF16, 512, 32, 8, 128, 512, 32, 0, 0, 1, 0)
+    need = lib.lsa_decode_flat_scratch_bytes(_abi.LSA_BF16, 512, 32, 8, 128, 512, 32, 0, 0, 1, 32)
     assert need > 15 << 20
     rc = lib.lsa_decode_flat_noalloc(16, 16, 16, _abi.LSA_BF16, 512, 32768, 32, 8, 128, 0, 1024, 128, 16, 16, 16,
                                      1, 512, 256, 0, 1, _abi.SCORE_BF16, 16, 64, 1, 32, 0, 0, 8192,
-                                     ctypes.c_float(0.088), 1, 0, 0, 16, 16, 16, None, None)
+                                     ctypes.c_float(0.088), 1, 32, 0, 16, 16, 16, None, None)
     assert rc == -5 and b"exceed" in lib.lsa_last_error()
