@@ -44,7 +44,7 @@ enum lsa_status {
 
 enum lsa_dtype { LSA_F32 = 0, LSA_BF16 = 1, LSA_F16 = 2 };
 enum lsa_score_mode { LSA_SCORE_BF16 = 0, LSA_SCORE_F32 = 1 };
-enum lsa_centroid_mode { LSA_CENTROID_MEAN = 0, LSA_CENTROID_NORMALIZED = 1 };
+enum lsa_centroid_mode { LSA_CENTROID_MEAN = 0, LSA_CENTROID_NORMALIZED = 1, LSA_CENTROID_SUM = 2 };
 
 int lsa_abi_version(void);
 const char* lsa_last_error(void);
@@ -125,6 +125,32 @@ int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int32_t G, int3
                     int32_t block_buckets, int32_t node_block, int32_t beam_width, int32_t top_p, int32_t window,
                     int32_t sink, int32_t top_k, int32_t* lists, int32_t* lengths, void* stream);
 
+/* Multi-level beam select (reference pipeline.py:319-337 tree_select over a hierarchy of
+ * several node levels: _tree.py:318-373 _beam_pick_rows, _tree.py:306-315 _dedup_scores,
+ * with the growth of _tree.py:100-142 _growth_replay at page end V = the row's visible
+ * bucket count). Level l + 1 (l = 0 .. n_levels - 1, bottom up) has n_nodes[l] nodes:
+ * node_centroids[l] [tables, n_nodes[l], D] (bf16 or fp32 as score_mode), children[l]
+ * [tables, n_nodes[l], node_size] int32 rows of the level below (bucket rows for l = 0).
+ * Growth: covered C = floor(V / node_block) * node_block buckets make C / node_size level-1
+ * nodes; a level's nodes close in whole node_block blocks, closed / node_size nodes of the
+ * level above being made, for min(n_levels, top_level) levels, each capped by n_nodes. The
+ * walk starts at the highest level with a made node (all its made nodes are candidates);
+ * below, the carried children plus the level's open nodes [closed, made); at the buckets
+ * the carried children below V plus the fresh buckets [C, V). Each level scores each
+ * candidate once and keeps the best beam_width (top_p at the buckets), a tie to the lower
+ * row; then the flat expansion. Unlike the reference's torch walk, fewer candidates than
+ * top_p leave -1 picks (its tail repeats -inf-scored candidates). Limits: n_levels <=
+ * LSA_BEAM_MAX_LEVELS, rows and n_nodes[l] <= 8192, at most 4096 candidates a level.
+ * table_flags as lsa_select_flat. */
+#define LSA_BEAM_MAX_LEVELS 4
+int lsa_select_beam(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D, int32_t n_levels,
+                    const void* const* node_centroids, const int32_t* const* children, const int32_t* n_nodes,
+                    int32_t node_size, int32_t node_block, int32_t top_level, const void* centroids,
+                    const int32_t* members, const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap,
+                    int64_t row_tables, int64_t group_tables, int score_mode, const int32_t* positions,
+                    int32_t cluster_block_size, int32_t block_buckets, int32_t beam_width, int32_t top_p,
+                    int32_t window, int32_t sink, int32_t top_k, int32_t* lists, int32_t* lengths, void* stream);
+
 /* GQA-collapsed index queries (reference gates.py:50-59 make_index_space, per-kv-head
  * form): out [B, T/chunk, Hkv, D] fp32 = fp32 mean of q [B, T, Hq, D] over each
  * kv-head's query group and `chunk` consecutive tokens (tokens outer, heads inner). */
@@ -132,7 +158,8 @@ int lsa_index_queries(const void* q, int q_dtype, int64_t B, int64_t T, int32_t 
                       int32_t chunk, float* out, void* stream);
 
 /* Bucket centroids (reference pipeline.py:108-115, :396-403): for each of n_tables *
- * rows buckets, the mean (or L2-normalized sum) of its member keys. keys: element
+ * rows buckets, the mean, the L2-normalized sum or the sum (the hierarchy's key sums,
+ * reference pipeline.py:163-164) of its member keys. keys: element
  * (t, d) of table k lives at keys[k_off(k) + t * token_stride + d] with k_off(k) =
  * (k / kv_heads) * batch_stride + (k % kv_heads) * D; member ids outside [0, tokens) are
  * skipped. Out fp32 and bf16 [tables, rows, D]. */

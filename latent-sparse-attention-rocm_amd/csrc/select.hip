@@ -501,48 +501,11 @@ __global__ __launch_bounds__(LSA_BLOCK) void centroids_kernel(const KT* keys, in
   for (int d = threadIdx.x; d < D; d += LSA_BLOCK) {
     float c;
     if (mode == LSA_CENTROID_NORMALIZED) c = sums[d] / norm;
+    else if (mode == LSA_CENTROID_SUM) c = sums[d];
     else c = count > 0 ? sums[d] / (float)count : 0.0f;
     out_f32[bucket * D + d] = c;
     if (out_bf16) out_bf16[bucket * D + d] = f32_to_bf16(c);
   }
-}
-
-int check_tables(int32_t rows, int32_t cap, int64_t row_tables, int64_t group_tables) {
-  LSA_REQUIRE(rows >= 1, LSA_ERR_SHAPE, "bucket table needs >= 1 row, got %d", rows);
-  LSA_REQUIRE(cap >= 1, LSA_ERR_SHAPE, "bucket cap must be >= 1, got %d", cap);
-  LSA_REQUIRE(row_tables >= 0 && group_tables >= 0, LSA_ERR_SHAPE, "table strides must be >= 0");
-  return LSA_OK;
-}
-
-int check_dim(int32_t D) {
-  LSA_REQUIRE(D >= 16 && D <= 256 && is_pow2(D), LSA_ERR_SHAPE,
-              "index dim must be a power of two in [16, 256], got %d", D);
-  return LSA_OK;
-}
-
-int check_dtype(int dtype) {
-  LSA_REQUIRE(dtype == LSA_F32 || dtype == LSA_BF16 || dtype == LSA_F16, LSA_ERR_DTYPE, "unknown dtype %d", dtype);
-  return LSA_OK;
-}
-
-// The scoring loads a lane's D/16 centroid elements with vector loads and the expansion
-// loads member rows as 16-byte vectors when cap % 32 == 0: both need aligned tables.
-int check_query_aligned(const void* q, int q_dtype, int D) {
-  size_t need = (size_t)(D / 16) * (q_dtype == LSA_F32 ? 4 : 2);
-  need = need > 16 ? 16 : need;
-  LSA_REQUIRE(((uintptr_t)q % need) == 0, LSA_ERR_ALIGN, "query rows must be %zu-byte aligned", need);
-  return LSA_OK;
-}
-
-int check_aligned(const void* centroids, int D, int score_mode, const int32_t* members, int cap) {
-  const size_t esize = score_mode == LSA_SCORE_F32 ? 4 : 2;
-  size_t need = (size_t)(D / 16) * esize;
-  need = need > 16 ? 16 : need;
-  LSA_REQUIRE(centroids == nullptr || ((uintptr_t)centroids % need) == 0, LSA_ERR_ALIGN,
-              "centroid table must be %zu-byte aligned", need);
-  LSA_REQUIRE(members == nullptr || cap % 32 != 0 || ((uintptr_t)members % 16) == 0, LSA_ERR_ALIGN,
-              "member table must be 16-byte aligned");
-  return LSA_OK;
 }
 
 }  // namespace
@@ -844,7 +807,9 @@ extern "C" int lsa_bucket_centroids(const void* keys, int k_dtype, int64_t token
   LSA_REQUIRE(D >= 1 && D <= 512 && kv_heads >= 1 && n_tables >= 0 && rows >= 0 && cap >= 1 && tokens >= 0,
               LSA_ERR_SHAPE,
               "lsa_bucket_centroids: bad sizes");
-  LSA_REQUIRE(centroid_mode == LSA_CENTROID_MEAN || centroid_mode == LSA_CENTROID_NORMALIZED, LSA_ERR_SHAPE,
+  LSA_REQUIRE(centroid_mode == LSA_CENTROID_MEAN || centroid_mode == LSA_CENTROID_NORMALIZED ||
+                  centroid_mode == LSA_CENTROID_SUM,
+              LSA_ERR_SHAPE,
               "lsa_bucket_centroids: bad centroid mode");
   const int64_t n = n_tables * rows;
   if (n == 0) return LSA_OK;

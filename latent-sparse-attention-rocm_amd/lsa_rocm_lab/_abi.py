@@ -22,7 +22,8 @@ LSA_F32, LSA_BF16, LSA_F16 = 0, 1, 2
 CHUNKED_AUTO, CHUNKED_GATHER, CHUNKED_MFMA = 0, 1, 2
 SCORE_BF16, SCORE_F32 = 0, 1
 TABLE_SPANS = 1  # LSA_TABLE_SPANS: every bucket row holds exactly its span of `ends`
-CENTROID_MEAN, CENTROID_NORMALIZED = 0, 1
+BEAM_MAX_LEVELS = 4  # LSA_BEAM_MAX_LEVELS: node levels lsa_select_beam walks
+CENTROID_MEAN, CENTROID_NORMALIZED, CENTROID_SUM = 0, 1, 2
 
 _ERRORS = {
     -1: "LSA_ERR_NULL",
@@ -58,6 +59,8 @@ SIGNATURES = {
                                _i32, _i32, _i32, _i32, _i32, _p, _p, _sz, _p, _p, _p]),
     "lsa_select_tree": (_int, [_p, _int, _i64, _i32, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i64, _i64,
                                _int, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
+    "lsa_select_beam": (_int, [_p, _int, _i64, _i32, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _p, _p, _p, _i32, _i32,
+                               _i32, _i64, _i64, _int, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
     "lsa_index_queries": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p]),
     "lsa_bucket_centroids": (_int, [_p, _int, _i64, _i64, _i64, _i32, _i32, _p, _i64, _i32, _i32, _int, _p, _p, _p]),
     "lsa_ward_segments_scratch_bytes": (_sz, [_i64, _i64, _i32, _i32]),

@@ -1,18 +1,21 @@
-"""The tree beam on the GPU (reference src/lsa_rocm_lab/port/_tree.py), one HIP kernel.
+"""The tree beam on the GPU (reference src/lsa_rocm_lab/port/_tree.py), one HIP kernel a call.
 
-Scope: a node tree of ONE level over the buckets (e.g. 128 nodes of 16 buckets). Per
-(query row, kv-head) one workgroup replays the row's growth (reference :100-142 with one
-level: nodes are made over whole ``node_cluster_block_size`` blocks of the row's visible
-buckets), scores the made nodes, keeps the best ``beam_width`` (a tie to the lower
-node), gathers their visible children plus the fresh buckets ``[covered, visible)``,
-removes duplicates, keeps the best ``top_p`` (a tie to the lower bucket), and expands
-them in rank order - the semantics of the reference's ``_beam_pick_rows`` (:318-373)
-with one level, whose start level is taken whole. Invalid candidates are never picked
-(the list tail is -1).
+Per (query row, kv-head) one workgroup replays the row's growth (reference :100-142:
+nodes are made over whole ``node_cluster_block_size`` blocks of the row's visible
+buckets, and a level's nodes close in whole blocks into the level above, up to
+``top_level`` levels), walks the levels from the highest one holding a made node down
+(candidates: the carried children plus the level's open nodes, each once), keeps the
+best ``beam_width`` a level (a tie to the lower node), then the best ``top_p`` of the
+carried buckets plus the fresh buckets ``[covered, visible)`` (a tie to the lower
+bucket), and expands them in rank order - the semantics of the reference's
+``_beam_pick_rows`` (:318-373) with ``_dedup_scores`` (:306-315). A one-level tree runs
+``lsa_select_tree``, deeper ones ``lsa_select_beam``. Invalid candidates are never
+picked (the list tail is -1).
 """
 
 from __future__ import annotations
 
+import ctypes
 import os
 
 import torch
@@ -39,55 +42,72 @@ def tree_select_batched(
     top_k: int | None = None,
     score_dtype: str = "fp32",
 ):
-    """Select by the one-level beam, expand in rank order - see ``pipeline.tree_select``.
+    """Select by the beam, expand in rank order - see ``pipeline.tree_select``.
 
     ``LSA_TREE_IMPL`` (reference _tree.py:53) is read for compatibility; ``per_page``
     and ``batched`` name the same kernel here.
     """
     os.environ.get("LSA_TREE_IMPL", "per_page")
     top_k = config.top_k if top_k is None else top_k
-    if len(hierarchy.levels) != 1:
-        raise NotImplementedError(
-            f"tree_select covers a one-level node tree, got {len(hierarchy.levels)} levels"
-        )
+    n_levels = len(hierarchy.levels)
+    if not 1 <= n_levels <= _abi.BEAM_MAX_LEVELS:
+        raise NotImplementedError(f"tree_select covers 1 to {_abi.BEAM_MAX_LEVELS} node levels, got {n_levels}")
     if config.start_nodes is not None:
         raise NotImplementedError("tree_select covers start_nodes=None (the top level down)")
-    level = hierarchy.levels[0]
-    device = _on_device("tree_select", index_queries, buckets.centroids, level.centroids)
+    device = _on_device("tree_select", index_queries, buckets.centroids,
+                        *[level.centroids for level in hierarchy.levels])
     if positions.shape[0] != index_queries.shape[0]:
         raise ValueError(
             f"a position a query: {index_queries.shape[0]} queries, {positions.shape[0]} positions"
         )
     layout = _Layout(index_queries, buckets.centroids)
-    node_layout = _Layout(index_queries, level.centroids)
-    if (node_layout.row_tables, node_layout.group_tables) != (layout.row_tables, layout.group_tables):
-        raise ValueError("node and bucket tables must share the same leading axes")
+    for level in hierarchy.levels:
+        node_layout = _Layout(index_queries, level.centroids)
+        if (node_layout.row_tables, node_layout.group_tables) != (layout.row_tables, layout.group_tables):
+            raise ValueError("node and bucket tables must share the same leading axes")
     if score_dtype == "fp32":
         if buckets.centroids_f32 is None:
             raise ValueError("fp32 scoring needs buckets.centroids_f32")
-        ncent, bcent, mode = level.centroids.float(), buckets.centroids_f32.float(), _abi.SCORE_F32
+        ncents = [level.centroids.float() for level in hierarchy.levels]
+        bcent, mode = buckets.centroids_f32.float(), _abi.SCORE_F32
     elif score_dtype == "bf16":
-        nb = level.centroids_bf16 if level.centroids_bf16 is not None else level.centroids.to(torch.bfloat16)
-        ncent, bcent, mode = nb, buckets.centroids.to(torch.bfloat16), _abi.SCORE_BF16
+        ncents = [level.centroids_bf16 if level.centroids_bf16 is not None else level.centroids.to(torch.bfloat16)
+                  for level in hierarchy.levels]
+        bcent, mode = buckets.centroids.to(torch.bfloat16), _abi.SCORE_BF16
     else:
         raise ValueError(f"score_dtype must be bf16|fp32, got {score_dtype!r}")
-    ncent, bcent = ncent.contiguous(), bcent.contiguous()
-    children = level.children.to(device=device, dtype=torch.int32).contiguous()
+    ncents = [c.contiguous() for c in ncents]
+    bcent = bcent.contiguous()
+    kids = [level.children.to(device=device, dtype=torch.int32).contiguous() for level in hierarchy.levels]
+    node_size = kids[0].shape[-1]
+    if any(k.shape[-1] != node_size for k in kids):
+        raise ValueError("every node level must hold node_bucket_size children a node")
     members = buckets.members.to(device=device, dtype=torch.int32).contiguous()
-    n_nodes, node_size = children.shape[-2], children.shape[-1]
     q = _queries(index_queries)
     pos = _positions32(positions, device)
     ends = _ends(buckets)
+    flags = _abi.TABLE_SPANS if (buckets.spans and ends is not None) else 0
     width = top_k + config.window_size + config.sink_size
     lists = torch.empty(layout.out_shape(width), dtype=torch.int32, device=device)
     lengths = torch.empty(layout.out_shape(), dtype=torch.int32, device=device)
-    _abi.call("lsa_select_tree", q.data_ptr(), _abi.dtype_code(q.dtype), layout.R, layout.G, layout.D,
-              ncent.data_ptr(), children.data_ptr(), n_nodes, node_size, bcent.data_ptr(), members.data_ptr(),
-              _abi.ptr(ends), _abi.TABLE_SPANS if (buckets.spans and ends is not None) else 0, layout.rows,
-              members.shape[-1], layout.row_tables, layout.group_tables, mode,
-              pos.data_ptr(), config.cluster_block_size, config.block_bucket_count, config.node_cluster_block_size,
-              config.beam_width, config.top_p, config.window_size, config.sink_size, top_k, lists.data_ptr(),
-              lengths.data_ptr(), _abi.stream(device))
+    if n_levels == 1:
+        _abi.call("lsa_select_tree", q.data_ptr(), _abi.dtype_code(q.dtype), layout.R, layout.G, layout.D,
+                  ncents[0].data_ptr(), kids[0].data_ptr(), kids[0].shape[-2], node_size, bcent.data_ptr(),
+                  members.data_ptr(), _abi.ptr(ends), flags, layout.rows, members.shape[-1], layout.row_tables,
+                  layout.group_tables, mode, pos.data_ptr(), config.cluster_block_size, config.block_bucket_count,
+                  config.node_cluster_block_size, config.beam_width, config.top_p, config.window_size,
+                  config.sink_size, top_k, lists.data_ptr(), lengths.data_ptr(), _abi.stream(device))
+        return lists, lengths
+    cent_ptrs = (ctypes.c_void_p * n_levels)(*[c.data_ptr() for c in ncents])
+    kid_ptrs = (ctypes.c_void_p * n_levels)(*[k.data_ptr() for k in kids])
+    n_nodes = (ctypes.c_int32 * n_levels)(*[k.shape[-2] for k in kids])
+    _abi.call("lsa_select_beam", q.data_ptr(), _abi.dtype_code(q.dtype), layout.R, layout.G, layout.D, n_levels,
+              ctypes.addressof(cent_ptrs), ctypes.addressof(kid_ptrs), ctypes.addressof(n_nodes), node_size,
+              config.node_cluster_block_size, config.top_level, bcent.data_ptr(), members.data_ptr(),
+              _abi.ptr(ends), flags, layout.rows, members.shape[-1], layout.row_tables, layout.group_tables, mode,
+              pos.data_ptr(), config.cluster_block_size, config.block_bucket_count, config.beam_width,
+              config.top_p, config.window_size, config.sink_size, top_k, lists.data_ptr(), lengths.data_ptr(),
+              _abi.stream(device))
     return lists, lengths
 
 

@@ -10,7 +10,9 @@ a HIP kernel in liblsa_rocm.so:
   kernel from the index queries to the read lists (score + top-k + expansion, split
   over workgroups when there are few rows); ``fused_unpack`` keeps the listing +
   top-k and expands from the keys; ``reference`` is the unfused chain;
-* ``tree_select`` (:319-337), ``lsa_read`` (:373-375), ``position_buckets`` (:378-403);
+* ``tree_select`` (:319-337) over a one- to four-level hierarchy from
+  ``build_hierarchy_gpu`` (:153-178), ``lsa_read`` (:373-375), ``position_buckets``
+  (:378-403);
 * ``dense_read`` (:340-370) stays torch SDPA - it is the dense comparator.
 
 Per-kv-head selection (the benchmark geometry) extends the shapes: index queries
@@ -390,7 +392,7 @@ def tree_select(
     top_k: int | None = None,
     score_dtype: str = "fp32",
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Select each query's keys by a beam down a one-level node tree (reference pipeline.py:319-337).
+    """Select each query's keys by a beam down the node levels (reference pipeline.py:319-337).
 
     See ``_tree.tree_select_batched``.
     """
@@ -570,13 +572,14 @@ def index_queries(q: torch.Tensor, heads_kv: int, chunk: int = 1) -> torch.Tenso
 
 
 def bucket_centroids(keys: torch.Tensor, members: torch.Tensor, centroid: str = "mean"):
-    """Bucket centroids (fp32, bf16) from member keys: the mean key, or the L2-normalized
-    sum (reference pipeline.py:108-115). keys [T, d] with members [rows, cap], or keys
+    """Bucket centroids (fp32, bf16) from member keys: the mean key, the L2-normalized sum
+    (reference pipeline.py:108-115), or the plain sum ("sum": the hierarchy's key sums,
+    :163-164). keys [T, d] with members [rows, cap], or keys
     [B, T, Hkv, D] with members [Hkv, rows, cap] (B == 1) / [B, Hkv, rows, cap]."""
     device = _on_device("bucket_centroids", keys, members)
     keys = keys.contiguous()
     members = members.to(torch.int32).contiguous()
-    mode = {"mean": _abi.CENTROID_MEAN, "normalized": _abi.CENTROID_NORMALIZED}[centroid]
+    mode = {"mean": _abi.CENTROID_MEAN, "normalized": _abi.CENTROID_NORMALIZED, "sum": _abi.CENTROID_SUM}[centroid]
     rows, cap = members.shape[-2:]
     if keys.dim() == 2:
         T, D = keys.shape
@@ -753,3 +756,49 @@ def position_buckets(index_keys: torch.Tensor, config: PortConfig, centroid: str
     sizes = (members >= 0).sum(-1, dtype=torch.int32)
     c32, c16 = bucket_centroids(index_keys, members, centroid)
     return Buckets(c16, members, sizes, centroids_f32=c32, centroid=centroid)
+
+
+def build_hierarchy_gpu(index_keys: torch.Tensor, buckets: Buckets, config: PortConfig) -> Hierarchy:
+    """Node levels over the buckets (reference pipeline.py:153-178 build_hierarchy_gpu).
+
+    The bucket key sums (the sum of each bucket's member index keys, :162-164) are the
+    level-0 sums. While the level below holds a full ``node_cluster_block_size`` block and
+    fewer than ``top_level`` levels exist, every full block of its rows becomes
+    ``block / node_bucket_size`` nodes of ``node_bucket_size`` rows each; a node's key sum
+    is the sum of its rows' key sums and its centroid the L2-normalized key sum (:175-177).
+    Children are rows of the level below, block after block (:170-173). The reference
+    groups a block's rows by the Ward pairing cost (the upstream Triton pairing kernel);
+    here a node takes consecutive rows of its block - a grouping that follows the
+    bucket order, and one the walk treats like any other: the beam only assumes a node's
+    children lie in the blocks closed before it was made. Sums and centroids come from
+    the centroid kernel (``LSA_CENTROID_SUM`` / ``LSA_CENTROID_NORMALIZED``).
+
+    index_keys [T, D] with one bucket table, or [B, T, Hkv, D] with tables [Hkv, ...]
+    (B == 1) / [B, Hkv, ...]; node tables share the bucket tables' leading axes.
+    """
+    device = _on_device("build_hierarchy_gpu", index_keys, buckets.members)
+    sums, _ = bucket_centroids(index_keys, buckets.members, "sum")
+    hierarchy = Hierarchy(bucket_key_sums=sums)
+    size, block = config.node_bucket_size, config.node_cluster_block_size
+    if size < 1 or block < size or block % size:
+        raise ValueError(f"node_cluster_block_size ({block}) must be a positive multiple of "
+                         f"node_bucket_size ({size})")
+    lead = sums.shape[:-2]
+    n_tables = math.prod(lead)
+    D = sums.shape[-1]
+    while True:
+        below = sums.shape[-2]
+        blocks = below // block
+        if not blocks or len(hierarchy.levels) >= config.top_level:
+            break
+        n_nodes = blocks * block // size
+        children = torch.arange(n_nodes * size, device=device, dtype=torch.int32).view(n_nodes, size)
+        children = children.expand(*lead, n_nodes, size).contiguous()
+        keys = sums.reshape(n_tables, below, 1, D)
+        kids = children.reshape(n_tables, n_nodes, size)
+        node_sums, _ = bucket_centroids(keys, kids, "sum")
+        c32, c16 = bucket_centroids(keys, kids, "normalized")
+        sums = node_sums.reshape(*lead, n_nodes, D)
+        hierarchy.levels.append(NodeLevel(c32.reshape(*lead, n_nodes, D), children, sums.clone(),
+                                          c16.reshape(*lead, n_nodes, D)))
+    return hierarchy

@@ -27,6 +27,13 @@ Pinning (what each function is checked against in tests/test_oracle.py):
   tree_select_row / tree_growth  brute-force sort of every candidate on tiny trees; the
                                  growth replay of _tree.py:100-142 restated literally
                                  (page ends, block counts) on small tables
+  beam_growth / beam_select_row  the multi-level replay restated literally (every page
+                                 end, every level's block closing); a brute-force walk of
+                                 every level by plain sorting on tiny three-level trees
+  build_hierarchy                level counts vs the reference loop's stop rule
+                                 (:166-170) by hand; sums by linearity (a level's total =
+                                 the buckets' total, fp64); unit-norm centroids. The
+                                 grouping is this build's (the Ward pairing is upstream's).
   ward_pair_cost                 exact rational arithmetic (fractions) and math.fsum
   ward_segments_keys             brute force (every adjacent cost recomputed from the
                                  segments each step, no links), two-cluster closed form,
@@ -277,7 +284,8 @@ def bucket_centroids(keys: np.ndarray, members: np.ndarray, mode: str = "mean") 
     """Bucket centroids from member keys, fp32.
 
     ``mean``: the bucket-mean key (the benchmark workloads). ``normalized``: the L2-normalized
-    sum (reference pipeline.py:108-115, :396-403, F.normalize eps 1e-12). Canonical
+    sum (reference pipeline.py:108-115, :396-403, F.normalize eps 1e-12). ``sum``: the
+    plain sum (the hierarchy's key sums, pipeline.py:162-164). Canonical
     order: fp32 sum over member slots in table order; the norm is
     ``fp32(sqrt(sum_d fp64(s_d)^2))`` with the fp64 squares summed in dim order.
     keys [T, D], members [rows, cap] -> [rows, D].
@@ -295,8 +303,10 @@ def bucket_centroids(keys: np.ndarray, members: np.ndarray, mode: str = "mean") 
     if mode == "mean":
         return np.where(count[:, None] > 0, acc / np.maximum(count, 1).astype(np.float32)[:, None],
                         np.float32(0)).astype(np.float32)
+    if mode == "sum":
+        return acc
     if mode != "normalized":
-        raise ValueError(f"centroid mode must be mean|normalized, got {mode!r}")
+        raise ValueError(f"centroid mode must be mean|normalized|sum, got {mode!r}")
     sq = np.zeros(rows, dtype=np.float64)
     for d in range(acc.shape[1]):
         sq = sq + acc[:, d].astype(np.float64) * acc[:, d].astype(np.float64)
@@ -464,6 +474,98 @@ def tree_select_row(query: np.ndarray, node_centroids: np.ndarray, children: np.
     fresh = np.arange(covered, max(covered, visible))
     kids = kids[(kids >= 0) & (kids < visible)]
     cand = np.unique(np.concatenate([kids, fresh]).astype(np.int64))
+    picks = np.full(top_p, -1, dtype=np.int32)
+    if cand.size:
+        scores = canonical_scores(query[None, :], bucket_centroids_[cand], mode)[0]
+        keys = (ordered_bits(scores).astype(np.int64) << np.int64(32)) | (COL_TOP - cand)
+        best = np.sort(keys)[::-1][:top_p]
+        picks[: best.size] = unpack_ids(best)
+    lst, length = expand_row(picks, members, position, window, sink, top_k)
+    return lst, length, picks
+
+
+def beam_growth(visible: int, n_levels: int, node_size: int, node_block: int, top_level: int,
+                n_nodes: list[int] | None = None) -> tuple[int, list[int], list[int]]:
+    """(covered buckets, made nodes per level, closed nodes per level) of a multi-level tree
+    for a row seeing ``visible`` buckets (reference _tree.py:100-142 ``_growth_replay``,
+    page end = the row's visible count): whole ``node_block`` blocks of buckets are covered
+    and make ``node_block / node_size`` level-1 nodes each; a level's nodes close in whole
+    blocks of ``node_block`` and make ``node_block / node_size`` nodes of the level above
+    each, up to ``top_level`` levels (and the ``n_levels`` a tree holds). ``n_nodes`` caps
+    each level at the nodes the table holds. Closed form of the replay (every page end
+    covers all whole blocks not yet covered and closes all whole blocks of open nodes)."""
+    levels = min(int(n_levels), int(top_level))
+    visible = max(int(visible), 0)
+    covered = visible // node_block * node_block
+    made, closed = [0] * levels, [0] * levels
+    if levels == 0:
+        return 0, made, closed
+    made[0] = covered // node_size
+    if n_nodes is not None and made[0] > n_nodes[0]:
+        made[0] = n_nodes[0]
+        covered = made[0] * node_size
+    for lv in range(1, levels):
+        closed[lv - 1] = made[lv - 1] // node_block * node_block
+        made[lv] = closed[lv - 1] // node_size
+        if n_nodes is not None and made[lv] > n_nodes[lv]:
+            made[lv] = n_nodes[lv]
+            closed[lv - 1] = made[lv] * node_size
+    return covered, made, closed
+
+
+def build_hierarchy(bucket_key_sums: np.ndarray, node_size: int, node_block: int,
+                    top_level: int) -> list[tuple[np.ndarray, np.ndarray, np.ndarray]]:
+    """Node levels over one table's bucket key sums [rows, D] (reference pipeline.py:153-178
+    ``build_hierarchy_gpu``): while the level below holds a full ``node_block`` block and
+    fewer than ``top_level`` levels exist (:166-170), each full block's rows make
+    ``node_block / node_size`` nodes; a node's sum is its rows' sums added in child order,
+    its centroid the normalized sum (:175-177). A node takes ``node_size`` consecutive rows
+    of its block (the reference pairs a block's rows by the Ward cost in an upstream
+    Triton kernel that is not vendored). Returns [(centroids, children, sums)] bottom up."""
+    sums = np.asarray(bucket_key_sums, dtype=np.float32)
+    levels = []
+    while sums.shape[0] // node_block and len(levels) < top_level:
+        n = sums.shape[0] // node_block * node_block // node_size
+        children = np.arange(n * node_size, dtype=np.int32).reshape(n, node_size)
+        node_sums = bucket_centroids(sums, children, "sum")
+        levels.append((bucket_centroids(sums, children, "normalized"), children, node_sums))
+        sums = node_sums
+    return levels
+
+
+def beam_select_row(query: np.ndarray, levels: list[tuple[np.ndarray, np.ndarray]], bucket_centroids_: np.ndarray,
+                    members: np.ndarray, position: int, visible: int, node_size: int, node_block: int,
+                    top_level: int, beam_width: int, top_p: int, top_k: int, window: int, sink: int,
+                    mode: str = "fp32") -> tuple[np.ndarray, int, np.ndarray]:
+    """The multi-level beam for one (row, table) (reference _tree.py:318-373 ``_beam_pick_rows``
+    with the growth of ``beam_growth``). levels[l] = (centroids [N_l, D], children [N_l,
+    node_size]) of the level-(l+1) nodes; children are rows of the level below (buckets for
+    l = 0).
+
+    From the highest level holding a made node down to level 1: the candidates are the
+    carried children plus the level's open nodes [closed, made) (at the start level: all
+    its made nodes, :344-346), each once (first-occurrence dedup, :306-315); the best
+    ``beam_width`` by score are kept (a tie to the lower node: the stable descending argsort
+    over ascending candidates, :350-351) and their children carried (:353-355). Level 0:
+    the carried buckets plus the fresh buckets [covered, visible) (:359-361), each once,
+    the best ``top_p`` (tie -> lower bucket), -1 padded; then the flat expansion. Returns
+    (list, length, picks)."""
+    n_nodes = [lv[0].shape[0] for lv in levels]
+    visible = max(int(visible), 0)
+    covered, made, closed = beam_growth(visible, len(levels), node_size, node_block, top_level, n_nodes)
+    start = sum(1 for m in made if m)
+    carried = np.zeros(0, dtype=np.int64)
+    for lv in range(start, 0, -1):
+        first_open = 0 if lv == start else closed[lv - 1]
+        cand = np.unique(np.concatenate([carried, np.arange(first_open, made[lv - 1])]).astype(np.int64))
+        cent, children = levels[lv - 1]
+        scores = canonical_scores(query[None, :], cent[cand], mode)[0]
+        keys = (ordered_bits(scores).astype(np.int64) << np.int64(32)) | (COL_TOP - cand)
+        kept = unpack_ids(np.sort(keys)[::-1][:beam_width]).astype(np.int64)
+        carried = children[kept].reshape(-1).astype(np.int64)
+    fresh = np.arange(covered, max(covered, visible))
+    carried = carried[(carried >= 0) & (carried < visible)]
+    cand = np.unique(np.concatenate([carried, fresh]).astype(np.int64))
     picks = np.full(top_p, -1, dtype=np.int32)
     if cand.size:
         scores = canonical_scores(query[None, :], bucket_centroids_[cand], mode)[0]

@@ -75,6 +75,44 @@ def test_select_limits_rejected():
                   None, None, 0, 16, 16, None)
 
 
+def _beam_args(levels=3, n_nodes=(1024, 256, 64), **kw):
+    """lsa_select_beam arguments at the reference defaults (4096 buckets of cap 16, node
+    size 4, block 64, beam 64, top_p 1024) with fake (never dereferenced) pointers."""
+    ptrs = (ctypes.c_void_p * max(levels, 1))(*([16] * max(levels, 1)))
+    counts = (ctypes.c_int32 * max(levels, 1))(*(list(n_nodes) + [64] * levels)[: max(levels, 1)])
+    args = dict(q=16, q_dtype=_abi.LSA_F32, R=1, G=1, D=128, n_levels=levels, cents=ctypes.addressof(ptrs),
+                kids=ctypes.addressof(ptrs), n_nodes=ctypes.addressof(counts), node_size=4, node_block=64,
+                top_level=3, centroids=16, members=16, ends=None, flags=0, rows=4096, cap=16, row_tables=0,
+                group_tables=0, mode=_abi.SCORE_F32, pos=16, cbs=512, bb=64, beam=64, top_p=1024, window=512,
+                sink=4, top_k=4096, lists=16, lengths=16, stream=None)
+    args.update(kw)
+    return [ptrs, counts], list(args.values())
+
+
+def test_beam_arguments_rejected_before_launch():
+    keep, args = _beam_args(levels=5, n_nodes=(1024, 256, 64, 16, 4))
+    with pytest.raises(ValueError, match="node levels"):
+        _abi.call("lsa_select_beam", *args)
+    keep, args = _beam_args(node_block=6)
+    with pytest.raises(ValueError, match="multiple of node_size"):
+        _abi.call("lsa_select_beam", *args)
+    keep, args = _beam_args(beam=2048)  # 8192 carried children exceed a level's LDS keys
+    with pytest.raises(ValueError, match="candidates"):
+        _abi.call("lsa_select_beam", *args)
+    keep, args = _beam_args(n_nodes=(1024, 256, 64), rows=16384)  # too many buckets for the dedup bitmap
+    with pytest.raises(ValueError, match="buckets"):
+        _abi.call("lsa_select_beam", *args)
+    keep, args = _beam_args(n_nodes=(1024, 0, 64))
+    with pytest.raises(ValueError, match="level 2"):
+        _abi.call("lsa_select_beam", *args)
+    keep, args = _beam_args(cents=None)
+    with pytest.raises(ValueError, match="NULL"):
+        _abi.call("lsa_select_beam", *args)
+    keep, args = _beam_args(flags=_abi.TABLE_SPANS)
+    with pytest.raises(ValueError, match="span ends"):
+        _abi.call("lsa_select_beam", *args)
+
+
 def _decode_args(**kw):
     """lsa_decode_flat arguments for a flat 32k decode shape with fake (never dereferenced)
     pointers; kw overrides by name."""

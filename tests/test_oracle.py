@@ -328,6 +328,131 @@ def test_tree_select_row_equals_brute_force():
             assert lst[:n].tolist() == [int(m) for b in want for m in members[b]]
 
 
+def _beam_growth_literal(visible, page_buckets, node_size, node_block, top_level):
+    """_tree.py:100-142 ``_growth_replay`` for one page, stepped page end by page end as
+    written there (top_level levels), up to the page whose end is the row's visible count;
+    returns (covered, made, closed)."""
+    covered, made, closed = 0, [0] * top_level, [0] * top_level
+    for end in range(page_buckets, visible + 1, page_buckets):
+        blocks = (end - covered) // node_block
+        if blocks < max(1, page_buckets // node_block):
+            continue
+        covered += blocks * node_block
+        made[0] += blocks * node_block // node_size
+        for level in range(1, top_level):
+            taken = (made[level - 1] - closed[level - 1]) // node_block * node_block
+            if not taken:
+                break
+            closed[level - 1] += taken
+            made[level] += taken // node_size
+    return covered, made, closed
+
+
+@pytest.mark.parametrize("page_buckets,node_size,node_block,top_level",
+                         [(64, 4, 64, 3), (16, 4, 64, 3), (128, 4, 64, 3), (64, 2, 16, 4), (8, 4, 16, 3)])
+def test_beam_growth_is_the_reference_replay(page_buckets, node_size, node_block, top_level):
+    for pages in range(0, 200):
+        visible = pages * page_buckets
+        assert oracle.beam_growth(visible, top_level, node_size, node_block, top_level) == \
+            _beam_growth_literal(visible, page_buckets, node_size, node_block, top_level), pages
+
+
+def _tiny_tree(rng, rows, size, block, levels_wanted, D=16):
+    """A tree of contiguous node groups over `rows` bucket centroids: level l+1 groups whole
+    blocks of `block` level-l rows into nodes of `size` consecutive rows."""
+    bcent = rng.standard_normal((rows, D)).astype(np.float32)
+    levels, below = [], bcent
+    while len(levels) < levels_wanted:
+        count = below.shape[0] // block * block
+        if not count:
+            break
+        children = np.arange(count, dtype=np.int32).reshape(-1, size)
+        cent = below[:count].reshape(-1, size, D).mean(1).astype(np.float32)
+        levels.append((cent, children))
+        below = cent
+    return bcent, levels
+
+
+def _beam_brute(q, bcent, levels, visible, size, block, top_level, beam, top_p):
+    """The beam by plain sorting: growth by the literal replay at page size `block`, every
+    level's candidates as a set, ranked by (-float64 score, id)."""
+    covered, made, closed = _beam_growth_literal(visible, block, size, block, top_level)
+    made = [min(m, lv[0].shape[0]) for m, lv in zip(made, levels)] + [0] * (top_level - len(levels))
+    start = max([l + 1 for l in range(len(levels)) if made[l]], default=0)
+    carried = set()
+    for lv in range(start, 0, -1):
+        first = 0 if lv == start else closed[lv - 1]
+        cand = carried | set(range(first, made[lv - 1]))
+        cent, children = levels[lv - 1]
+        sc = cent.astype(np.float64) @ q.astype(np.float64)
+        kept = sorted(cand, key=lambda j: (-sc[j], j))[:beam]
+        carried = {int(c) for j in kept for c in children[j]}
+    cand = {c for c in carried if c < visible} | set(range(covered, visible))
+    sc = bcent.astype(np.float64) @ q.astype(np.float64)
+    return sorted(cand, key=lambda j: (-sc[j], j))[:top_p]
+
+
+def test_beam_select_row_equals_brute_force():
+    rng = np.random.default_rng(17)
+    size, block, top_level = 2, 8, 3
+    bcent, levels = _tiny_tree(rng, 160, size, block, 3)
+    assert len(levels) == 3
+    members = np.arange(160 * 3, dtype=np.int32).reshape(160, 3)
+    for trial in range(40):
+        q = rng.standard_normal(16).astype(np.float32)
+        visible = int(rng.integers(0, 161))
+        for beam, top_p in ((2, 5), (3, 12), (8, 40)):
+            lst, n, picks = oracle.beam_select_row(q, levels, bcent, members, position=10_000, visible=visible,
+                                                   node_size=size, node_block=block, top_level=top_level,
+                                                   beam_width=beam, top_p=top_p, top_k=1000, window=0, sink=0,
+                                                   mode="fp32")
+            want = _beam_brute(q, bcent, levels, visible, size, block, top_level, beam, top_p)
+            assert picks[: len(want)].tolist() == want and (picks[len(want):] == -1).all(), (trial, visible, beam)
+            assert lst[:n].tolist() == [int(m) for b in want for m in members[b]]
+
+
+def test_beam_with_one_level_is_the_tree_select():
+    """A one-level tree through the beam equals tree_select_row's two-level walk."""
+    rng = np.random.default_rng(18)
+    bcent, levels = _tiny_tree(rng, 96, 4, 16, 1)
+    members = np.arange(96 * 2, dtype=np.int32).reshape(96, 2)
+    for visible in range(0, 97, 5):
+        q = rng.standard_normal(16).astype(np.float32)
+        a = oracle.beam_select_row(q, levels, bcent, members, 500, visible, 4, 16, 1, 3, 10, 100, 0, 0)
+        b = oracle.tree_select_row(q, levels[0][0], levels[0][1], bcent, members, 500, visible, 16, 3, 10, 100, 0, 0)
+        assert np.array_equal(a[0], b[0]) and a[1] == b[1] and np.array_equal(a[2], b[2])
+
+
+@pytest.mark.parametrize("rows,size,block,top_level,want", [
+    (4096, 4, 64, 3, [1024, 256, 64]),   # the reference defaults at 32k keys (8 keys a bucket)
+    (1000, 4, 64, 3, [240, 48]),          # 960 of 1000 rows in whole blocks; 48 nodes close no block
+    (4096, 4, 64, 2, [1024, 256]),        # top_level stops the loop
+    (63, 4, 64, 3, []),                   # no full block, no level
+    (1024, 2, 8, 4, [512, 256, 128, 64]),
+])
+def test_build_hierarchy_levels_sums_and_norms(rows, size, block, top_level, want):
+    """Level counts follow the reference loop's stop rule (pipeline.py:166-170: stop when
+    the level below holds no full block or top_level levels exist), worked by hand; every
+    level's sums add up (fp64) to the covered buckets' sums; centroids have unit norm and
+    point along their sums."""
+    rng = np.random.default_rng(rows + size)
+    sums = rng.standard_normal((rows, 16)).astype(np.float32)
+    levels = oracle.build_hierarchy(sums, size, block, top_level)
+    assert [lv[0].shape[0] for lv in levels] == want
+    reach = sums.shape[0]
+    for lvl, (cent, children, node_sums) in enumerate(levels):
+        assert children.shape == (want[lvl], size) and (children.reshape(-1) == np.arange(want[lvl] * size)).all()
+        covered = want[lvl] * size
+        for _ in range(lvl):
+            covered *= size
+        total = sums[:covered].astype(np.float64).sum(0)
+        np.testing.assert_allclose(node_sums.astype(np.float64).sum(0), total, rtol=1e-4, atol=1e-3)
+        np.testing.assert_allclose(np.linalg.norm(cent.astype(np.float64), axis=1), 1.0, rtol=1e-6)
+        cos = (cent.astype(np.float64) * node_sums).sum(1) / np.linalg.norm(node_sums.astype(np.float64), axis=1)
+        np.testing.assert_allclose(cos, 1.0, rtol=1e-6)
+        assert covered <= reach
+
+
 # --------------------------------------------------------------------------- segment build
 
 
