@@ -448,6 +448,93 @@ def tree_decode_leg(args, torch, np):
                        "read_mean_abs": float(err.mean())}}
 
 
+# ----------------------------------------------------------------------------- reference knobs
+
+
+def refcfg_decode_leg(args, torch, np, dense_us):
+    """The reference's own decode arms at its default knobs (pipeline.py:32-54: blocks of
+    512 keys, buckets of 8 keys cap 16 (64 a block), top_p 1024, top_k 4096, window 512,
+    sink 4; tree: node size 4, node blocks of 64, 3 levels, beam 64) on its benchmark
+    geometry (port/bench.py:75-81, :113-153: B=1, 32k, Hq 32 / Hkv 8, D 128 bf16, q/k/v ~
+    0.2 N(0,1); one index-space table shared by every head). Index keys / queries: the
+    mean over the key / query heads (a stand-in for upstream's regroup). Flat: the fused
+    select (bf16 scores) + the split-K read; tree: the hierarchy of 1024/256/64 nodes, the
+    multi-level beam (fp32 scores) + the same read. Each step rotates over the last 4 query
+    tokens (positions T-4 .. T-1); lists bit-exact against the numpy oracle on all 4, the
+    read within the bf16 bar on one."""
+    import oracle
+    from lsa_rocm_lab.port import pipeline
+    from lsa_rocm_lab.port.pipeline import PortConfig
+    from lsa_rocm_lab.port.read_kernel_tiled import sparse_read_auto
+
+    config = PortConfig()
+    T, NQ = T_CTX, 4
+    gen = torch.Generator(device="cuda").manual_seed(20261105)
+    q, k, v = ((torch.randn(1, T, h, D, device="cuda", generator=gen) * 0.2).to(torch.bfloat16)
+               for h in (HQ, HKV, HKV))
+    idx_k = pipeline.index_queries(k, 1)[0, :, 0].contiguous()          # [T, D]
+    idx_q = pipeline.index_queries(q[:, -NQ:], 1)[0, :, 0].contiguous()  # [NQ, D]
+    buckets = pipeline.build_buckets(idx_k, config)
+    tree = pipeline.build_hierarchy_gpu(idx_k, buckets, config)
+    pos = torch.arange(T - NQ, T, device="cuda", dtype=torch.int32)
+    qs = [q[:, T - NQ + i:T - NQ + i + 1].contiguous() for i in range(NQ)]
+    os.environ["LSA_SELECT_IMPL"] = "fused"
+    sel = {"flat": lambda i: pipeline.flat_select(idx_q[i:i + 1], pos[i:i + 1], buckets, config),
+           "tree": lambda i: pipeline.tree_select(idx_q[i:i + 1], pos[i:i + 1], buckets, tree, config)}
+    out = {}
+    reps = max(1, args.tree_steps // NQ)
+    for name, fn in sel.items():
+        res = [fn(i) for i in range(NQ)]
+        torch.cuda.synchronize()
+
+        def step(i, fn=fn):
+            lists, lengths = fn(i % NQ)
+            return sparse_read_auto(qs[i % NQ], k, v, lists[None], lengths[None], D ** -0.5)
+
+        read = lambda i, res=res: sparse_read_auto(qs[i % NQ], k, v, res[i % NQ][0][None], res[i % NQ][1][None],
+                                                   D ** -0.5)
+        sel_us = graph_launch_us(lambda i, fn=fn: fn(i % NQ), NQ, reps, torch)
+        read_us = graph_launch_us(read, NQ, reps, torch)
+        step_us = graph_launch_us(step, NQ, reps, torch)
+        toks = statistics.mean(int(r[1][0]) for r in res)
+        gathered = toks * HKV * D * 2 * 2
+        # parity: the four rows' lists against the oracle, row 0's read against the fp64 read
+        lists_np = np.stack([r[0][0].cpu().numpy() for r in res])
+        lengths_np = np.array([int(r[1][0]) for r in res])
+        members = buckets.members.cpu().numpy()
+        if name == "flat":
+            want_l, want_n = oracle.flat_select(idx_q.cpu().numpy(), pos.cpu().numpy(),
+                                                buckets.centroids.float().cpu().numpy(), members,
+                                                cluster_block_size=config.cluster_block_size,
+                                                block_buckets=config.block_bucket_count, top_p=config.top_p,
+                                                top_k=config.top_k, window=config.window_size,
+                                                sink=config.sink_size, mode="bf16")
+        else:
+            levels = [(lv.centroids.cpu().numpy(), lv.children.cpu().numpy()) for lv in tree.levels]
+            vis = oracle.visible_counts(pos.cpu().numpy(), buckets.rows, config.cluster_block_size,
+                                        config.block_bucket_count)
+            rows = [oracle.beam_select_row(idx_q[i].cpu().numpy(), levels, buckets.centroids_f32.cpu().numpy(),
+                                           members, int(pos[i]), int(vis[i]), config.node_bucket_size,
+                                           config.node_cluster_block_size, config.top_level, config.beam_width,
+                                           config.top_p, config.top_k, config.window_size, config.sink_size,
+                                           mode="fp32") for i in range(NQ)]
+            want_l, want_n = np.stack([r[0] for r in rows]), np.array([r[1] for r in rows])
+        o0 = step(0)
+        want = oracle.sparse_read(qs[0].float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
+                                  lists_np[None, :1], lengths_np[None, :1], D ** -0.5)
+        err = np.abs(o0.float().cpu().numpy() - want)
+        out[name] = {"select_us": round(sel_us, 2), "read_us": round(read_us, 2), "us_per_step": round(step_us, 2),
+                     "tokens_read": round(toks, 1), "read_gbps": round(gathered / (read_us * 1e-6) / 1e9, 1),
+                     "speedup_vs_dense": None if dense_us is None else round(dense_us / step_us, 2),
+                     "lists_bit_exact": bool(np.array_equal(lists_np, want_l)
+                                             and np.array_equal(lengths_np, want_n)),
+                     "read_max_abs": float(err.max()), "read_mean_abs": float(err.mean())}
+        log(f"refcfg {name} decode {out[name]}")
+    return {"workload": "refcfg_decode_32k", "batch": 1, "context": T, "buckets": buckets.rows,
+            "nodes": [lv.centroids.shape[0] for lv in tree.levels], "knobs": "reference PortConfig defaults",
+            "timing": "hip graphs of back-to-back steps over 4 query tokens, HIP events", **out}
+
+
 # ----------------------------------------------------------------------------- config 1 and the CPU
 
 
@@ -794,6 +881,11 @@ def main() -> int:
         tree = tree_decode_leg(args, torch, np)
         log(f"tree {tree}")
 
+    # ---- the reference's decode arms at its default knobs (flat and the 3-level tree)
+    refcfg = None
+    if not args.no_tree:
+        refcfg = refcfg_decode_leg(args, torch, np, dense.get("us_per_step") if dense else None)
+
     # ---- the bucket-table build (the index build before the path)
     build = None
     if not args.no_build:
@@ -881,6 +973,7 @@ def main() -> int:
         "block_sparse_decode": block_sparse,
         "batched_flat_decode": batched,
         "tree_decode": tree,
+        "refcfg_decode": refcfg,
         "bucket_build": build,
         "cpu_baseline": cpu,
         "parity": parity,
