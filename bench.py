@@ -694,9 +694,25 @@ def bucket_build_leg(args, torch):
         times.append(e0.elapsed_time(e1))
     ms = sorted(times)[len(times) // 2]
     merges = T // POOL - TARGET
+    # in-place growth during decode: reference-knob block tables (512-key blocks of 64
+    # buckets of at most 16 keys, 8 kv-heads) reserved for 64k keys; the step that closes
+    # the last block of the 32k cache builds its 64 rows a table into the reserved rows
+    cfg = pipeline.PortConfig()
+    tabs = pipeline.reserve_buckets(pipeline.build_buckets(data.k[:, :T - 256], cfg), 2 * T // cfg.bucket_size)
+    start = tabs.built_rows
+    grow = []
+    for _ in range(7):
+        tabs.built_rows = start
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        pipeline.grow_buckets_(tabs, data.k, cfg)
+        torch.cuda.synchronize()
+        grow.append((time.perf_counter() - w0) * 1e3)
     return {"workload": "segment_starts_32k", "tables": HKV, "positions": T, "pool": POOL, "buckets": TARGET,
             "max_size": CAP, "ms": round(ms, 3), "merges_per_table": merges,
-            "us_per_merge": round(ms * 1e3 / merges, 3), "deterministic": bool(torch.equal(first, again))}
+            "us_per_merge": round(ms * 1e3 / merges, 3), "deterministic": bool(torch.equal(first, again)),
+            "grow_one_block_ms": round(sorted(grow)[len(grow) // 2], 3),
+            "grow": "one closed 512-key block x 8 kv-heads into reserved rows (wall, synchronized)"}
 
 
 def main() -> int:

@@ -15,6 +15,10 @@ a HIP kernel in liblsa_rocm.so:
   (:378-403);
 * ``dense_read`` (:340-370) stays torch SDPA - it is the dense comparator.
 
+The index grows with the cache: ``extend_buckets`` appends newly closed blocks, and
+capacity tables (``reserve_buckets``, allocated once for the longest context) take them
+in place (``grow_buckets_``) with no tensor moved.
+
 Per-kv-head selection (the benchmark geometry) extends the shapes: index queries
 [R, G, D] against tables with a leading group axis [G, rows, ...] (one table per
 kv-head) or [R, G, rows, ...] (one per sequence and kv-head) give lists [R, G, W] and
@@ -76,6 +80,10 @@ class Buckets:
     # how the centroids were made ("mean" or "normalized"), when a builder here made them;
     # extend_buckets builds appended rows the same way
     centroid: str | None = None
+    # capacity tables (reserve_buckets): rows [0, built_rows) hold buckets, the rest are
+    # reserved for blocks that have not closed yet (members -1, size 0, zero centroids,
+    # span end INT32_MAX, so no query sees them); None: every row is built
+    built_rows: int | None = None
 
     @property
     def rows(self) -> int:
@@ -716,7 +724,10 @@ def extend_buckets(buckets: Buckets, keys: torch.Tensor, config: PortConfig, **b
     blocks rows // block_bucket_count .. T // cluster_block_size - 1, built as
     ``build_buckets`` builds them, concatenated after the existing rows. The new rows keep
     the tables' centroid kind (``buckets.centroid``, else ``build_kw["centroid"]``), span
-    flag and optional tensors: a table without ``centroids_f32`` or ``ends`` gets none."""
+    flag and optional tensors: a table without ``centroids_f32`` or ``ends`` gets none.
+    Capacity tables (``reserve_buckets``) grow in place instead (``grow_buckets_``)."""
+    if buckets.built_rows is not None:  # capacity tables grow in place
+        return grow_buckets_(buckets, keys, config, **build_kw)
     bpb = config.block_bucket_count
     have = buckets.rows // bpb
     T = keys.shape[0] if keys.dim() == 2 else keys.shape[1]
@@ -802,3 +813,72 @@ def build_hierarchy_gpu(index_keys: torch.Tensor, buckets: Buckets, config: Port
         hierarchy.levels.append(NodeLevel(c32.reshape(*lead, n_nodes, D), children, sums.clone(),
                                           c16.reshape(*lead, n_nodes, D)))
     return hierarchy
+
+
+UNBUILT_END = 0x7FFFFFFF  # span end of a reserved row: never <= position + 1
+
+
+def reserve_buckets(buckets: Buckets, capacity: int) -> Buckets:
+    """Capacity tables for in-place growth (the decode cache's incremental index,
+    reference pipeline.py:184-186 visibility as blocks close; docs/PORT_NOTES.md:12-14):
+    every table of ``buckets`` copied into tables of ``capacity`` rows, allocated once. The
+    rows past the built ones are reserved: members -1, size 0, zero centroids and, for
+    tables with span ends, the end ``UNBUILT_END``, so no position sees them. Every select
+    and decode entry takes the capacity tables as they are (``rows`` = capacity);
+    ``grow_buckets_`` writes newly closed blocks into the reserved rows without moving any
+    tensor, so pointers captured in a HIP graph stay valid.
+
+    Visibility: with span ends a reserved row is never visible. Without them the
+    reference's block rule ``pos // cluster_block_size * block_bucket_count`` applies,
+    which reaches a reserved row only for a position past the blocks built, so a caller
+    grows the tables before it queries a position in a newly closed block (as a decode
+    step does: the block closes, the index grows, then the step selects)."""
+    built = buckets.rows if buckets.built_rows is None else buckets.built_rows
+    if capacity < built:
+        raise ValueError(f"reserve_buckets: capacity {capacity} < the {built} rows built")
+    lead = buckets.centroids.shape[:-2]
+    device = buckets.centroids.device
+
+    def grown(t, fill):
+        axis = len(lead)  # the row axis
+        out = torch.full((*lead, capacity, *t.shape[axis + 1:]), fill, dtype=t.dtype, device=device)
+        out.narrow(axis, 0, built).copy_(t.narrow(axis, 0, built))
+        return out
+
+    return Buckets(grown(buckets.centroids, 0), grown(buckets.members, -1), grown(buckets.sizes, 0),
+                   centroids_f32=None if buckets.centroids_f32 is None else grown(buckets.centroids_f32, 0),
+                   ends=None if buckets.ends is None else grown(buckets.ends, UNBUILT_END),
+                   spans=buckets.spans, centroid=buckets.centroid, built_rows=built)
+
+
+def grow_buckets_(buckets: Buckets, keys: torch.Tensor, config: PortConfig, **build_kw) -> Buckets:
+    """In place: the blocks closed since the tables were built (blocks built_rows //
+    block_bucket_count .. T // cluster_block_size - 1 of ``keys``), built as
+    ``build_buckets`` builds them (same centroid kind, span ends when the tables carry
+    them), copied into the reserved rows of the capacity tables from ``reserve_buckets``.
+    No tensor is reallocated. Returns ``buckets`` with ``built_rows`` advanced; raises
+    ValueError when the capacity is exhausted."""
+    if buckets.built_rows is None:
+        raise ValueError("grow_buckets_ takes capacity tables (reserve_buckets); extend_buckets grows others")
+    bpb = config.block_bucket_count
+    have = buckets.built_rows // bpb
+    T = keys.shape[0] if keys.dim() == 2 else keys.shape[1]
+    blocks = T // config.cluster_block_size
+    if blocks <= have:
+        return buckets
+    new_rows = (blocks - have) * bpb
+    if buckets.built_rows + new_rows > buckets.rows:
+        raise ValueError(f"grow_buckets_: {buckets.built_rows + new_rows} rows exceed the capacity {buckets.rows}")
+    kind = buckets.centroid or build_kw.pop("centroid", "normalized")
+    build_kw.pop("centroid", None)
+    new = build_buckets(keys, config, first_block=have, spans=buckets.ends is not None, centroid=kind, **build_kw)
+    lo, hi = buckets.built_rows, buckets.built_rows + new_rows
+    buckets.centroids[..., lo:hi, :].copy_(new.centroids)
+    buckets.members[..., lo:hi, :].copy_(new.members)
+    buckets.sizes[..., lo:hi].copy_(new.sizes)
+    if buckets.centroids_f32 is not None:
+        buckets.centroids_f32[..., lo:hi, :].copy_(new.centroids_f32)
+    if buckets.ends is not None:
+        buckets.ends[..., lo:hi].copy_(new.ends)
+    buckets.built_rows = hi
+    return buckets

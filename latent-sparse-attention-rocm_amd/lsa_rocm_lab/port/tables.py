@@ -33,7 +33,14 @@ FORMAT = "lsa-bucket-tables/1"
 
 
 def save_buckets(path: str | os.PathLike, buckets: Buckets) -> None:
-    """Write `buckets` (any device) to `path` in the CSR format above."""
+    """Write `buckets` (any device) to `path` in the CSR format above. Capacity tables
+    (reserve_buckets) write their built rows only."""
+    if buckets.built_rows is not None:
+        b = buckets.built_rows
+        buckets = Buckets(buckets.centroids[..., :b, :], buckets.members[..., :b, :], buckets.sizes[..., :b],
+                          centroids_f32=None if buckets.centroids_f32 is None else buckets.centroids_f32[..., :b, :],
+                          ends=None if buckets.ends is None else buckets.ends[..., :b], spans=buckets.spans,
+                          centroid=buckets.centroid)
     members = buckets.members.detach().to("cpu", torch.int32)
     sizes = buckets.sizes.detach().to("cpu", torch.int64)
     if members.dim() < 2 or tuple(sizes.shape) != tuple(members.shape[:-1]):

@@ -12,6 +12,8 @@ matches the oracle per block and drives the flat select; a cache extended block 
 as it grows equals one built once.
 """
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -172,6 +174,68 @@ def test_extend_buckets_keeps_centroid_kind_and_optional_fields():
         bare = dataclasses.replace(part, centroids_f32=None, centroid=None)
         grown = pipeline.extend_buckets(bare, keys, config, centroid="mean")
         assert grown.centroids_f32 is None and torch.equal(grown.centroids, full.centroids)
+
+
+def test_grow_buckets_in_place_equals_a_full_build(tmp_path):
+    """Capacity tables reserved at 3 closed blocks (96 rows, 80 needed at 5 blocks) grow in
+    place as the cache grows (a step that closes no block, then one block, then one more):
+    no tensor moves; the built rows equal the tables built once at 5 blocks, the reserved
+    rows stay empty (members -1, size 0, zero centroids, span end INT32_MAX); the flat
+    select (both implementations) and the fused decode give the same lists and outputs on
+    the capacity tables as on the full build; growth past the capacity raises; a saved
+    capacity table loads as its built rows."""
+    import dataclasses
+
+    from lsa_rocm_lab.port import tables
+
+    config = pipeline.PortConfig(cluster_block_size=256, bucket_size=16, bucket_cap=32, pool_size=8, top_p=8,
+                                 top_k=200, window_size=32, sink_size=4)
+    T_full = 5 * 256 + 40
+    keys = clustered_keys(1, T_full, 2, 64, torch.bfloat16, seed=47).to(DEV)
+    gen = torch.Generator().manual_seed(48)
+    vals = torch.randn(1, T_full, 2, 64, generator=gen).to(torch.bfloat16).to(DEV)
+    q = torch.randn(1, 1, 4, 64, generator=gen).to(torch.bfloat16).to(DEV)
+    for spans in (False, True):
+        full = pipeline.build_buckets(keys, config, spans=spans)
+        grown = pipeline.reserve_buckets(pipeline.build_buckets(keys[:, :3 * 256 + 10], config, spans=spans), 96)
+        assert grown.built_rows == 48 and grown.rows == 96
+        fields = ("centroids", "members", "sizes", "centroids_f32", "ends")
+        ptrs = {f: getattr(grown, f).data_ptr() for f in fields if getattr(grown, f) is not None}
+        for T in (3 * 256 + 200, 4 * 256, T_full):
+            assert pipeline.grow_buckets_(grown, keys[:, :T], config) is grown
+        assert grown.built_rows == 80
+        assert {f: getattr(grown, f).data_ptr() for f in ptrs} == ptrs
+        for f in fields:
+            a, b = getattr(grown, f), getattr(full, f)
+            assert (a is None and b is None) or torch.equal(a[:, :80], b), (spans, f)
+        assert bool((grown.members[:, 80:] == -1).all()) and bool((grown.sizes[:, 80:] == 0).all())
+        assert bool((grown.centroids[:, 80:] == 0).all()) and bool((grown.centroids_f32[:, 80:] == 0).all())
+        if spans:
+            assert bool((grown.ends[:, 80:] == pipeline.UNBUILT_END).all())
+        idx = pipeline.index_queries(keys[:, -5:], 2)[0]  # five query rows [5, 2, 64]
+        pos = torch.tensor([T_full - 1, 1300, 1100, 600, 250], dtype=torch.int32, device=DEV)
+        for impl in ("fused", "reference"):
+            os.environ["LSA_SELECT_IMPL"] = impl
+            a = pipeline.flat_select(idx, pos, grown, config)
+            b = pipeline.flat_select(idx, pos, full, config)
+            assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), (spans, impl)
+        os.environ.pop("LSA_SELECT_IMPL")
+        last = torch.tensor([T_full - 1], dtype=torch.int32, device=DEV)
+        out_g, lists_g, n_g = pipeline.flat_decode(q, keys, vals, last, grown, config, scale=0.125)
+        out_f, lists_f, n_f = pipeline.flat_decode(q, keys, vals, last, full, config, scale=0.125)
+        assert torch.equal(lists_g, lists_f) and torch.equal(n_g, n_f) and torch.equal(out_g, out_f), spans
+        assert pipeline.extend_buckets(grown, keys, config) is grown  # capacity tables grow in place
+        path = tmp_path / f"grown{int(spans)}.safetensors"
+        tables.save_buckets(path, grown)
+        back = tables.load_buckets(path, DEV)
+        assert back.rows == 80 and torch.equal(back.members, full.members) and back.built_rows is None
+    small = pipeline.reserve_buckets(pipeline.build_buckets(keys[:, :3 * 256], config), 64)
+    with pytest.raises(ValueError, match="capacity"):
+        pipeline.grow_buckets_(small, keys, config)
+    with pytest.raises(ValueError, match="capacity"):
+        pipeline.reserve_buckets(full, 40)
+    with pytest.raises(ValueError, match="capacity tables"):
+        pipeline.grow_buckets_(dataclasses.replace(full), keys, config)
 
 
 def test_tables_saved_and_loaded_select_alike(tmp_path):
