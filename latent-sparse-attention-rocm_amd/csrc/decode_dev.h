@@ -139,9 +139,12 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
       group_mean_slice<T, SPAN, GQ>(qrow, tid & 15, true, qs);
       ScreenLds& scr = *(ScreenLds*)(smem + sel_keys_offset());  // in place of the keys
       uint64_t* sbest = (uint64_t*)(smem + sel_keys_offset() + sizeof(ScreenLds));
+      // span ends are nondecreasing: the visible rows are a prefix, counted once (a span-end
+      // load per screened row would sit on the screen's critical path)
+      __shared__ int vis_lds[2 * LSA_WAVES];
+      const int nvis = ends ? visible_count_block(position, a.rows, ends, vis_lds) : vis;
       screen_topk<D, 4>(
-          qs, cent, a.rows, [](int j) { return j; },
-          [&](int j) { return ends ? (int64_t)ends[j] <= lim : j < vis; }, a.K, a.kp, sbest, scr);
+          qs, cent, a.rows, [](int j) { return j; }, [&](int j) { return j < nvis; }, a.K, a.kp, sbest, scr);
       for (int j = tid; j < a.K; j += LSA_BLOCK) {
         const int32_t b = key_column(u_to_key(sbest[j]));
         sh.pick[j] = (b >= 0 && b < a.rows) ? b : -1;
@@ -450,7 +453,6 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
   T* outp = (T*)a.out + (r * a.Hq + (int64_t)g * GQ) * D;
   float* parts = a.ws_part + i * (int64_t)a.NR * PSTRIDE;
   if (role < n_part) {
-    merge_token_groups<T, D, GQ>(st);
     finish_span<T, D, GQ>(sh.rd, st, n_part == 1, outp, n_part > 1 ? parts + (int64_t)role * PSTRIDE : nullptr, 0);
   }
   // the list's padding [length, W) is shared out over the unit's readers
@@ -599,8 +601,9 @@ __device__ __forceinline__ void rep_role(const DecodeArgs& a, char* smem, int64_
   qr.load(qrow, a.scale_log2);
   float qs[SPAN];
   group_mean_slice<T, SPAN, GQ>(qrow, tid & 15, true, qs);
+  __syncthreads();  // the span ends in LDS
   screen_topk<D, 2>(
-      qs, cent, rows, [](int j) { return j; }, [&](int j) { return (int64_t)ends[j] <= lim; }, K, a.kp, ex.best,
+      qs, cent, rows, [](int j) { return j; }, [&](int j) { return (int64_t)ex.ends[j] <= lim; }, K, a.kp, ex.best,
       ex.scr);
   DECODE_MARK(11);
   if (w == 0) {

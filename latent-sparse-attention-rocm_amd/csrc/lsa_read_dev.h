@@ -474,7 +474,7 @@ __device__ __forceinline__ void merge_token_groups(AttnState<T, D, GQ>& st) {
 }
 
 // Attention of the GQ query heads of one kv-head over list slots [lo, hi) from an empty
-// state, token groups merged (qrow: the GQ contiguous query rows).
+// state (qrow: the GQ contiguous query rows); the token groups are merged by finish_span.
 template <typename T, int D, int GQ, typename IdOf>
 __device__ __forceinline__ void attend_span(const T* qrow, const T* kb, const T* vb, int64_t tstride, int64_t Tk,
                                             int lo, int hi, IdOf id_of, float scale_log2, AttnState<T, D, GQ>& st) {
@@ -482,26 +482,88 @@ __device__ __forceinline__ void attend_span(const T* qrow, const T* kb, const T*
   q.load(qrow, scale_log2);
   st.clear();
   attend_tiles<T, D, GQ, true>(q, kb, vb, tstride, Tk, lo, hi, id_of, scale_log2, true, st);
-  merge_token_groups<T, D, GQ>(st);
 }
 
-// Merges the four waves' states of a span. direct: writes the normalised output to outp
+// Sums each of N values (N % 4 == 0) over the four 16-lane rows of the wave by two rounds
+// of row swaps, each swap serving two values: after the 16-row swap of values a and b, one
+// register holds rows [a0, b0, a2, b2] and the other [a1, b1, a3, b3], whose sum packs two
+// half-reductions into one register; the 32-row swap of two such registers does the same
+// for the row pairs. Value v's wave total lands in out[v / 4], row v % 4 (every lane of
+// that row, for its own column): 1.5 N instructions instead of the 4 N of a butterfly that
+// keeps every value in every row.
+template <int N>
+__device__ __forceinline__ void row_transpose_sum(const float (&x)[N], float (&out)[N / 4]) {
+  static_assert(N % 4 == 0, "row_transpose_sum packs four values a register");
+  // The swaps are written as instructions: the permlane swap builtins' second result is
+  // mis-modelled by this compiler when both results feed one expression (it reuses the
+  // first). s_nop 1: the wait states a swap needs after a VALU write of its operands.
+  float half[N / 2];
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    float a = x[2 * i], b = x[2 * i + 1];
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    half[i] = a + b;
+  }
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) {
+    float a = half[2 * i], b = half[2 * i + 1];
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    out[i] = a + b;
+  }
+}
+
+// Merges the token groups of each wave and then the four waves' states of a span (st: a
+// lane's state as attend_tiles leaves it). direct: writes the normalised output to outp
 // (GQ rows of D); otherwise publishes the partial (m[GQ], l[GQ], acc[GQ][D]) at part with
 // write-through stores. Every thread calls it.
 template <typename T, int D, int GQ, int MAXS>
-__device__ __forceinline__ void finish_span(ReadLds<D, GQ, MAXS>& sh, const AttnState<T, D, GQ>& st, bool direct,
+__device__ __forceinline__ void finish_span(ReadLds<D, GQ, MAXS>& sh, AttnState<T, D, GQ>& st, bool direct,
                                             T* outp, float* part, int empty_nan) {
   using S = ReadShape<T, D, GQ>;
   constexpr int VEC = S::VEC, LPT = S::LPT;
   const int lane = threadIdx.x & (LSA_WAVE - 1);
   const int w = threadIdx.x / LSA_WAVE;
   const int tg = lane / LPT, lp = lane % LPT;
-  if (tg == 0) {
+  constexpr bool ON = ReadMfma<T, D, GQ>::ON;
+  // matrix-core instances: the accumulators in LDS as the row-transposed sums leave them,
+  // register i of lane l of wave w at stage[(w * NA + i) * 64 + l] (within sh.acc)
+  constexpr int NA = GQ * VEC / 4;
+  float* stage = &sh.acc[0][0][0];
+  if constexpr (ON) {
+    // one running maximum per head for the whole wave (the token groups are the four
+    // 16-lane rows): the groups merge by sums, packed four values a register, stored as
+    // whole wave rows (conflict-free)
+    float x[GQ * VEC], tot[NA];
 #pragma unroll
     for (int h = 0; h < GQ; ++h) {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) sh.acc[w][h][lp * VEC + e] = st.acc[h][e];
-      if (lp == 0) { sh.m[w][h] = st.m[h]; sh.l[w][h] = st.l[h]; }
+      for (int e = 0; e < VEC; ++e) x[h * VEC + e] = st.acc[h][e];
+    }
+    row_transpose_sum<GQ * VEC>(x, tot);
+#pragma unroll
+    for (int i = 0; i < NA; ++i) stage[(w * NA + i) * LSA_WAVE + lane] = tot[i];
+    constexpr int NL = (GQ + 3) / 4 * 4;
+    float xl[NL], tl[NL / 4];
+#pragma unroll
+    for (int h = 0; h < NL; ++h) xl[h] = h < GQ ? st.l[h] : 0.0f;
+    row_transpose_sum<NL>(xl, tl);
+#pragma unroll
+    for (int i = 0; i < NL / 4; ++i) {
+      if (lp == 0 && 4 * i + tg < GQ) sh.l[w][4 * i + tg] = tl[i];
+    }
+    if (lane == 0) {  // the maxima are uniform over the wave (static indices keep st in registers)
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) sh.m[w][h] = st.m[h];
+    }
+  } else {
+    merge_token_groups<T, D, GQ>(st);
+    if (tg == 0) {
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) sh.acc[w][h][lp * VEC + e] = st.acc[h][e];
+        if (lp == 0) { sh.m[w][h] = st.m[h]; sh.l[w][h] = st.l[h]; }
+      }
     }
   }
   __syncthreads();
@@ -512,11 +574,15 @@ __device__ __forceinline__ void finish_span(ReadLds<D, GQ, MAXS>& sh, const Attn
 #pragma unroll
     for (int ww = 0; ww < LSA_WAVES; ++ww) M = fmaxf(M, sh.m[ww][h]);
     float L = 0.0f, A = 0.0f;
+    // the staged slot of (h, d): value v = h VEC + d % VEC of column d / VEC, register v / 4
+    // of row v % 4
+    const int v = h * VEC + d % VEC;
+    const int slot = (v / 4) * LSA_WAVE + 16 * (v % 4) + d / VEC;
 #pragma unroll
     for (int ww = 0; ww < LSA_WAVES; ++ww) {
       const float f = fast_exp2(sh.m[ww][h] - M);
       L += sh.l[ww][h] * f;
-      A += sh.acc[ww][h][d] * f;
+      A += (ON ? stage[ww * NA * LSA_WAVE + slot] : sh.acc[ww][h][d]) * f;
     }
     if (direct) {
       store_out<T>(outp + j, L > 0.0f ? A / L : (empty_nan ? NAN : 0.0f));

@@ -215,9 +215,11 @@ __global__ __launch_bounds__(LSA_BLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)
     if (a.screen) {  // the whole table on the matrix cores, exact (screen_topk)
       ScreenLds& scr = *(ScreenLds*)smem;
       uint64_t* sbest = (uint64_t*)((char*)smem + sizeof(ScreenLds));
+      // span ends are nondecreasing: the visible rows are a prefix, counted once
+      __shared__ int vis_lds[2 * LSA_WAVES];
+      const int nvis = ends ? visible_count_block(position, a.rows, ends, vis_lds) : vis;
       screen_topk<D, 2>(
-          qs, cent, a.rows, [](int j) { return j; },
-          [&](int j) { return ends ? (int64_t)ends[j] <= lim : j < vis; }, a.K, a.kp, sbest, scr);
+          qs, cent, a.rows, [](int j) { return j; }, [&](int j) { return j < nvis; }, a.K, a.kp, sbest, scr);
       for (int j = threadIdx.x; j < a.K; j += LSA_BLOCK) pk[j] = key_column(u_to_key(sbest[j]));
       __syncthreads();
       expand_row(a, pk, t, ends, position, i, scan);

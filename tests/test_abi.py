@@ -131,7 +131,7 @@ def test_decode_workspace_sizes():
     stride = ((units * 2 * K + 1023) // 1024) * 1024 + 64
     assert n == 2 * units + 8 * stride  # arrival counters + 8 record copies
     keys = 8 * 512 * 8  # every column key of 16 select splits
-    parts = 8 * 32 * 4 * 130 * 4  # 32 readers' partials per unit (one a pick)
+    parts = 8 * 16 * 4 * 130 * 4  # 16 readers' partials per unit (one a pick, at most 16 by default)
     got = _abi.size("lsa_decode_flat_scratch_bytes", _abi.LSA_BF16, 1, 32, 8, 128, 512, 32, 0, 0, 16, 0)
     assert got == ((keys + 255) // 256) * 256 + parts
     assert _abi.size("lsa_decode_flat_counters", 1, 8, 512, 65) == 0  # more than 64 picks is not served
