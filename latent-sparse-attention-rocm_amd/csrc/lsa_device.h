@@ -71,6 +71,40 @@ __device__ __forceinline__ int32_t key_column(int64_t key) {
 
 // ---------------------------------------------------------------- wave / block scans
 
+// DPP lane exchange inside a row of 16: dpp_ctrl quad_perm / row mirrors.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+// v_permlane16_swap / v_permlane32_swap of a and b (gfx950): the odd 16-lane rows of a
+// trade places with the even rows of b (16), or a's upper 32 lanes with b's lower 32 (32).
+// Written as instructions: this compiler's builtins mis-model the swap's second result when
+// both results feed one expression (it reuses the first). s_nop 1: the wait states a swap
+// needs after a VALU write of its operands.
+__device__ __forceinline__ void row_swap16(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void row_swap32(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+// The partner value of lane ^ x for x in {16, 32} (v_permlane16/32_swap of two copies),
+// else a bpermute shuffle. The builtins serve here: each result is used alone.
+__device__ __forceinline__ float lane_xor(float v, int x) {
+  const int iv = __builtin_bit_cast(int, v);
+  const int row = (threadIdx.x & (LSA_WAVE - 1)) >> 4;
+  if (x == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);  // [v0, v0, v2, v2], [v1, v1, v3, v3]
+    return __builtin_bit_cast(float, (row & 1) ? r[0] : r[1]);
+  }
+  if (x == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);  // [v0, v1, v0, v1], [v2, v3, v2, v3]
+    return __builtin_bit_cast(float, (row & 2) ? r[0] : r[1]);
+  }
+  return __shfl_xor(v, x, LSA_WAVE);
+}
+
 __device__ __forceinline__ int wave_inclusive_sum(int x) {
   const int lane = threadIdx.x & (LSA_WAVE - 1);
 #pragma unroll

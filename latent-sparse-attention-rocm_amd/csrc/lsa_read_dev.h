@@ -68,28 +68,6 @@ struct ReadShape {
 // to zero, which the normaliser never notices.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// DPP lane exchange inside a row of 16: dpp_ctrl quad_perm / row mirrors.
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
-}
-
-// The partner value of lane ^ x for x in {16, 32} (v_permlane16/32_swap on gfx950), else
-// a bpermute shuffle.
-__device__ __forceinline__ float lane_xor(float v, int x) {
-  const int iv = __builtin_bit_cast(int, v);
-  const int row = (threadIdx.x & (LSA_WAVE - 1)) >> 4;
-  if (x == 16) {
-    const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
-    return __builtin_bit_cast(float, (row & 1) ? r[0] : r[1]);
-  }
-  if (x == 32) {
-    const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
-    return __builtin_bit_cast(float, (row & 2) ? r[0] : r[1]);
-  }
-  return __shfl_xor(v, x, LSA_WAVE);
-}
-
 // Sum over each group of N consecutive lanes (N a power of two <= 64), in every lane of
 // the group: DPP adds inside rows of 16, lane swaps across rows.
 template <int N>
@@ -494,20 +472,17 @@ __device__ __forceinline__ void attend_span(const T* qrow, const T* kb, const T*
 template <int N>
 __device__ __forceinline__ void row_transpose_sum(const float (&x)[N], float (&out)[N / 4]) {
   static_assert(N % 4 == 0, "row_transpose_sum packs four values a register");
-  // The swaps are written as instructions: the permlane swap builtins' second result is
-  // mis-modelled by this compiler when both results feed one expression (it reuses the
-  // first). s_nop 1: the wait states a swap needs after a VALU write of its operands.
   float half[N / 2];
 #pragma unroll
   for (int i = 0; i < N / 2; ++i) {
     float a = x[2 * i], b = x[2 * i + 1];
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    row_swap16(a, b);
     half[i] = a + b;
   }
 #pragma unroll
   for (int i = 0; i < N / 4; ++i) {
     float a = half[2 * i], b = half[2 * i + 1];
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    row_swap32(a, b);
     out[i] = a + b;
   }
 }
