@@ -452,7 +452,7 @@ __device__ __forceinline__ void merge_token_groups(AttnState<T, D, GQ>& st) {
 }
 
 // Attention of the GQ query heads of one kv-head over list slots [lo, hi) from an empty
-// state (qrow: the GQ contiguous query rows); the token groups are merged by finish_span.
+// state, token groups merged (qrow: the GQ contiguous query rows).
 template <typename T, int D, int GQ, typename IdOf>
 __device__ __forceinline__ void attend_span(const T* qrow, const T* kb, const T* vb, int64_t tstride, int64_t Tk,
                                             int lo, int hi, IdOf id_of, float scale_log2, AttnState<T, D, GQ>& st) {
@@ -460,6 +460,7 @@ __device__ __forceinline__ void attend_span(const T* qrow, const T* kb, const T*
   q.load(qrow, scale_log2);
   st.clear();
   attend_tiles<T, D, GQ, true>(q, kb, vb, tstride, Tk, lo, hi, id_of, scale_log2, true, st);
+  merge_token_groups<T, D, GQ>(st);
 }
 
 // Sums each of N values (N % 4 == 0) over the four 16-lane rows of the wave by two rounds
@@ -491,7 +492,7 @@ __device__ __forceinline__ void row_transpose_sum(const float (&x)[N], float (&o
 // lane's state as attend_tiles leaves it). direct: writes the normalised output to outp
 // (GQ rows of D); otherwise publishes the partial (m[GQ], l[GQ], acc[GQ][D]) at part with
 // write-through stores. Every thread calls it.
-template <typename T, int D, int GQ, int MAXS>
+template <typename T, int D, int GQ, int MAXS, bool MERGED = false>
 __device__ __forceinline__ void finish_span(ReadLds<D, GQ, MAXS>& sh, AttnState<T, D, GQ>& st, bool direct,
                                             T* outp, float* part, int empty_nan) {
   using S = ReadShape<T, D, GQ>;
@@ -499,7 +500,7 @@ __device__ __forceinline__ void finish_span(ReadLds<D, GQ, MAXS>& sh, AttnState<
   const int lane = threadIdx.x & (LSA_WAVE - 1);
   const int w = threadIdx.x / LSA_WAVE;
   const int tg = lane / LPT, lp = lane % LPT;
-  constexpr bool ON = ReadMfma<T, D, GQ>::ON;
+  constexpr bool ON = ReadMfma<T, D, GQ>::ON && !MERGED;
   // matrix-core instances: the accumulators in LDS as the row-transposed sums leave them,
   // register i of lane l of wave w at stage[(w * NA + i) * 64 + l] (within sh.acc)
   constexpr int NA = GQ * VEC / 4;
@@ -531,7 +532,7 @@ __device__ __forceinline__ void finish_span(ReadLds<D, GQ, MAXS>& sh, AttnState<
       for (int h = 0; h < GQ; ++h) sh.m[w][h] = st.m[h];
     }
   } else {
-    merge_token_groups<T, D, GQ>(st);
+    if constexpr (!MERGED) merge_token_groups<T, D, GQ>(st);
     if (tg == 0) {
 #pragma unroll
       for (int h = 0; h < GQ; ++h) {

@@ -126,7 +126,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void read_kernel(ReadArgs a) {
   attend_span<T, D, GQ>(qrow, kb, vb, a.kv_st, a.Tk, lo, hi, [&](int j) { return slot_id(list, j, hi); },
                         a.scale_log2, st);
   float* part = n_act > 1 ? a.ws_part + (i * (int64_t)gridDim.y + s) * PSTRIDE : nullptr;
-  finish_span<T, D, GQ>(sh, st, n_act == 1, outp, part, a.empty_nan);
+  finish_span<T, D, GQ, kMaxSplits, true>(sh, st, n_act == 1, outp, part, a.empty_nan);
   if (n_act == 1) return;
   if (!arrive_last(&a.ws_count[i], n_act, &sh.flag)) return;
   combine_partials<T, D, GQ>(sh, a.ws_part + i * (int64_t)gridDim.y * PSTRIDE, n_act, outp, a.empty_nan);
