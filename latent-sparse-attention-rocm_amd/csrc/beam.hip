@@ -117,7 +117,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_beam_kernel(const QT* q, boo
     const int K = min(a.beam, a.cand_pow2);
     bool done = false;
     if constexpr (__is_same(CT, bf16_t) && SPAN >= 2 && SPAN <= 8) {
-      if (a.screen && a.cand_pow2 <= kScreenMaxRows && K <= LSA_WAVE) {
+      if (a.screen && screen_pays(D, a.cand_pow2, K)) {
         screen_topk<D, 2>(
             qs, ncent, a.cand_pow2, [&](int j) { return cand[j]; }, [](int) { return true; }, K, a.beam_pow2, best,
             scr);
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_beam_kernel(const QT* q, boo
   const int K0 = min(a.top_p, a.cand_pow2);
   bool done0 = false;
   if constexpr (__is_same(CT, bf16_t) && SPAN >= 2 && SPAN <= 8) {
-    if (a.screen && a.cand_pow2 <= kScreenMaxRows && K0 <= LSA_WAVE) {
+    if (a.screen && screen_pays(D, a.cand_pow2, K0)) {
       screen_topk<D, 2>(
           qs, bcent, a.cand_pow2, [&](int j) { return cand[j]; }, [](int) { return true; }, K0, a.top_pow2, best,
           scr);

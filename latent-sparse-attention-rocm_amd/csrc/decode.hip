@@ -258,7 +258,7 @@ extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int 
   a.cluster_block = cluster_block_size; a.block_buckets = block_buckets;
   a.K = p.K; a.kp = p.kp; a.window = window; a.sink = sink; a.top_k = top_k; a.W = top_k + window + sink;
   a.S = select_splits; a.cs = select_splits > 0 ? (rows + select_splits - 1) / select_splits : rows;
-  a.screen = select_splits == 1 && score_mode == LSA_SCORE_BF16 && screen_fits(D, rows, p.K) ? 1 : 0;
+  a.screen = select_splits == 1 && score_mode == LSA_SCORE_BF16 && screen_pays(D, rows, p.K) ? 1 : 0;
   a.span = p.span; a.NR = p.NR;
   a.scale_log2 = scale * kLog2e;
   a.spin_limit = decode_debug().spin_limit > 0 ? decode_debug().spin_limit

@@ -696,7 +696,7 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
   const size_t base_lds = sizeof(uint64_t) * (((size_t)rows + kp + 1) & ~(size_t)1);
   const size_t stage_lds = sizeof(int32_t) * ((size_t)width + 4);
   a.stage = (!a.spans && width % 4 == 0 && ((uintptr_t)lists % 16) == 0 && base_lds + stage_lds <= kMaxDynLds) ? 1 : 0;
-  a.screen = splits == 1 && score_mode == LSA_SCORE_BF16 && screen_fits(D, rows, K) ? 1 : 0;
+  a.screen = splits == 1 && score_mode == LSA_SCORE_BF16 && screen_pays(D, rows, K) ? 1 : 0;
   size_t shmem = base_lds + (a.stage ? stage_lds : 0);
   const size_t screen_lds = sizeof(ScreenLds) + sizeof(uint64_t) * (size_t)kp;
   if (a.screen && screen_lds > shmem) shmem = screen_lds;
@@ -755,8 +755,8 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
   a.cand_pow2 = next_pow2((int)(cand_cap > 0 ? cand_cap : 1)); a.top_pow2 = next_pow2(top_p);
   a.window = window; a.sink = sink; a.top_k = top_k; a.lists = lists; a.lengths = lengths;
   a.spans = (table_flags & LSA_TABLE_SPANS) && top_p <= LSA_WAVE ? 1 : 0;  // else the member rows
-  a.screen1 = score_mode == LSA_SCORE_BF16 && screen_fits(D, n_nodes, beam) ? 1 : 0;
-  a.screen0 = score_mode == LSA_SCORE_BF16 && screen_fits(D, a.cand_pow2, top_p < a.cand_pow2 ? top_p : a.cand_pow2)
+  a.screen1 = score_mode == LSA_SCORE_BF16 && screen_pays(D, n_nodes, beam) ? 1 : 0;
+  a.screen0 = score_mode == LSA_SCORE_BF16 && screen_pays(D, a.cand_pow2, top_p < a.cand_pow2 ? top_p : a.cand_pow2)
                   ? 1 : 0;
   const int keys_slots = a.nodes_pow2 > a.cand_pow2 ? a.nodes_pow2 : a.cand_pow2;
   const int best_slots = a.beam_pow2 > a.top_pow2 ? a.beam_pow2 : a.top_pow2;
