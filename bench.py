@@ -400,6 +400,15 @@ def tree_decode_leg(args, torch, np):
     read_gbps = gathered / (read_us * 1e-6) / 1e9
     log(f"tree decode {us:.1f} us/step (select {sel_us:.1f} + read {read_us:.1f} us); read {read_gbps:.0f} GB/s "
         f"on {gathered / 1e6:.1f} MB gathered")
+    # the same step in one launch (the tree select role in the fused decode kernel)
+    fused = lambda i: pipeline.tree_decode(qs[i % NQ], data.k, data.v, pos, buckets, tree, config)
+    f0 = fused(0)
+    torch.cuda.synchronize()
+    fused_same = bool(torch.equal(f0[1], res[0][0]) and torch.equal(f0[2], res[0][1]))
+    fused_err = float((f0[0].float() - res[0][2].float()).abs().max().item())
+    fused_us = graph_launch_us(fused, NQ, reps, torch)
+    log(f"fused tree decode {fused_us:.1f} us/step ({gathered / (fused_us * 1e-6) / 1e9:.0f} GB/s); lists equal: "
+        f"{fused_same}")
     # dense SDPA decode over the whole 17 GB cache
     dense_us = None
     try:
@@ -442,6 +451,10 @@ def tree_decode_leg(args, torch, np):
             "gathered_bytes": int(gathered), "read_gbps": round(read_gbps, 1),
             "read_roofline_frac": round(read_gbps / HBM_PEAK_GBS, 4),
             "step_gbps": round(gathered / (us * 1e-6) / 1e9, 1),
+            "fused_us_per_step": round(fused_us, 2),
+            "fused_gbps": round(gathered / (fused_us * 1e-6) / 1e9, 1),
+            "fused_roofline_frac": round(gathered / (fused_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "fused_lists_equal": fused_same, "fused_vs_unfused_read_max_abs": fused_err,
             "dense_us": None if dense_us is None else round(dense_us, 1),
             "speedup_vs_dense": None if dense_us is None else round(dense_us / us, 2),
             "parity": {"lists_bit_exact_sampled": exact, "read_max_abs": float(err.max()),

@@ -271,6 +271,25 @@ int lsa_decode_flat(const void* q, const void* k, const void* v, int dtype, int6
                     int64_t n_counters, void* scratch, size_t scratch_bytes, int32_t* lists, int32_t* lengths,
                     void* out, int32_t* status, void* stream);
 
+/* The fused decode step over a one-level node tree (reference port/bench.py:147-153 with
+ * tree_select for flat_select: pipeline.py:319-337, _tree.py:318-373 with one node level,
+ * the growth of _tree.py:100-142): one launch holds one select workgroup per (row,
+ * kv-head) - the group-mean index query, the made nodes' best beam_width, then the best
+ * top_p of their visible children plus the fresh buckets, exactly lsa_select_tree's lists -
+ * and the readers of lsa_decode_flat. node_centroids [tables, n_nodes, D] in the scoring
+ * type, children [tables, n_nodes, node_size] int32 bucket rows; at most 64 picks and 8192
+ * buckets a table. Counters and scratch as lsa_decode_flat with one select split
+ * (lsa_decode_flat_counters, lsa_decode_flat_scratch_bytes(..., select_splits = 1, ...)). */
+int lsa_decode_tree(const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk, int32_t Hq,
+                    int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride, int64_t kv_head_stride,
+                    const void* node_centroids, const int32_t* children, int32_t n_nodes, int32_t node_size,
+                    int32_t node_block, int32_t beam_width, const void* centroids, const int32_t* members,
+                    const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables,
+                    int64_t group_tables, int score_mode, const int32_t* positions, int32_t cluster_block_size,
+                    int32_t block_buckets, int32_t top_p, int32_t window, int32_t sink, int32_t top_k, float scale,
+                    int32_t readers, int32_t* counters, int64_t n_counters, void* scratch, size_t scratch_bytes,
+                    int32_t* lists, int32_t* lengths, void* out, int32_t* status, void* stream);
+
 /* lsa_decode_flat without caller buffers, for callers that cannot allocate (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart
  * in the reference. The counters and scratch live in a 16 MiB file-scope device array per

@@ -179,73 +179,107 @@ extern "C" size_t lsa_decode_flat_scratch_bytes(int dtype, int64_t R, int32_t Hq
   return ((p.keys_bytes + 255) & ~(size_t)255) + p.part_bytes;
 }
 
-extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk,
-                               int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride,
-                               int64_t kv_head_stride, const void* centroids, const int32_t* members,
-                               const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables,
-                               int64_t group_tables, int score_mode, const int32_t* positions,
-                               int32_t cluster_block_size, int32_t block_buckets, int32_t top_p, int32_t window,
-                               int32_t sink, int32_t top_k, float scale, int32_t select_splits, int32_t readers,
-                               int32_t* counters, int64_t n_counters, void* scratch, size_t scratch_bytes,
-                               int32_t* lists, int32_t* lengths, void* out, int32_t* status, void* stream) {
+namespace {
+
+// A one-level node tree for the fused decode's select (lsa_decode_tree).
+struct TreeSpec {
+  const void* node_centroids;
+  const int32_t* children;
+  int32_t n_nodes, node_size, node_block, beam_width;
+};
+
+int decode_launch(const char* who, const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk,
+                  int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride,
+                  int64_t kv_head_stride, const void* centroids, const int32_t* members, const int32_t* ends,
+                  int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables, int64_t group_tables,
+                  int score_mode, const int32_t* positions, int32_t cluster_block_size, int32_t block_buckets,
+                  int32_t top_p, int32_t window, int32_t sink, int32_t top_k, float scale, int32_t select_splits,
+                  int32_t readers, int32_t* counters, int64_t n_counters, void* scratch, size_t scratch_bytes,
+                  int32_t* lists, int32_t* lengths, void* out, int32_t* status, void* stream, const TreeSpec* tree) {
   LSA_REQUIRE(q && k && v && centroids && members && positions && lists && lengths && out && counters, LSA_ERR_NULL,
-              "lsa_decode_flat: NULL pointer");
+              "%s: NULL pointer", who);
   LSA_REQUIRE(dtype == LSA_F32 || dtype == LSA_BF16 || dtype == LSA_F16, LSA_ERR_DTYPE,
-              "lsa_decode_flat: dtype %d", dtype);
+              "%s: dtype %d", who, dtype);
   LSA_REQUIRE(D == 32 || D == 64 || D == 128 || D == 256, LSA_ERR_SHAPE,
-              "lsa_decode_flat: head dim %d not in {32,64,128,256}", D);
-  LSA_REQUIRE(Hq >= 1 && Hkv >= 1 && Hq % Hkv == 0, LSA_ERR_SHAPE, "lsa_decode_flat: Hq %d must group onto Hkv %d",
+              "%s: head dim %d not in {32,64,128,256}", who, D);
+  LSA_REQUIRE(Hq >= 1 && Hkv >= 1 && Hq % Hkv == 0, LSA_ERR_SHAPE, "%s: Hq %d must group onto Hkv %d", who,
               Hq, Hkv);
   const int gq = Hq / Hkv;
   LSA_REQUIRE(gq == 1 || gq == 2 || gq == 4 || gq == 8, LSA_ERR_SHAPE,
-              "lsa_decode_flat: group size %d not in {1,2,4,8}", gq);
+              "%s: group size %d not in {1,2,4,8}", who, gq);
   LSA_REQUIRE(score_mode == LSA_SCORE_BF16 || score_mode == LSA_SCORE_F32, LSA_ERR_DTYPE,
-              "lsa_decode_flat: bad score mode");
+              "%s: bad score mode", who);
   LSA_REQUIRE(rows >= 1 && cap >= 1 && row_tables >= 0 && group_tables >= 0, LSA_ERR_SHAPE,
-              "lsa_decode_flat: bad table sizes");
-  LSA_REQUIRE(R >= 0 && Tk >= 0 && Tk <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_decode_flat: bad sizes");
+              "%s: bad table sizes", who);
+  LSA_REQUIRE(R >= 0 && Tk >= 0 && Tk <= 0x7FFFFFFF, LSA_ERR_SHAPE, "%s: bad sizes", who);
   LSA_REQUIRE(top_p >= 1 && window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE,
-              "lsa_decode_flat: top_p >= 1, window/sink/top_k >= 0");
-  LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "lsa_decode_flat: cluster_block_size must be >= 1");
-  LSA_REQUIRE((table_flags & ~LSA_TABLE_SPANS) == 0, LSA_ERR_SHAPE, "lsa_decode_flat: unknown table flags %d",
+              "%s: top_p >= 1, window/sink/top_k >= 0", who);
+  LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "%s: cluster_block_size must be >= 1", who);
+  LSA_REQUIRE((table_flags & ~LSA_TABLE_SPANS) == 0, LSA_ERR_SHAPE, "%s: unknown table flags %d", who,
               table_flags);
   LSA_REQUIRE(!(table_flags & LSA_TABLE_SPANS) || ends, LSA_ERR_SHAPE,
-              "lsa_decode_flat: LSA_TABLE_SPANS needs the span ends");
+              "%s: LSA_TABLE_SPANS needs the span ends", who);
   const int K = top_p < rows ? top_p : rows;
-  LSA_REQUIRE(K <= kMaxPicks, LSA_ERR_SHAPE, "lsa_decode_flat: %d picks exceed %d", K, kMaxPicks);
+  LSA_REQUIRE(K <= kMaxPicks, LSA_ERR_SHAPE, "%s: %d picks exceed %d", who, K, kMaxPicks);
   LSA_REQUIRE((int64_t)K * cap < 0x7FFFFFFF && (int64_t)top_k + window + sink <= 0x7FFFFFFF, LSA_ERR_SHAPE,
-              "lsa_decode_flat: list too wide");
+              "%s: list too wide", who);
   LSA_REQUIRE(select_splits >= 0 && select_splits <= 256 && select_splits <= rows, LSA_ERR_SHAPE,
-              "lsa_decode_flat: select splits in [0, min(256, rows)], got %d", select_splits);
+              "%s: select splits in [0, min(256, rows)], got %d", who, select_splits);
   if (select_splits == 0) {
     const char* why = rep_unfit(dtype, D, gq, rows, top_p, score_mode, table_flags);
-    LSA_REQUIRE(why == nullptr, LSA_ERR_SHAPE, "lsa_decode_flat: the replicated select (splits 0) does not apply: %s",
+    LSA_REQUIRE(why == nullptr, LSA_ERR_SHAPE, "%s: the replicated select (splits 0) does not apply: %s", who,
                 why ? why : "");
   }
   const uintptr_t mis = ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)centroids) & 15;
-  LSA_REQUIRE(mis == 0, LSA_ERR_ALIGN, "lsa_decode_flat: q/k/v/centroids must be 16-byte aligned");
+  LSA_REQUIRE(mis == 0, LSA_ERR_ALIGN, "%s: q/k/v/centroids must be 16-byte aligned", who);
   const int64_t esize = dtype == LSA_F32 ? 4 : 2;
   LSA_REQUIRE(kv_batch_stride >= 0 && kv_token_stride >= D && kv_head_stride >= D, LSA_ERR_SHAPE,
-              "lsa_decode_flat: K/V strides must leave rows of %d elements apart", D);
+              "%s: K/V strides must leave rows of %d elements apart", who, D);
   LSA_REQUIRE(((kv_batch_stride | kv_token_stride | kv_head_stride) * esize) % 16 == 0, LSA_ERR_ALIGN,
-              "lsa_decode_flat: K/V strides must keep rows 16-byte aligned");
+              "%s: K/V strides must keep rows 16-byte aligned", who);
   const int64_t units = R * Hkv;
   if (units == 0) return LSA_OK;
   Plan p;
   LSA_TRY(plan_decode(dtype, D, gq, units, rows, top_p, window, sink, select_splits, readers, &p));
   LSA_REQUIRE(p.rep || p.kp + rows <= 6144, LSA_ERR_SHAPE,
-              "lsa_decode_flat: %d columns + %d picks exceed 6144 LDS keys", rows, p.kp);
-  LSA_REQUIRE(p.shmem <= kMaxLds, LSA_ERR_SHAPE, "lsa_decode_flat: %zu bytes of LDS exceed %zu", p.shmem, kMaxLds);
+              "%s: %d columns + %d picks exceed 6144 LDS keys", who, rows, p.kp);
+  int nodes_pow2 = 0, beam_pow2 = 0, cand_pow2 = 0, top_pow2 = 0;
+  if (tree) {
+    LSA_REQUIRE(tree->node_centroids && tree->children, LSA_ERR_NULL, "%s: NULL node tables", who);
+    LSA_REQUIRE(tree->n_nodes >= 1 && tree->node_size >= 1 && tree->node_block >= 1 && tree->beam_width >= 1,
+                LSA_ERR_SHAPE, "%s: n_nodes, node_size, node_block, beam_width >= 1", who);
+    LSA_REQUIRE(rows <= 8192, LSA_ERR_SHAPE, "%s: %d buckets exceed the 8192 of the dedup bitmap", who, rows);
+    LSA_REQUIRE((((uintptr_t)tree->node_centroids) & 15) == 0, LSA_ERR_ALIGN,
+                "%s: node centroids must be 16-byte aligned", who);
+    const int beam = tree->beam_width < tree->n_nodes ? tree->beam_width : tree->n_nodes;
+    // fresh buckets [covered, visible): fewer than node_block past the made nodes, or every
+    // bucket past the nodes' reach
+    const int64_t reach = (int64_t)tree->n_nodes * tree->node_size;
+    const int64_t max_fresh = rows - reach > (int64_t)tree->node_block - 1 ? rows - reach : tree->node_block - 1;
+    const int64_t cand_cap = (int64_t)beam * tree->node_size + (max_fresh < rows ? max_fresh : rows);
+    LSA_REQUIRE(tree->n_nodes <= 6144 && cand_cap <= 6144, LSA_ERR_SHAPE,
+                "%s: %d nodes / %lld candidates exceed 6144 LDS keys", who, tree->n_nodes, (long long)cand_cap);
+    nodes_pow2 = next_pow2(tree->n_nodes);
+    beam_pow2 = next_pow2(beam);
+    cand_pow2 = next_pow2((int)(cand_cap > 0 ? cand_cap : 1));
+    top_pow2 = next_pow2(p.K < cand_pow2 ? p.K : cand_pow2);
+    const size_t sel = sel_keys_offset() + sizeof(uint64_t) * (size_t)((nodes_pow2 > cand_pow2 ? nodes_pow2 : cand_pow2) +
+                                                                      (beam_pow2 > top_pow2 ? beam_pow2 : top_pow2)) +
+                       sizeof(int32_t) * (size_t)cand_pow2 + sizeof(uint32_t) * (size_t)((rows + 31) / 32);
+    const size_t rd = reader_lds_d(D, gq, p.span);
+    p.shmem = sel > rd ? sel : rd;
+  }
+  LSA_REQUIRE(p.shmem <= kMaxLds, LSA_ERR_SHAPE, "%s: %zu bytes of LDS exceed %zu", who, p.shmem, kMaxLds);
   const int64_t grid = units * (select_splits + p.NR);
-  LSA_REQUIRE(grid <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_decode_flat: too many workgroups");
+  LSA_REQUIRE(grid <= 0x7FFFFFFF, LSA_ERR_SHAPE, "%s: too many workgroups", who);
   const int64_t need_counters = lsa_decode_flat_counters(R, Hkv, rows, top_p);
   LSA_REQUIRE(need_counters > 0 && n_counters >= need_counters, LSA_ERR_WORKSPACE,
-              "lsa_decode_flat: %lld counters < %lld", (long long)n_counters, (long long)need_counters);
+              "%s: %lld counters < %lld", who, (long long)n_counters, (long long)need_counters);
   const size_t keys_at = (p.keys_bytes + 255) & ~(size_t)255;
   const size_t need = keys_at + p.part_bytes;
   LSA_REQUIRE(need == 0 || (scratch && scratch_bytes >= need), LSA_ERR_WORKSPACE,
-              "lsa_decode_flat: scratch %zu < %zu bytes", scratch_bytes, need);
-  LSA_REQUIRE(((uintptr_t)scratch % 16) == 0, LSA_ERR_ALIGN, "lsa_decode_flat: scratch must be 16-byte aligned");
+              "%s: scratch %zu < %zu bytes", who, scratch_bytes, need);
+  LSA_REQUIRE(((uintptr_t)scratch % 16) == 0, LSA_ERR_ALIGN, "%s: scratch must be 16-byte aligned", who);
 
   DecodeArgs a;
   a.q = q; a.k = k; a.v = v; a.out = out;
@@ -260,6 +294,15 @@ extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int 
   a.S = select_splits; a.cs = select_splits > 0 ? (rows + select_splits - 1) / select_splits : rows;
   a.screen = select_splits == 1 && score_mode == LSA_SCORE_BF16 && screen_pays(D, rows, p.K) ? 1 : 0;
   a.span = p.span; a.NR = p.NR;
+  a.tree = tree ? 1 : 0;
+  a.node_centroids = tree ? tree->node_centroids : nullptr;
+  a.children = tree ? tree->children : nullptr;
+  a.n_nodes = tree ? tree->n_nodes : 0;
+  a.node_size = tree ? tree->node_size : 0;
+  a.node_block = tree ? tree->node_block : 0;
+  a.beam = tree ? tree->beam_width : 0;
+  a.nodes_pow2 = nodes_pow2; a.beam_pow2 = beam_pow2; a.cand_pow2 = cand_pow2; a.top_pow2 = top_pow2;
+  if (tree) a.screen = 0;
   a.scale_log2 = scale * kLog2e;
   a.spin_limit = decode_debug().spin_limit > 0 ? decode_debug().spin_limit
                                               : 1 << 22;  // polls of about a microsecond each: seconds
@@ -277,6 +320,43 @@ extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int 
   if (dtype == LSA_BF16) decode::launch_bf16(a, p.rep, bf16, D, gq, g3, p.shmem, s);
   else if (dtype == LSA_F16) decode::launch_f16(a, p.rep, bf16, D, gq, g3, p.shmem, s);
   else decode::launch_f32(a, p.rep, bf16, D, gq, g3, p.shmem, s);
-  LSA_LAUNCHED("lsa_decode_flat");
+  LSA_LAUNCHED(who);
   return LSA_OK;
+}
+
+}  // namespace
+
+extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk,
+                               int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride,
+                               int64_t kv_head_stride, const void* centroids, const int32_t* members,
+                               const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables,
+                               int64_t group_tables, int score_mode, const int32_t* positions,
+                               int32_t cluster_block_size, int32_t block_buckets, int32_t top_p, int32_t window,
+                               int32_t sink, int32_t top_k, float scale, int32_t select_splits, int32_t readers,
+                               int32_t* counters, int64_t n_counters, void* scratch, size_t scratch_bytes,
+                               int32_t* lists, int32_t* lengths, void* out, int32_t* status, void* stream) {
+  return decode_launch("lsa_decode_flat", q, k, v, dtype, R, Tk, Hq, Hkv, D, kv_batch_stride, kv_token_stride,
+                       kv_head_stride, centroids, members, ends, table_flags, rows, cap, row_tables, group_tables,
+                       score_mode, positions, cluster_block_size, block_buckets, top_p, window, sink, top_k, scale,
+                       select_splits, readers, counters, n_counters, scratch, scratch_bytes, lists, lengths, out,
+                       status, stream, nullptr);
+}
+
+extern "C" int lsa_decode_tree(const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk,
+                               int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride,
+                               int64_t kv_head_stride, const void* node_centroids, const int32_t* children,
+                               int32_t n_nodes, int32_t node_size, int32_t node_block, int32_t beam_width,
+                               const void* centroids, const int32_t* members, const int32_t* ends,
+                               int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables,
+                               int64_t group_tables, int score_mode, const int32_t* positions,
+                               int32_t cluster_block_size, int32_t block_buckets, int32_t top_p, int32_t window,
+                               int32_t sink, int32_t top_k, float scale, int32_t readers, int32_t* counters,
+                               int64_t n_counters, void* scratch, size_t scratch_bytes, int32_t* lists,
+                               int32_t* lengths, void* out, int32_t* status, void* stream) {
+  const TreeSpec tree{node_centroids, children, n_nodes, node_size, node_block, beam_width};
+  return decode_launch("lsa_decode_tree", q, k, v, dtype, R, Tk, Hq, Hkv, D, kv_batch_stride, kv_token_stride,
+                       kv_head_stride, centroids, members, ends, table_flags, rows, cap, row_tables, group_tables,
+                       score_mode, positions, cluster_block_size, block_buckets, top_p, window, sink, top_k, scale, 1,
+                       readers, counters, n_counters, scratch, scratch_bytes, lists, lengths, out, status, stream,
+                       &tree);
 }

@@ -47,6 +47,12 @@ struct DecodeArgs {
   int S, cs;           // select splits and columns per split
   int screen;          // S == 1 with bf16 tables that fit screen_topk: the select screens its table
   int span, NR;        // slots per read part, readers per unit
+  // tree select (one workgroup a unit): node level over the bucket table
+  int tree;                     // 1: the select role walks a one-level node tree
+  const void* node_centroids;   // [tables, n_nodes, D], the centroid type
+  const int32_t* children;      // [tables, n_nodes, node_size] bucket rows
+  int n_nodes, node_size, node_block, beam;
+  int nodes_pow2, beam_pow2, cand_pow2, top_pow2;
   float scale_log2;
   int spin_limit;
   int skip_publish;    // test hook: select workgroups never publish the record (readers give up)
@@ -107,6 +113,109 @@ __device__ __forceinline__ void group_mean_slice(const QT* q, int p, bool bf16_m
 __device__ __forceinline__ int64_t window_start_of(int64_t position, int window) {
   const int64_t ws = position + 1 - window;
   return ws > 0 ? ws : 0;
+}
+
+// The select's last step, once sh.pick[0..K) holds the unit's picks (bucket rows, -1 =
+// none): each pick's kept members are counted, the list length written and the unit's
+// record published (every copy, write-through). Every thread calls it.
+__device__ __forceinline__ void publish_picks(const DecodeArgs& a, SelLds& sh, int64_t i, int64_t t, int64_t position,
+                                              const int32_t* ends) {
+  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
+  // kept members of every pick (sink <= id < window start). Span tables: the range
+  // [ends[b - 1], ends[b]) clipped to [sink, window start), from two ends words. Otherwise
+  // wave w counts picks w, w + 4, ... eight at a time; a member row streams through the
+  // wave in 16-byte lane loads (256 slots per wave load; 64 four-byte loads without
+  // vec_rows), counted with ballots
+  const int32_t* tab = a.members + t * (int64_t)a.rows * a.cap;
+  const int64_t wstart = window_start_of(position, a.window);
+  constexpr int MJ = 8;
+  if (a.spans) {
+    if (w == 0 && lane < a.K) {
+      const int b = sh.pick[lane];
+      const int64_t begin = b > 0 ? ends[b - 1] : 0, end = b >= 0 ? ends[b] : 0;
+      const int64_t lo = begin > a.sink ? begin : a.sink, hi = end < wstart ? end : wstart;
+      sh.cnt[lane] = b >= 0 && hi > lo ? (int)(hi - lo) : 0;
+      sh.first[lane] = (int)lo;
+    }
+  }
+  for (int jb = 0; jb < (a.spans ? 0 : a.K); jb += MJ * LSA_WAVES) {
+    int cnt[MJ];
+    int b[MJ];
+#pragma unroll
+    for (int m = 0; m < MJ; ++m) {
+      const int j = jb + m * LSA_WAVES + w;
+      b[m] = j < a.K ? sh.pick[j] : -1;
+      cnt[m] = 0;
+    }
+    const int step = a.vec_rows ? 4 * LSA_WAVE : LSA_WAVE;
+    for (int c0 = 0; c0 < a.cap; c0 += step) {
+      if (a.vec_rows) {
+        int4 x[MJ];
+        const int e = c0 + 4 * lane;
+#pragma unroll
+        for (int m = 0; m < MJ; ++m) {  // unconditional (clamped) loads: all in flight
+          const bool ok = b[m] >= 0 && e < a.cap;
+          x[m] = *(const int4*)(tab + (ok ? (int64_t)b[m] * a.cap + e : 0));
+          if (!ok) x[m] = make_int4(-1, -1, -1, -1);
+        }
+#pragma unroll
+        for (int m = 0; m < MJ; ++m) {
+          const int32_t v4[4] = {x[m].x, x[m].y, x[m].z, x[m].w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            cnt[m] += (int)__popcll(__ballot(v4[k] >= a.sink && (int64_t)v4[k] < wstart));
+        }
+      } else {
+        int32_t x[MJ];
+        const int e = c0 + lane;
+#pragma unroll
+        for (int m = 0; m < MJ; ++m) {
+          const bool ok = b[m] >= 0 && e < a.cap;
+          x[m] = tab[ok ? (int64_t)b[m] * a.cap + e : 0];
+          if (!ok) x[m] = -1;
+        }
+#pragma unroll
+        for (int m = 0; m < MJ; ++m) cnt[m] += (int)__popcll(__ballot(x[m] >= a.sink && (int64_t)x[m] < wstart));
+      }
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int m = 0; m < MJ; ++m) {
+        const int j = jb + m * LSA_WAVES + w;
+        if (j < a.K) sh.cnt[j] = cnt[m];
+      }
+    }
+  }
+  __syncthreads();
+  DECODE_MARK(5);
+  if (w == 0) {
+    const int c = lane < a.K ? sh.cnt[lane] : 0;
+    int incl = c;
+#pragma unroll
+    for (int d = 1; d < LSA_WAVE; d <<= 1) {
+      const int y = __shfl_up(incl, d, LSA_WAVE);
+      if (lane >= d) incl += y;
+    }
+    const int end = incl < a.top_k ? incl : a.top_k;
+    if (lane < a.K) {
+      sh.rec[lane] = (a.spans ? sh.first[lane] : sh.pick[lane]) + 2;  // pick, or its first kept id
+      sh.rec[a.K + lane] = end + 1;
+    }
+    if (lane == a.K - 1) {
+      const int64_t n_win = position + 1 - wstart > 0 ? position + 1 - wstart : 0;
+      const int64_t n_sink = a.sink < wstart ? a.sink : wstart;
+      a.lengths[i] = end + (int)n_win + (int)n_sink;
+    }
+  }
+  __syncthreads();
+  if (a.skip_publish) return;
+  // every copy of the record, write-through
+  const int words = 2 * a.K;
+  for (int x = tid; x < kRecordCopies * words; x += LSA_BLOCK) {
+    const int c = x / words, k = x - c * words;
+    coherent_store_i32(a.record + c * a.cstride + i * words + k, sh.rec[k]);
+  }
+  DECODE_MARK(6);
 }
 
 template <typename T, typename CT, int D, int GQ>
@@ -231,101 +340,82 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
     DECODE_MARK(4);
   }
 
-  // kept members of every pick (sink <= id < window start). Span tables: the range
-  // [ends[b - 1], ends[b]) clipped to [sink, window start), from two ends words. Otherwise
-  // wave w counts picks w, w + 4, ... eight at a time; a member row streams through the
-  // wave in 16-byte lane loads (256 slots per wave load; 64 four-byte loads without
-  // vec_rows), counted with ballots
-  const int32_t* tab = a.members + t * (int64_t)a.rows * a.cap;
-  const int64_t wstart = window_start_of(position, a.window);
-  constexpr int MJ = 8;
-  if (a.spans) {
-    if (w == 0 && lane < a.K) {
-      const int b = sh.pick[lane];
-      const int64_t begin = b > 0 ? ends[b - 1] : 0, end = b >= 0 ? ends[b] : 0;
-      const int64_t lo = begin > a.sink ? begin : a.sink, hi = end < wstart ? end : wstart;
-      sh.cnt[lane] = b >= 0 && hi > lo ? (int)(hi - lo) : 0;
-      sh.first[lane] = (int)lo;
+  publish_picks(a, sh, i, t, position, ends);
+}
+
+// The tree select of unit i (one workgroup; reference _tree.py:318-373 with one node
+// level, the growth of :100-142 at page end V = the unit's visible bucket count): the
+// made nodes are [0, C / node_size) with C = min(floor(V / node_block) * node_block,
+// n_nodes * node_size); the best `beam` made nodes (a tie to the lower node), then the
+// best top_p of their visible children plus the fresh buckets [C, V), each bucket once (an
+// LDS bitmap over bucket ids), a tie to the lower bucket; exact canonical scores at both
+// levels. The picks then go out as the flat select's do (publish_picks). The same
+// selection as select_tree_kernel.
+template <typename T, typename CT, int D, int GQ>
+__device__ __forceinline__ void tree_role(const DecodeArgs& a, char* smem, int64_t i) {
+  constexpr int SPAN = D / 16;
+  constexpr bool BF16_MODE = __is_same(CT, bf16_t);
+  SelLds& sh = *(SelLds*)smem;
+  uint64_t* keys = (uint64_t*)(smem + sel_keys_offset());                 // [max(nodes_pow2, cand_pow2)]
+  uint64_t* best = keys + max(a.nodes_pow2, a.cand_pow2);                 // [max(beam_pow2, top_pow2)]
+  int32_t* cand = (int32_t*)(best + max(a.beam_pow2, a.top_pow2));        // [cand_pow2]
+  uint32_t* seen = (uint32_t*)(cand + a.cand_pow2);                       // [(rows + 31) / 32]
+  const int tid = threadIdx.x;
+  const int64_t r = (uint32_t)i / (uint32_t)a.G;
+  const int g = (int)((uint32_t)i % (uint32_t)a.G);
+  const int64_t position = a.positions[r];
+  const int64_t t = r * a.row_tables + g * a.group_tables;
+  const int32_t* ends = a.ends ? a.ends + t * a.rows : nullptr;
+  DECODE_MARK(0);
+  float qs[SPAN];
+  const T* qrow = (const T*)a.q + (r * a.Hq + (int64_t)g * GQ) * D;
+  group_mean_slice<T, SPAN, GQ>(qrow, tid & 15, BF16_MODE, qs);
+  __shared__ int vis_lds[2 * LSA_WAVES];
+  const int visible = max(0, ends ? visible_count_block(position, a.rows, ends, vis_lds)
+                                  : visible_count(position, a.rows, a.cluster_block, a.block_buckets, nullptr));
+  const int covered = min(visible / a.node_block * a.node_block, a.n_nodes * a.node_size);
+  const int made = covered / a.node_size;
+
+  // the node level: the made nodes, the best `beam`
+  const CT* ncent = (const CT*)a.node_centroids + t * (int64_t)a.n_nodes * D;
+  const int beam = min(a.beam, a.n_nodes);
+  score_slice_keys<CT, SPAN>(qs, ncent, D, 0, a.n_nodes, made, keys);
+  __syncthreads();
+  block_topk_sorted(keys, a.n_nodes, beam, a.beam_pow2, best, &sh.tks, &sh.st);
+  DECODE_MARK(1);
+
+  // the buckets: the kept nodes' visible children, then the fresh buckets, each once
+  const int n_fresh = max(0, visible - covered);
+  const int n_kids = beam * a.node_size;
+  const int n_cand = n_kids + n_fresh;
+  const int32_t* kids = a.children + t * (int64_t)a.n_nodes * a.node_size;
+  for (int x = tid; x < (a.rows + 31) / 32; x += LSA_BLOCK) seen[x] = 0;
+  __syncthreads();
+  for (int j = tid; j < a.cand_pow2; j += LSA_BLOCK) {
+    int32_t c = -1;
+    if (j < n_kids) {
+      const int node = key_column(u_to_key(best[j / a.node_size]));
+      if (node >= 0) c = kids[(int64_t)node * a.node_size + j % a.node_size];
+    } else if (j < n_cand) {
+      c = covered + (j - n_kids);
     }
-  }
-  for (int jb = 0; jb < (a.spans ? 0 : a.K); jb += MJ * LSA_WAVES) {
-    int cnt[MJ];
-    int b[MJ];
-#pragma unroll
-    for (int m = 0; m < MJ; ++m) {
-      const int j = jb + m * LSA_WAVES + w;
-      b[m] = j < a.K ? sh.pick[j] : -1;
-      cnt[m] = 0;
-    }
-    const int step = a.vec_rows ? 4 * LSA_WAVE : LSA_WAVE;
-    for (int c0 = 0; c0 < a.cap; c0 += step) {
-      if (a.vec_rows) {
-        int4 x[MJ];
-        const int e = c0 + 4 * lane;
-#pragma unroll
-        for (int m = 0; m < MJ; ++m) {  // unconditional (clamped) loads: all in flight
-          const bool ok = b[m] >= 0 && e < a.cap;
-          x[m] = *(const int4*)(tab + (ok ? (int64_t)b[m] * a.cap + e : 0));
-          if (!ok) x[m] = make_int4(-1, -1, -1, -1);
-        }
-#pragma unroll
-        for (int m = 0; m < MJ; ++m) {
-          const int32_t v4[4] = {x[m].x, x[m].y, x[m].z, x[m].w};
-#pragma unroll
-          for (int k = 0; k < 4; ++k)
-            cnt[m] += (int)__popcll(__ballot(v4[k] >= a.sink && (int64_t)v4[k] < wstart));
-        }
-      } else {
-        int32_t x[MJ];
-        const int e = c0 + lane;
-#pragma unroll
-        for (int m = 0; m < MJ; ++m) {
-          const bool ok = b[m] >= 0 && e < a.cap;
-          x[m] = tab[ok ? (int64_t)b[m] * a.cap + e : 0];
-          if (!ok) x[m] = -1;
-        }
-#pragma unroll
-        for (int m = 0; m < MJ; ++m) cnt[m] += (int)__popcll(__ballot(x[m] >= a.sink && (int64_t)x[m] < wstart));
-      }
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int m = 0; m < MJ; ++m) {
-        const int j = jb + m * LSA_WAVES + w;
-        if (j < a.K) sh.cnt[j] = cnt[m];
-      }
-    }
+    c = (c >= 0 && c < visible) ? c : -1;
+    const uint32_t bit = 1u << (c & 31);
+    cand[j] = (c >= 0 && !(atomicOr(&seen[c >> 5], bit) & bit)) ? c : -1;
   }
   __syncthreads();
-  DECODE_MARK(5);
-  if (w == 0) {
-    const int c = lane < a.K ? sh.cnt[lane] : 0;
-    int incl = c;
-#pragma unroll
-    for (int d = 1; d < LSA_WAVE; d <<= 1) {
-      const int y = __shfl_up(incl, d, LSA_WAVE);
-      if (lane >= d) incl += y;
-    }
-    const int end = incl < a.top_k ? incl : a.top_k;
-    if (lane < a.K) {
-      sh.rec[lane] = (a.spans ? sh.first[lane] : sh.pick[lane]) + 2;  // pick, or its first kept id
-      sh.rec[a.K + lane] = end + 1;
-    }
-    if (lane == a.K - 1) {
-      const int64_t n_win = position + 1 - wstart > 0 ? position + 1 - wstart : 0;
-      const int64_t n_sink = a.sink < wstart ? a.sink : wstart;
-      a.lengths[i] = end + (int)n_win + (int)n_sink;
-    }
+  const CT* bcent = (const CT*)a.centroids + t * (int64_t)a.rows * D;
+  const int k = min(a.K, a.cand_pow2);
+  score_keys<CT, SPAN>(qs, bcent, D, a.cand_pow2, [&](int j) { return cand[j]; }, keys);
+  __syncthreads();
+  block_topk_sorted(keys, a.cand_pow2, k, a.top_pow2, best, &sh.tks, &sh.st);
+  for (int j = tid; j < a.K; j += LSA_BLOCK) {
+    const int32_t b = j < k ? key_column(u_to_key(best[j])) : -1;
+    sh.pick[j] = (b >= 0 && b < a.rows) ? b : -1;
   }
   __syncthreads();
-  if (a.skip_publish) return;
-  // every copy of the record, write-through
-  const int words = 2 * a.K;
-  for (int x = tid; x < kRecordCopies * words; x += LSA_BLOCK) {
-    const int c = x / words, k = x - c * words;
-    coherent_store_i32(a.record + c * a.cstride + i * words + k, sh.rec[k]);
-  }
-  DECODE_MARK(6);
+  DECODE_MARK(4);
+  publish_picks(a, sh, i, t, position, ends);
 }
 
 // The reader's work once it holds its unit's picks (sh.pick: a pick's bucket, or its first
@@ -668,7 +758,8 @@ __global__ __launch_bounds__(LSA_BLOCK) void decode_flat_kernel(DecodeArgs a) {
   const uint32_t nsel = units * (uint32_t)a.S;
   DECODE_TRACE_BEGIN();
   if (id < nsel) {
-    select_role<T, CT, D, GQ>(a, smem, id % units, (int)(id / units));
+    if (a.tree) tree_role<T, CT, D, GQ>(a, smem, id);  // one select workgroup a unit
+    else select_role<T, CT, D, GQ>(a, smem, id % units, (int)(id / units));
   } else {
     const uint32_t rid = id - nsel;  // readers: unit fastest, then role (low roles have work)
     reader_role<T, D, GQ>(a, smem, rid % units, (int)(rid / units));

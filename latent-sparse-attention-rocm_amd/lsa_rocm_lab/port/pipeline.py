@@ -528,6 +528,89 @@ def flat_decode(
     return out, lists, lengths
 
 
+def tree_decode(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    positions: torch.Tensor,
+    buckets: Buckets,
+    hierarchy: Hierarchy,
+    config: PortConfig,
+    scale: float | None = None,
+    top_k: int | None = None,
+    score_dtype: str = "bf16",
+    readers: int | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """One decode step over a one-level node tree - index queries, tree select, sparse
+    read - in one HIP launch (the reference's decode step, port/bench.py:147-153, with
+    ``tree_select``, pipeline.py:319-337, in place of ``flat_select``). Shapes as
+    ``flat_decode``; the lists and lengths are byte-identical to
+    ``tree_select(index_queries(q, Hkv)[:, 0], positions, buckets, hierarchy, config,
+    score_dtype=score_dtype)``'s. Deeper hierarchies take ``tree_select`` + ``lsa_read``."""
+    from lsa_rocm_lab.port.read_kernel_tiled import _kv_layout
+
+    if len(hierarchy.levels) != 1:
+        raise NotImplementedError(f"tree_decode walks one node level, got {len(hierarchy.levels)}")
+    if config.start_nodes is not None:
+        raise NotImplementedError("tree_decode covers start_nodes=None (the top level down)")
+    level = hierarchy.levels[0]
+    device = _on_device("tree_decode", q, k, v, buckets.centroids, buckets.members, level.centroids)
+    if q.dim() != 4 or q.shape[1] != 1:
+        raise ValueError(f"tree_decode takes one query token per batch row: q [B, 1, Hq, D], got {tuple(q.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"q/k/v dtypes differ: {q.dtype} {k.dtype} {v.dtype}")
+    B, _, Hq, D = q.shape
+    Tk, Hkv = k.shape[1], k.shape[2]
+    if k.dim() != 4 or k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
+        raise ValueError(f"k/v must be [B={B}, Tk, Hkv, D={D}], got {tuple(k.shape)} / {tuple(v.shape)}")
+    if Hq % Hkv:
+        raise ValueError(f"{Hq} query heads do not group onto {Hkv} kv-heads")
+    q = q.contiguous()
+    k, v, sb, st, sh = _kv_layout(k, v)
+    layout = _Layout(torch.empty((B, Hkv, D), device="meta"), buckets.centroids)
+    node_layout = _Layout(torch.empty((B, Hkv, D), device="meta"), level.centroids)
+    if (node_layout.row_tables, node_layout.group_tables) != (layout.row_tables, layout.group_tables):
+        raise ValueError("node and bucket tables must share the same leading axes")
+    table, mode = _score_table(buckets, score_dtype)
+    if mode == _abi.SCORE_BF16:
+        ncent = level.centroids_bf16 if level.centroids_bf16 is not None else level.centroids.to(torch.bfloat16)
+    else:
+        ncent = level.centroids.float()
+    ncent = ncent.contiguous()
+    children = level.children.to(device=device, dtype=torch.int32).contiguous()
+    members = buckets.members.to(device=device, dtype=torch.int32).contiguous()
+    ends = _ends(buckets)
+    flags = _abi.TABLE_SPANS if (buckets.spans and ends is not None) else 0
+    pos = _positions32(positions, device)
+    if pos.numel() != B:
+        raise ValueError(f"a position a batch row: {B} rows, {pos.numel()} positions")
+    top_k = config.top_k if top_k is None else top_k
+    scale = D ** -0.5 if scale is None else scale
+    rows, cap = layout.rows, members.shape[-1]
+    width = top_k + config.window_size + config.sink_size
+    lists = torch.empty(B, Hkv, width, dtype=torch.int32, device=device)
+    lengths = torch.empty(B, Hkv, dtype=torch.int32, device=device)
+    out = torch.empty_like(q)
+    dt = _abi.dtype_code(q.dtype)
+    readers = int(os.environ.get("LSA_DECODE_READERS", "0")) if readers is None else readers
+    n_counters = _abi.size("lsa_decode_flat_counters", B, Hkv, rows, config.top_p)
+    nbytes = _abi.size("lsa_decode_flat_scratch_bytes", dt, B, Hq, Hkv, D, rows, config.top_p,
+                       config.window_size, config.sink_size, 1, readers)
+    status = _abi.StatusWord.get(device)
+    if int(status[0]) != 0:
+        _decode_gave_up(device, status)
+    ws = _abi.Workspace.get(device, "decode", nbytes)
+    counters = _abi.Counters.get(device, max(n_counters, 1))
+    _abi.call("lsa_decode_tree", q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, Tk, Hq, Hkv, D, sb, st, sh,
+              ncent.data_ptr(), children.data_ptr(), children.shape[-2], children.shape[-1],
+              config.node_cluster_block_size, config.beam_width, table.data_ptr(), members.data_ptr(),
+              _abi.ptr(ends), flags, rows, cap, layout.row_tables, layout.group_tables, mode, pos.data_ptr(),
+              config.cluster_block_size, config.block_bucket_count, config.top_p, config.window_size,
+              config.sink_size, top_k, float(scale), readers, counters.data_ptr(), counters.numel(), _abi.ptr(ws),
+              nbytes, lists.data_ptr(), lengths.data_ptr(), out.data_ptr(), _abi.ptr(status), _abi.stream(device))
+    return out, lists, lengths
+
+
 def _decode_gave_up(device: torch.device, status: torch.Tensor) -> None:
     """A fused decode launch gave up waiting: its outputs were invalid and a late record
     may sit in the counters. Zero them (outside graph capture) and raise."""

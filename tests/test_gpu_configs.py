@@ -231,6 +231,34 @@ def test_tree_decode_ragged_positions_follow_growth():
                 assert (picks[picks >= 0] < visible).all()
 
 
+@pytest.mark.parametrize("spans", [True, False])
+def test_fused_tree_decode_equals_select_then_read(spans):
+    """The one-launch tree decode (lsa_decode_tree): lists and lengths byte-identical to
+    tree_select on the group-mean index queries, at ragged positions (growth covers only
+    whole node blocks; the rest are fresh), with span tables or member rows, in both
+    scoring types; the output within the bf16 bar of the fp64 read over those lists."""
+    import dataclasses
+
+    B, T, Hq, Hkv, D = 3, 16384, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=256, seed=6, B=B, device=DEV)
+    buckets = dataclasses.replace(workloads.cluster_buckets(data, target=T // 64), spans=spans)
+    tree = workloads.node_tree(buckets, node_size=16)
+    config = pipeline.PortConfig(**{**workloads.TREE_131K.__dict__, "beam_width": 4, "top_p": 16,
+                                    "window_size": 128, "sink_size": 4})
+    pos = torch.tensor([T - 1, 9000, 2500], device=DEV, dtype=torch.int32)
+    q = data.q[:, -1:].contiguous()
+    idx = pipeline.index_queries(q, Hkv)[:, 0]
+    for score_dtype in ("bf16", "fp32"):
+        out, lists, lengths = pipeline.tree_decode(q, data.k, data.v, pos, buckets, tree, config,
+                                                   score_dtype=score_dtype)
+        want_l, want_n = pipeline.tree_select(idx, pos, buckets, tree, config, score_dtype=score_dtype)
+        assert torch.equal(lists, want_l) and torch.equal(lengths, want_n), score_dtype
+        want = oracle.sparse_read(_np(q.float()), _np(data.k.float()), _np(data.v.float()), _np(lists)[:, None],
+                                  _np(lengths)[:, None], D ** -0.5)
+        err = np.abs(_np(out.float()) - want)
+        assert err.max() <= 2e-2 and err.mean() <= 2e-3, (score_dtype, err.max(), err.mean())
+
+
 def test_tree_decode_configured_geometry():
     """The batched tree decode at its configured size: B=32 sequences x 131072 tokens,
     Hq 32 / Hkv 8, D 128 bf16, 2048 buckets = 128 nodes x 16 per (sequence, kv-head), top-8
