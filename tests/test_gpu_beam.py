@@ -109,7 +109,7 @@ def test_build_hierarchy_matches_the_oracle_builder():
 def test_beam_per_kv_head_four_levels_narrow_beam():
     """One table per kv-head (keys [1, T, Hkv, D]), 1024 buckets of 16 keys, node size 2
     in blocks of 8 (levels of 512, 256, 128, 64 nodes), beam 4, top_p 24, bf16 and fp32:
-    the beam prunes at every level and the matrix-core screen serves the node levels."""
+    the beam prunes at every level."""
     T, Hkv, D = 16384, 2, 64
     config = PortConfig(cluster_block_size=256, bucket_size=16, bucket_cap=16, top_p=24, top_k=300,
                         window_size=64, sink_size=4, node_bucket_size=2, node_cluster_block_size=8, top_level=4,
@@ -170,3 +170,28 @@ def test_beam_ragged_span_tables(spans):
     for score_dtype in ("bf16", "fp32"):
         lists, lengths = pipeline.tree_select(idx, positions, buckets, tree, config, score_dtype=score_dtype)
         _check(lists, lengths, idx, positions, buckets, tree, config, score_dtype, Hkv)
+
+
+def test_beam_edges_no_growth_top_level_one_and_bf16_queries():
+    """Rows that see no bucket or fewer than one node block (no node is made: the fresh
+    buckets alone, or nothing and the tail only); top_level 1 over a 3-level hierarchy
+    walks only level 1 and equals the one-level tree kernel; bf16 index queries."""
+    T, D = 16384, 64
+    config = PortConfig(cluster_block_size=128, bucket_size=8, bucket_cap=8, top_p=32, top_k=2000,
+                        window_size=32, sink_size=4, node_bucket_size=2, node_cluster_block_size=16, top_level=3,
+                        beam_width=3)
+    gen = torch.Generator().manual_seed(46)
+    keys = torch.randn(T, D, generator=gen).to(DEV)
+    buckets = pipeline.position_buckets(keys, config)
+    tree = pipeline.build_hierarchy_gpu(keys, buckets, config)
+    assert len(tree.levels) == 3
+    positions = torch.tensor([0, 5, 127, 128, 200, 2047, 2048, 16383], dtype=torch.int32, device=DEV)
+    idx = torch.randn(positions.shape[0], D, generator=gen).to(DEV)
+    for q in (idx, idx.to(torch.bfloat16)):
+        lists, lengths = pipeline.tree_select(q, positions, buckets, tree, config, score_dtype="bf16")
+        _check(lists, lengths, q.float(), positions, buckets, tree, config, "bf16", None)
+    one = dataclasses.replace(config, top_level=1)
+    a = pipeline.tree_select(idx, positions, buckets, tree, one)
+    b = pipeline.tree_select(idx, positions, buckets, dataclasses.replace(tree, levels=tree.levels[:1]), one)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    _check(a[0], a[1], idx, positions, buckets, tree, one, "fp32", None)

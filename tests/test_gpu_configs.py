@@ -235,7 +235,8 @@ def test_tree_decode_ragged_positions_follow_growth():
 def test_fused_tree_decode_equals_select_then_read(spans):
     """The one-launch tree decode (lsa_decode_tree): lists and lengths byte-identical to
     tree_select on the group-mean index queries, at ragged positions (growth covers only
-    whole node blocks; the rest are fresh), with span tables or member rows, in both
+    whole node blocks, the rest are fresh; a row early enough to see no bucket reads its
+    window and sinks alone), with span tables or member rows, in both
     scoring types; the output within the bf16 bar of the fp64 read over those lists."""
     import dataclasses
 
@@ -245,7 +246,7 @@ def test_fused_tree_decode_equals_select_then_read(spans):
     tree = workloads.node_tree(buckets, node_size=16)
     config = pipeline.PortConfig(**{**workloads.TREE_131K.__dict__, "beam_width": 4, "top_p": 16,
                                     "window_size": 128, "sink_size": 4})
-    pos = torch.tensor([T - 1, 9000, 2500], device=DEV, dtype=torch.int32)
+    pos = torch.tensor([T - 1, 2500, 40], device=DEV, dtype=torch.int32)  # the last row sees no bucket
     q = data.q[:, -1:].contiguous()
     idx = pipeline.index_queries(q, Hkv)[:, 0]
     for score_dtype in ("bf16", "fp32"):
