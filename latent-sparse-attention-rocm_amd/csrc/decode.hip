@@ -302,6 +302,7 @@ int decode_launch(const char* who, const void* q, const void* k, const void* v, 
   a.node_block = tree ? tree->node_block : 0;
   a.beam = tree ? tree->beam_width : 0;
   a.nodes_pow2 = nodes_pow2; a.beam_pow2 = beam_pow2; a.cand_pow2 = cand_pow2; a.top_pow2 = top_pow2;
+  a.ends4 = (ends && rows % 4 == 0 && ((uintptr_t)ends % 16) == 0) ? 1 : 0;
   if (tree) a.screen = 0;
   a.scale_log2 = scale * kLog2e;
   a.spin_limit = decode_debug().spin_limit > 0 ? decode_debug().spin_limit

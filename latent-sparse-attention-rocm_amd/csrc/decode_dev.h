@@ -52,6 +52,7 @@ struct DecodeArgs {
   const void* node_centroids;   // [tables, n_nodes, D], the centroid type
   const int32_t* children;      // [tables, n_nodes, node_size] bucket rows
   int n_nodes, node_size, node_block, beam;
+  int ends4;                    // span ends readable as 16-byte vectors (rows % 4 == 0, aligned)
   int nodes_pow2, beam_pow2, cand_pow2, top_pow2;
   float scale_log2;
   int spin_limit;
@@ -351,62 +352,177 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
 // LDS bitmap over bucket ids), a tie to the lower bucket; exact canonical scores at both
 // levels. The picks then go out as the flat select's do (publish_picks). The same
 // selection as select_tree_kernel.
+//
+// Laid out for few memory round trips: the query rows, the first tree_node_rows() node
+// rows of each 16-lane group and the span ends (16-byte loads, kTreeEndVecs a thread) are
+// all in flight before any of them is used; the fresh buckets' rows (when at most
+// kTreeFreshRows a group) are loaded while the beam is chosen. What remains on the chain:
+// nodes -> beam -> children -> their rows -> picks.
+constexpr int kTreeEndVecs = 2;       // 4-end vectors a thread counts from the first round trip
+constexpr int kTreeFreshRows = 4;     // fresh bucket rows a 16-lane group loads ahead of the beam
+
+template <typename CT>
+constexpr int tree_node_rows() {  // node rows a 16-lane group loads in the first round trip
+  return sizeof(CT) == 2 ? 8 : 4;
+}
+
 template <typename T, typename CT, int D, int GQ>
 __device__ __forceinline__ void tree_role(const DecodeArgs& a, char* smem, int64_t i) {
   constexpr int SPAN = D / 16;
+  constexpr int GROUPS = LSA_BLOCK / 16;
+  constexpr int NB = tree_node_rows<CT>();
   constexpr bool BF16_MODE = __is_same(CT, bf16_t);
   SelLds& sh = *(SelLds*)smem;
   uint64_t* keys = (uint64_t*)(smem + sel_keys_offset());                 // [max(nodes_pow2, cand_pow2)]
   uint64_t* best = keys + max(a.nodes_pow2, a.cand_pow2);                 // [max(beam_pow2, top_pow2)]
   int32_t* cand = (int32_t*)(best + max(a.beam_pow2, a.top_pow2));        // [cand_pow2]
   uint32_t* seen = (uint32_t*)(cand + a.cand_pow2);                       // [(rows + 31) / 32]
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
+  const int grp = tid >> 4, p = tid & 15;
   const int64_t r = (uint32_t)i / (uint32_t)a.G;
   const int g = (int)((uint32_t)i % (uint32_t)a.G);
   const int64_t position = a.positions[r];
+  const int64_t lim = position + 1;
   const int64_t t = r * a.row_tables + g * a.group_tables;
   const int32_t* ends = a.ends ? a.ends + t * a.rows : nullptr;
-  DECODE_MARK(0);
-  float qs[SPAN];
+  const int n_nodes = a.n_nodes, ns = a.node_size, words = n_nodes * ns;
+  const CT* ncent = (const CT*)a.node_centroids + t * (int64_t)n_nodes * D;
+  const CT* bcent = (const CT*)a.centroids + t * (int64_t)a.rows * D;
+  const int32_t* kids = a.children + t * (int64_t)words;
   const T* qrow = (const T*)a.q + (r * a.Hq + (int64_t)g * GQ) * D;
-  group_mean_slice<T, SPAN, GQ>(qrow, tid & 15, BF16_MODE, qs);
-  __shared__ int vis_lds[2 * LSA_WAVES];
-  const int visible = max(0, ends ? visible_count_block(position, a.rows, ends, vis_lds)
-                                  : visible_count(position, a.rows, a.cluster_block, a.block_buckets, nullptr));
-  const int covered = min(visible / a.node_block * a.node_block, a.n_nodes * a.node_size);
-  const int made = covered / a.node_size;
+  DECODE_MARK(0);
 
-  // the node level: the made nodes, the best `beam`
-  const CT* ncent = (const CT*)a.node_centroids + t * (int64_t)a.n_nodes * D;
-  const int beam = min(a.beam, a.n_nodes);
-  score_slice_keys<CT, SPAN>(qs, ncent, D, 0, a.n_nodes, made, keys);
-  __syncthreads();
-  block_topk_sorted(keys, a.n_nodes, beam, a.beam_pow2, best, &sh.tks, &sh.st);
-  DECODE_MARK(1);
+  // round trip 1: query rows, node rows, span ends, children - all issued before any use
+  SpanRaw<T, SPAN> qraw[GQ];
+#pragma unroll
+  for (int h = 0; h < GQ; ++h) qraw[h].load(qrow + (int64_t)h * D + p * SPAN);
+  SpanRaw<CT, SPAN> nraw[NB];
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    const int j = k * GROUPS + grp;
+    nraw[k].load(ncent + (int64_t)(j < n_nodes ? j : 0) * D + p * SPAN);
+  }
+  // span ends as 16-byte vectors when the table's rows allow (ends4), else one at a time
+  const bool ends4 = ends && a.ends4;
+  const int nvec = ends4 ? a.rows / 4 : 0;
+  int4 ev[kTreeEndVecs];
+#pragma unroll
+  for (int m = 0; m < kTreeEndVecs; ++m) {
+    const int x = tid + m * LSA_BLOCK;
+    ev[m] = x < nvec ? ((const int4*)ends)[x] : make_int4(0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF);
+  }
 
-  // the buckets: the kept nodes' visible children, then the fresh buckets, each once
-  const int n_fresh = max(0, visible - covered);
-  const int n_kids = beam * a.node_size;
-  const int n_cand = n_kids + n_fresh;
-  const int32_t* kids = a.children + t * (int64_t)a.n_nodes * a.node_size;
+  // the index query (group mean, rounded like the unfused select's), the node scores
+  float qs[SPAN];
+#pragma unroll
+  for (int j = 0; j < SPAN; ++j) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) acc += qraw[h].at(j);
+    const float x = acc / (float)GQ;
+    qs[j] = BF16_MODE ? bf16_round(x) : x;
+  }
+  float nsc[NB];
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    double acc = 0.0;
+#pragma unroll
+    for (int e = 0; e < SPAN; ++e) acc = fma((double)qs[e], (double)nraw[k].at(e), acc);
+    nsc[k] = score_tree16(acc);
+  }
+  // visible buckets: span ends <= position + 1 (nondecreasing, so a count), or closed form
+  int nv = 0;
+  if (ends4) {
+#pragma unroll
+    for (int m = 0; m < kTreeEndVecs; ++m) {
+      nv += ((int64_t)ev[m].x <= lim ? 1 : 0) + ((int64_t)ev[m].y <= lim ? 1 : 0);
+      nv += ((int64_t)ev[m].z <= lim ? 1 : 0) + ((int64_t)ev[m].w <= lim ? 1 : 0);
+    }
+    for (int x = tid + kTreeEndVecs * LSA_BLOCK; x < nvec; x += LSA_BLOCK) {
+      const int4 e = ((const int4*)ends)[x];
+      nv += ((int64_t)e.x <= lim ? 1 : 0) + ((int64_t)e.y <= lim ? 1 : 0);
+      nv += ((int64_t)e.z <= lim ? 1 : 0) + ((int64_t)e.w <= lim ? 1 : 0);
+    }
+  } else if (ends) {
+    for (int x = tid; x < a.rows; x += LSA_BLOCK) nv += (int64_t)ends[x] <= lim ? 1 : 0;
+  }
+#pragma unroll
+  for (int x = LSA_WAVE / 2; x >= 1; x >>= 1) nv += __shfl_xor(nv, x, LSA_WAVE);
+  __shared__ int vis_lds[LSA_WAVES];
+  if (lane == 0) vis_lds[w] = nv;
   for (int x = tid; x < (a.rows + 31) / 32; x += LSA_BLOCK) seen[x] = 0;
   __syncthreads();
-  for (int j = tid; j < a.cand_pow2; j += LSA_BLOCK) {
+  const int visible =
+      max(0, ends ? vis_lds[0] + vis_lds[1] + vis_lds[2] + vis_lds[3]
+                  : visible_count(position, a.rows, a.cluster_block, a.block_buckets, nullptr));
+  const int covered = min(visible / a.node_block * a.node_block, n_nodes * ns);
+  const int made = covered / ns;
+  const int n_fresh = max(0, visible - covered);
+
+  // the node keys (made nodes only); nodes past the first batch take another round trip
+  if (p == 0) {
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int j = k * GROUPS + grp;
+      if (j < n_nodes) keys[j] = j < made ? key_to_u(pack_key(nsc[k], j)) : 0;
+    }
+  }
+  if (n_nodes > NB * GROUPS) score_slice_keys<CT, SPAN>(qs, ncent, D, NB * GROUPS, n_nodes, made, keys + NB * GROUPS);
+  // the fresh buckets' rows, in flight while the beam is chosen
+  const bool fresh_ahead = n_fresh <= kTreeFreshRows * GROUPS;
+  SpanRaw<CT, SPAN> fraw[kTreeFreshRows];
+  if (fresh_ahead) {
+#pragma unroll
+    for (int k = 0; k < kTreeFreshRows; ++k) {
+      const int j = k * GROUPS + grp;
+      fraw[k].load(bcent + (int64_t)(j < n_fresh ? covered + j : 0) * D + p * SPAN);
+    }
+  }
+  __syncthreads();
+  const int beam = min(a.beam, n_nodes);
+  block_topk_sorted(keys, n_nodes, beam, a.beam_pow2, best, &sh.tks, &sh.st);
+  DECODE_MARK(1);
+
+  // candidates: the fresh buckets [covered, visible) (distinct; marked in the bitmap first),
+  // then the kept nodes' visible children that are not already candidates
+  const int n_kids = beam * ns;
+  const int n_cand = n_fresh + n_kids;
+  for (int j = tid; j < n_fresh; j += LSA_BLOCK) {
+    const int c = covered + j;
+    cand[j] = c;
+    atomicOr(&seen[c >> 5], 1u << (c & 31));
+  }
+  if (fresh_ahead) {
+#pragma unroll
+    for (int k = 0; k < kTreeFreshRows; ++k) {
+      const int j = k * GROUPS + grp;
+      double acc = 0.0;
+#pragma unroll
+      for (int e = 0; e < SPAN; ++e) acc = fma((double)qs[e], (double)fraw[k].at(e), acc);
+      const float sc = score_tree16(acc);
+      if (p == 0 && j < n_fresh) keys[j] = key_to_u(pack_key(sc, covered + j));
+    }
+  }
+  __syncthreads();  // the fresh buckets' bits
+  for (int m = tid; m < n_kids; m += LSA_BLOCK) {
+    const int node = key_column(u_to_key(best[m / ns]));
     int32_t c = -1;
-    if (j < n_kids) {
-      const int node = key_column(u_to_key(best[j / a.node_size]));
-      if (node >= 0) c = kids[(int64_t)node * a.node_size + j % a.node_size];
-    } else if (j < n_cand) {
-      c = covered + (j - n_kids);
+    if (node >= 0 && node < n_nodes) {
+      const int x = node * ns + m % ns;
+      c = kids[x];
     }
     c = (c >= 0 && c < visible) ? c : -1;
     const uint32_t bit = 1u << (c & 31);
-    cand[j] = (c >= 0 && !(atomicOr(&seen[c >> 5], bit) & bit)) ? c : -1;
+    cand[n_fresh + m] = (c >= 0 && !(atomicOr(&seen[c >> 5], bit) & bit)) ? c : -1;
   }
   __syncthreads();
-  const CT* bcent = (const CT*)a.centroids + t * (int64_t)a.rows * D;
   const int k = min(a.K, a.cand_pow2);
-  score_keys<CT, SPAN>(qs, bcent, D, a.cand_pow2, [&](int j) { return cand[j]; }, keys);
+  if (fresh_ahead) {
+    score_keys<CT, SPAN>(qs, bcent, D, n_kids, [&](int m) { return cand[n_fresh + m]; }, keys + n_fresh);
+  } else {
+    score_keys<CT, SPAN>(qs, bcent, D, n_cand, [&](int j) { return cand[j]; }, keys);
+  }
+  for (int j = n_cand + tid; j < a.cand_pow2; j += LSA_BLOCK) keys[j] = 0;
   __syncthreads();
   block_topk_sorted(keys, a.cand_pow2, k, a.top_pow2, best, &sh.tks, &sh.st);
   for (int j = tid; j < a.K; j += LSA_BLOCK) {
