@@ -191,12 +191,7 @@ __device__ __forceinline__ void publish_picks(const DecodeArgs& a, SelLds& sh, i
   DECODE_MARK(5);
   if (w == 0) {
     const int c = lane < a.K ? sh.cnt[lane] : 0;
-    int incl = c;
-#pragma unroll
-    for (int d = 1; d < LSA_WAVE; d <<= 1) {
-      const int y = __shfl_up(incl, d, LSA_WAVE);
-      if (lane >= d) incl += y;
-    }
+    const int incl = wave_inclusive_sum(c);
     const int end = incl < a.top_k ? incl : a.top_k;
     if (lane < a.K) {
       sh.rec[lane] = (a.spans ? sh.first[lane] : sh.pick[lane]) + 2;  // pick, or its first kept id

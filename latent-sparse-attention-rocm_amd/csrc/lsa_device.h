@@ -105,13 +105,65 @@ __device__ __forceinline__ float lane_xor(float v, int x) {
   return __shfl_xor(v, x, LSA_WAVE);
 }
 
+// Cross-lane moves by DPP (the data-parallel primitives of the VALU, no LDS round trip):
+// the lane's value from the lane named by `ctrl`, or `ident` where the control names no
+// source lane or the lane's row is outside `row_mask`.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_or(int ident, int x) {
+  return __builtin_amdgcn_update_dpp(ident, x, CTRL, ROW_MASK, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1;      // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;      // quad_perm [2, 3, 0, 1]
+constexpr int kDppRowShr1 = 0x111;  // row_shr:n = 0x110 + n
+constexpr int kDppRowShr2 = 0x112;
+constexpr int kDppRowShr4 = 0x114;
+constexpr int kDppRowShr8 = 0x118;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+constexpr int kDppBcast15 = 0x142;  // lane 15 of each row to the next row
+constexpr int kDppBcast31 = 0x143;  // lane 31 to rows 2 and 3
+
+// Wave-wide reduction of an associative, commutative op with identity `ident` (int bits):
+// pairs, quads, 8-lane halves and rows by DPP, then rows 1 and 3 take their lower
+// neighbour's total and rows 2 and 3 take lane 31's; lane 63 ends with the whole wave's,
+// which every lane reads.
+template <typename Op>
+__device__ __forceinline__ int wave_reduce_bits(int x, int ident, Op op) {
+  x = op(x, dpp_or<kDppXor1>(ident, x));
+  x = op(x, dpp_or<kDppXor2>(ident, x));
+  x = op(x, dpp_or<kDppHalfMirror>(ident, x));
+  x = op(x, dpp_or<kDppMirror>(ident, x));
+  x = op(x, dpp_or<kDppBcast15, 0xA>(ident, x));
+  x = op(x, dpp_or<kDppBcast31, 0xC>(ident, x));
+  return __builtin_amdgcn_readlane(x, LSA_WAVE - 1);
+}
+__device__ __forceinline__ int wave_sum(int x) {
+  return wave_reduce_bits(x, 0, [](int a, int b) { return a + b; });
+}
+__device__ __forceinline__ int wave_or(int x) {
+  return wave_reduce_bits(x, 0, [](int a, int b) { return a | b; });
+}
+__device__ __forceinline__ float wave_max(float x) {
+  return __int_as_float(wave_reduce_bits(__float_as_int(x), __float_as_int(-INFINITY), [](int a, int b) {
+    return __float_as_int(fmaxf(__int_as_float(a), __int_as_float(b)));
+  }));
+}
+__device__ __forceinline__ float wave_min(float x) {
+  return __int_as_float(wave_reduce_bits(__float_as_int(x), __float_as_int(INFINITY), [](int a, int b) {
+    return __float_as_int(fminf(__int_as_float(a), __int_as_float(b)));
+  }));
+}
+
+// Inclusive prefix sum over the wave's lanes: Hillis-Steele within each 16-lane row by DPP
+// row shifts (a lane with no source adds 0), then rows 1 and 3 add their lower neighbour's
+// total and rows 2 and 3 add lane 31's.
 __device__ __forceinline__ int wave_inclusive_sum(int x) {
-  const int lane = threadIdx.x & (LSA_WAVE - 1);
-#pragma unroll
-  for (int d = 1; d < LSA_WAVE; d <<= 1) {
-    int y = __shfl_up(x, d, LSA_WAVE);
-    if (lane >= d) x += y;
-  }
+  x += dpp_or<kDppRowShr1>(0, x);
+  x += dpp_or<kDppRowShr2>(0, x);
+  x += dpp_or<kDppRowShr4>(0, x);
+  x += dpp_or<kDppRowShr8>(0, x);
+  x += dpp_or<kDppBcast15, 0xA>(0, x);
+  x += dpp_or<kDppBcast31, 0xC>(0, x);
   return x;
 }
 

@@ -233,13 +233,10 @@ __device__ __forceinline__ bool block_topk_hist(const uint64_t* keys, int n, int
   }
   sc->hist[tid] = 0;  // LSA_BLOCK == 256 bins
   sc->fill[tid] = 0;
-#pragma unroll
-  for (int x = LSA_WAVE / 2; x >= 1; x >>= 1) {
-    mn = fminf(mn, __shfl_xor(mn, x, LSA_WAVE));
-    mx = fmaxf(mx, __shfl_xor(mx, x, LSA_WAVE));
-    cnt += __shfl_xor(cnt, x, LSA_WAVE);
-    bad |= __shfl_xor(bad, x, LSA_WAVE);
-  }
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  cnt = wave_sum(cnt);
+  bad = wave_or(bad);
   if (lane == 0) { sc->wmin[w] = mn; sc->wmax[w] = mx; sc->wcnt[w] = cnt; sc->wbad[w] = bad; }
   __syncthreads();
   mn = fminf(fminf(sc->wmin[0], sc->wmin[1]), fminf(sc->wmin[2], sc->wmin[3]));
@@ -275,8 +272,8 @@ __device__ __forceinline__ bool block_topk_hist(const uint64_t* keys, int n, int
     const int total = o1 >= kc ? o1 : (o2 >= kc ? o2 : (o3 >= kc ? o3 : inc));
     const uint64_t m = __ballot(here);
     const int src = m ? __ffsll((long long)m) - 1 : 0;
-    const int cut = __shfl(d, src, LSA_WAVE);
-    const int tot = __shfl(total, src, LSA_WAVE);
+    const int cut = __builtin_amdgcn_readlane(d, src);  // src is the same in every lane
+    const int tot = __builtin_amdgcn_readlane(total, src);
     if (lane == 0) { sc->cut = m ? cut : 256; sc->ok = (m == 0 || tot <= LSA_WAVE) ? 1 : 0; }
   }
   __syncthreads();
