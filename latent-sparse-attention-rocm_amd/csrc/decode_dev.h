@@ -441,8 +441,7 @@ __device__ __forceinline__ void tree_role(const DecodeArgs& a, char* smem, int64
   } else if (ends) {
     for (int x = tid; x < a.rows; x += LSA_BLOCK) nv += (int64_t)ends[x] <= lim ? 1 : 0;
   }
-#pragma unroll
-  for (int x = LSA_WAVE / 2; x >= 1; x >>= 1) nv += __shfl_xor(nv, x, LSA_WAVE);
+  nv = wave_sum(nv);
   __shared__ int vis_lds[LSA_WAVES];
   if (lane == 0) vis_lds[w] = nv;
   for (int x = tid; x < (a.rows + 31) / 32; x += LSA_BLOCK) seen[x] = 0;
@@ -719,7 +718,7 @@ __device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int
       __builtin_amdgcn_s_sleep(2);
     }
     const int end = wb - 1;
-    int prev = __shfl_up(end, 1, LSA_WAVE);
+    int prev = dpp_or<kDppWaveShr1>(0, end);  // lane - 1's
     if (lane == 0) prev = 0;
     const int n = lane < K ? end - prev : 0;
     if (lane < K) {
@@ -727,7 +726,7 @@ __device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int
       sh.start[lane] = prev;
       sh.n[lane] = n;
     }
-    const int filled = __shfl(end, K - 1, LSA_WAVE);
+    const int filled = __builtin_amdgcn_readlane(end, K - 1);
     if (lane == 0) {
       sh.filled = filled;
       sh.bad = bad;
@@ -827,7 +826,7 @@ __device__ __forceinline__ void rep_role(const DecodeArgs& a, char* smem, int64_
     }
     const int incl = wave_inclusive_sum(cntk);
     const int end = incl < a.top_k ? incl : a.top_k;
-    int prev = __shfl_up(end, 1, LSA_WAVE);
+    int prev = dpp_or<kDppWaveShr1>(0, end);  // lane - 1's
     if (lane == 0) prev = 0;
     const int n = lane < K ? end - prev : 0;
     if (lane < K) {
@@ -835,7 +834,7 @@ __device__ __forceinline__ void rep_role(const DecodeArgs& a, char* smem, int64_
       sh.start[lane] = prev;
       sh.n[lane] = n;
     }
-    const int filled = __shfl(end, K - 1, LSA_WAVE);  // every lane takes part in the shuffle
+    const int filled = __builtin_amdgcn_readlane(end, K - 1);
     if (lane == 0) {
       sh.filled = filled;
       if (role == 0) {

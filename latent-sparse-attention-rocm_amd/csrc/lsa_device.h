@@ -122,6 +122,7 @@ constexpr int kDppHalfMirror = 0x141;
 constexpr int kDppMirror = 0x140;
 constexpr int kDppBcast15 = 0x142;  // lane 15 of each row to the next row
 constexpr int kDppBcast31 = 0x143;  // lane 31 to rows 2 and 3
+constexpr int kDppWaveShr1 = 0x138; // the whole wave shifted up one lane (lane 0 has no source)
 
 // Wave-wide reduction of an associative, commutative op with identity `ident` (int bits):
 // pairs, quads, 8-lane halves and rows by DPP, then rows 1 and 3 take their lower
@@ -142,6 +143,11 @@ __device__ __forceinline__ int wave_sum(int x) {
 }
 __device__ __forceinline__ int wave_or(int x) {
   return wave_reduce_bits(x, 0, [](int a, int b) { return a | b; });
+}
+__device__ __forceinline__ float wave_sum(float x) {  // a fixed order: the same bits every run
+  return __int_as_float(wave_reduce_bits(__float_as_int(x), 0, [](int a, int b) {
+    return __float_as_int(__int_as_float(a) + __int_as_float(b));
+  }));
 }
 __device__ __forceinline__ float wave_max(float x) {
   return __int_as_float(wave_reduce_bits(__float_as_int(x), __float_as_int(-INFINITY), [](int a, int b) {
@@ -435,14 +441,35 @@ __device__ __forceinline__ void wave_topk_sorted(const uint64_t* keys, int n, in
 
 // ---------------------------------------------------------------- canonical score
 
+// The value of lane ^ X (X in {1, 2, 4, 8}: within a 16-lane row) by DPP: quad
+// permutations for 1 and 2; for 4 and 8, row shifts up and down on the 4-lane banks that
+// take their partner from above or below.
+template <int X>
+__device__ __forceinline__ int xor_dpp_bits(int x) {
+  if constexpr (X == 1) return __builtin_amdgcn_update_dpp(x, x, kDppXor1, 0xF, 0xF, false);
+  if constexpr (X == 2) return __builtin_amdgcn_update_dpp(x, x, kDppXor2, 0xF, 0xF, false);
+  if constexpr (X == 4) {
+    const int t = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xF, 0x5, false);  // row_shl:4, banks 0, 2
+    return __builtin_amdgcn_update_dpp(t, x, 0x114, 0xF, 0xA, false);         // row_shr:4, banks 1, 3
+  }
+  const int t = __builtin_amdgcn_update_dpp(x, x, 0x108, 0xF, 0x3, false);    // row_shl:8, banks 0, 1
+  return __builtin_amdgcn_update_dpp(t, x, 0x118, 0xF, 0xC, false);           // row_shr:8, banks 2, 3
+}
+template <int X>
+__device__ __forceinline__ double xor_dpp(double v) {
+  const uint64_t b = __double_as_longlong(v);
+  const int lo = xor_dpp_bits<X>((int)(uint32_t)b), hi = xor_dpp_bits<X>((int)(uint32_t)(b >> 32));
+  return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+
 // One canonical dot product shared by 16 lanes: lane p (0..15 within its group) has
 // already summed dims [p*span, (p+1)*span) in order into `partial` (fp64).
 // Returns the fp32 score in every lane of the 16-lane group.
 __device__ __forceinline__ float score_tree16(double partial) {
-  partial += __shfl_xor(partial, 8, 16);
-  partial += __shfl_xor(partial, 4, 16);
-  partial += __shfl_xor(partial, 2, 16);
-  partial += __shfl_xor(partial, 1, 16);
+  partial += xor_dpp<8>(partial);
+  partial += xor_dpp<4>(partial);
+  partial += xor_dpp<2>(partial);
+  partial += xor_dpp<1>(partial);
   return (float)partial;
 }
 

@@ -608,16 +608,14 @@ __device__ __forceinline__ void combine_partials(ReadLds<D, GQ, MAXS>& sh, const
   for (int h = w; h < GQ; h += LSA_WAVES) {
     float M = kNegBig;
     for (int sp = lane; sp < n_act; sp += LSA_WAVE) M = fmaxf(M, sh.w[sp][h]);
-#pragma unroll
-    for (int x = LSA_WAVE / 2; x >= 1; x >>= 1) M = fmaxf(M, __shfl_xor(M, x, LSA_WAVE));
+    M = wave_max(M);
     float L = 0.0f;
     for (int sp = lane; sp < n_act; sp += LSA_WAVE) {
       const float f = fast_exp2(sh.w[sp][h] - M);
       L += sh.pl[sp][h] * f;
       sh.w[sp][h] = f;
     }
-#pragma unroll
-    for (int x = LSA_WAVE / 2; x >= 1; x >>= 1) L += __shfl_xor(L, x, LSA_WAVE);
+    L = wave_sum(L);
     if (lane == 0) sh.ltot[h] = L;
   }
   __syncthreads();
