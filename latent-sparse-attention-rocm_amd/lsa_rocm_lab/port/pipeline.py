@@ -318,7 +318,11 @@ def _decode_splits(dtype, D: int, group: int, units: int, rows: int, top_p: int,
         raise ValueError("LSA_DECODE_MODE=rep: the replicated select does not apply to this shape")
     if ok and (mode == "rep" or (mode == "auto" and units <= _REP_MAX_UNITS)):
         return 0
-    return _select_splits(units, 1, rows, top_p)
+    if os.environ.get("LSA_SELECT_SPLITS") or units >= 256:
+        return _select_splits(units, 1, rows, top_p)
+    # the fused decode: ~64 columns a select workgroup (32k decode, 512 buckets: 19.8 us with
+    # 8 splits, 20.2 with 16, 21.4 with 4); its last split then collects half as many keys
+    return max(1, min(math.ceil(rows / 64), rows, 256, max(1, 2048 // max(units, 1))))
 
 
 # (row, kv-head) units up to which the fused decode selects in every reader
