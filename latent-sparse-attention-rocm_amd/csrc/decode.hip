@@ -16,6 +16,15 @@
 // written, so a reader that sees all 2K words nonzero holds the whole record: no flag and
 // no fence. It also writes the unit's list length.
 //
+// Rank form (span tables of at most kRankMaxRows buckets, more than one split, the
+// published keys fit the counters region): no split collects. Each split publishes its
+// columns' keys + 1 (nonzero once written) into the counters region and exits; every reader
+// of the unit waits until all of the unit's keys are nonzero, ranks them itself (the same
+// top-K on the same keys), takes each pick's kept range from the span ends it loaded while
+// waiting, and reads its share. Role 0 writes the list length; the last reader to arrive
+// zeroes the published keys. This drops the last split's arrival, its reload of the keys,
+// the record and its poll from the step's chain.
+//
 // Reader workgroup (unit i, pick j, part u) or (unit i, tail part t): waits for the record
 // with a bounded poll (past the limit it sets *status and exits), expands its share of the
 // list - the kept members of pick j at ranks [u*span, u*span + span), or a slice of the
@@ -69,6 +78,25 @@ size_t reader_lds_d(int D, int gq, int span) {
 }
 
 template <int D>
+size_t rank_lds_gq(int gq, int rows) {
+  switch (gq) {
+    case 1: return rank_lds<D, 1>(rows);
+    case 2: return rank_lds<D, 2>(rows);
+    case 4: return rank_lds<D, 4>(rows);
+    default: return rank_lds<D, 8>(rows);
+  }
+}
+
+size_t rank_lds_d(int D, int gq, int rows) {
+  switch (D) {
+    case 32: return rank_lds_gq<32>(gq, rows);
+    case 64: return rank_lds_gq<64>(gq, rows);
+    case 128: return rank_lds_gq<128>(gq, rows);
+    default: return rank_lds_gq<256>(gq, rows);
+  }
+}
+
+template <int D>
 size_t rep_lds_gq(int gq, int span) {
   switch (gq) {
     case 1: return rep_ids_offset<D, 1>() + sizeof(int32_t) * (size_t)kChunkTiles * span;
@@ -109,11 +137,13 @@ int64_t record_stride(int64_t units, int K) {
 
 // Readers per unit: with few units, about one tile of the list a reader (picks are buckets
 // of ~one tile, plus the tail's tiles), so the gather spreads over as many CUs as it can
-// use, but at most kDefaultMaxReaders: past ~16 a unit, the wider combine and the extra
-// workgroups' launch cost more than the shorter gathers save (32k decode, B=1: 22.5 us
-// with 32 readers, 21.2 us with 16 or 24); with many units, enough readers for ~1024
-// workgroups in all, each streaming a run of tiles through the pipelined gather.
-constexpr int kDefaultMaxReaders = 16;
+// use, but at most kDefaultMaxReaders: past ~24 a unit, the wider combine and the extra
+// workgroups' launch cost more than the shorter gathers save (32k decode, B=1, rank form
+// with 32 select splits: 18.4 us with 24 readers, 18.6 with 16, 19.1 with 32, 20.4 with
+// 40; the record form: 22.5 us with 32, 21.2 with 16 or 24); with many units, enough
+// readers for ~1024 workgroups in all, each streaming a run of tiles through the
+// pipelined gather.
+constexpr int kDefaultMaxReaders = 24;
 
 int default_readers(int64_t units, int K, int span, int window, int sink) {
   const int64_t tail = ((int64_t)window + sink + span - 1) / span;
@@ -160,11 +190,19 @@ extern "C" int lsa_decode_flat_rep_ok(int dtype, int32_t D, int32_t group, int32
   return rep_unfit(dtype, D, group, rows, top_p, score_mode, table_flags) == nullptr ? 1 : 0;
 }
 
+// Word offset of the rank form's published keys in the counters region (after the arrival
+// counters and the record copies, 256-byte aligned), and whether a table shape has them.
+int64_t rank_keys_at(int64_t units, int K) {
+  return ((2 * units + kRecordCopies * record_stride(units, K)) + 63) / 64 * 64;
+}
+bool rank_slots(int64_t units, int rows) { return rows <= kRankMaxRows && units * rows <= kRankMaxSlots; }
+
 extern "C" int64_t lsa_decode_flat_counters(int64_t R, int32_t Hkv, int32_t rows, int32_t top_p) {
   if (R <= 0 || Hkv <= 0 || rows <= 0 || top_p <= 0) return 0;
   const int K = top_p < rows ? top_p : rows;
   if (K > kMaxPicks) return 0;
   const int64_t units = R * Hkv;
+  if (rank_slots(units, rows)) return rank_keys_at(units, K) + 2 * units * rows;
   return 2 * units + kRecordCopies * record_stride(units, K);
 }
 
@@ -269,6 +307,11 @@ int decode_launch(const char* who, const void* q, const void* k, const void* v, 
     const size_t rd = reader_lds_d(D, gq, p.span);
     p.shmem = sel > rd ? sel : rd;
   }
+  // the rank form: more than one select split over a span table whose keys fit the readers
+  // and the counters region (which then holds the published keys)
+  const bool rank = !tree && !p.rep && select_splits > 1 && (table_flags & LSA_TABLE_SPANS) &&
+                    rank_slots(units, rows) && rank_lds_d(D, gq, rows) <= kMaxLds;
+  if (rank && rank_lds_d(D, gq, rows) > p.shmem) p.shmem = rank_lds_d(D, gq, rows);
   LSA_REQUIRE(p.shmem <= kMaxLds, LSA_ERR_SHAPE, "%s: %zu bytes of LDS exceed %zu", who, p.shmem, kMaxLds);
   const int64_t grid = units * (select_splits + p.NR);
   LSA_REQUIRE(grid <= 0x7FFFFFFF, LSA_ERR_SHAPE, "%s: too many workgroups", who);
@@ -308,6 +351,8 @@ int decode_launch(const char* who, const void* q, const void* k, const void* v, 
   a.spin_limit = decode_debug().spin_limit > 0 ? decode_debug().spin_limit
                                               : 1 << 22;  // polls of about a microsecond each: seconds
   a.skip_publish = decode_debug().skip_publish;
+  a.rank = rank ? 1 : 0;
+  a.pub = rank ? (uint64_t*)(counters + rank_keys_at(units, p.K)) : nullptr;
   a.sel_count = counters;
   a.rd_count = counters + units;
   a.record = counters + 2 * units;

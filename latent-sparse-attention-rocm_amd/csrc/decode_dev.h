@@ -17,6 +17,13 @@ constexpr int kMaxPicks = LSA_WAVE;  // the record of a unit is polled by one wa
 constexpr int kMaxReaders = 256;     // readers per unit (split partials of the combine)
 constexpr int kRecordCopies = 8;     // copies of every record, polled by different readers
 constexpr size_t kMaxLds = 64 * 1024;
+// Rank form (readers rank the select splits' published keys themselves): at most this many
+// bucket rows a table (a reader holds their keys and span ends in LDS, a polling lane
+// kRankKeysPerLane keys) and this many published key slots in all (they sit in the
+// counters region, which must start zero).
+constexpr int kRankMaxRows = 1024;
+constexpr int kRankKeysPerLane = kRankMaxRows / LSA_WAVE;
+constexpr int64_t kRankMaxSlots = 1 << 16;
 
 // Phase hooks: no-ops unless a build defines DECODE_MARK(k) (timestamps for profiling; k < 16:
 // 0-6 the exchange form's select and reader phases, 8-11 the replicated select's).
@@ -56,7 +63,9 @@ struct DecodeArgs {
   int nodes_pow2, beam_pow2, cand_pow2, top_pow2;
   float scale_log2;
   int spin_limit;
-  int skip_publish;    // test hook: select workgroups never publish the record (readers give up)
+  int skip_publish;    // test hook: select workgroups never publish (readers give up)
+  int rank;            // rank form: splits publish their keys, every reader ranks them itself
+  uint64_t* pub;       // rank form: [units][rows] published keys + 1 (0: not yet written)
   int* sel_count;      // [units] select arrivals
   int* rd_count;       // [units] reader arrivals
   int32_t* record;     // kRecordCopies copies, `cstride` words apart: [units][2K] words A then B
@@ -91,6 +100,26 @@ constexpr size_t sel_keys_offset() { return (sizeof(SelLds) + 15) & ~(size_t)15;
 template <int D, int GQ>
 constexpr size_t rd_ids_offset() {
   return (sizeof(RdLds<D, GQ>) + 15) & ~(size_t)15;
+}
+
+// A ranking reader's selection state, in the space of its id chunk (dead until the read):
+// the top-K scratch, then the table's span ends [rows], then the keys [rows].
+struct RankLds {
+  RadixState st;
+  TopkScratch tks;
+  uint64_t best[kMaxPicks];
+};
+template <int D, int GQ>
+constexpr size_t rank_ends_offset() {
+  return (rd_ids_offset<D, GQ>() + sizeof(RankLds) + 15) & ~(size_t)15;
+}
+template <int D, int GQ>
+__host__ __device__ constexpr size_t rank_keys_offset(int rows) {
+  return (rank_ends_offset<D, GQ>() + sizeof(int32_t) * (size_t)rows + 15) & ~(size_t)15;
+}
+template <int D, int GQ>
+__host__ __device__ constexpr size_t rank_lds(int rows) {
+  return rank_keys_offset<D, GQ>(rows) + sizeof(uint64_t) * (size_t)rows;
 }
 
 // The unit's index query slice of lane group p: fp32 mean of the group's GQ query rows
@@ -305,6 +334,14 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
   if (!picked) {
     DECODE_MARK(1);
 
+    if (a.rank) {  // publish the keys (+ 1, so that a written slot is nonzero); the readers rank them
+      __syncthreads();
+      if (a.skip_publish) return;
+      uint64_t* mine = a.pub + i * (int64_t)a.rows;
+      for (int j = tid; j < n_local; j += LSA_BLOCK) coherent_store_u64(mine + c0 + j, keys[c0 + j] + 1);
+      DECODE_MARK(6);
+      return;
+    }
     if (a.S > 1) {
       __syncthreads();
       uint64_t* mine = a.ws_keys + i * (int64_t)a.rows;
@@ -535,13 +572,13 @@ __device__ __forceinline__ void tree_role(const DecodeArgs& a, char* smem, int64
 // the last tile of a list is partial. The run is expanded into `ids` (and the list) in
 // chunks of up to kChunkTiles tiles and read with the software-pipelined tile loop; then
 // the reader writes its share of the list padding, publishes its split partial and
-// arrives. The last reader of the unit combines the partials (and, with clear_record,
-// zeroes the unit's record copies for the next launch).
+// arrives. The last reader of the unit combines the partials and leaves the unit's hand-off
+// words zero for the next launch (`clear`: 1 the record copies, 2 the published keys).
 constexpr int kChunkTiles = 8;
 
 template <typename T, int D, int GQ>
 __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh, int32_t* ids, int64_t i, int role,
-                                           const QueryRegs<T, D, GQ>& qr, int64_t position, bool clear_record) {
+                                           const QueryRegs<T, D, GQ>& qr, int64_t position, int clear) {
   using S = ReadShape<T, D, GQ>;
   constexpr int VEC = S::VEC, LPT = S::LPT;
   constexpr int PSTRIDE = GQ * (D + 2);
@@ -670,13 +707,113 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
   } else if (n_part == 0) {  // nothing to read: zeros
     for (int k = tid; k < GQ * D; k += LSA_BLOCK) store_out<T>(outp + k, 0.0f);
   }
-  if (clear_record) {
+  if (clear == 1) {
     for (int x = tid; x < kRecordCopies * words; x += LSA_BLOCK) {
       const int c = x / words, k = x - c * words;
       coherent_store_i32(a.record + c * a.cstride + i * words + k, 0);
     }
+  } else if (clear == 2) {
+    uint64_t* mine = a.pub + i * (int64_t)a.rows;
+    for (int x = tid; x < a.rows; x += LSA_BLOCK) coherent_store_u64(mine + x, 0);
   }
   DECODE_MARK(6);
+}
+
+// Reader of the rank form: no record. The unit's select splits publish their columns' keys
+// (+ 1) and every reader ranks them itself: it loads its query rows and the table's span
+// ends, waits (bounded) until all `rows` published keys are nonzero, selects the K best
+// (block_topk_sorted, the last split's selection of the exchange form, on the same keys),
+// turns each pick's span into its kept range and list slots as publish_picks does, and
+// reads its share. Role 0 writes the list length; the last reader clears the published
+// keys. Span tables only.
+template <typename T, int D, int GQ>
+__device__ __forceinline__ void rank_reader(const DecodeArgs& a, char* smem, int64_t i, int role) {
+  RdLds<D, GQ>& sh = *(RdLds<D, GQ>*)smem;
+  RankLds& rk = *(RankLds*)(smem + rd_ids_offset<D, GQ>());
+  int32_t* ends_l = (int32_t*)(smem + rank_ends_offset<D, GQ>());       // [rows]
+  uint64_t* keys = (uint64_t*)(smem + rank_keys_offset<D, GQ>(a.rows));  // [rows]
+  int32_t* ids = (int32_t*)(smem + rd_ids_offset<D, GQ>());              // after the selection
+  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
+  const int K = a.K, rows = a.rows;
+  const int64_t r = (uint32_t)i / (uint32_t)a.G;
+  const int g = (int)((uint32_t)i % (uint32_t)a.G);
+  const int64_t position = a.positions[r];
+  const int64_t wstart = window_start_of(position, a.window);
+  const int64_t n_win = position + 1 - wstart > 0 ? position + 1 - wstart : 0;
+  const int64_t n_sink = a.sink < wstart ? a.sink : wstart;
+  const int32_t* ends = a.ends + (r * a.row_tables + g * a.group_tables) * (int64_t)rows;
+  uint64_t* pub = a.pub + i * (int64_t)rows;
+  DECODE_MARK(0);
+
+  // the query rows and the span ends go out before the wait
+  const T* qrow = (const T*)a.q + (r * a.Hq + (int64_t)g * GQ) * D;
+  QueryRegs<T, D, GQ> qr;
+  qr.load(qrow, a.scale_log2);
+  for (int m = tid; m < rows; m += LSA_BLOCK) ends_l[m] = ends[m];
+
+  // wave 0 polls the published keys: every slot is nonzero once its split has written it
+  if (w == 0) {
+    uint64_t x[kRankKeysPerLane];
+    int bad = 0;
+    for (int it = 0;; ++it) {
+      bool ok = true;
+#pragma unroll
+      for (int m = 0; m < kRankKeysPerLane; ++m) {  // unconditional (clamped) loads: all in flight
+        const int j = m * LSA_WAVE + lane;
+        x[m] = coherent_load_u64(pub + (j < rows ? j : 0));
+        ok &= j >= rows || x[m] != 0;
+      }
+      if (__all(ok)) break;
+      if (it >= a.spin_limit) {
+        bad = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+#pragma unroll
+    for (int m = 0; m < kRankKeysPerLane; ++m) {
+      const int j = m * LSA_WAVE + lane;
+      if (j < rows) keys[j] = x[m] - 1;
+    }
+    if (lane == 0) {
+      sh.bad = bad;
+      if (bad && a.status) __hip_atomic_store(a.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  }
+  __syncthreads();
+  DECODE_MARK(1);
+  if (sh.bad) {  // no keys: this reader writes nothing but still arrives (see reader_role)
+    if (arrive_last(&a.rd_count[i], a.NR, &sh.rd.flag)) {
+      for (int x = tid; x < rows; x += LSA_BLOCK) coherent_store_u64(pub + x, 0);
+    }
+    return;
+  }
+  block_topk_sorted(keys, rows, K, a.kp, rk.best, &rk.tks, &rk.st);
+  // each pick's kept range [max(begin, sink), min(end, window start)) and its list slots
+  if (w == 0) {
+    const int32_t col = key_column(u_to_key(lane < K ? rk.best[lane] : 0));
+    const int b = (lane < K && col >= 0 && col < rows) ? col : -1;
+    const int64_t begin = b > 0 ? ends_l[b - 1] : 0, end_b = b >= 0 ? ends_l[b] : 0;
+    const int64_t lo = begin > a.sink ? begin : a.sink, hi = end_b < wstart ? end_b : wstart;
+    const int cnt = b >= 0 && hi > lo ? (int)(hi - lo) : 0;
+    const int incl = wave_inclusive_sum(cnt);
+    const int end = incl < a.top_k ? incl : a.top_k;
+    int prev = dpp_or<kDppWaveShr1>(0, end);  // lane - 1's
+    if (lane == 0) prev = 0;
+    if (lane < K) {
+      sh.pick[lane] = (int)lo;
+      sh.start[lane] = prev;
+      sh.n[lane] = end - prev;
+    }
+    const int filled = __builtin_amdgcn_readlane(end, K - 1);
+    if (lane == 0) {
+      sh.filled = filled;
+      if (role == 0) a.lengths[i] = filled + (int)n_win + (int)n_sink;
+    }
+  }
+  __syncthreads();
+  DECODE_MARK(2);
+  read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, 2);
 }
 
 template <typename T, int D, int GQ>
@@ -747,7 +884,7 @@ __device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int
     return;
   }
 
-  read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, true);
+  read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, 1);
 }
 
 // ------------------------------------------------------------------ replicated select
@@ -845,7 +982,7 @@ __device__ __forceinline__ void rep_role(const DecodeArgs& a, char* smem, int64_
     }
   }
   __syncthreads();
-  read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, false);
+  read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, 0);
 }
 
 // One workgroup per (unit, reader), unit fastest: every workgroup is a reader that
@@ -872,7 +1009,8 @@ __global__ __launch_bounds__(LSA_BLOCK) void decode_flat_kernel(DecodeArgs a) {
     else select_role<T, CT, D, GQ>(a, smem, id % units, (int)(id / units));
   } else {
     const uint32_t rid = id - nsel;  // readers: unit fastest, then role (low roles have work)
-    reader_role<T, D, GQ>(a, smem, rid % units, (int)(rid / units));
+    if (a.rank) rank_reader<T, D, GQ>(a, smem, rid % units, (int)(rid / units));
+    else reader_role<T, D, GQ>(a, smem, rid % units, (int)(rid / units));
   }
   DECODE_TRACE_END();
 }

@@ -127,11 +127,16 @@ def _decode_args(**kw):
 
 def test_decode_workspace_sizes():
     n = _abi.size("lsa_decode_flat_counters", 1, 8, 512, 32)
-    units, K = 8, 32
+    units, K, rows = 8, 32, 512
     stride = ((units * 2 * K + 1023) // 1024) * 1024 + 64
-    assert n == 2 * units + 8 * stride  # arrival counters + 8 record copies
+    record = 2 * units + 8 * stride  # arrival counters + 8 record copies
+    # then, 256-byte aligned, the rank form's published keys: one u64 per (unit, bucket)
+    assert n == (record + 63) // 64 * 64 + 2 * units * rows
+    # past 65536 key slots (B=32: 256 units x 512 buckets) the counters hold no keys
+    big = _abi.size("lsa_decode_flat_counters", 32, 8, 512, 32)
+    assert big == 2 * 256 + 8 * (((256 * 2 * K + 1023) // 1024) * 1024 + 64)
     keys = 8 * 512 * 8  # every column key of 16 select splits
-    parts = 8 * 16 * 4 * 130 * 4  # 16 readers' partials per unit (one a pick, at most 16 by default)
+    parts = 8 * 24 * 4 * 130 * 4  # 24 readers' partials per unit (one a pick, at most 24 by default)
     got = _abi.size("lsa_decode_flat_scratch_bytes", _abi.LSA_BF16, 1, 32, 8, 128, 512, 32, 0, 0, 16, 0)
     assert got == ((keys + 255) // 256) * 256 + parts
     assert _abi.size("lsa_decode_flat_counters", 1, 8, 512, 65) == 0  # more than 64 picks is not served

@@ -6,9 +6,13 @@ those lists within the dtype's bar (max-abs / mean-abs vs fp64: fp32 1e-4 / 1e-5
 2e-2 / 2e-3). Cases: the clustered decode geometry up to 32k, positional buckets with
 window and sink tails, top_k cutting a bucket short, fewer visible buckets than picks,
 nothing visible (zeros), batch rows with their own tables and positions, every select
-split count, both scoring dtypes, and repeated launches (the record, counters and
+split count, both hand-off forms (the rank form of span tables: every reader ranks the
+splits' published keys; the exchange form: the last split publishes a record), both
+scoring dtypes, and repeated launches (the record or published keys, counters and
 partials are reused and must come back clean).
 """
+
+import dataclasses
 
 import numpy as np
 import pytest
@@ -222,27 +226,33 @@ def test_tied_scores_take_the_block_top_k():
         assert torch.equal(lists[0, g, :n].cpu(), torch.arange(n, dtype=torch.int32))
 
 
-def test_give_up_is_reported_and_the_next_launch_is_clean():
+@pytest.mark.parametrize("form", ["rank", "exchange"])
+def test_give_up_is_reported_and_the_next_launch_is_clean(form):
     """The host makes every reader's bounded wait give up (select workgroups skip
     publishing, a 64-poll limit): all workgroups exit normally, the status word reads 1,
     the next flat_decode call zeroes the counters and raises, and the launch after it is
-    bit-identical to one before the failure."""
+    bit-identical to one before the failure. Both hand-off forms: span tables take the rank
+    form (readers wait for the splits' published keys), member tables the exchange form
+    (readers wait for the last split's record)."""
     from lsa_rocm_lab import _abi
 
     T, Hq, Hkv, D = 4096, 8, 2, 128
     data = workloads.clustered(T, Hq, Hkv, D, n_clusters=64, seed=31, device=DEV)
     buckets = workloads.cluster_buckets(data, target=T // 64)
+    assert buckets.spans
+    if form == "exchange":
+        buckets = dataclasses.replace(buckets, spans=False)
     config = PortConfig(cluster_block_size=64, bucket_size=64, bucket_cap=256, top_p=16, top_k=4096,
                         window_size=64, sink_size=4)
     q = data.q[:, -1:].contiguous()
     pos = torch.tensor([T - 1], dtype=torch.int32, device=DEV)
-    run = lambda: pipeline.flat_decode(q, data.k, data.v, pos, buckets, config, splits=2)  # the exchange form
+    run = lambda: pipeline.flat_decode(q, data.k, data.v, pos, buckets, config, splits=2)
     good = run()
     torch.cuda.synchronize()
     word = _abi.StatusWord.get(torch.device(DEV))
     assert int(word[0]) == 0
     lib = _abi.load()
-    print("case give-up: skip_publish=1 spin_limit=64", flush=True)
+    print(f"case give-up ({form} form): skip_publish=1 spin_limit=64", flush=True)
     lib.lsa_debug_decode(1, 64)
     try:
         run()
