@@ -15,10 +15,15 @@
 // the sub-tile has any, runs the online softmax in the exp2 domain per query column, and
 // accumulates O^T += V^T P^T: the S^T accumulator layout is exactly the P^T B operand
 // (lane (h, q) holds keys 8(r/4) + 4h + r%4 of column q), so P needs no shuffle; the V^T
-// A operand comes from the row-major V tile through transposing LDS reads. The running
-// max is rescaled lazily: only when a column's max grows by more than 2^8 is the state
-// rescaled, so P stays below 256 in the 16-bit operand and most tiles skip the
-// 128-register rescale. The softmax normaliser sums the 16-bit weights the matrix ops use.
+// A operand comes from the row-major V tile through transposing LDS reads. A wave's
+// sub-tiles are software-pipelined three deep: while the matrix core forms the next
+// sub-tile's scores and the previous sub-tile's P V product, the VALU makes this
+// sub-tile's weights. The running max is rescaled lazily: only when a column's max grows by
+// more than 2^8 is the state rescaled, so P stays below 256 in the 16-bit operand and most
+// tiles skip the 128-register rescale; the weights are made against the current max
+// first, and the column maxima are taken only when some lane's weight sum reaches 2^8
+// (which every such growth implies). The softmax normaliser sums the 16-bit weights the
+// matrix ops use.
 #include <math.h>
 
 #include <type_traits>
@@ -282,21 +287,116 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
 #pragma unroll
     for (int s = 0; s < KS; ++s)
       ka[s] = __builtin_bit_cast(op_t, *(const uint4*)&sh.k[buf][TS * half + ln][16 * s + 8 * hh]);
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) st[qb] = M::run(ka[s], qop[qb][s], st[qb]);
     }
   };
-  // One sub-tile of math for a wave: the softmax of sub-tile (cb, ch) (raw scores cur)
-  // and O^T += V^T P^T, with the scores of the next sub-tile (nb, nh) into nxt interleaved
-  // with the exponentials, so the matrix core runs while the VALU works. After the last
-  // sub-tile the next scores read a stale buffer and are never used. hook(s) runs after
-  // k-step s (the loads and LDS stores of the pipeline, placed between matrix ops).
-  auto tile_math = [&](int cb, int ch, int ctile, int nb, int nh, f32x16_t (&cur)[QB], f32x16_t (&nxt)[QB],
+  // The weights of one sub-tile from its raw scores s: p = exp2(s * scale - m) per query
+  // column, packed in pairs into the 16-bit P^T B operand (accumulator regs 8 s' .. 8 s' + 7
+  // are keys 16 s' + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}), and their sum in two
+  // chains, taken from the packed weights the matrix ops consume.
+  auto weights = [&](const f32x16_t (&cur)[QB], uint32_t (&pw)[QB][8], float (&ls)[QB][2]) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      ls[qb][0] = ls[qb][1] = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = fast_exp2(fmaf(cur[qb][r], a.scale_log2, -m_run[qb]));
+        const float p1 = fast_exp2(fmaf(cur[qb][r + 1], a.scale_log2, -m_run[qb]));
+        pw[qb][r / 2] = M::pack2(p0, p1);
+        ls[qb][(r / 2) & 1] = M::sum2(pw[qb][r / 2], ls[qb][(r / 2) & 1]);
+      }
+    }
+  };
+  // The running max moves lazily: only when some column's max grows by more than
+  // 2^kRescale is the state rescaled, so every weight stays at most 2^kRescale. The weights
+  // are first made against the current max; a lane whose sum of 16 weights is below
+  // 2^kRescale (the common case) holds no weight that large, so no column of the wave can
+  // have grown that much and the max is not needed. Otherwise (some sum reached 2^kRescale,
+  // or is not a number) the column maxima are taken and, where a column grew by more than
+  // 2^kRescale, the state is rescaled and the weights made again: the same rescales, at
+  // the same sub-tiles, as taking the max every time.
+  auto settle = [&](const f32x16_t (&cur)[QB], uint32_t (&pw)[QB][8], float (&ls)[QB][2]) {
+    bool big = false;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) big |= !(ls[qb][0] + ls[qb][1] < 256.0f);
+    static_assert(kRescale == 8.0f, "the sum test is against 2^kRescale");
+    if (__any(big)) {
+      float mt[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        float mx = cur[qb][0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, cur[qb][r]);
+        mt[qb] = fmaxf(mx, lane_xor(mx, 32)) * a.scale_log2;
+      }
+      bool grow = false;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) grow |= mt[qb] > m_run[qb] + kRescale;
+      if (__any(grow)) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const float mn = fmaxf(m_run[qb], mt[qb]);
+          const float alpha = fast_exp2(m_run[qb] - mn);
+          m_run[qb] = mn;
+          l_run[qb] *= alpha;
+#pragma unroll
+          for (int d = 0; d < DB; ++d) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[d][qb][r] *= alpha;
+          }
+        }
+        weights(cur, pw, ls);
+      }
+    }
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) l_run[qb] += ls[qb][0] + ls[qb][1];
+  };
+  // V^T operands of sub-tile `half` of the tile in buffer `buf`: lane (hh, ln) holds dim
+  // 32 d + ln at keys 16 sp + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}, two
+  // transposing 8-byte reads each.
+  constexpr int VROW = 2 * (D + VPAD);  // bytes per V row
+  auto v_operands = [&](int buf, int half, op_t (&va)[2][DB]) {
+    const lds_char* vbase = (const lds_char*)&sh.v[buf][TS * half][0] + vlane;
+#pragma unroll
+    for (int sp = 0; sp < 2; ++sp) {
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const uint2 lo = v_column4(vbase, 16 * sp * VROW + 64 * d);
+        const uint2 hi = v_column4(vbase, (16 * sp + 8) * VROW + 64 * d);
+        va[sp][d] = __builtin_bit_cast(op_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+      }
+    }
+  };
+  // O^T += V^T P^T for one sub-tile
+  auto pv = [&](const op_t (&va)[2][DB], const uint32_t (&pw)[QB][8]) {
+#pragma unroll
+    for (int sp = 0; sp < 2; ++sp) {
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const op_t pb = __builtin_bit_cast(
+              op_t, make_uint4(pw[qb][4 * sp], pw[qb][4 * sp + 1], pw[qb][4 * sp + 2], pw[qb][4 * sp + 3]));
+          o[d][qb] = M::run(va[sp][d], pb, o[d][qb]);
+        }
+      }
+    }
+  };
+  // One sub-tile step of a wave, software-pipelined over three sub-tiles so that its matrix
+  // and vector work are independent: the weights of sub-tile (cb, ch) (raw scores cur) are
+  // made while the matrix core forms the scores of the next sub-tile (nb, nh) into nxt and
+  // O^T += V^T P^T of the previous one (buffer pbuf, half ph, weights pwp). One scheduling
+  // region (between the issue-priority changes) holds the 16 matrix ops, the exponentials
+  // and the pipeline's gathers (hook), none of which depend on each other; the rescale test
+  // follows. pre() runs before the region (it may branch). After the last sub-tile the next
+  // scores read a stale buffer and are never used.
+  auto tile_math = [&](int cb, int ch, int ctile, int nb, int nh, int pbuf, int ph, f32x16_t (&cur)[QB],
+                       f32x16_t (&nxt)[QB], uint32_t (&pw)[QB][8], const uint32_t (&pwp)[QB][8], auto&& pre,
                        auto&& hook) {
-    // the next tile's K operands and this sub-tile's tag, in flight together
+    // the next sub-tile's K operands and this sub-tile's tag, in flight together
     op_t ka[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s)
@@ -321,49 +421,36 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
         }
       }
     }
-    // column max (raw scores; the scale is positive) over both lane halves, in log2 units
-    float mt[QB];
+    pre();
+    // The two waves of a SIMD alternate between this matrix-heavy region and the rescale
+    // test; raising the wave's issue priority here lets its matrix ops issue first.
+    __builtin_amdgcn_s_setprio(1);
+    op_t va[2][DB];
+    v_operands(pbuf, ph, va);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      float mx = cur[qb][0];
-#pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, cur[qb][r]);
-      mt[qb] = fmaxf(mx, lane_xor(mx, 32)) * a.scale_log2;
-    }
-    // lazy rescale: only when some column's max grew by more than 2^kRescale
-    bool grow = false;
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) grow |= mt[qb] > m_run[qb] + kRescale;
-    if (__any(grow)) {
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        const float mn = fmaxf(m_run[qb], mt[qb]);
-        const float alpha = fast_exp2(m_run[qb] - mn);
-        m_run[qb] = mn;
-        l_run[qb] *= alpha;
-#pragma unroll
-        for (int d = 0; d < DB; ++d) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[d][qb][r] *= alpha;
-        }
-      }
-    }
-    // next scores, one k-step at a time, each followed by its share of this tile's
-    // weights p = exp2(s * scale - m) (the accumulator regs 8 s' .. 8 s' + 7 are keys
-    // 16 s' + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}: the P^T B operand)
-    constexpr int EPS = 16 / KS;  // exponentials per k-step (even)
-    uint32_t pw[QB][8];           // the weights, packed in pairs as they are made
-    float ls[QB][2];              // their sum, in two chains
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      ls[qb][0] = ls[qb][1] = 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) nxt[qb][r] = 0.0f;
     }
-    // The two waves of a SIMD alternate between this matrix-heavy part and the vector-only
-    // part above; raising the wave's issue priority here lets its matrix ops issue first, so
-    // the other wave's max/rescale work fills the matrix ops' shadow.
-    __builtin_amdgcn_s_setprio(1);
+    float ls[QB][2];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) ls[qb][0] = ls[qb][1] = 0.0f;
+    // k-step s: the score op s, its share of the weights, the P V op s - 1, then hook(s).
+    // The weights are pinned where they are made (an empty asm that uses them): otherwise
+    // instruction selection sinks the exponentials to their uses after the last matrix op.
+    // The scheduler then interleaves freely: a sched_barrier after each k-step (the source
+    // order exactly) measured 6% slower.
+    constexpr int EPS = 16 / KS;  // weights per k-step (even)
+    constexpr int NPV = 2 * DB;   // P V ops
+    auto pv_op = [&](int j) {
+      const int sp = j / DB, d = j % DB;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const op_t pb = __builtin_bit_cast(
+            op_t, make_uint4(pwp[qb][4 * sp], pwp[qb][4 * sp + 1], pwp[qb][4 * sp + 2], pwp[qb][4 * sp + 3]));
+        o[d][qb] = M::run(va[sp][d], pb, o[d][qb]);
+      }
+    };
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
 #pragma unroll
@@ -376,72 +463,63 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
           const float p0 = fast_exp2(fmaf(cur[qb][r], a.scale_log2, -m_run[qb]));
           const float p1 = fast_exp2(fmaf(cur[qb][r + 1], a.scale_log2, -m_run[qb]));
           pw[qb][r / 2] = M::pack2(p0, p1);
-          ls[qb][(r / 2) & 1] = M::sum2(pw[qb][r / 2], ls[qb][(r / 2) & 1]);  // the 16-bit weights the MFMA uses
+          ls[qb][(r / 2) & 1] = M::sum2(pw[qb][r / 2], ls[qb][(r / 2) & 1]);
+          asm volatile("" ::"v"(pw[qb][r / 2]));
         }
       }
-      __builtin_amdgcn_sched_barrier(0);  // this k-step's MFMA, then its weights, in order
+      if (s >= 1 && s - 1 < NPV) pv_op(s - 1);
       hook(s);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // V^T operands of this tile: lane (hh, ln) holds dim 32 d + ln at keys
-    // 16 sp + {4 hh .. 4 hh + 3, 8 + 4 hh .. 8 + 4 hh + 3}, two transposing 8-byte reads
-    // (issued after the score MFMAs have taken their K operands)
-    op_t va[2][DB];
-    constexpr int VROW = 2 * (D + VPAD);  // bytes per V row
-    const lds_char* vbase = (const lds_char*)&sh.v[cb][TS * ch][0] + vlane;
-#pragma unroll
-    for (int sp = 0; sp < 2; ++sp) {
-#pragma unroll
-      for (int d = 0; d < DB; ++d) {
-        const uint2 lo = v_column4(vbase, 16 * sp * VROW + 64 * d);
-        const uint2 hi = v_column4(vbase, (16 * sp + 8) * VROW + 64 * d);
-        va[sp][d] = __builtin_bit_cast(op_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
-      }
-    }
-    op_t pb[QB][2];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      l_run[qb] += ls[qb][0] + ls[qb][1];
-#pragma unroll
-      for (int sp = 0; sp < 2; ++sp)
-        pb[qb][sp] = __builtin_bit_cast(op_t, make_uint4(pw[qb][4 * sp], pw[qb][4 * sp + 1], pw[qb][4 * sp + 2],
-                                                         pw[qb][4 * sp + 3]));
     }
 #pragma unroll
-    for (int sp = 0; sp < 2; ++sp) {
-#pragma unroll
-      for (int d = 0; d < DB; ++d) {
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) o[d][qb] = M::run(va[sp][d], pb[qb][sp], o[d][qb]);
-      }
-    }
+    for (int j = KS - 1; j < NPV; ++j) pv_op(j);
     __builtin_amdgcn_s_setprio(0);
+    settle(cur, pw, ls);
   };
 
-  // Pipeline, one barrier per tile over NBUF = 4 LDS buffers. Iteration t computes tile t
-  // (its second sub-tile's math also takes the scores of tile t + 1's first sub-tile);
-  // inside the first sub-tile's math it stores tile t + 2 (gathered in iteration t - 1) and
-  // gathers tile t + 3 (ids fetched in iteration t - 1), inside the second it fetches the
-  // ids of tile t + 4. Buffer (t + 2) % 4 last held tile t - 2, whose readers finished
-  // before the barrier of iteration t - 1; tile t + 2 is first read after the barrier of
-  // iteration t + 1. The vector-memory counter retires in order, and every wait is for the
-  // oldest loads outstanding.
-  auto step = [&](int tile, f32x16_t (&cur)[QB], f32x16_t (&nxt)[QB]) {
+  // Pipeline, one barrier per tile over NBUF = 4 LDS buffers. Iteration t makes the weights
+  // of tile t's two sub-tiles; with them the matrix core forms the scores of the sub-tile
+  // after each (tile t's second, tile t + 1's first) and the P V product of the sub-tile
+  // before each (tile t - 1's second, tile t's first). Before the first sub-tile's region
+  // it stores tile t + 2 (gathered in iteration t - 1); inside the region it gathers tile
+  // t + 3 (ids fetched in iteration t - 1), inside the second it fetches the ids of tile
+  // t + 4. Iteration t reads buffers t - 1, t and t + 1 (mod 4) and writes buffer t + 2 =
+  // t - 2, whose last reads were in iteration t - 1, before the barrier; tile t + 2 is first
+  // read after the barrier of iteration t + 1. The vector-memory counter retires in order,
+  // and every wait is for the oldest loads outstanding.
+  f32x16_t st_a[QB], st_b[QB];
+  uint32_t pw_a[QB][8], pw_b[QB][8];
+  auto step = [&](int tile) {
     __syncthreads();
     const bool store_next = tile + 2 < n_tiles;
-    tile_math(tile % NBUF, 0, tile, tile % NBUF, 1, cur, nxt, [&](int s) {
-      if (s == 1 && store_next) store_tile(rows, (tile + 2) % NBUF, tile + 2);
-      if (s == 3) load_tile(rows, tile + 3);
-    });
-    tile_math(tile % NBUF, 1, tile, (tile + 1) % NBUF, 0, nxt, cur, [&](int s) {
-      if (s == 1) fetch_ids(rows, tile + 4);
-    });
+    tile_math(
+        tile % NBUF, 0, tile, tile % NBUF, 1, (tile + NBUF - 1) % NBUF, 1, st_a, st_b, pw_a, pw_b,
+        [&] {
+          if (store_next) store_tile(rows, (tile + 2) % NBUF, tile + 2);
+        },
+        [&](int s) {
+          if (s == 3) load_tile(rows, tile + 3);
+        });
+    tile_math(
+        tile % NBUF, 1, tile, (tile + 1) % NBUF, 0, tile % NBUF, 0, st_b, st_a, pw_b, pw_a, [] {},
+        [&](int s) {
+          if (s == 1) fetch_ids(rows, tile + 4);
+        });
   };
-  f32x16_t st_a[QB], st_b[QB];
   fetch_ids(rows, 0);
   fetch_ids(rows_b, 1);
   load_tile(rows, 0);
   load_tile(rows_b, 1);
+  // the first sub-tile has no previous one: its P V product takes zero weights and the
+  // second half of buffer NBUF - 1, zeroed here (tile 3 is first stored there in iteration 1)
+  {
+    uint4* z = (uint4*)&sh.v[NBUF - 1][TS][0];  // rows TS .. TK - 1, contiguous
+    for (int x = tid; x < TS * (D + VPAD) / 8; x += NTH) z[x] = make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pw_b[qb][j] = 0u;
+  }
   store_tile(rows, 0, 0);
   fetch_ids(rows, 2);
   store_tile(rows_b, 1, 1);
@@ -449,7 +527,13 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
   fetch_ids(rows, 3);
   __syncthreads();
   scores(0, 0, st_a);
-  for (int tile = 0; tile < n_tiles; ++tile) step(tile, st_a, st_b);
+  for (int tile = 0; tile < n_tiles; ++tile) step(tile);
+  // the last sub-tile's P V product
+  {
+    op_t va[2][DB];
+    v_operands((n_tiles - 1) % NBUF, 1, va);
+    pv(va, pw_b);
+  }
 
   // normalise and store: lane (hh, q) holds dims 32 d + 8 (r / 4) + 4 hh + r % 4 of column q
 #pragma unroll
