@@ -26,7 +26,8 @@ constexpr int kRankKeysPerLane = kRankMaxRows / LSA_WAVE;
 constexpr int64_t kRankMaxSlots = 1 << 16;
 
 // Phase hooks: no-ops unless a build defines DECODE_MARK(k) (timestamps for profiling; k < 16:
-// 0-6 the exchange form's select and reader phases, 8-11 the replicated select's).
+// 0-6 the select and reader phases, 7 a ranking reader holding its picks, 8-11 the
+// replicated select's).
 #ifndef DECODE_MARK
 #define DECODE_MARK(k) ((void)0)
 #define DECODE_TRACE_BEGIN() ((void)0)
@@ -108,6 +109,7 @@ struct RankLds {
   RadixState st;
   TopkScratch tks;
   uint64_t best[kMaxPicks];
+  int fast;  // wave 0 ranked the keys itself (wave_topk_hist)
 };
 template <int D, int GQ>
 constexpr size_t rank_ends_offset() {
@@ -719,6 +721,47 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
   DECODE_MARK(6);
 }
 
+// Wave 0 of a ranking reader: clears the top-K scratch's histogram, polls the unit's `rows`
+// published keys (KPL a lane, all loads in flight each round) until every one is nonzero
+// or the spin limit passes (*bad), then ranks them: wave_topk_hist into rk->best (*fast),
+// or, when the histogram cut does not serve, the keys go to LDS for block_topk_sorted.
+template <int KPL>
+__device__ __forceinline__ void poll_and_rank(const DecodeArgs& a, const uint64_t* pub, int rows, uint64_t* keys,
+                                              RankLds* rk, int* bad, int* fast) {
+  const int lane = threadIdx.x & (LSA_WAVE - 1);
+  for (int b = lane; b < 256; b += LSA_WAVE) {
+    rk->tks.hist[b] = 0;
+    rk->tks.fill[b] = 0;
+  }
+  uint64_t x[KPL];
+  for (int it = 0;; ++it) {
+    bool ok = true;
+#pragma unroll
+    for (int m = 0; m < KPL; ++m) {  // unconditional (clamped) loads: all in flight
+      const int j = m * LSA_WAVE + lane;
+      x[m] = coherent_load_u64(pub + (j < rows ? j : 0));
+      ok &= j >= rows || x[m] != 0;
+    }
+    if (__all(ok)) break;
+    if (it >= a.spin_limit) {
+      *bad = 1;
+      return;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+#pragma unroll
+  for (int m = 0; m < KPL; ++m) x[m] = m * LSA_WAVE + lane < rows ? x[m] - 1 : 0;  // EMPTY past the table
+  if (wave_topk_hist<KPL>(x, a.K, a.kp, rk->best, &rk->tks)) {
+    *fast = 1;
+    return;
+  }
+#pragma unroll
+  for (int m = 0; m < KPL; ++m) {
+    const int j = m * LSA_WAVE + lane;
+    if (j < rows) keys[j] = x[m];
+  }
+}
+
 // Reader of the rank form: no record. The unit's select splits publish their columns' keys
 // (+ 1) and every reader ranks them itself: it loads its query rows and the table's span
 // ends, waits (bounded) until all `rows` published keys are nonzero, selects the K best
@@ -751,32 +794,16 @@ __device__ __forceinline__ void rank_reader(const DecodeArgs& a, char* smem, int
   qr.load(qrow, a.scale_log2);
   for (int m = tid; m < rows; m += LSA_BLOCK) ends_l[m] = ends[m];
 
-  // wave 0 polls the published keys: every slot is nonzero once its split has written it
+  // wave 0 polls the published keys (every slot is nonzero once its split has written it)
+  // and ranks them in its registers (wave_topk_hist); keys that defeat the histogram cut go
+  // to LDS for the block's top-K
   if (w == 0) {
-    uint64_t x[kRankKeysPerLane];
-    int bad = 0;
-    for (int it = 0;; ++it) {
-      bool ok = true;
-#pragma unroll
-      for (int m = 0; m < kRankKeysPerLane; ++m) {  // unconditional (clamped) loads: all in flight
-        const int j = m * LSA_WAVE + lane;
-        x[m] = coherent_load_u64(pub + (j < rows ? j : 0));
-        ok &= j >= rows || x[m] != 0;
-      }
-      if (__all(ok)) break;
-      if (it >= a.spin_limit) {
-        bad = 1;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-    }
-#pragma unroll
-    for (int m = 0; m < kRankKeysPerLane; ++m) {
-      const int j = m * LSA_WAVE + lane;
-      if (j < rows) keys[j] = x[m] - 1;
-    }
+    int bad = 0, fast = 0;
+    if (rows <= 8 * LSA_WAVE) poll_and_rank<8>(a, pub, rows, keys, &rk, &bad, &fast);
+    else poll_and_rank<kRankKeysPerLane>(a, pub, rows, keys, &rk, &bad, &fast);
     if (lane == 0) {
       sh.bad = bad;
+      rk.fast = fast;
       if (bad && a.status) __hip_atomic_store(a.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
   }
@@ -788,7 +815,7 @@ __device__ __forceinline__ void rank_reader(const DecodeArgs& a, char* smem, int
     }
     return;
   }
-  block_topk_sorted(keys, rows, K, a.kp, rk.best, &rk.tks, &rk.st);
+  if (!rk.fast) block_topk_sorted(keys, rows, K, a.kp, rk.best, &rk.tks, &rk.st);
   // each pick's kept range [max(begin, sink), min(end, window start)) and its list slots
   if (w == 0) {
     const int32_t col = key_column(u_to_key(lane < K ? rk.best[lane] : 0));
@@ -812,7 +839,7 @@ __device__ __forceinline__ void rank_reader(const DecodeArgs& a, char* smem, int
     }
   }
   __syncthreads();
-  DECODE_MARK(2);
+  DECODE_MARK(7);
   read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, 2);
 }
 

@@ -301,6 +301,83 @@ __device__ __forceinline__ bool block_topk_hist(const uint64_t* keys, int n, int
   return true;
 }
 
+// The histogram cut of block_topk_hist run by one wave on keys held in its registers, with
+// no block barrier: x[m] is key m * LSA_WAVE + lane (u-ordered, 0 = EMPTY). The same bins,
+// cut and ranking, so the same out[0..kp) (the K best sorted descending, EMPTY past them).
+// sc->hist and sc->fill must be zero on entry (the wave clears them ahead of time). Returns
+// false (in every lane) when a score is not finite or more than 64 keys survive the cut;
+// the caller then takes block_topk_sorted. The wave's LDS accesses run in program order,
+// and wave_barrier keeps the compiler from moving them across the phases.
+template <int KPL>
+__device__ __forceinline__ bool wave_topk_hist(const uint64_t* x, int K, int kp, uint64_t* out, TopkScratch* sc) {
+  const int lane = threadIdx.x & (LSA_WAVE - 1);
+  float mn = INFINITY, mx = -INFINITY;
+  int cnt = 0, bad = 0;
+#pragma unroll
+  for (int m = 0; m < KPL; ++m) {
+    const float s = key_score(x[m]);
+    const bool live = x[m] != 0;
+    bad |= (live && s - s != 0.0f) ? 1 : 0;  // NaN or infinite
+    mn = live ? fminf(mn, s) : mn;
+    mx = live ? fmaxf(mx, s) : mx;
+    cnt += live ? 1 : 0;
+  }
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  cnt = wave_sum(cnt);
+  if (wave_or(bad)) return false;
+  const int kc = cnt < K ? cnt : K;
+  const float scale = mx > mn ? 256.0f / (mx - mn) : 0.0f;
+  auto bin_of = [&](uint64_t k) {
+    const int b = (int)((key_score(k) - mn) * scale);
+    return b < 0 ? 0 : (b > 255 ? 255 : b);
+  };
+  int bin[KPL];
+#pragma unroll
+  for (int m = 0; m < KPL; ++m) {
+    bin[m] = bin_of(x[m]);
+    if (x[m] != 0) atomicAdd(&sc->hist[bin[m]], 1);
+  }
+  __builtin_amdgcn_wave_barrier();
+  // lane l owns bins 255-4l .. 252-4l; exclusive suffix offsets from the top bin
+  const int c0 = sc->hist[255 - 4 * lane], c1 = sc->hist[254 - 4 * lane];
+  const int c2 = sc->hist[253 - 4 * lane], c3 = sc->hist[252 - 4 * lane];
+  const int mine = c0 + c1 + c2 + c3;
+  const int inc = wave_inclusive_sum(mine);
+  const int o0 = inc - mine, o1 = o0 + c0, o2 = o1 + c1, o3 = o2 + c2;
+  sc->off[255 - 4 * lane] = o0;
+  sc->off[254 - 4 * lane] = o1;
+  sc->off[253 - 4 * lane] = o2;
+  sc->off[252 - 4 * lane] = o3;
+  // the bin holding the kc-th key, and the keys in it and above
+  const bool here = kc > 0 && o0 < kc && kc <= inc;
+  const int d = o1 >= kc ? 255 - 4 * lane : (o2 >= kc ? 254 - 4 * lane : (o3 >= kc ? 253 - 4 * lane : 252 - 4 * lane));
+  const int total = o1 >= kc ? o1 : (o2 >= kc ? o2 : (o3 >= kc ? o3 : inc));
+  const uint64_t hm = __ballot(here);
+  const int src = hm ? __ffsll((long long)hm) - 1 : 0;
+  const int cut = hm ? __builtin_amdgcn_readlane(d, src) : 256;
+  if (hm && __builtin_amdgcn_readlane(total, src) > LSA_WAVE) return false;
+  __builtin_amdgcn_wave_barrier();
+  // the candidates at their bins' offsets
+#pragma unroll
+  for (int m = 0; m < KPL; ++m) {
+    if (x[m] != 0 && bin[m] >= cut) sc->cand[sc->off[bin[m]] + atomicAdd(&sc->fill[bin[m]], 1)] = x[m];
+  }
+  __builtin_amdgcn_wave_barrier();
+  // ranks: a candidate's bin offset plus the larger keys of its own bin
+  const int nc = cut < 256 ? sc->off[cut] + sc->hist[cut] : 0;
+  if (lane < nc) {
+    const uint64_t y = sc->cand[lane];
+    const int b = bin_of(y);
+    const int lo = sc->off[b], hi = lo + sc->hist[b];
+    int rank = lo;
+    for (int m = lo; m < hi; ++m) rank += sc->cand[m] > y ? 1 : 0;  // nonempty keys are distinct
+    if (rank < K) out[rank] = y;
+  }
+  for (int m = kc + lane; m < kp; m += LSA_WAVE) out[m] = 0;  // EMPTY past the nonempty keys
+  return true;
+}
+
 // The K best of keys[0..n) (u-ordered, in LDS), sorted descending into out[0..kp) with
 // u == 0 past K (kp = next_pow2(K)). K <= 64 takes the histogram cut when it leaves at
 // most 64 candidates; otherwise a radix select + bitonic sort. 1 <= K <= n. Every thread
