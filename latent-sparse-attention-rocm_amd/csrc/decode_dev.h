@@ -306,7 +306,7 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
     for (int k = 0; k < 2; ++k) {
       const int j = k * GROUPS + grp;
       col[k] = j < n_local ? c0 + j : -1;
-      const int cc = col[k] >= 0 ? col[k] : c0;
+      const int cc = col[k] >= 0 ? col[k] : 0;  // row 0: a split may hold no column (c0 >= rows)
       craw[k].load(cent + (int64_t)cc * D + p * SPAN);
       e[k] = ends ? ends[cc] : 0;
     }

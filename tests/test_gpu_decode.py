@@ -87,6 +87,25 @@ def test_clustered_decode_matches_oracle(splits):
                  label=f"clustered splits={splits}")
 
 
+@pytest.mark.parametrize("form", ["rank", "exchange"])
+@pytest.mark.parametrize("splits", [48, 100])
+def test_select_splits_past_the_table(form, splits):
+    """More select splits than the table's columns fill: with 128 buckets, 48 splits take 3
+    columns each and splits 43..47 start past the table (100 splits: 2 columns, 64..99
+    empty). An empty split scores nothing and still publishes (rank form) or arrives
+    (exchange form); its loads stay inside the table. Lists bit-exact vs the oracle."""
+    T, Hq, Hkv, D = 8192, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=128, seed=5, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    rows = buckets.rows
+    assert buckets.spans and (splits - 1) * -(-rows // splits) >= rows  # the last split is empty
+    if form == "exchange":
+        buckets = dataclasses.replace(buckets, spans=False)
+    pos = torch.tensor([T - 1], dtype=torch.int32)
+    check_decode(data.q[:, -1:], data.k, data.v, pos, buckets, workloads.FLAT_32K, splits=splits,
+                 label=f"{form} splits={splits} rows=128")
+
+
 @pytest.mark.parametrize("dtype,hq,hkv", [(torch.bfloat16, 8, 8), (torch.bfloat16, 8, 4), (torch.bfloat16, 16, 2),
                                           (torch.float16, 8, 2), (torch.float16, 16, 2), (torch.float16, 4, 4)])
 def test_matrix_core_decode_group_sizes(dtype, hq, hkv):
