@@ -246,8 +246,11 @@ int lsa_read_chunked_mfma_ok(int dtype, int32_t D, int32_t chunk);
  * system-scope store) is set to 1 if a reader workgroup gave up waiting for its unit's
  * selection (not expected: readers wait only on lower-numbered workgroups, which never
  * wait). Such a reader writes nothing and still arrives, so the arrival counters reset,
- * but that launch's outputs are invalid and a record published after the give-up can
- * outlive it: the caller zeroes the counters before the next launch.
+ * but that launch's outputs are invalid and a record (or published keys) written after the
+ * give-up can outlive it: the caller zeroes the counters before the next launch. With
+ * LSA_TABLE_SPANS, more than one select split and a table that fits the counters' key
+ * slots (at most 1024 buckets, 65 536 (row, kv-head, bucket) slots in all), the splits
+ * publish their keys and every reader ranks them itself (the rank form: the same lists).
  * table_flags: 0, or LSA_TABLE_SPANS when every bucket row j holds exactly the consecutive
  * ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0) in order, -1 after (the contiguous-segment
  * tables): the kept members of a pick are then a range, counted and expanded without
@@ -310,7 +313,7 @@ int lsa_decode_flat_noalloc(const void* q, const void* k, const void* v, int dty
                             void* stream);
 
 /* Test hook (thread-local, this thread's later lsa_decode_flat calls): skip_publish != 0
- * makes the select workgroups skip publishing the record, and spin_limit > 0 replaces the
+ * makes the select workgroups skip publishing the record or their keys, and spin_limit > 0 replaces the
  * readers' poll limit, so a test can make the bounded wait give up with every workgroup
  * still exiting normally. lsa_debug_decode(0, 0) restores the defaults. No counterpart in
  * the reference (its decode has no cross-workgroup wait). */
