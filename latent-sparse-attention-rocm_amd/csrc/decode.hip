@@ -16,12 +16,12 @@
 // written, so a reader that sees all 2K words nonzero holds the whole record: no flag and
 // no fence. It also writes the unit's list length.
 //
-// Rank form (span tables of at most kRankMaxRows buckets, more than one split, the
-// published keys fit the counters region): no split collects. Each split publishes its
-// columns' keys + 1 (nonzero once written) into the counters region and exits; every reader
-// of the unit waits until all of the unit's keys are nonzero, ranks them itself (the same
-// top-K on the same keys), takes each pick's kept range from the span ends it loaded while
-// waiting, and reads its share. Role 0 writes the list length; the last reader to arrive
+// Rank form (tables of at most kRankMaxRows buckets, more than one split, the published
+// keys fit the counters region): no split collects. Each split publishes its columns' keys
+// + 1 (nonzero once written) into the counters region and exits; every reader of the unit
+// waits until all of the unit's keys are nonzero, ranks them itself (the same top-K on the
+// same keys), takes each pick's kept count from the span ends it loaded while waiting (or
+// from the picks' member rows), and reads its share. Role 0 writes the list length; the last reader to arrive
 // zeroes the published keys. This drops the last split's arrival, its reload of the keys,
 // the record and its poll from the step's chain.
 //
@@ -307,10 +307,10 @@ int decode_launch(const char* who, const void* q, const void* k, const void* v, 
     const size_t rd = reader_lds_d(D, gq, p.span);
     p.shmem = sel > rd ? sel : rd;
   }
-  // the rank form: more than one select split over a span table whose keys fit the readers
-  // and the counters region (which then holds the published keys)
-  const bool rank = !tree && !p.rep && select_splits > 1 && (table_flags & LSA_TABLE_SPANS) &&
-                    rank_slots(units, rows) && rank_lds_d(D, gq, rows) <= kMaxLds;
+  // the rank form: more than one select split over a table whose keys fit the readers and
+  // the counters region (which then holds the published keys)
+  const bool rank = !tree && !p.rep && select_splits > 1 && rank_slots(units, rows) &&
+                    rank_lds_d(D, gq, rows) <= kMaxLds;
   if (rank && rank_lds_d(D, gq, rows) > p.shmem) p.shmem = rank_lds_d(D, gq, rows);
   LSA_REQUIRE(p.shmem <= kMaxLds, LSA_ERR_SHAPE, "%s: %zu bytes of LDS exceed %zu", who, p.shmem, kMaxLds);
   const int64_t grid = units * (select_splits + p.NR);

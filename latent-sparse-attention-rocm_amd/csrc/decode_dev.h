@@ -147,36 +147,22 @@ __device__ __forceinline__ int64_t window_start_of(int64_t position, int window)
   return ws > 0 ? ws : 0;
 }
 
-// The select's last step, once sh.pick[0..K) holds the unit's picks (bucket rows, -1 =
-// none): each pick's kept members are counted, the list length written and the unit's
-// record published (every copy, write-through). Every thread calls it.
-__device__ __forceinline__ void publish_picks(const DecodeArgs& a, SelLds& sh, int64_t i, int64_t t, int64_t position,
-                                              const int32_t* ends) {
-  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
-  // kept members of every pick (sink <= id < window start). Span tables: the range
-  // [ends[b - 1], ends[b]) clipped to [sink, window start), from two ends words. Otherwise
-  // wave w counts picks w, w + 4, ... eight at a time; a member row streams through the
-  // wave in 16-byte lane loads (256 slots per wave load; 64 four-byte loads without
-  // vec_rows), counted with ballots
-  const int32_t* tab = a.members + t * (int64_t)a.rows * a.cap;
-  const int64_t wstart = window_start_of(position, a.window);
+// Kept members (sink <= id < window start) of picks pick[0..K) (bucket rows of the member
+// table `tab`, -1 = none) into cnt_out[0..K): wave w counts picks w, w + 4, ... eight at a
+// time; a member row streams through the wave in 16-byte lane loads (256 slots per wave
+// load; 64 four-byte loads without vec_rows), counted with ballots. Every thread calls it;
+// cnt_out is complete after the caller's next barrier.
+__device__ __forceinline__ void count_members(const DecodeArgs& a, const int32_t* tab, const int* pick, int* cnt_out,
+                                              int64_t wstart) {
+  const int lane = threadIdx.x & (LSA_WAVE - 1), w = threadIdx.x / LSA_WAVE;
   constexpr int MJ = 8;
-  if (a.spans) {
-    if (w == 0 && lane < a.K) {
-      const int b = sh.pick[lane];
-      const int64_t begin = b > 0 ? ends[b - 1] : 0, end = b >= 0 ? ends[b] : 0;
-      const int64_t lo = begin > a.sink ? begin : a.sink, hi = end < wstart ? end : wstart;
-      sh.cnt[lane] = b >= 0 && hi > lo ? (int)(hi - lo) : 0;
-      sh.first[lane] = (int)lo;
-    }
-  }
-  for (int jb = 0; jb < (a.spans ? 0 : a.K); jb += MJ * LSA_WAVES) {
+  for (int jb = 0; jb < a.K; jb += MJ * LSA_WAVES) {
     int cnt[MJ];
     int b[MJ];
 #pragma unroll
     for (int m = 0; m < MJ; ++m) {
       const int j = jb + m * LSA_WAVES + w;
-      b[m] = j < a.K ? sh.pick[j] : -1;
+      b[m] = j < a.K ? pick[j] : -1;
       cnt[m] = 0;
     }
     const int step = a.vec_rows ? 4 * LSA_WAVE : LSA_WAVE;
@@ -214,9 +200,33 @@ __device__ __forceinline__ void publish_picks(const DecodeArgs& a, SelLds& sh, i
 #pragma unroll
       for (int m = 0; m < MJ; ++m) {
         const int j = jb + m * LSA_WAVES + w;
-        if (j < a.K) sh.cnt[j] = cnt[m];
+        if (j < a.K) cnt_out[j] = cnt[m];
       }
     }
+  }
+}
+
+// The select's last step, once sh.pick[0..K) holds the unit's picks (bucket rows, -1 =
+// none): each pick's kept members are counted, the list length written and the unit's
+// record published (every copy, write-through). Every thread calls it.
+__device__ __forceinline__ void publish_picks(const DecodeArgs& a, SelLds& sh, int64_t i, int64_t t, int64_t position,
+                                              const int32_t* ends) {
+  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
+  // kept members of every pick (sink <= id < window start). Span tables: the range
+  // [ends[b - 1], ends[b]) clipped to [sink, window start), from two ends words. Otherwise
+  // counted from the member rows (count_members)
+  const int32_t* tab = a.members + t * (int64_t)a.rows * a.cap;
+  const int64_t wstart = window_start_of(position, a.window);
+  if (a.spans) {
+    if (w == 0 && lane < a.K) {
+      const int b = sh.pick[lane];
+      const int64_t begin = b > 0 ? ends[b - 1] : 0, end = b >= 0 ? ends[b] : 0;
+      const int64_t lo = begin > a.sink ? begin : a.sink, hi = end < wstart ? end : wstart;
+      sh.cnt[lane] = b >= 0 && hi > lo ? (int)(hi - lo) : 0;
+      sh.first[lane] = (int)lo;
+    }
+  } else {
+    count_members(a, tab, sh.pick, sh.cnt, wstart);
   }
   __syncthreads();
   DECODE_MARK(5);
@@ -763,12 +773,12 @@ __device__ __forceinline__ void poll_and_rank(const DecodeArgs& a, const uint64_
 }
 
 // Reader of the rank form: no record. The unit's select splits publish their columns' keys
-// (+ 1) and every reader ranks them itself: it loads its query rows and the table's span
-// ends, waits (bounded) until all `rows` published keys are nonzero, selects the K best
-// (block_topk_sorted, the last split's selection of the exchange form, on the same keys),
-// turns each pick's span into its kept range and list slots as publish_picks does, and
-// reads its share. Role 0 writes the list length; the last reader clears the published
-// keys. Span tables only.
+// (+ 1) and every reader ranks them itself: it loads its query rows (and a span table's
+// ends), waits (bounded) until all `rows` published keys are nonzero, selects the K best
+// (the last split's selection of the exchange form, on the same keys), counts each pick's
+// kept members (span ends, or the member rows) and their list slots as publish_picks does,
+// and reads its share. Role 0 writes the list length; the last reader clears the published
+// keys.
 template <typename T, int D, int GQ>
 __device__ __forceinline__ void rank_reader(const DecodeArgs& a, char* smem, int64_t i, int role) {
   RdLds<D, GQ>& sh = *(RdLds<D, GQ>*)smem;
@@ -784,15 +794,18 @@ __device__ __forceinline__ void rank_reader(const DecodeArgs& a, char* smem, int
   const int64_t wstart = window_start_of(position, a.window);
   const int64_t n_win = position + 1 - wstart > 0 ? position + 1 - wstart : 0;
   const int64_t n_sink = a.sink < wstart ? a.sink : wstart;
-  const int32_t* ends = a.ends + (r * a.row_tables + g * a.group_tables) * (int64_t)rows;
+  const int64_t t = r * a.row_tables + g * a.group_tables;
   uint64_t* pub = a.pub + i * (int64_t)rows;
   DECODE_MARK(0);
 
-  // the query rows and the span ends go out before the wait
+  // the query rows and (span tables) the span ends go out before the wait
   const T* qrow = (const T*)a.q + (r * a.Hq + (int64_t)g * GQ) * D;
   QueryRegs<T, D, GQ> qr;
   qr.load(qrow, a.scale_log2);
-  for (int m = tid; m < rows; m += LSA_BLOCK) ends_l[m] = ends[m];
+  if (a.spans) {
+    const int32_t* ends = a.ends + t * rows;
+    for (int m = tid; m < rows; m += LSA_BLOCK) ends_l[m] = ends[m];
+  }
 
   // wave 0 polls the published keys (every slot is nonzero once its split has written it)
   // and ranks them in its registers (wave_topk_hist); keys that defeat the histogram cut go
@@ -816,19 +829,34 @@ __device__ __forceinline__ void rank_reader(const DecodeArgs& a, char* smem, int
     return;
   }
   if (!rk.fast) block_topk_sorted(keys, rows, K, a.kp, rk.best, &rk.tks, &rk.st);
-  // each pick's kept range [max(begin, sink), min(end, window start)) and its list slots
+  // the picks (bucket rows, -1 = none); member tables count each pick's kept members from
+  // its member row (count_members, the exchange form's count)
+  const int32_t col = key_column(u_to_key(w == 0 && lane < K ? rk.best[lane] : 0));
+  const int b = (w == 0 && lane < K && col >= 0 && col < rows) ? col : -1;
+  if (!a.spans) {
+    if (w == 0 && lane < K) sh.pick[lane] = b;
+    __syncthreads();
+    count_members(a, a.members + t * (int64_t)rows * a.cap, sh.pick, sh.n, wstart);
+    __syncthreads();
+  }
+  // each pick's kept count (span tables: the range [max(begin, sink), min(end, window
+  // start)) from the span ends) and its list slots
   if (w == 0) {
-    const int32_t col = key_column(u_to_key(lane < K ? rk.best[lane] : 0));
-    const int b = (lane < K && col >= 0 && col < rows) ? col : -1;
-    const int64_t begin = b > 0 ? ends_l[b - 1] : 0, end_b = b >= 0 ? ends_l[b] : 0;
-    const int64_t lo = begin > a.sink ? begin : a.sink, hi = end_b < wstart ? end_b : wstart;
-    const int cnt = b >= 0 && hi > lo ? (int)(hi - lo) : 0;
+    int cnt = 0, first = b;
+    if (a.spans) {
+      const int64_t begin = b > 0 ? ends_l[b - 1] : 0, end_b = b >= 0 ? ends_l[b] : 0;
+      const int64_t lo = begin > a.sink ? begin : a.sink, hi = end_b < wstart ? end_b : wstart;
+      cnt = b >= 0 && hi > lo ? (int)(hi - lo) : 0;
+      first = (int)lo;  // a pick's kept members are consecutive ids from here
+    } else {
+      cnt = lane < K ? sh.n[lane] : 0;
+    }
     const int incl = wave_inclusive_sum(cnt);
     const int end = incl < a.top_k ? incl : a.top_k;
     int prev = dpp_or<kDppWaveShr1>(0, end);  // lane - 1's
     if (lane == 0) prev = 0;
     if (lane < K) {
-      sh.pick[lane] = (int)lo;
+      sh.pick[lane] = first;
       sh.start[lane] = prev;
       sh.n[lane] = end - prev;
     }

@@ -305,7 +305,7 @@ def _select_splits(R: int, G: int, rows: int, top_p: int) -> int:
 def _decode_splits(dtype, D: int, group: int, units: int, rows: int, top_p: int, score_mode: int,
                    table_flags: int) -> int:
     """Select workgroups per (row, kv-head) of the fused decode: the splits of the rank form
-    (span tables that fit it: every split publishes its columns' keys and each reader ranks
+    (tables that fit it: every split publishes its columns' keys and each reader ranks
     them) or of the exchange form (the last split to arrive ranks the keys and publishes the
     picks), or 0 - the replicated form, where every reader selects for itself - when
     ``LSA_DECODE_MODE=rep`` asks for it (or ``auto`` with at most ``LSA_DECODE_REP_UNITS``
@@ -323,7 +323,7 @@ def _decode_splits(dtype, D: int, group: int, units: int, rows: int, top_p: int,
     if os.environ.get("LSA_SELECT_SPLITS") or units >= 256:
         return _select_splits(units, 1, rows, top_p)
     cap = min(rows, 256, max(1, 2048 // max(units, 1)))
-    if table_flags & _abi.TABLE_SPANS and rows <= _RANK_MAX_ROWS and units * rows <= _RANK_MAX_SLOTS:
+    if rows <= _RANK_MAX_ROWS and units * rows <= _RANK_MAX_SLOTS:
         # the rank form (every reader ranks the splits' published keys; no split collects):
         # ~16 columns a split (32k decode, 512 buckets, 24 readers: 18.4 us with 32 splits,
         # 19.0 with 24, 19.1 with 64, 19.7 with 8)
@@ -333,7 +333,7 @@ def _decode_splits(dtype, D: int, group: int, units: int, rows: int, top_p: int,
     return max(1, min(math.ceil(rows / 64), cap))
 
 
-# The fused decode's rank form serves span tables of at most this many buckets, and at most
+# The fused decode's rank form serves tables of at most this many buckets, and at most
 # this many (row, kv-head, bucket) key slots in all (csrc/decode_dev.h kRankMaxRows,
 # kRankMaxSlots); other shapes take the exchange form.
 _RANK_MAX_ROWS = 1024

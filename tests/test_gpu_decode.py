@@ -6,8 +6,8 @@ those lists within the dtype's bar (max-abs / mean-abs vs fp64: fp32 1e-4 / 1e-5
 2e-2 / 2e-3). Cases: the clustered decode geometry up to 32k, positional buckets with
 window and sink tails, top_k cutting a bucket short, fewer visible buckets than picks,
 nothing visible (zeros), batch rows with their own tables and positions, every select
-split count, both hand-off forms (the rank form of span tables: every reader ranks the
-splits' published keys; the exchange form: the last split publishes a record), both
+split count, both hand-off forms (the rank form, span and member tables: every reader ranks the
+splits' published keys; with one split, the select's record), both
 scoring dtypes, and repeated launches (the record or published keys, counters and
 partials are reused and must come back clean).
 """
@@ -87,19 +87,20 @@ def test_clustered_decode_matches_oracle(splits):
                  label=f"clustered splits={splits}")
 
 
-@pytest.mark.parametrize("form", ["rank", "exchange"])
+@pytest.mark.parametrize("form", ["spans", "members"])
 @pytest.mark.parametrize("splits", [48, 100])
 def test_select_splits_past_the_table(form, splits):
     """More select splits than the table's columns fill: with 128 buckets, 48 splits take 3
     columns each and splits 43..47 start past the table (100 splits: 2 columns, 64..99
-    empty). An empty split scores nothing and still publishes (rank form) or arrives
-    (exchange form); its loads stay inside the table. Lists bit-exact vs the oracle."""
+    empty). An empty split scores nothing and still publishes; its loads stay inside the
+    table. Span tables and member tables (the rank form counts the picks' members from
+    their rows). Lists bit-exact vs the oracle."""
     T, Hq, Hkv, D = 8192, 8, 2, 128
     data = workloads.clustered(T, Hq, Hkv, D, n_clusters=128, seed=5, device=DEV)
     buckets = workloads.cluster_buckets(data, target=T // 64)
     rows = buckets.rows
     assert buckets.spans and (splits - 1) * -(-rows // splits) >= rows  # the last split is empty
-    if form == "exchange":
+    if form == "members":
         buckets = dataclasses.replace(buckets, spans=False)
     pos = torch.tensor([T - 1], dtype=torch.int32)
     check_decode(data.q[:, -1:], data.k, data.v, pos, buckets, workloads.FLAT_32K, splits=splits,
@@ -245,27 +246,28 @@ def test_tied_scores_take_the_block_top_k():
         assert torch.equal(lists[0, g, :n].cpu(), torch.arange(n, dtype=torch.int32))
 
 
-@pytest.mark.parametrize("form", ["rank", "exchange"])
+@pytest.mark.parametrize("form", ["rank-spans", "rank-members", "record"])
 def test_give_up_is_reported_and_the_next_launch_is_clean(form):
     """The host makes every reader's bounded wait give up (select workgroups skip
     publishing, a 64-poll limit): all workgroups exit normally, the status word reads 1,
     the next flat_decode call zeroes the counters and raises, and the launch after it is
-    bit-identical to one before the failure. Both hand-off forms: span tables take the rank
-    form (readers wait for the splits' published keys), member tables the exchange form
-    (readers wait for the last split's record)."""
+    bit-identical to one before the failure. Both hand-offs: with two splits the readers
+    wait for the splits' published keys (rank form; span and member tables), with one
+    split for the select's record."""
     from lsa_rocm_lab import _abi
 
     T, Hq, Hkv, D = 4096, 8, 2, 128
     data = workloads.clustered(T, Hq, Hkv, D, n_clusters=64, seed=31, device=DEV)
     buckets = workloads.cluster_buckets(data, target=T // 64)
     assert buckets.spans
-    if form == "exchange":
+    if form == "rank-members":
         buckets = dataclasses.replace(buckets, spans=False)
     config = PortConfig(cluster_block_size=64, bucket_size=64, bucket_cap=256, top_p=16, top_k=4096,
                         window_size=64, sink_size=4)
     q = data.q[:, -1:].contiguous()
     pos = torch.tensor([T - 1], dtype=torch.int32, device=DEV)
-    run = lambda: pipeline.flat_decode(q, data.k, data.v, pos, buckets, config, splits=2)
+    splits = 1 if form == "record" else 2
+    run = lambda: pipeline.flat_decode(q, data.k, data.v, pos, buckets, config, splits=splits)
     good = run()
     torch.cuda.synchronize()
     word = _abi.StatusWord.get(torch.device(DEV))
