@@ -248,9 +248,9 @@ int lsa_read_chunked_mfma_ok(int dtype, int32_t D, int32_t chunk);
  * wait). Such a reader writes nothing and still arrives, so the arrival counters reset,
  * but that launch's outputs are invalid and a record (or published keys) written after the
  * give-up can outlive it: the caller zeroes the counters before the next launch. With
- * LSA_TABLE_SPANS, more than one select split and a table that fits the counters' key
- * slots (at most 1024 buckets, 65 536 (row, kv-head, bucket) slots in all), the splits
- * publish their keys and every reader ranks them itself (the rank form: the same lists).
+ * more than one select split and a table that fits the counters' key slots (at most 1024
+ * buckets, 65 536 (row, kv-head, bucket) slots in all), the splits publish their keys and
+ * every reader ranks them itself (the rank form: the same lists).
  * table_flags: 0, or LSA_TABLE_SPANS when every bucket row j holds exactly the consecutive
  * ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0) in order, -1 after (the contiguous-segment
  * tables): the kept members of a pick are then a range, counted and expanded without
