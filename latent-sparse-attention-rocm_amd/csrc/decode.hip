@@ -282,6 +282,7 @@ int decode_launch(const char* who, const void* q, const void* k, const void* v, 
   LSA_REQUIRE(p.rep || p.kp + rows <= 6144, LSA_ERR_SHAPE,
               "%s: %d columns + %d picks exceed 6144 LDS keys", who, rows, p.kp);
   int nodes_pow2 = 0, beam_pow2 = 0, cand_pow2 = 0, top_pow2 = 0;
+  bool tree_stash = false, tree_kids4 = false;
   if (tree) {
     LSA_REQUIRE(tree->node_centroids && tree->children, LSA_ERR_NULL, "%s: NULL node tables", who);
     LSA_REQUIRE(tree->n_nodes >= 1 && tree->node_size >= 1 && tree->node_block >= 1 && tree->beam_width >= 1,
@@ -301,9 +302,16 @@ int decode_launch(const char* who, const void* q, const void* k, const void* v, 
     beam_pow2 = next_pow2(beam);
     cand_pow2 = next_pow2((int)(cand_cap > 0 ? cand_cap : 1));
     top_pow2 = next_pow2(p.K < cand_pow2 ? p.K : cand_pow2);
-    const size_t sel = sel_keys_offset() + sizeof(uint64_t) * (size_t)((nodes_pow2 > cand_pow2 ? nodes_pow2 : cand_pow2) +
-                                                                      (beam_pow2 > top_pow2 ? beam_pow2 : top_pow2)) +
-                       sizeof(int32_t) * (size_t)cand_pow2 + sizeof(uint32_t) * (size_t)((rows + 31) / 32);
+    size_t sel = sel_keys_offset() + sizeof(uint64_t) * (size_t)((nodes_pow2 > cand_pow2 ? nodes_pow2 : cand_pow2) +
+                                                                (beam_pow2 > top_pow2 ? beam_pow2 : top_pow2)) +
+                 sizeof(int32_t) * (size_t)cand_pow2 + sizeof(uint32_t) * (size_t)((rows + 31) / 32);
+    // the children table and span ends staged in LDS with the first round trip, when they fit
+    const int64_t words = (int64_t)tree->n_nodes * tree->node_size;
+    const size_t stash_end = tree_stash_offset(nodes_pow2, cand_pow2, beam_pow2, top_pow2, rows) +
+                             tree_stash_bytes((int)(words < (1 << 24) ? words : (1 << 24)), rows);
+    tree_stash = words < (1 << 24) && stash_end <= kMaxLds;
+    if (tree_stash) sel = stash_end;
+    tree_kids4 = words % 4 == 0 && (((uintptr_t)tree->children) & 15) == 0;
     const size_t rd = reader_lds_d(D, gq, p.span);
     p.shmem = sel > rd ? sel : rd;
   }
@@ -347,6 +355,8 @@ int decode_launch(const char* who, const void* q, const void* k, const void* v, 
   a.nodes_pow2 = nodes_pow2; a.beam_pow2 = beam_pow2; a.cand_pow2 = cand_pow2; a.top_pow2 = top_pow2;
   a.ends4 = (ends && rows % 4 == 0 && ((uintptr_t)ends % 16) == 0) ? 1 : 0;
   if (tree) a.screen = 0;
+  a.stash = tree_stash ? 1 : 0;
+  a.kids4 = tree_kids4 ? 1 : 0;
   a.scale_log2 = scale * kLog2e;
   a.spin_limit = decode_debug().spin_limit > 0 ? decode_debug().spin_limit
                                               : 1 << 22;  // polls of about a microsecond each: seconds

@@ -61,6 +61,8 @@ struct DecodeArgs {
   const int32_t* children;      // [tables, n_nodes, node_size] bucket rows
   int n_nodes, node_size, node_block, beam;
   int ends4;                    // span ends readable as 16-byte vectors (rows % 4 == 0, aligned)
+  int stash;                    // the tree select stages the children table and span ends in LDS
+  int kids4;                    // the children table readable as 16-byte vectors
   int nodes_pow2, beam_pow2, cand_pow2, top_pow2;
   float scale_log2;
   int spin_limit;
@@ -98,6 +100,21 @@ struct RdLds {
 };
 
 constexpr size_t sel_keys_offset() { return (sizeof(SelLds) + 15) & ~(size_t)15; }
+
+// The tree select's LDS after its keys, picks, candidates and dedup bitmap (laid out in
+// tree_role): where the stashed children table and span ends start, 16-byte aligned.
+__host__ __device__ inline size_t tree_stash_offset(int nodes_pow2, int cand_pow2, int beam_pow2, int top_pow2,
+                                                    int rows) {
+  const size_t keys = (size_t)(nodes_pow2 > cand_pow2 ? nodes_pow2 : cand_pow2);
+  const size_t best = (size_t)(beam_pow2 > top_pow2 ? beam_pow2 : top_pow2);
+  const size_t end = sel_keys_offset() + sizeof(uint64_t) * (keys + best) + sizeof(int32_t) * (size_t)cand_pow2 +
+                     sizeof(uint32_t) * (size_t)((rows + 31) / 32);
+  return (end + 15) & ~(size_t)15;
+}
+// Bytes of the stash: the children table and the span ends, each rounded to 16 bytes.
+__host__ __device__ inline size_t tree_stash_bytes(int words, int rows) {
+  return sizeof(int32_t) * (size_t)(((words + 3) & ~3) + ((rows + 3) & ~3));
+}
 template <int D, int GQ>
 constexpr size_t rd_ids_offset() {
   return (sizeof(RdLds<D, GQ>) + 15) & ~(size_t)15;
@@ -421,6 +438,9 @@ __device__ __forceinline__ void tree_role(const DecodeArgs& a, char* smem, int64
   uint64_t* best = keys + max(a.nodes_pow2, a.cand_pow2);                 // [max(beam_pow2, top_pow2)]
   int32_t* cand = (int32_t*)(best + max(a.beam_pow2, a.top_pow2));        // [cand_pow2]
   uint32_t* seen = (uint32_t*)(cand + a.cand_pow2);                       // [(rows + 31) / 32]
+  int32_t* kids_l = (int32_t*)(smem + tree_stash_offset(a.nodes_pow2, a.cand_pow2, a.beam_pow2, a.top_pow2,
+                                                        a.rows));               // stash: [words] children
+  int32_t* ends_l = kids_l + ((a.n_nodes * a.node_size + 3) & ~3);         // stash: [rows] span ends
   const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
   const int grp = tid >> 4, p = tid & 15;
   const int64_t r = (uint32_t)i / (uint32_t)a.G;
@@ -455,6 +475,14 @@ __device__ __forceinline__ void tree_role(const DecodeArgs& a, char* smem, int64
     const int x = tid + m * LSA_BLOCK;
     ev[m] = x < nvec ? ((const int4*)ends)[x] : make_int4(0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF, 0x7FFFFFFF);
   }
+  // the children table, for the LDS stash (the kept nodes' children then cost no round trip)
+  const int nkv = a.stash && a.kids4 ? words / 4 : 0;
+  int4 kv[kTreeEndVecs];
+#pragma unroll
+  for (int m = 0; m < kTreeEndVecs; ++m) {
+    const int x = tid + m * LSA_BLOCK;
+    kv[m] = nkv > 0 ? ((const int4*)kids)[x < nkv ? x : 0] : make_int4(-1, -1, -1, -1);
+  }
 
   // the index query (group mean, rounded like the unfused select's), the node scores
   float qs[SPAN];
@@ -481,14 +509,32 @@ __device__ __forceinline__ void tree_role(const DecodeArgs& a, char* smem, int64
     for (int m = 0; m < kTreeEndVecs; ++m) {
       nv += ((int64_t)ev[m].x <= lim ? 1 : 0) + ((int64_t)ev[m].y <= lim ? 1 : 0);
       nv += ((int64_t)ev[m].z <= lim ? 1 : 0) + ((int64_t)ev[m].w <= lim ? 1 : 0);
+      const int x = tid + m * LSA_BLOCK;
+      if (a.stash && x < nvec) ((int4*)ends_l)[x] = ev[m];
     }
     for (int x = tid + kTreeEndVecs * LSA_BLOCK; x < nvec; x += LSA_BLOCK) {
       const int4 e = ((const int4*)ends)[x];
       nv += ((int64_t)e.x <= lim ? 1 : 0) + ((int64_t)e.y <= lim ? 1 : 0);
       nv += ((int64_t)e.z <= lim ? 1 : 0) + ((int64_t)e.w <= lim ? 1 : 0);
+      if (a.stash) ((int4*)ends_l)[x] = e;
     }
   } else if (ends) {
-    for (int x = tid; x < a.rows; x += LSA_BLOCK) nv += (int64_t)ends[x] <= lim ? 1 : 0;
+    for (int x = tid; x < a.rows; x += LSA_BLOCK) {
+      const int32_t e = ends[x];
+      nv += (int64_t)e <= lim ? 1 : 0;
+      if (a.stash) ends_l[x] = e;
+    }
+  }
+  if (a.stash) {
+#pragma unroll
+    for (int m = 0; m < kTreeEndVecs; ++m) {
+      const int x = tid + m * LSA_BLOCK;
+      if (x < nkv) ((int4*)kids_l)[x] = kv[m];
+    }
+    for (int x = tid + kTreeEndVecs * LSA_BLOCK; x < nkv; x += LSA_BLOCK) ((int4*)kids_l)[x] = ((const int4*)kids)[x];
+    if (!a.kids4) {
+      for (int x = tid; x < words; x += LSA_BLOCK) kids_l[x] = kids[x];
+    }
   }
   nv = wave_sum(nv);
   __shared__ int vis_lds[LSA_WAVES];
@@ -552,7 +598,7 @@ __device__ __forceinline__ void tree_role(const DecodeArgs& a, char* smem, int64
     int32_t c = -1;
     if (node >= 0 && node < n_nodes) {
       const int x = node * ns + m % ns;
-      c = kids[x];
+      c = a.stash ? kids_l[x] : kids[x];
     }
     c = (c >= 0 && c < visible) ? c : -1;
     const uint32_t bit = 1u << (c & 31);
@@ -574,7 +620,7 @@ __device__ __forceinline__ void tree_role(const DecodeArgs& a, char* smem, int64
   }
   __syncthreads();
   DECODE_MARK(4);
-  publish_picks(a, sh, i, t, position, ends);
+  publish_picks(a, sh, i, t, position, a.stash && ends ? ends_l : ends);
 }
 
 // The reader's work once it holds its unit's picks (sh.pick: a pick's bucket, or its first
