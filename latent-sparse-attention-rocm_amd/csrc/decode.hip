@@ -141,14 +141,16 @@ int64_t record_stride(int64_t units, int K) {
 // workgroups' launch cost more than the shorter gathers save (32k decode, B=1, rank form
 // with 32 select splits: 18.4 us with 24 readers, 18.6 with 16, 19.1 with 32, 20.4 with
 // 40; the record form: 22.5 us with 32, 21.2 with 16 or 24); with many units, enough
-// readers for ~1024 workgroups in all, each streaming a run of tiles through the
-// pipelined gather.
+// readers for ~512 workgroups in all, each streaming a run of tiles through the pipelined
+// gather (B=32 x 32k flat: 82.8 us with 2 readers a unit, 88.4 with 3, 83.5 with 4, 85.6
+// with 6; the B=32 x 131k tree: 76.9 / 83.9 / 78.5 / 81.0).
 constexpr int kDefaultMaxReaders = 24;
+constexpr int kReaderSpread = 512;
 
 int default_readers(int64_t units, int K, int span, int window, int sink) {
   const int64_t tail = ((int64_t)window + sink + span - 1) / span;
   int64_t nr = (int64_t)K + tail;
-  const int64_t spread = (1024 + units - 1) / units;
+  const int64_t spread = (kReaderSpread + units - 1) / units;
   if (spread < nr) nr = spread;
   if (nr > kDefaultMaxReaders) nr = kDefaultMaxReaders;
   if (nr < 1) nr = 1;
