@@ -142,6 +142,24 @@ def test_decode_workspace_sizes():
     assert _abi.size("lsa_decode_flat_counters", 1, 8, 512, 65) == 0  # more than 64 picks is not served
 
 
+def test_rank_form_limits_match_the_library():
+    """pipeline's rank-form limits (the split planner's) are the library's: the counters hold
+    the published keys exactly when rows <= _RANK_MAX_ROWS and (row, kv-head, bucket) slots
+    <= _RANK_MAX_SLOTS."""
+    from lsa_rocm_lab.port import pipeline
+
+    def record_only(R, Hkv, K):
+        units = R * Hkv
+        return 2 * units + 8 * (((units * 2 * K + 1023) // 1024) * 1024 + 64)
+
+    K = 32
+    for R, Hkv, rows in ((16, 8, 512), (17, 8, 512), (1, 8, pipeline._RANK_MAX_ROWS),
+                         (1, 8, pipeline._RANK_MAX_ROWS + 4), (1, 2, 2048)):
+        fits = rows <= pipeline._RANK_MAX_ROWS and R * Hkv * rows <= pipeline._RANK_MAX_SLOTS
+        n = _abi.size("lsa_decode_flat_counters", R, Hkv, rows, K)
+        assert (n > record_only(R, Hkv, K)) == fits, (R, Hkv, rows, n)
+
+
 def test_decode_arguments_rejected_before_launch():
     with pytest.raises(ValueError, match="NULL"):
         _abi.call("lsa_decode_flat", *_decode_args(q=None))
