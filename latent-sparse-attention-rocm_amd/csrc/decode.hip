@@ -99,10 +99,10 @@ size_t rank_lds_d(int D, int gq, int rows) {
 template <int D>
 size_t rep_lds_gq(int gq, int span) {
   switch (gq) {
-    case 1: return rep_ids_offset<D, 1>() + sizeof(int32_t) * (size_t)kChunkTiles * span;
-    case 2: return rep_ids_offset<D, 2>() + sizeof(int32_t) * (size_t)kChunkTiles * span;
-    case 4: return rep_ids_offset<D, 4>() + sizeof(int32_t) * (size_t)kChunkTiles * span;
-    default: return rep_ids_offset<D, 8>() + sizeof(int32_t) * (size_t)kChunkTiles * span;
+    case 1: return rep_ids_offset<D, 1>() + sizeof(int32_t) * (size_t)kRepChunkTiles * span;
+    case 2: return rep_ids_offset<D, 2>() + sizeof(int32_t) * (size_t)kRepChunkTiles * span;
+    case 4: return rep_ids_offset<D, 4>() + sizeof(int32_t) * (size_t)kRepChunkTiles * span;
+    default: return rep_ids_offset<D, 8>() + sizeof(int32_t) * (size_t)kRepChunkTiles * span;
   }
 }
 
@@ -347,6 +347,7 @@ int decode_launch(const char* who, const void* q, const void* k, const void* v, 
   a.S = select_splits; a.cs = select_splits > 0 ? (rows + select_splits - 1) / select_splits : rows;
   a.screen = select_splits == 1 && score_mode == LSA_SCORE_BF16 && screen_pays(D, rows, p.K) ? 1 : 0;
   a.span = p.span; a.NR = p.NR;
+  a.chunk = p.rep ? kRepChunkTiles : kChunkTiles;
   a.tree = tree ? 1 : 0;
   a.node_centroids = tree ? tree->node_centroids : nullptr;
   a.children = tree ? tree->children : nullptr;

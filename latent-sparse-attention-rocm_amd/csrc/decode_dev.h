@@ -55,6 +55,7 @@ struct DecodeArgs {
   int S, cs;           // select splits and columns per split
   int screen;          // S == 1 with bf16 tables that fit screen_topk: the select screens its table
   int span, NR;        // slots per read part, readers per unit
+  int chunk;           // tiles of a reader's id chunk (the LDS holds chunk * span ids)
   // tree select (one workgroup a unit): node level over the bucket table
   int tree;                     // 1: the select role walks a one-level node tree
   const void* node_centroids;   // [tables, n_nodes, D], the centroid type
@@ -628,11 +629,15 @@ __device__ __forceinline__ void tree_role(const DecodeArgs& a, char* smem, int64
 // the unit's list of L = filled + tail slots is cut into tiles of `span` slots, and reader
 // `role` takes a contiguous run of them (the first TT % NR readers one tile more), so only
 // the last tile of a list is partial. The run is expanded into `ids` (and the list) in
-// chunks of up to kChunkTiles tiles and read with the software-pipelined tile loop; then
+// chunks of up to a.chunk tiles and read with the software-pipelined tile loop; then
 // the reader writes its share of the list padding, publishes its split partial and
 // arrives. The last reader of the unit combines the partials and leaves the unit's hand-off
 // words zero for the next launch (`clear`: 1 the record copies, 2 the published keys).
-constexpr int kChunkTiles = 8;
+// Tiles of an id chunk: a reader restarts its gather pipeline once a chunk, so the exchange
+// and rank forms expand whole runs (B=32 x 32k flat 82.1 -> 81.0 us, B=32 x 131k tree
+// 77.3 -> 76.5 with 32 against 8); the replicated form keeps 8 (its LDS holds the table).
+constexpr int kChunkTiles = 32;
+constexpr int kRepChunkTiles = 8;
 
 template <typename T, int D, int GQ>
 __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh, int32_t* ids, int64_t i, int role,
@@ -673,8 +678,8 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
   AttnState<T, D, GQ> st;
   st.clear();
   bool fresh = true;
-  for (int c_lo = lo; c_lo < hi; c_lo += kChunkTiles * span) {
-    const int c_hi = min(hi, c_lo + kChunkTiles * span);
+  for (int c_lo = lo; c_lo < hi; c_lo += a.chunk * span) {
+    const int c_hi = min(hi, c_lo + a.chunk * span);
     const int n = c_hi - c_lo;
     if (a.spans) {  // a pick's kept members are consecutive ids from the record's first one
       for (int k = tid; k < n; k += LSA_BLOCK) {
