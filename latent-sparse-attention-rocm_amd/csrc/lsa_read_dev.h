@@ -214,12 +214,12 @@ struct AttnState {
 // so a masked token's weight is already 0 there. The state leaves in the layout of the
 // other instances (m uniform, l and acc per token group).
 //
-// With PIPE, spans of three tiles or more are software-pipelined: tile t + 1's K/V loads are issued
+// With PIPE, spans of two tiles or more are software-pipelined: tile t + 1's K/V loads are issued
 // before tile t is computed, and each lane's slot id is fetched two tiles ahead, ahead of
 // the loads it does not feed (memory counters retire in order, so a wait for an id must
 // not also wait for the rows in flight). The V side's ids come from the K side's by lane
-// permutes. Past the span the slots read -1: those rows load token 0 (cache hits) and
-// weigh nothing.
+// permutes. Slots past the span read -1 (a partial last tile): those rows load token 0
+// (cache hits) and weigh nothing.
 template <typename T, int D, int GQ>
 struct MfmaTile {
   static constexpr int NM = D / 32;
@@ -310,18 +310,22 @@ __device__ __forceinline__ void attend_tiles_mfma(const QueryRegs<T, D, GQ>& q, 
   };
 
   MfmaTile<T, D, GQ> cur;
-  if (PIPE && hi - lo > 2 * NT) {  // pipelined
+  if (PIPE && hi - lo > NT) {  // pipelined
     int32_t id1 = id_of(lo + s0);
     int32_t id2 = id_of(lo + NT + s0);
     issue(id1, cur);
     id1 = id2;
     for (int base = lo; base < hi; base += NT) {
-      id2 = id_of(base + 2 * NT + s0);  // ids two tiles ahead, before the rows they do not feed
-      MfmaTile<T, D, GQ> nxt;
-      issue(id1, nxt);
-      compute(cur);
-      cur = nxt;
-      id1 = id2;
+      if (base + NT < hi) {  // uniform: a next tile
+        id2 = id_of(base + 2 * NT + s0);  // ids two tiles ahead, before the rows they do not feed
+        MfmaTile<T, D, GQ> nxt;
+        issue(id1, nxt);
+        compute(cur);
+        cur = nxt;
+        id1 = id2;
+      } else {
+        compute(cur);
+      }
     }
   } else {
     int32_t id1 = id_of(lo + s0);
