@@ -287,27 +287,6 @@ __device__ __forceinline__ void bitonic_sort_desc(uint64_t* a, int n) {
   }
 }
 
-// Sorts 64 values held one per lane descending across the wave (lane 0 = largest).
-__device__ __forceinline__ uint64_t wave_sort64_desc(uint64_t v) {
-  const int lane = threadIdx.x & (LSA_WAVE - 1);
-#pragma unroll
-  for (int size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      uint32_t lo32 = (uint32_t)v, hi32 = (uint32_t)(v >> 32);
-      uint32_t olo = __shfl_xor(lo32, stride, LSA_WAVE), ohi = __shfl_xor(hi32, stride, LSA_WAVE);
-      uint64_t o = ((uint64_t)ohi << 32) | olo;
-      bool desc = ((lane & size) == 0);
-      bool lower = ((lane & stride) == 0);
-      // in a descending block the lower lane keeps the max
-      bool keep_max = (lower == desc);
-      uint64_t mx = v > o ? v : o, mn = v > o ? o : v;
-      v = keep_max ? mx : mn;
-    }
-  }
-  return v;
-}
-
 // ---------------------------------------------------------------- cross-workgroup exchange
 
 // Values handed between workgroups that may sit on different XCDs (whose L2s are not

@@ -16,7 +16,7 @@
 //     canonical K-th best score is >= L and every row of the canonical top-K has hi >= L.
 //     L is the lower edge of a 256-bin histogram of lo; the candidates are the rows whose
 //     hi falls in that bin or above (a superset of hi >= L: the bin map is monotone).
-//  3. the candidates (usually K plus a few) get the canonical score and one wave sorts
+//  3. the candidates (usually K plus a few) get the canonical score and one wave ranks
 //     their packed keys; the best K are the canonical top-K, ties to the lower bucket.
 // Non-finite screens or more than 64 candidates take the exact path for every row.
 #pragma once
@@ -223,7 +223,7 @@ __device__ __forceinline__ void screen_topk(const float* qs, const bf16_t* cent,
 
   if (!slow) {
     // 3. canonical scores of the candidates (16 lanes a row, 16 rows a pass); one wave
-    // sorts their keys
+    // ranks their keys
     const int nc = ex.ncand;
     for (int jb = 0; jb < nc; jb += LSA_BLOCK / 16) {
       const int jj = jb + (tid >> 4);
@@ -239,9 +239,16 @@ __device__ __forceinline__ void screen_topk(const float* qs, const bf16_t* cent,
     }
     __syncthreads();
     if (w == 0) {
-      uint64_t v = lane < nc ? ex.ckey[lane] : 0;
-      v = wave_sort64_desc(v);
-      if (lane < kp) out[lane] = lane < K ? v : 0;
+      // each candidate's rank among the nc keys (read back from LDS, a broadcast a step; a
+      // tie goes to the lower slot), then the K best in rank order, zeros up to kp
+      const uint64_t v = lane < nc ? ex.ckey[lane] : 0;
+      int rank = 0;
+      for (int j = 0; j < nc; ++j) {
+        const uint64_t o = ex.ckey[j];
+        rank += (o > v || (o == v && j < lane)) ? 1 : 0;
+      }
+      if (lane < nc && rank < kp) out[rank] = rank < K ? v : 0;
+      if (lane >= nc && lane < kp) out[lane] = 0;
     }
   } else {
     // the canonical score of every visible candidate, then the block top-K
