@@ -166,13 +166,10 @@ __device__ __forceinline__ void screen_topk(const float* qs, const bf16_t* cent,
     mx = live ? fmaxf(mx, x) : mx;
     cnt += live ? 1 : 0;
   }
-#pragma unroll
-  for (int x = LSA_WAVE / 2; x >= 1; x >>= 1) {
-    mn = fminf(mn, __shfl_xor(mn, x, LSA_WAVE));
-    mx = fmaxf(mx, __shfl_xor(mx, x, LSA_WAVE));
-    cnt += __shfl_xor(cnt, x, LSA_WAVE);
-    bad |= __shfl_xor(bad, x, LSA_WAVE);
-  }
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  cnt = wave_sum(cnt);
+  bad = wave_or(bad);
   if (lane == 0) { ex.wmin[w] = mn; ex.wmax[w] = mx; ex.wcnt[w] = cnt; ex.wbad[w] = bad; }
   __syncthreads();
   mn = fminf(fminf(ex.wmin[0], ex.wmin[1]), fminf(ex.wmin[2], ex.wmin[3]));
@@ -210,12 +207,18 @@ __device__ __forceinline__ void screen_topk(const float* qs, const bf16_t* cent,
     cut = ex.cut;
   }
   if (!slow) {
-    for (int j = tid; j < n; j += LSA_BLOCK) {
-      const float x = ex.hi[j];
-      if (x != -INFINITY && (cnt <= K || bin_of(x) >= cut)) {
-        const int slot = atomicAdd(&ex.ncand, 1);
-        if (slot < kScreenMaxCand) ex.cand[slot] = j;
-      }
+    const uint64_t below = (1ull << lane) - 1ull;
+    for (int j0 = w * LSA_WAVE; j0 < n; j0 += LSA_BLOCK) {  // one LDS atomic a wave and pass
+      const int j = j0 + lane;
+      const float x = j < n ? ex.hi[j] : -INFINITY;
+      const bool take = x != -INFINITY && (cnt <= K || bin_of(x) >= cut);
+      const uint64_t m = __ballot(take);
+      if (m == 0) continue;  // wave-uniform
+      int base = 0;
+      if (lane == 0) base = atomicAdd(&ex.ncand, (int)__popcll(m));
+      base = __builtin_amdgcn_readfirstlane(base);
+      const int slot = base + (int)__popcll(m & below);
+      if (take && slot < kScreenMaxCand) ex.cand[slot] = j;
     }
     __syncthreads();
     slow = ex.ncand > kScreenMaxCand;
