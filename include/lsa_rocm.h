@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define LSA_ABI_VERSION 2
+#define LSA_ABI_VERSION 3
 
 enum lsa_status {
   LSA_OK = 0,
@@ -45,6 +45,23 @@ enum lsa_status {
 enum lsa_dtype { LSA_F32 = 0, LSA_BF16 = 1, LSA_F16 = 2 };
 enum lsa_score_mode { LSA_SCORE_BF16 = 0, LSA_SCORE_F32 = 1 };
 enum lsa_centroid_mode { LSA_CENTROID_MEAN = 0, LSA_CENTROID_NORMALIZED = 1, LSA_CENTROID_SUM = 2 };
+
+/* A paged K/V cache's slot table (upstream's paged decode: the reference's expansion kernel
+ * maps every kept id and the window/sink tail through a slot table, select_fused.py:147-205
+ * `slot_table_ptr` / `slot_rows_ptr` / `MAP_SLOTS`). Logical position p of query row r lives
+ * in physical cache row table[rows[r] * stride + p]. The selects and the fused decode apply
+ * the map where they write a read list - once per listed id - so lists hold physical rows
+ * and the gather reads them with no extra load; which ids are kept (sink <= id < window
+ * start, top_k) is decided on the logical positions, as the reference does. The chunked
+ * prefill read maps its causal block the same way (its chunk lists are already physical).
+ * Passed as `const lsa_slot_map*`; NULL means ids are cache rows (no paging). */
+typedef struct lsa_slot_map {
+  const int32_t* table; /* [n_rows, stride] int32 physical cache rows (-1: no row) */
+  const int32_t* rows;  /* [R] int32: the table row of each query row (decode: batch row) */
+  int64_t stride;       /* elements between table rows, >= width */
+  int32_t width;        /* logical positions a table row maps (>= 1); ids at or past it map to -1 */
+  int32_t n_rows;       /* table rows; a row index outside [0, n_rows) maps every id to -1 */
+} lsa_slot_map;
 
 int lsa_abi_version(void);
 const char* lsa_last_error(void);
@@ -87,7 +104,8 @@ int lsa_unpack_ids(const int64_t* keys, int64_t n, int32_t* ids, void* stream);
  * and lengths [R, G] int32. */
 int lsa_expand(const void* picks, int picks_are_keys, int64_t R, int32_t G, int32_t P, const int32_t* members,
                int32_t rows, int32_t cap, int64_t row_tables, int64_t group_tables, const int32_t* positions,
-               int32_t window, int32_t sink, int32_t top_k, int32_t* lists, int32_t* lengths, void* stream);
+               const lsa_slot_map* slots, int32_t window, int32_t sink, int32_t top_k, int32_t* lists,
+               int32_t* lengths, void* stream);
 
 /* Fused flat select: score + top-k + expansion in one launch (reference pipeline.py:
  * 274-316 flat_select, LSA_SELECT_IMPL=fused). queries [R, G, D]; tables as above
@@ -103,10 +121,10 @@ size_t lsa_select_flat_scratch_bytes(int64_t R, int32_t G, int32_t top_p, int32_
 int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D, const void* centroids,
                     const int32_t* members, const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap,
                     int64_t row_tables,
-                    int64_t group_tables, int score_mode, const int32_t* positions, int32_t cluster_block_size,
-                    int32_t block_buckets, int32_t top_p, int32_t window, int32_t sink, int32_t top_k,
-                    int32_t splits, int32_t* counters, void* scratch, size_t scratch_bytes, int32_t* lists,
-                    int32_t* lengths, void* stream);
+                    int64_t group_tables, int score_mode, const int32_t* positions, const lsa_slot_map* slots,
+                    int32_t cluster_block_size, int32_t block_buckets, int32_t top_p, int32_t window, int32_t sink,
+                    int32_t top_k, int32_t splits, int32_t* counters, void* scratch, size_t scratch_bytes,
+                    int32_t* lists, int32_t* lengths, void* stream);
 
 /* Two-level tree select (reference pipeline.py:319-337 tree_select, _tree.py:318-373
  * _beam_pick_rows with one node level, _tree.py:100-142 _growth_replay): per (row, group)
@@ -121,9 +139,10 @@ int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int32_t G, int3
 int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D, const void* node_centroids,
                     const int32_t* children, int32_t n_nodes, int32_t node_size, const void* centroids,
                     const int32_t* members, const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables,
-                    int64_t group_tables, int score_mode, const int32_t* positions, int32_t cluster_block_size,
-                    int32_t block_buckets, int32_t node_block, int32_t beam_width, int32_t top_p, int32_t window,
-                    int32_t sink, int32_t top_k, int32_t* lists, int32_t* lengths, void* stream);
+                    int64_t group_tables, int score_mode, const int32_t* positions, const lsa_slot_map* slots,
+                    int32_t cluster_block_size, int32_t block_buckets, int32_t node_block, int32_t beam_width,
+                    int32_t top_p, int32_t window, int32_t sink, int32_t top_k, int32_t* lists, int32_t* lengths,
+                    void* stream);
 
 /* Multi-level beam select (reference pipeline.py:319-337 tree_select over a hierarchy of
  * several node levels: _tree.py:318-373 _beam_pick_rows, _tree.py:306-315 _dedup_scores,
@@ -148,8 +167,9 @@ int lsa_select_beam(const void* queries, int q_dtype, int64_t R, int32_t G, int3
                     int32_t node_size, int32_t node_block, int32_t top_level, const void* centroids,
                     const int32_t* members, const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap,
                     int64_t row_tables, int64_t group_tables, int score_mode, const int32_t* positions,
-                    int32_t cluster_block_size, int32_t block_buckets, int32_t beam_width, int32_t top_p,
-                    int32_t window, int32_t sink, int32_t top_k, int32_t* lists, int32_t* lengths, void* stream);
+                    const lsa_slot_map* slots, int32_t cluster_block_size, int32_t block_buckets,
+                    int32_t beam_width, int32_t top_p, int32_t window, int32_t sink, int32_t top_k, int32_t* lists,
+                    int32_t* lengths, void* stream);
 
 /* GQA-collapsed index queries (reference gates.py:50-59 make_index_space, per-kv-head
  * form): out [B, T/chunk, Hkv, D] fp32 = fp32 mean of q [B, T, Hq, D] over each
@@ -175,13 +195,17 @@ int lsa_bucket_centroids(const void* keys, int k_dtype, int64_t tokens, int64_t 
  * merges past max_size positions skipped) until `target` segments remain. starts
  * [B * Hkv, target + 1] int32 receives each table's segment start positions (last = T);
  * status [B * Hkv] int32 receives 0, or 1 where no pair could merge before the target
- * (that table's starts are then unset). scratch: lsa_ward_segments_scratch_bytes bytes of
- * device memory. Limits: ceil(T / pool) <= 4096 pools, target <= pools, max_size >= pool,
+ * (that table's starts are then the even cut floor(j * T / target), so every later kernel
+ * reads valid positions). failed (nullable; device or pinned host memory) is set to 1 with
+ * a system-scope store when any table fails, so a caller learns of it without a device sync
+ * (it is never cleared here). scratch: lsa_ward_segments_scratch_bytes bytes of device
+ * memory. Limits: ceil(T / pool) <= 4096 pools, target <= pools, max_size >= pool,
  * D <= 1024. */
 size_t lsa_ward_segments_scratch_bytes(int64_t tables, int64_t T, int32_t D, int32_t pool);
 int lsa_ward_segments(const void* keys, int k_dtype, int64_t B, int64_t T, int32_t kv_heads, int32_t D,
                       int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int32_t pool, int32_t target, int32_t max_size,
-                      void* scratch, size_t scratch_bytes, int32_t* starts, int32_t* status, void* stream);
+                      void* scratch, size_t scratch_bytes, int32_t* starts, int32_t* status, int32_t* failed,
+                      void* stream);
 
 /* Sparse gather read (reference read_kernel_tiled.py:30-156 sparse_read_auto / tiled,
  * read_kernel.py:26-120 v1): q [B, Tq, Hq, D] dense; k/v [B, Tk, Hkv, D] (dtype) with the
@@ -215,7 +239,7 @@ int lsa_read(const void* q, const void* k, const void* v, int dtype, int64_t B, 
 int lsa_read_chunked(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t T, int64_t Tk,
                      int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride,
                      int64_t kv_head_stride, const int32_t* ids, const int32_t* lengths, int32_t W, int32_t chunk,
-                     float scale, int32_t path, void* out, void* stream);
+                     const lsa_slot_map* slots, float scale, int32_t path, void* out, void* stream);
 /* 1 when the MFMA tile kernel serves lsa_read_chunked for this shape: bf16/fp16 rows, head
  * dim 64 or 128, chunk in {16, 32, 64, 128, 256}. */
 int lsa_read_chunked_mfma_ok(int dtype, int32_t D, int32_t chunk);
@@ -269,10 +293,10 @@ int lsa_decode_flat(const void* q, const void* k, const void* v, int dtype, int6
                     const void* centroids, const int32_t* members, const int32_t* ends, int32_t table_flags,
                     int32_t rows, int32_t cap,
                     int64_t row_tables, int64_t group_tables, int score_mode, const int32_t* positions,
-                    int32_t cluster_block_size, int32_t block_buckets, int32_t top_p, int32_t window, int32_t sink,
-                    int32_t top_k, float scale, int32_t select_splits, int32_t readers, int32_t* counters,
-                    int64_t n_counters, void* scratch, size_t scratch_bytes, int32_t* lists, int32_t* lengths,
-                    void* out, int32_t* status, void* stream);
+                    const lsa_slot_map* slots, int32_t cluster_block_size, int32_t block_buckets, int32_t top_p,
+                    int32_t window, int32_t sink, int32_t top_k, float scale, int32_t select_splits,
+                    int32_t readers, int32_t* counters, int64_t n_counters, void* scratch, size_t scratch_bytes,
+                    int32_t* lists, int32_t* lengths, void* out, int32_t* status, void* stream);
 
 /* The fused decode step over a one-level node tree (reference port/bench.py:147-153 with
  * tree_select for flat_select: pipeline.py:319-337, _tree.py:318-373 with one node level,
@@ -288,10 +312,11 @@ int lsa_decode_tree(const void* q, const void* k, const void* v, int dtype, int6
                     const void* node_centroids, const int32_t* children, int32_t n_nodes, int32_t node_size,
                     int32_t node_block, int32_t beam_width, const void* centroids, const int32_t* members,
                     const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables,
-                    int64_t group_tables, int score_mode, const int32_t* positions, int32_t cluster_block_size,
-                    int32_t block_buckets, int32_t top_p, int32_t window, int32_t sink, int32_t top_k, float scale,
-                    int32_t readers, int32_t* counters, int64_t n_counters, void* scratch, size_t scratch_bytes,
-                    int32_t* lists, int32_t* lengths, void* out, int32_t* status, void* stream);
+                    int64_t group_tables, int score_mode, const int32_t* positions, const lsa_slot_map* slots,
+                    int32_t cluster_block_size, int32_t block_buckets, int32_t top_p, int32_t window, int32_t sink,
+                    int32_t top_k, float scale, int32_t readers, int32_t* counters, int64_t n_counters,
+                    void* scratch, size_t scratch_bytes, int32_t* lists, int32_t* lengths, void* out,
+                    int32_t* status, void* stream);
 
 /* lsa_decode_flat without caller buffers, for callers that cannot allocate (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart
@@ -300,8 +325,10 @@ int lsa_decode_tree(const void* q, const void* k, const void* v, int dtype, int6
  * LSA_ERR_WORKSPACE. The library never allocates on this path. The first call on a device
  * clears the counters with a fill kernel on `stream`; every launch leaves them zero.
  * Calls share the device's array and keep its last contents: calls that overlap on one
- * GPU race and must not. reset_counters != 0 clears the counters first (after a launch
- * that set *status). Arguments and outputs otherwise as lsa_decode_flat. */
+ * GPU race and must not. reset_counters != 0 clears the whole 1 MiB counters region first
+ * (after a launch that set *status: a late select workgroup of that launch may have left
+ * keys anywhere its own shape reached). No slot map: the cache is not paged here. Arguments
+ * and outputs otherwise as lsa_decode_flat. */
 int lsa_decode_flat_noalloc(const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk,
                             int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride,
                             int64_t kv_head_stride, const void* centroids, const int32_t* members,

@@ -44,6 +44,7 @@ struct BeamArgs {
   int spans;   // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0), top_p <= 64
   int screen;  // bf16 tables of a head dim screen_topk serves
   int cand_pow2, beam_pow2, top_pow2, carry_cap;
+  SlotMap slots;  // a paged cache's slot table (table == nullptr: none)
   int32_t* lists;
   int32_t* lengths;
 };
@@ -170,15 +171,16 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_beam_kernel(const QT* q, boo
   for (int j = threadIdx.x; j < a.top_p; j += LSA_BLOCK) cand[j] = j < K0 ? key_column(u_to_key(best[j])) : -1;
   __syncthreads();
   const int width = a.top_k + a.window + a.sink;
+  const SlotRow map = slot_row_of(a.slots, r);
   int len;
   if (a.spans) {  // span tables: kept ids from the picks' span ends, no member rows
     __shared__ int span_lds[2 * LSA_WAVE + 1];
     len = expand_spans(cand, a.top_p, a.ends + t * a.rows, a.rows, position, a.window, a.sink, a.top_k,
-                       a.lists + i * width, width, span_lds);
+                       a.lists + i * width, width, span_lds, map);
   } else {
     const int32_t* tab = a.members + t * (int64_t)a.rows * a.cap;
     len = expand_walk(cand, a.top_p, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k, a.lists + i * width,
-                      width, scan, nullptr);
+                      width, scan, nullptr, map);
   }
   if (threadIdx.x == 0) a.lengths[i] = len;
 }
@@ -191,12 +193,14 @@ extern "C" int lsa_select_beam(const void* queries, int q_dtype, int64_t R, int3
                                const void* centroids, const int32_t* members, const int32_t* ends,
                                int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables,
                                int64_t group_tables, int score_mode, const int32_t* positions,
-                               int32_t cluster_block_size, int32_t block_buckets, int32_t beam_width, int32_t top_p,
-                               int32_t window, int32_t sink, int32_t top_k, int32_t* lists, int32_t* lengths,
-                               void* stream) {
+                               const lsa_slot_map* slots, int32_t cluster_block_size, int32_t block_buckets,
+                               int32_t beam_width, int32_t top_p, int32_t window, int32_t sink, int32_t top_k,
+                               int32_t* lists, int32_t* lengths, void* stream) {
   LSA_REQUIRE(queries && node_centroids && children && n_nodes && centroids && members && positions && lists &&
                   lengths,
               LSA_ERR_NULL, "lsa_select_beam: NULL pointer");
+  SlotMap sm;
+  LSA_TRY(check_slots("lsa_select_beam", slots, &sm));
   LSA_TRY(check_dtype(q_dtype));
   LSA_TRY(check_dim(D));
   LSA_TRY(check_tables(rows, cap, row_tables, group_tables));
@@ -261,7 +265,7 @@ extern "C" int lsa_select_beam(const void* queries, int q_dtype, int64_t R, int3
   a.beam_pow2 = next_pow2(beam_width < a.cand_pow2 ? beam_width : a.cand_pow2);
   a.top_pow2 = next_pow2(top_p < a.cand_pow2 ? top_p : a.cand_pow2);
   a.carry_cap = (beam_width < a.cand_pow2 ? beam_width : a.cand_pow2) * node_size;
-  a.lists = lists; a.lengths = lengths;
+  a.lists = lists; a.lengths = lengths; a.slots = sm;
   const int best_slots = a.beam_pow2 > a.top_pow2 ? a.beam_pow2 : a.top_pow2;
   const int cand_slots = a.cand_pow2 > top_p ? a.cand_pow2 : top_p;
   const size_t shmem = sizeof(uint64_t) * (size_t)(a.cand_pow2 + best_slots) +

@@ -80,7 +80,8 @@ __device__ double pair_cost(const double* sa, const double* sb, int na, int nb, 
 // first pool; cost[i] is the cost of segment i with the segment after it.
 __global__ __launch_bounds__(kMergeThreads) void ward_merge_kernel(double* sums, int64_t T, int D, int pool,
                                                                    int npool, int target, int max_size,
-                                                                   int32_t* starts, int32_t* status) {
+                                                                   int32_t* starts, int32_t* status,
+                                                                   int32_t* failed_any) {
   __shared__ double cost[kMaxPools];
   __shared__ int size[kMaxPools];
   __shared__ int nxt[kMaxPools];
@@ -171,17 +172,23 @@ __global__ __launch_bounds__(kMergeThreads) void ward_merge_kernel(double* sums,
     __syncthreads();
     --alive;
   }
+  int32_t* out = starts + table * (int64_t)(target + 1);
+  if (failed) {
+    // the even cut: valid, increasing positions for every kernel that reads the table later
+    for (int r = tid; r < target; r += kMergeThreads) out[r] = (int32_t)((int64_t)r * T / target);
+  }
   if (tid == 0) {
     status[table] = failed;
-    int32_t* out = starts + table * (int64_t)(target + 1);
     if (!failed) {
       int p = 0;
       for (int r = 0; r < target; ++r) {
         out[r] = p * pool;
         p = nxt[p];
       }
-      out[target] = (int32_t)T;
+    } else if (failed_any) {  // system scope: the word may live in pinned host memory
+      __hip_atomic_store(failed_any, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
+    out[target] = (int32_t)T;
   }
 }
 
@@ -196,7 +203,7 @@ extern "C" size_t lsa_ward_segments_scratch_bytes(int64_t tables, int64_t T, int
 extern "C" int lsa_ward_segments(const void* keys, int k_dtype, int64_t B, int64_t T, int32_t kv_heads, int32_t D,
                                  int64_t kv_sb, int64_t kv_st, int64_t kv_sh, int32_t pool, int32_t target,
                                  int32_t max_size, void* scratch, size_t scratch_bytes, int32_t* starts,
-                                 int32_t* status, void* stream) {
+                                 int32_t* status, int32_t* failed, void* stream) {
   LSA_REQUIRE(keys && scratch && starts && status, LSA_ERR_NULL, "lsa_ward_segments: NULL pointer");
   LSA_REQUIRE(k_dtype == LSA_F32 || k_dtype == LSA_BF16 || k_dtype == LSA_F16, LSA_ERR_DTYPE,
               "lsa_ward_segments: dtype %d", k_dtype);
@@ -225,7 +232,7 @@ extern "C" int lsa_ward_segments(const void* keys, int k_dtype, int64_t B, int64
   })
   LSA_LAUNCHED("lsa_ward_segments (pool sums)");
   ward_merge_kernel<<<dim3((unsigned)tables), kMergeThreads, 0, s>>>(sums, T, D, pool, (int)npool, target, max_size,
-                                                                     starts, status);
+                                                                     starts, status, failed);
   LSA_LAUNCHED("lsa_ward_segments (merge)");
   return LSA_OK;
 }

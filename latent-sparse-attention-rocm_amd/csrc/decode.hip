@@ -232,12 +232,15 @@ int decode_launch(const char* who, const void* q, const void* k, const void* v, 
                   int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride,
                   int64_t kv_head_stride, const void* centroids, const int32_t* members, const int32_t* ends,
                   int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables, int64_t group_tables,
-                  int score_mode, const int32_t* positions, int32_t cluster_block_size, int32_t block_buckets,
-                  int32_t top_p, int32_t window, int32_t sink, int32_t top_k, float scale, int32_t select_splits,
-                  int32_t readers, int32_t* counters, int64_t n_counters, void* scratch, size_t scratch_bytes,
-                  int32_t* lists, int32_t* lengths, void* out, int32_t* status, void* stream, const TreeSpec* tree) {
+                  int score_mode, const int32_t* positions, const lsa_slot_map* slots, int32_t cluster_block_size,
+                  int32_t block_buckets, int32_t top_p, int32_t window, int32_t sink, int32_t top_k, float scale,
+                  int32_t select_splits, int32_t readers, int32_t* counters, int64_t n_counters, void* scratch,
+                  size_t scratch_bytes, int32_t* lists, int32_t* lengths, void* out, int32_t* status, void* stream,
+                  const TreeSpec* tree) {
   LSA_REQUIRE(q && k && v && centroids && members && positions && lists && lengths && out && counters, LSA_ERR_NULL,
               "%s: NULL pointer", who);
+  SlotMap sm;
+  LSA_TRY(check_slots(who, slots, &sm));
   LSA_REQUIRE(dtype == LSA_F32 || dtype == LSA_BF16 || dtype == LSA_F16, LSA_ERR_DTYPE,
               "%s: dtype %d", who, dtype);
   LSA_REQUIRE(D == 32 || D == 64 || D == 128 || D == 256, LSA_ERR_SHAPE,
@@ -373,6 +376,7 @@ int decode_launch(const char* who, const void* q, const void* k, const void* v, 
   a.ws_keys = p.keys_bytes ? (uint64_t*)scratch : nullptr;
   a.ws_part = p.part_bytes ? (float*)((char*)scratch + keys_at) : nullptr;
   a.lists = lists; a.lengths = lengths; a.status = status;
+  a.slots = sm;
   const dim3 g3((unsigned)grid);
   hipStream_t s = (hipStream_t)stream;
   const bool bf16 = score_mode == LSA_SCORE_BF16;
@@ -390,13 +394,15 @@ extern "C" int lsa_decode_flat(const void* q, const void* k, const void* v, int 
                                int64_t kv_head_stride, const void* centroids, const int32_t* members,
                                const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables,
                                int64_t group_tables, int score_mode, const int32_t* positions,
-                               int32_t cluster_block_size, int32_t block_buckets, int32_t top_p, int32_t window,
-                               int32_t sink, int32_t top_k, float scale, int32_t select_splits, int32_t readers,
-                               int32_t* counters, int64_t n_counters, void* scratch, size_t scratch_bytes,
-                               int32_t* lists, int32_t* lengths, void* out, int32_t* status, void* stream) {
+                               const lsa_slot_map* slots, int32_t cluster_block_size, int32_t block_buckets,
+                               int32_t top_p, int32_t window, int32_t sink, int32_t top_k, float scale,
+                               int32_t select_splits, int32_t readers, int32_t* counters, int64_t n_counters,
+                               void* scratch, size_t scratch_bytes, int32_t* lists, int32_t* lengths, void* out,
+                               int32_t* status, void* stream) {
   return decode_launch("lsa_decode_flat", q, k, v, dtype, R, Tk, Hq, Hkv, D, kv_batch_stride, kv_token_stride,
                        kv_head_stride, centroids, members, ends, table_flags, rows, cap, row_tables, group_tables,
-                       score_mode, positions, cluster_block_size, block_buckets, top_p, window, sink, top_k, scale,
+                       score_mode, positions, slots, cluster_block_size, block_buckets, top_p, window, sink, top_k,
+                       scale,
                        select_splits, readers, counters, n_counters, scratch, scratch_bytes, lists, lengths, out,
                        status, stream, nullptr);
 }
@@ -408,14 +414,16 @@ extern "C" int lsa_decode_tree(const void* q, const void* k, const void* v, int 
                                const void* centroids, const int32_t* members, const int32_t* ends,
                                int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables,
                                int64_t group_tables, int score_mode, const int32_t* positions,
-                               int32_t cluster_block_size, int32_t block_buckets, int32_t top_p, int32_t window,
-                               int32_t sink, int32_t top_k, float scale, int32_t readers, int32_t* counters,
-                               int64_t n_counters, void* scratch, size_t scratch_bytes, int32_t* lists,
-                               int32_t* lengths, void* out, int32_t* status, void* stream) {
+                               const lsa_slot_map* slots, int32_t cluster_block_size, int32_t block_buckets,
+                               int32_t top_p, int32_t window, int32_t sink, int32_t top_k, float scale,
+                               int32_t readers, int32_t* counters, int64_t n_counters, void* scratch,
+                               size_t scratch_bytes, int32_t* lists, int32_t* lengths, void* out, int32_t* status,
+                               void* stream) {
   const TreeSpec tree{node_centroids, children, n_nodes, node_size, node_block, beam_width};
   return decode_launch("lsa_decode_tree", q, k, v, dtype, R, Tk, Hq, Hkv, D, kv_batch_stride, kv_token_stride,
                        kv_head_stride, centroids, members, ends, table_flags, rows, cap, row_tables, group_tables,
-                       score_mode, positions, cluster_block_size, block_buckets, top_p, window, sink, top_k, scale, 1,
+                       score_mode, positions, slots, cluster_block_size, block_buckets, top_p, window, sink, top_k,
+                       scale, 1,
                        readers, counters, n_counters, scratch, scratch_bytes, lists, lengths, out, status, stream,
                        &tree);
 }

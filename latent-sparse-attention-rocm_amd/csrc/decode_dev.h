@@ -80,6 +80,7 @@ struct DecodeArgs {
   int32_t* lengths;    // [units]
   int32_t* status;     // optional: set to 1 by a reader whose wait timed out (system scope:
                        // the word may live in pinned host memory)
+  SlotMap slots;       // a paged cache's slot table (table == nullptr: ids are cache rows)
 };
 
 struct SelLds {
@@ -639,9 +640,13 @@ __device__ __forceinline__ void tree_role(const DecodeArgs& a, char* smem, int64
 constexpr int kChunkTiles = 32;
 constexpr int kRepChunkTiles = 8;
 
+// `map` turns a logical position into its cache row (a paged cache's slot table row of the
+// unit's query row, loaded by the caller before its wait; the identity without one): the
+// list and the gather hold mapped ids, while which ids are kept was decided on positions.
 template <typename T, int D, int GQ>
 __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh, int32_t* ids, int64_t i, int role,
-                                           const QueryRegs<T, D, GQ>& qr, int64_t position, int clear) {
+                                           const QueryRegs<T, D, GQ>& qr, int64_t position, int clear,
+                                           const SlotRow map) {
   using S = ReadShape<T, D, GQ>;
   constexpr int VEC = S::VEC, LPT = S::LPT;
   constexpr int PSTRIDE = GQ * (D + 2);
@@ -691,6 +696,7 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
         } else {
           id = tail_id(s_ - filled, wstart, n_win, n_sink);
         }
+        id = map(id);
         ids[k] = id;
         lrow[s_] = id;
       }
@@ -698,7 +704,7 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
       for (int k = tid; k < n; k += LSA_BLOCK) {
         const int s_ = c_lo + k;
         if (s_ >= filled) {
-          const int32_t id = tail_id(s_ - filled, wstart, n_win, n_sink);
+          const int32_t id = map(tail_id(s_ - filled, wstart, n_win, n_sink));
           ids[k] = id;
           lrow[s_] = id;
         }
@@ -727,8 +733,9 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
           }
           const int rank = run + off + (int)__popcll(m & below) - lo_rank;
           if (keep && rank >= 0 && rank < nn) {
-            ids[s0 - c_lo + rank] = id;
-            lrow[s0 + rank] = id;
+            const int32_t m = map(id);
+            ids[s0 - c_lo + rank] = m;
+            lrow[s0 + rank] = m;
           }
           run += tot;
           __syncthreads();  // wcnt is rewritten by the next chunk of the row
@@ -849,10 +856,11 @@ __device__ __forceinline__ void rank_reader(const DecodeArgs& a, char* smem, int
   uint64_t* pub = a.pub + i * (int64_t)rows;
   DECODE_MARK(0);
 
-  // the query rows and (span tables) the span ends go out before the wait
+  // the query rows, the slot table row and (span tables) the span ends go out before the wait
   const T* qrow = (const T*)a.q + (r * a.Hq + (int64_t)g * GQ) * D;
   QueryRegs<T, D, GQ> qr;
   qr.load(qrow, a.scale_log2);
+  const SlotRow map = slot_row_of(a.slots, r);
   if (a.spans) {
     const int32_t* ends = a.ends + t * rows;
     for (int m = tid; m < rows; m += LSA_BLOCK) ends_l[m] = ends[m];
@@ -919,7 +927,7 @@ __device__ __forceinline__ void rank_reader(const DecodeArgs& a, char* smem, int
   }
   __syncthreads();
   DECODE_MARK(7);
-  read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, 2);
+  read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, 2, map);
 }
 
 template <typename T, int D, int GQ>
@@ -941,10 +949,11 @@ __device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int
   const int32_t* mine = a.record + (role % kRecordCopies) * a.cstride + i * words;
   DECODE_MARK(0);
 
-  // the query rows go out before the wait
+  // the query rows and the slot table row go out before the wait
   const T* qrow = (const T*)a.q + (r * a.Hq + (int64_t)g * GQ) * D;
   QueryRegs<T, D, GQ> qr;
   qr.load(qrow, a.scale_log2);
+  const SlotRow map = slot_row_of(a.slots, r);
 
   // wait for the unit's record; wave 0 polls its copy and decodes it
   if (w == 0) {
@@ -990,7 +999,7 @@ __device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int
     return;
   }
 
-  read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, 1);
+  read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, 1, map);
 }
 
 // ------------------------------------------------------------------ replicated select
@@ -1042,6 +1051,7 @@ __device__ __forceinline__ void rep_role(const DecodeArgs& a, char* smem, int64_
   for (int m = tid; m < rows; m += LSA_BLOCK) ex.ends[m] = ends[m];
   QueryRegs<T, D, GQ> qr;
   qr.load(qrow, a.scale_log2);
+  const SlotRow map = slot_row_of(a.slots, r);
   float qs[SPAN];
   group_mean_slice<T, SPAN, GQ>(qrow, tid & 15, true, qs);
   __syncthreads();  // the span ends in LDS
@@ -1088,7 +1098,7 @@ __device__ __forceinline__ void rep_role(const DecodeArgs& a, char* smem, int64_
     }
   }
   __syncthreads();
-  read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, 0);
+  read_parts<T, D, GQ>(a, sh, ids, i, role, qr, position, 0, map);
 }
 
 // One workgroup per (unit, reader), unit fastest: every workgroup is a reader that

@@ -80,13 +80,16 @@ extern "C" int lsa_decode_flat_noalloc(const void* q, const void* k, const void*
   hipStream_t s = (hipStream_t)stream;
   char* base = nullptr;
   LSA_TRY(scratch_base(s, &base));
-  if (reset_counters) {  // after a launch gave up waiting (status set): clear on the stream
-    zero_words<<<64, 256, 0, s>>>((int32_t*)base, n_counters);
+  if (reset_counters) {
+    // after a launch gave up waiting (status set): a late select split of that launch may
+    // have left published keys or record words anywhere its own (perhaps larger) shape
+    // reached, so the whole counters region is cleared, not only this call's words
+    zero_words<<<64, 256, 0, s>>>((int32_t*)base, kCounterWords);
     LSA_LAUNCHED("lsa_decode_flat_noalloc (counter reset)");
   }
   return lsa_decode_flat(q, k, v, dtype, R, Tk, Hq, Hkv, D, kv_batch_stride, kv_token_stride, kv_head_stride,
                          centroids, members, ends, table_flags, rows, cap, row_tables, group_tables, score_mode,
-                         positions, cluster_block_size, block_buckets, top_p, window, sink, top_k, scale,
+                         positions, nullptr, cluster_block_size, block_buckets, top_p, window, sink, top_k, scale,
                          select_splits, readers, (int32_t*)base, n_counters, need ? base + kCounterBytes : nullptr,
                          need, lists, lengths, out, status, stream);
 }

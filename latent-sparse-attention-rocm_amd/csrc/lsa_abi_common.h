@@ -76,9 +76,22 @@ inline int check_aligned(const void* centroids, int D, int score_mode, const int
   return LSA_OK;
 }
 
+// Checks an optional slot map and copies it into the kernels' by-value form `out` (the
+// device SlotMap: table == nullptr when there is none).
+template <typename SlotMapT>
+inline int check_slots(const char* who, const lsa_slot_map* m, SlotMapT* out) {
+  *out = SlotMapT{nullptr, nullptr, 0, 0, 0};
+  if (m == nullptr) return LSA_OK;
+  LSA_REQUIRE(m->table && m->rows, LSA_ERR_NULL, "%s: slot map with a NULL table or rows", who);
+  LSA_REQUIRE(m->width >= 1 && m->n_rows >= 1 && m->stride >= m->width, LSA_ERR_SHAPE,
+              "%s: slot map needs n_rows >= 1 and stride >= width >= 1", who);
+  *out = SlotMapT{m->table, m->rows, m->stride, m->width, m->n_rows};
+  return LSA_OK;
+}
+
 }  // namespace lsa
 
-#define LSA_LAUNCHED(what)                                                                     \
+#define LSA_LAUNCHED(what)                                                                    \
   do {                                                                                         \
     hipError_t err_ = hipGetLastError();                                                       \
     if (err_ != hipSuccess) return ::lsa::fail(LSA_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(err_)); \

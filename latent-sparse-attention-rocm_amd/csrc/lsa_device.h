@@ -287,6 +287,41 @@ __device__ __forceinline__ void bitonic_sort_desc(uint64_t* a, int n) {
   }
 }
 
+// ---------------------------------------------------------------- paged caches
+
+// A paged cache's slot table, by value in kernel arguments (table == nullptr: ids are
+// cache rows). Row r of the query rows maps logical position p to table[rows[r] * stride + p].
+struct SlotMap {
+  const int32_t* table;
+  const int32_t* rows;
+  int64_t stride;
+  int32_t width;   // positions a table row maps; ids at or past it map to -1
+  int32_t n_rows;  // table rows; a row index outside [0, n_rows) maps every id to -1
+};
+
+// One query row's view of the slot table: map(id) is the physical cache row of logical
+// position id (-1 stays -1; ids outside [0, width) map to -1); the identity without a table.
+struct SlotRow {
+  const int32_t* row;  // nullptr: identity
+  int32_t width;
+  __device__ __forceinline__ int32_t operator()(int32_t id) const {
+    if (row == nullptr || id < 0) return id;
+    return id < width ? row[id] : -1;
+  }
+};
+
+// The slot row of query row r (one load of rows[r], issued where called).
+__device__ __forceinline__ SlotRow slot_row_of(const SlotMap& m, int64_t r) {
+  SlotRow s{nullptr, 0};
+  if (m.table != nullptr) {
+    const int32_t k = m.rows[r];
+    const bool ok = k >= 0 && k < m.n_rows;
+    s.row = m.table + (ok ? (int64_t)k : 0) * m.stride;
+    s.width = ok ? m.width : 0;  // a bad row index maps everything to -1
+  }
+  return s;
+}
+
 // ---------------------------------------------------------------- cross-workgroup exchange
 
 // Values handed between workgroups that may sit on different XCDs (whose L2s are not

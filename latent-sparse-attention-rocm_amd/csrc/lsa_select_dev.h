@@ -412,10 +412,12 @@ __device__ __forceinline__ int32_t tail_id(int64_t i, int64_t window_start, int6
 // [max(begin_b, sink), min(ends[b], window_start)), so the kept list is a concatenation of
 // ranges, stored in rank order until top_k, then the window and sink tail, then -1 to
 // `width`. The same list expand_walk builds from the member rows, with no member loads.
-// n_picks <= 64; lds: 129 ints. Every thread of the block calls it; returns the length.
+// Every listed id is stored as map(id) (a paged cache's physical row; the identity without
+// a slot table). n_picks <= 64; lds: 129 ints. Every thread of the block calls it; returns
+// the length.
 __device__ __forceinline__ int expand_spans(const int32_t* picks, int n_picks, const int32_t* ends, int rows,
                                             int64_t position, int window, int sink, int top_k, int32_t* out,
-                                            int width, int* lds) {
+                                            int width, int* lds, SlotRow map = SlotRow{nullptr, 0}) {
   const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
   const int64_t ws = position + 1 - window;
   const int64_t window_start = ws > 0 ? ws : 0;
@@ -440,11 +442,11 @@ __device__ __forceinline__ int expand_spans(const int32_t* picks, int n_picks, c
     const int lo = lds[j], p0 = lds[LSA_WAVE + j];
     const int p1 = j + 1 < LSA_WAVE ? lds[LSA_WAVE + j + 1] : total;
     const int e = p1 < kept ? p1 : kept;
-    for (int x = p0 + lane; x < e; x += LSA_WAVE) out[x] = lo + (x - p0);
+    for (int x = p0 + lane; x < e; x += LSA_WAVE) out[x] = map(lo + (x - p0));
   }
   const int64_t n_win = position + 1 - window_start > 0 ? position + 1 - window_start : 0;
   const int64_t n_sink = sink < window_start ? sink : window_start;
-  for (int x = kept + tid; x < width; x += LSA_BLOCK) out[x] = tail_id(x - kept, window_start, n_win, n_sink);
+  for (int x = kept + tid; x < width; x += LSA_BLOCK) out[x] = map(tail_id(x - kept, window_start, n_win, n_sink));
   return kept + (int)n_win + (int)n_sink;
 }
 
@@ -458,10 +460,12 @@ __device__ __forceinline__ int expand_spans(const int32_t* picks, int n_picks, c
 // is then 16-byte aligned). With `stage` (LDS for width + 4 ints, width % 4 == 0, `out`
 // 16-byte aligned) the kept ids are scattered into the LDS row without branches and the
 // whole row - ids, tail and padding - leaves in coalesced 16-byte stores; without it they
-// are stored directly. Every thread of the block calls it.
+// are stored directly. Listed ids are stored as map(id) (see expand_spans). Every thread of
+// the block calls it.
 __device__ __forceinline__ int expand_walk(const int32_t* picks, int n_picks, const int32_t* members, int rows,
                                            int cap, int64_t position, int window, int sink, int top_k,
-                                           int32_t* out, int width, int* scan, int32_t* stage) {
+                                           int32_t* out, int width, int* scan, int32_t* stage,
+                                           SlotRow map = SlotRow{nullptr, 0}) {
   constexpr int E = 32;
   const int tid = threadIdx.x;
   const int64_t ws = position + 1 - window;
@@ -513,7 +517,7 @@ __device__ __forceinline__ int expand_walk(const int32_t* picks, int n_picks, co
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         if ((keep >> e) & 1u) {
-          if (pos < top_k) out[pos] = ids[e];
+          if (pos < top_k) out[pos] = map(ids[e]);
           ++pos;
         }
       }
@@ -542,10 +546,12 @@ __device__ __forceinline__ int expand_walk(const int32_t* picks, int n_picks, co
         }
         v = make_int4(e[0], e[1], e[2], e[3]);
       }
+      if (map.row != nullptr) v = make_int4(map(v.x), map(v.y), map(v.z), map(v.w));
       ((int4*)out)[c] = v;
     }
   } else {
-    for (int i = tid; i < width - filled; i += LSA_BLOCK) out[filled + i] = tail_id(i, window_start, n_win, n_sink);
+    for (int i = tid; i < width - filled; i += LSA_BLOCK)
+      out[filled + i] = map(tail_id(i, window_start, n_win, n_sink));
   }
   return length;
 }

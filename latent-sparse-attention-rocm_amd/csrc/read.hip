@@ -27,8 +27,8 @@ using namespace lsa;
 namespace lsa {
 int launch_read_chunked_mfma(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t T, int64_t Tk,
                              int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
-                             const int32_t* ids, const int32_t* lengths, int32_t W, int32_t chunk, float scale,
-                             void* out, hipStream_t s);
+                             const int32_t* ids, const int32_t* lengths, int32_t W, int32_t chunk,
+                             const SlotMap& slots, float scale, void* out, hipStream_t s);
 }  // namespace lsa
 
 namespace {
@@ -45,6 +45,7 @@ struct ReadArgs {
   int Hq, Hkv, W;
   int ids_per_head;
   int chunk;  // > 0: chunked-prefill lists (shared list of the row's chunk + its causal block)
+  SlotMap slots;  // chunked reads of a paged cache: the causal block's positions -> cache rows
   float scale_log2;
   int empty_nan;
   int span;   // list slots per split (a multiple of the tile)
@@ -59,6 +60,7 @@ struct RowList {
   int n_list;
   int n;
   int64_t local_start;
+  SlotRow map;  // the causal block's positions -> cache rows (identity without a slot table)
 };
 
 __device__ __forceinline__ RowList row_list(const ReadArgs& a, int64_t row, int g) {
@@ -74,6 +76,7 @@ __device__ __forceinline__ RowList row_list(const ReadArgs& a, int64_t row, int 
     r.n_list = n;
     r.local_start = c * a.chunk;
     r.n = n + (int)(t - c * a.chunk + 1);
+    r.map = slot_row_of(a.slots, b);
   } else {
     const int64_t li = a.ids_per_head ? row * a.Hkv + g : row;
     int n = a.lengths[li];
@@ -82,6 +85,7 @@ __device__ __forceinline__ RowList row_list(const ReadArgs& a, int64_t row, int 
     r.n_list = n;
     r.local_start = 0;
     r.n = n;
+    r.map = SlotRow{nullptr, 0};
   }
   return r;
 }
@@ -90,7 +94,12 @@ __device__ __forceinline__ RowList row_list(const ReadArgs& a, int64_t row, int 
 __device__ __forceinline__ int32_t slot_id(const RowList& l, int j, int hi) {
   const int jl = j < l.n_list ? j : (l.n_list > 0 ? l.n_list - 1 : 0);
   const int32_t x = l.n_list > 0 ? l.ids[jl] : -1;
-  const int32_t local = (int32_t)(l.local_start + (j - l.n_list));
+  int32_t local = (int32_t)(l.local_start + (j - l.n_list));
+  if (l.map.row != nullptr) {  // a paged cache (uniform branch): the slot table, loaded unconditionally
+    const bool in = local >= 0 && local < l.map.width;
+    const int32_t m = l.map.row[in ? local : 0];
+    local = in ? m : -1;
+  }
   return j >= hi ? -1 : (j < l.n_list ? x : local);
 }
 
@@ -235,6 +244,7 @@ extern "C" int lsa_read(const void* q, const void* k, const void* v, int dtype, 
   ReadArgs a;
   a.q = q; a.k = k; a.v = v; a.out = out; a.ids = ids; a.lengths = lengths;
   a.Tq = Tq; a.Tk = Tk; a.Hq = Hq; a.Hkv = Hkv; a.W = W; a.ids_per_head = ids_per_head ? 1 : 0; a.chunk = 0;
+  a.slots = SlotMap{nullptr, nullptr, 0, 0, 0};
   a.kv_sb = kv_batch_stride; a.kv_st = kv_token_stride; a.kv_sh = kv_head_stride;
   a.scale_log2 = scale * kLog2e; a.empty_nan = empty_nan ? 1 : 0;
   a.span = split_span(dtype, D, Hq / Hkv, W, splits);
@@ -253,14 +263,17 @@ extern "C" int lsa_read(const void* q, const void* k, const void* v, int dtype, 
 extern "C" int lsa_read_chunked(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t T,
                                 int64_t Tk, int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_batch_stride,
                                 int64_t kv_token_stride, int64_t kv_head_stride, const int32_t* ids,
-                                const int32_t* lengths, int32_t W, int32_t chunk, float scale, int32_t path,
-                                void* out, void* stream) {
+                                const int32_t* lengths, int32_t W, int32_t chunk, const lsa_slot_map* slots,
+                                float scale, int32_t path, void* out, void* stream) {
   int rc = check_read_common(q, k, v, dtype, B, T, Tk, Hq, Hkv, D, kv_batch_stride, kv_token_stride,
                              kv_head_stride, ids, lengths, W, out);
   if (rc != LSA_OK) return rc;
+  SlotMap sm;
+  LSA_TRY(check_slots("lsa_read_chunked", slots, &sm));
   LSA_REQUIRE(chunk >= 1, LSA_ERR_SHAPE, "lsa_read_chunked: chunk must be >= 1");
-  LSA_REQUIRE(T <= Tk, LSA_ERR_SHAPE, "lsa_read_chunked: %lld query rows exceed the cache %lld", (long long)T,
-              (long long)Tk);
+  // positions are cache rows unless the cache is paged (then the slot table maps them)
+  LSA_REQUIRE(slots || T <= Tk, LSA_ERR_SHAPE, "lsa_read_chunked: %lld query rows exceed the cache %lld",
+              (long long)T, (long long)Tk);
   LSA_REQUIRE(B * T * Hkv <= 0x7FFFFFFF, LSA_ERR_SHAPE, "lsa_read_chunked: too many rows");
   LSA_REQUIRE(path >= LSA_CHUNKED_AUTO && path <= LSA_CHUNKED_MFMA, LSA_ERR_SHAPE, "lsa_read_chunked: path %d", path);
   const int mfma_ok = lsa_read_chunked_mfma_ok(dtype, D, chunk);
@@ -269,10 +282,10 @@ extern "C" int lsa_read_chunked(const void* q, const void* k, const void* v, int
   if (B * T * Hkv == 0) return LSA_OK;
   if (mfma_ok && path != LSA_CHUNKED_GATHER)
     return launch_read_chunked_mfma(q, k, v, dtype, B, T, Tk, Hq, Hkv, D, kv_batch_stride, kv_token_stride,
-                                    kv_head_stride, ids, lengths, W, chunk, scale, out, (hipStream_t)stream);
+                                    kv_head_stride, ids, lengths, W, chunk, sm, scale, out, (hipStream_t)stream);
   ReadArgs a;
   a.q = q; a.k = k; a.v = v; a.out = out; a.ids = ids; a.lengths = lengths;
-  a.Tq = T; a.Tk = Tk; a.Hq = Hq; a.Hkv = Hkv; a.W = W; a.ids_per_head = 1; a.chunk = chunk;
+  a.Tq = T; a.Tk = Tk; a.Hq = Hq; a.Hkv = Hkv; a.W = W; a.ids_per_head = 1; a.chunk = chunk; a.slots = sm;
   a.kv_sb = kv_batch_stride; a.kv_st = kv_token_stride; a.kv_sh = kv_head_stride;
   a.scale_log2 = scale * kLog2e; a.empty_nan = 0;
   a.span = split_span(dtype, D, Hq / Hkv, W + chunk, 1);  // one split covers the whole row

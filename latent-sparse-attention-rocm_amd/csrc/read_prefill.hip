@@ -113,6 +113,7 @@ struct PrefillArgs {
   int Hq, Hkv, W, chunk, C;
   int hpw;   // query heads per workgroup (256 / chunk, at most the group)
   int n_hg;  // head groups per kv-head
+  SlotMap slots;  // a paged cache: the causal block's positions -> cache rows
   float scale_log2;
 };
 
@@ -150,6 +151,10 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
   const int n_tiles = (n_tot + TK - 1) / TK;
   const T* kb = (const T*)a.k + b * a.kv_sb + (int64_t)g * a.kv_sh;
   const T* vb = (const T*)a.v + b * a.kv_sb + (int64_t)g * a.kv_sh;
+  // a paged cache (uniform): the causal block's positions go through the slot table row of
+  // batch row b, fetched where the list ids are (the chunk lists already hold cache rows)
+  const SlotRow smap = slot_row_of(a.slots, b);
+  const bool paged = smap.row != nullptr;
 
   // this lane's query columns: qi = 32 QB w + 32 qb + ln -> (local head, token)
   int tok[QB];
@@ -197,7 +202,12 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
     for (int p = 0; p < PASSES; ++p) {
       const int j = tile * TK + p * KPP + (loader ? tid / SEGS : 0);
       const int jl = j < n_list ? j : (n_list > 0 ? n_list - 1 : 0);
-      r.id[p] = lsrc[jl];
+      const int32_t* src = lsrc + jl;
+      if (paged) {  // a causal-block key: its slot (one unconditional load either way)
+        const int64_t loc = c0 + (j - n_list);
+        src = j < n_list ? src : smap.row + (loc < smap.width ? loc : 0);
+      }
+      r.id[p] = *src;
     }
   };
   auto load_tile = [&](Rows& r, int tile) {
@@ -206,8 +216,10 @@ __global__ __launch_bounds__(64 * (8 / QB)) void prefill_mfma_kernel(PrefillArgs
       const int j = tile * TK + p * KPP + (loader ? tid / SEGS : 0);
       const int32_t l = r.id[p];
       const bool in_list = j < n_list;
-      const bool valid = in_list ? (unsigned)l < (unsigned)a.Tk : j < n_tot;
-      const int32_t id = in_list ? l : (int32_t)c0 + (j - n_list);
+      const int64_t loc = c0 + (j - n_list);
+      const bool valid = in_list ? (unsigned)l < (unsigned)a.Tk
+                                 : j < n_tot && (!paged || (loc < smap.width && (unsigned)l < (unsigned)a.Tk));
+      const int32_t id = in_list || paged ? l : (int32_t)loc;
       r.info[p] = valid ? (in_list ? -1 : j - n_list) : -2;
       const uint32_t row = valid ? (uint32_t)id : 0u;
       if constexpr (OFF32) {
@@ -581,9 +593,10 @@ namespace lsa {
 // Launches the MFMA chunked read (arguments already checked by lsa_read_chunked).
 int launch_read_chunked_mfma(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t T, int64_t Tk,
                              int32_t Hq, int32_t Hkv, int32_t D, int64_t kv_sb, int64_t kv_st, int64_t kv_sh,
-                             const int32_t* ids, const int32_t* lengths, int32_t W, int32_t chunk, float scale,
-                             void* out, hipStream_t s) {
+                             const int32_t* ids, const int32_t* lengths, int32_t W, int32_t chunk,
+                             const SlotMap& slots, float scale, void* out, hipStream_t s) {
   PrefillArgs a;
+  a.slots = slots;
   a.q = q; a.k = k; a.v = v; a.out = out; a.ids = ids; a.lengths = lengths;
   a.T = T; a.Tk = Tk; a.kv_sb = kv_sb; a.kv_st = kv_st; a.kv_sh = kv_sh;
   a.Hq = Hq; a.Hkv = Hkv; a.W = W; a.chunk = chunk;

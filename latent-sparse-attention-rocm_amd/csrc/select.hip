@@ -114,8 +114,8 @@ template <bool KEYS>
 __global__ __launch_bounds__(LSA_BLOCK) void expand_kernel(const void* picks, int G, int P, const int32_t* members,
                                                            int rows, int cap, int64_t row_tables,
                                                            int64_t group_tables, const int32_t* positions,
-                                                           int window, int sink, int top_k, int32_t* lists,
-                                                           int32_t* lengths) {
+                                                           SlotMap slots, int window, int sink, int top_k,
+                                                           int32_t* lists, int32_t* lengths) {
   extern __shared__ int32_t pk[];
   __shared__ int scan[LSA_WAVES];
   const int64_t i = blockIdx.x;
@@ -127,7 +127,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void expand_kernel(const void* picks, in
   const int32_t* tab = members + (r * row_tables + g * group_tables) * (int64_t)rows * cap;
   const int width = top_k + window + sink;
   const int len = expand_walk(pk, P, tab, rows, cap, positions[r], window, sink, top_k, lists + i * width, width,
-                              scan, nullptr);
+                              scan, nullptr, slot_row_of(slots, r));
   if (threadIdx.x == 0) lengths[i] = len;
 }
 
@@ -151,6 +151,7 @@ struct FlatArgs {
   int spans;          // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0)
   uint64_t* ws_keys;  // [R*G, rows] every column's key (S > 1)
   int* ws_count;      // [R*G] arrival counters (S > 1)
+  SlotMap slots;      // a paged cache's slot table (table == nullptr: none)
   int32_t* lists;
   int32_t* lengths;
 };
@@ -162,16 +163,17 @@ __device__ __forceinline__ void expand_row(const FlatArgs& a, const int32_t* pk,
                                            int64_t position, int64_t i, int* scan) {
   extern __shared__ uint64_t smem[];
   const int width = a.top_k + a.window + a.sink;
+  const SlotRow map = slot_row_of(a.slots, i / a.G);
   int len;
   if (a.spans) {  // span tables: kept ids from the picks' span ends, no member rows
     __shared__ int span_lds[2 * LSA_WAVE + 1];
     len = expand_spans(pk, a.K, ends, a.rows, position, a.window, a.sink, a.top_k, a.lists + i * width, width,
-                       span_lds);
+                       span_lds, map);
   } else {
     const int32_t* tab = a.members + t * a.rows * (int64_t)a.cap;
     int32_t* stage = a.stage ? (int32_t*)(smem + ((a.rows + a.kp + 1) & ~1)) : nullptr;  // 16-byte aligned
     len = expand_walk(pk, a.K, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k, a.lists + i * width, width,
-                      scan, stage);
+                      scan, stage, map);
   }
   if (threadIdx.x == 0) a.lengths[i] = len;
 }
@@ -278,6 +280,7 @@ struct TreeArgs {
   int window, sink, top_k;
   int spans;  // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0)
   int screen1, screen0;  // bf16 tables that fit screen_topk: node / bucket level on the matrix cores
+  SlotMap slots;         // a paged cache's slot table (table == nullptr: none)
   int32_t* lists;
   int32_t* lengths;
 };
@@ -386,15 +389,16 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
   for (int j = threadIdx.x; j < a.top_p; j += LSA_BLOCK) cand[j] = j < k ? key_column(u_to_key(best[j])) : -1;
   __syncthreads();
   const int width = a.top_k + a.window + a.sink;
+  const SlotRow map = slot_row_of(a.slots, r);
   int len;
   if (a.spans) {  // span tables: kept ids from the picks' span ends, no member rows
     __shared__ int span_lds[2 * LSA_WAVE + 1];
     len = expand_spans(cand, a.top_p, a.ends + t * a.rows, a.rows, position, a.window, a.sink, a.top_k,
-                       a.lists + i * width, width, span_lds);
+                       a.lists + i * width, width, span_lds, map);
   } else {
     const int32_t* tab = a.members + t * (int64_t)a.rows * a.cap;
     len = expand_walk(cand, a.top_p, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k, a.lists + i * width,
-                      width, scan, nullptr);
+                      width, scan, nullptr, map);
   }
   if (threadIdx.x == 0) a.lengths[i] = len;
 }
@@ -615,9 +619,11 @@ extern "C" int lsa_select_topk_scores(const float* scores, const int32_t* length
 
 extern "C" int lsa_expand(const void* picks, int picks_are_keys, int64_t R, int32_t G, int32_t P,
                           const int32_t* members, int32_t rows, int32_t cap, int64_t row_tables, int64_t group_tables,
-                          const int32_t* positions, int32_t window, int32_t sink, int32_t top_k, int32_t* lists,
-                          int32_t* lengths, void* stream) {
+                          const int32_t* positions, const lsa_slot_map* slots, int32_t window, int32_t sink,
+                          int32_t top_k, int32_t* lists, int32_t* lengths, void* stream) {
   LSA_REQUIRE(picks && members && positions && lists && lengths, LSA_ERR_NULL, "lsa_expand: NULL pointer");
+  SlotMap sm;
+  LSA_TRY(check_slots("lsa_expand", slots, &sm));
   LSA_TRY(check_tables(rows, cap, row_tables, group_tables));
   LSA_TRY(check_aligned(nullptr, 16, LSA_SCORE_BF16, members, cap));
   LSA_REQUIRE(R >= 0 && G >= 1 && P >= 0 && P <= 2 * kMaxLdsKeys, LSA_ERR_SHAPE, "lsa_expand: bad sizes (P=%d)", P);
@@ -628,12 +634,12 @@ extern "C" int lsa_expand(const void* picks, int picks_are_keys, int64_t R, int3
   hipStream_t s = (hipStream_t)stream;
   if (picks_are_keys)
     expand_kernel<true><<<dim3((unsigned)(R * G)), LSA_BLOCK, shmem, s>>>(picks, G, P, members, rows, cap, row_tables,
-                                                                        group_tables, positions, window, sink,
+                                                                        group_tables, positions, sm, window, sink,
                                                                         top_k, lists, lengths);
   else
     expand_kernel<false><<<dim3((unsigned)(R * G)), LSA_BLOCK, shmem, s>>>(picks, G, P, members, rows, cap,
-                                                                         row_tables, group_tables, positions, window,
-                                                                         sink, top_k, lists, lengths);
+                                                                         row_tables, group_tables, positions, sm,
+                                                                         window, sink, top_k, lists, lengths);
   LSA_LAUNCHED("lsa_expand");
   return LSA_OK;
 }
@@ -650,12 +656,14 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
                                const void* centroids, const int32_t* members, const int32_t* ends,
                                int32_t table_flags, int32_t rows,
                                int32_t cap, int64_t row_tables, int64_t group_tables, int score_mode,
-                               const int32_t* positions, int32_t cluster_block_size, int32_t block_buckets,
-                               int32_t top_p, int32_t window, int32_t sink, int32_t top_k, int32_t splits,
-                               int32_t* counters, void* scratch, size_t scratch_bytes, int32_t* lists,
-                               int32_t* lengths, void* stream) {
+                               const int32_t* positions, const lsa_slot_map* slots, int32_t cluster_block_size,
+                               int32_t block_buckets, int32_t top_p, int32_t window, int32_t sink, int32_t top_k,
+                               int32_t splits, int32_t* counters, void* scratch, size_t scratch_bytes,
+                               int32_t* lists, int32_t* lengths, void* stream) {
   LSA_REQUIRE(queries && centroids && members && positions && lists && lengths, LSA_ERR_NULL,
               "lsa_select_flat: NULL pointer");
+  SlotMap sm;
+  LSA_TRY(check_slots("lsa_select_flat", slots, &sm));
   LSA_TRY(check_dtype(q_dtype));
   LSA_TRY(check_dim(D));
   LSA_TRY(check_tables(rows, cap, row_tables, group_tables));
@@ -689,6 +697,7 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
   a.S = splits; a.cs = cs;
   a.ws_count = counters;
   a.ws_keys = need ? (uint64_t*)scratch : nullptr;
+  a.slots = sm;
   a.lists = lists; a.lengths = lengths;
   a.spans = (table_flags & LSA_TABLE_SPANS) && K <= LSA_WAVE ? 1 : 0;  // more picks: the member rows
   // the list row is staged in LDS when it fits beside the keys (coalesced row stores)
@@ -715,11 +724,14 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
                                const void* node_centroids, const int32_t* children, int32_t n_nodes,
                                int32_t node_size, const void* centroids, const int32_t* members, const int32_t* ends,
                                int32_t table_flags, int32_t rows, int32_t cap, int64_t row_tables, int64_t group_tables, int score_mode,
-                               const int32_t* positions, int32_t cluster_block_size, int32_t block_buckets,
-                               int32_t node_block, int32_t beam_width, int32_t top_p, int32_t window, int32_t sink,
-                               int32_t top_k, int32_t* lists, int32_t* lengths, void* stream) {
+                               const int32_t* positions, const lsa_slot_map* slots, int32_t cluster_block_size,
+                               int32_t block_buckets, int32_t node_block, int32_t beam_width, int32_t top_p,
+                               int32_t window, int32_t sink, int32_t top_k, int32_t* lists, int32_t* lengths,
+                               void* stream) {
   LSA_REQUIRE(queries && node_centroids && children && centroids && members && positions && lists && lengths,
               LSA_ERR_NULL, "lsa_select_tree: NULL pointer");
+  SlotMap sm;
+  LSA_TRY(check_slots("lsa_select_tree", slots, &sm));
   LSA_TRY(check_dtype(q_dtype));
   LSA_TRY(check_dim(D));
   LSA_TRY(check_tables(rows, cap, row_tables, group_tables));
@@ -753,7 +765,7 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
   a.beam = beam_width; a.top_p = top_p;
   a.nodes_pow2 = next_pow2(n_nodes); a.beam_pow2 = next_pow2(beam); a.cand_cap = (int)cand_cap;
   a.cand_pow2 = next_pow2((int)(cand_cap > 0 ? cand_cap : 1)); a.top_pow2 = next_pow2(top_p);
-  a.window = window; a.sink = sink; a.top_k = top_k; a.lists = lists; a.lengths = lengths;
+  a.window = window; a.sink = sink; a.top_k = top_k; a.lists = lists; a.lengths = lengths; a.slots = sm;
   a.spans = (table_flags & LSA_TABLE_SPANS) && top_p <= LSA_WAVE ? 1 : 0;  // else the member rows
   a.screen1 = score_mode == LSA_SCORE_BF16 && screen_pays(D, n_nodes, beam) ? 1 : 0;
   a.screen0 = score_mode == LSA_SCORE_BF16 && screen_pays(D, a.cand_pow2, top_p < a.cand_pow2 ? top_p : a.cand_pow2)

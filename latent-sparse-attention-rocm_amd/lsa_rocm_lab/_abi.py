@@ -53,35 +53,37 @@ SIGNATURES = {
     "lsa_topk_keys": (_int, [_p, _p, _i64, _i32, _i32, _p, _p]),
     "lsa_select_topk_scores": (_int, [_p, _p, _i64, _i32, _i32, _p, _p]),
     "lsa_unpack_ids": (_int, [_p, _i64, _p, _p]),
-    "lsa_expand": (_int, [_p, _int, _i64, _i32, _i32, _p, _i32, _i32, _i64, _i64, _p, _i32, _i32, _i32, _p, _p, _p]),
+    "lsa_expand": (_int, [_p, _int, _i64, _i32, _i32, _p, _i32, _i32, _i64, _i64, _p, _p, _i32, _i32, _i32, _p, _p,
+                          _p]),
     "lsa_select_flat_scratch_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
-    "lsa_select_flat": (_int, [_p, _int, _i64, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i64, _i64, _int, _p, _i32, _i32,
-                               _i32, _i32, _i32, _i32, _i32, _p, _p, _sz, _p, _p, _p]),
+    "lsa_select_flat": (_int, [_p, _int, _i64, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i64, _i64, _int, _p, _p, _i32,
+                               _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _sz, _p, _p, _p]),
     "lsa_select_tree": (_int, [_p, _int, _i64, _i32, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i64, _i64,
-                               _int, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
+                               _int, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
     "lsa_select_beam": (_int, [_p, _int, _i64, _i32, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _p, _p, _p, _i32, _i32,
-                               _i32, _i64, _i64, _int, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
+                               _i32, _i64, _i64, _int, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p,
+                               _p]),
     "lsa_index_queries": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p]),
     "lsa_bucket_centroids": (_int, [_p, _int, _i64, _i64, _i64, _i32, _i32, _p, _i64, _i32, _i32, _int, _p, _p, _p]),
     "lsa_ward_segments_scratch_bytes": (_sz, [_i64, _i64, _i32, _i32]),
     "lsa_ward_segments": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _p, _sz, _p,
-                                 _p, _p]),
+                                 _p, _p, _p]),
     "lsa_read_scratch_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "lsa_read_tile_tokens": (_i32, [_int, _i32, _i32]),
     "lsa_read": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _i32, _int,
                         _f32, _int, _i32, _p, _p, _sz, _p, _p]),
     "lsa_read_chunked": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _i32,
-                                _i32, _f32, _i32, _p, _p]),
+                                _i32, _p, _f32, _i32, _p, _p]),
     "lsa_read_chunked_mfma_ok": (_int, [_int, _i32, _i32]),
     "lsa_decode_flat_counters": (_i64, [_i64, _i32, _i32, _i32]),
     "lsa_decode_flat_rep_ok": (_int, [_int, _i32, _i32, _i32, _i32, _int, _i32]),
     "lsa_decode_flat_scratch_bytes": (_sz, [_int, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "lsa_decode_flat": (_int, [_p, _p, _p, _int, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _p, _i32, _i32,
-                               _i32, _i64, _i64, _int, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p,
-                               _i64, _p, _sz, _p, _p, _p, _p, _p]),
+                               _i32, _i64, _i64, _int, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32,
+                               _p, _i64, _p, _sz, _p, _p, _p, _p, _p]),
     "lsa_decode_tree": (_int, [_p, _p, _p, _int, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _i32, _i32,
-                               _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i64, _i64, _int, _p, _i32, _i32, _i32, _i32,
-                               _i32, _i32, _f32, _i32, _p, _i64, _p, _sz, _p, _p, _p, _p, _p]),
+                               _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i64, _i64, _int, _p, _p, _i32, _i32, _i32,
+                               _i32, _i32, _i32, _f32, _i32, _p, _i64, _p, _sz, _p, _p, _p, _p, _p]),
     "lsa_decode_flat_noalloc": (_int, [_p, _p, _p, _int, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _p,
                                        _i32, _i32, _i32, _i64, _i64, _int, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                                        _f32, _i32, _i32, _i32, _p, _p, _p, _p, _p]),
@@ -140,6 +142,21 @@ def call(name: str, *args):
 
 def size(name: str, *args) -> int:
     return int(getattr(load(), name)(*args))
+
+
+class SlotMap(ctypes.Structure):
+    """``lsa_slot_map`` (include/lsa_rocm.h): a paged cache's slot table."""
+
+    _fields_ = [("table", _p), ("rows", _p), ("stride", _i64), ("width", _i32), ("n_rows", _i32)]
+
+
+def slot_map(table: torch.Tensor | None, rows: torch.Tensor | None):
+    """``const lsa_slot_map*`` for a call (None: no paging): table [n_rows, width] int32 with
+    contiguous rows, rows [R] int32. The caller keeps both tensors alive for the call."""
+    if table is None:
+        return None
+    return ctypes.pointer(SlotMap(table.data_ptr(), rows.data_ptr(), table.stride(0), table.shape[1],
+                                  table.shape[0]))
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
@@ -222,16 +239,18 @@ class Counters:
 
 
 class StatusWord:
-    """One int32 per device in pinned host memory that the fused decode sets (system-scope
-    store) when a reader gives up waiting; the host reads it without a device sync."""
+    """One int32 per (device, purpose) in pinned host memory that a kernel sets with a
+    system-scope store - the fused decode when a reader gives up waiting ("decode"), the
+    bucket-table build when a table cannot reach its segment count ("build") - and the host
+    reads without a device sync."""
 
-    _words: dict[int, torch.Tensor] = {}
+    _words: dict[tuple[int, str], torch.Tensor] = {}
 
     @classmethod
-    def get(cls, device: torch.device) -> torch.Tensor:
-        index = device_index(device)
-        word = cls._words.get(index)
+    def get(cls, device: torch.device, purpose: str = "decode") -> torch.Tensor:
+        key = (device_index(device), purpose)
+        word = cls._words.get(key)
         if word is None:
             word = torch.zeros(1, dtype=torch.int32, pin_memory=True)
-            cls._words[index] = word
+            cls._words[key] = word
         return word

@@ -30,6 +30,7 @@ from lsa_rocm_lab.port.pipeline import (
     _on_device,
     _positions32,
     _queries,
+    _slot_args,
 )
 
 
@@ -41,6 +42,8 @@ def tree_select_batched(
     config: PortConfig,
     top_k: int | None = None,
     score_dtype: str = "fp32",
+    slot_table: torch.Tensor | None = None,
+    slot_rows: torch.Tensor | None = None,
 ):
     """Select by the beam, expand in rank order - see ``pipeline.tree_select``.
 
@@ -90,11 +93,13 @@ def tree_select_batched(
     width = top_k + config.window_size + config.sink_size
     lists = torch.empty(layout.out_shape(width), dtype=torch.int32, device=device)
     lengths = torch.empty(layout.out_shape(), dtype=torch.int32, device=device)
+    slots, _keep = _slot_args(slot_table, slot_rows, layout.R, device)
     if n_levels == 1:
         _abi.call("lsa_select_tree", q.data_ptr(), _abi.dtype_code(q.dtype), layout.R, layout.G, layout.D,
                   ncents[0].data_ptr(), kids[0].data_ptr(), kids[0].shape[-2], node_size, bcent.data_ptr(),
                   members.data_ptr(), _abi.ptr(ends), flags, layout.rows, members.shape[-1], layout.row_tables,
-                  layout.group_tables, mode, pos.data_ptr(), config.cluster_block_size, config.block_bucket_count,
+                  layout.group_tables, mode, pos.data_ptr(), slots, config.cluster_block_size,
+                  config.block_bucket_count,
                   config.node_cluster_block_size, config.beam_width, config.top_p, config.window_size,
                   config.sink_size, top_k, lists.data_ptr(), lengths.data_ptr(), _abi.stream(device))
         return lists, lengths
@@ -105,12 +110,14 @@ def tree_select_batched(
               ctypes.addressof(cent_ptrs), ctypes.addressof(kid_ptrs), ctypes.addressof(n_nodes), node_size,
               config.node_cluster_block_size, config.top_level, bcent.data_ptr(), members.data_ptr(),
               _abi.ptr(ends), flags, layout.rows, members.shape[-1], layout.row_tables, layout.group_tables, mode,
-              pos.data_ptr(), config.cluster_block_size, config.block_bucket_count, config.beam_width,
+              pos.data_ptr(), slots, config.cluster_block_size, config.block_bucket_count, config.beam_width,
               config.top_p, config.window_size, config.sink_size, top_k, lists.data_ptr(), lengths.data_ptr(),
               _abi.stream(device))
     return lists, lengths
 
 
-def tree_select_per_page(index_queries, positions, buckets, hierarchy, config, top_k=None, score_dtype="fp32"):
+def tree_select_per_page(index_queries, positions, buckets, hierarchy, config, top_k=None, score_dtype="fp32",
+                         slot_table=None, slot_rows=None):
     """Reference _tree.py:63-85 entry name; the same kernel as ``tree_select_batched``."""
-    return tree_select_batched(index_queries, positions, buckets, hierarchy, config, top_k, score_dtype)
+    return tree_select_batched(index_queries, positions, buckets, hierarchy, config, top_k, score_dtype,
+                               slot_table, slot_rows)

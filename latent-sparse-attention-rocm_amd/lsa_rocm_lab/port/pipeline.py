@@ -17,7 +17,16 @@ a HIP kernel in liblsa_rocm.so:
 
 The index grows with the cache: ``extend_buckets`` appends newly closed blocks, and
 capacity tables (``reserve_buckets``, allocated once for the longest context) take them
-in place (``grow_buckets_``) with no tensor moved.
+in place (``grow_buckets_``) with no tensor moved and no host sync (a table that cannot be
+built is reported by a pinned status word: the next build raises, ``check_build`` syncs).
+
+Paged caches (upstream's paged decode; the reference's expansion kernel maps ids through a
+slot table, select_fused.py:147-205): every select, ``flat_decode``/``tree_decode`` and
+``lsa_read_chunked`` take ``slot_table`` [n_rows, width] int32 (logical position -> cache
+row) and ``slot_rows`` [R] int32 (each query row's table row). The expansion applies the
+map once per listed id - the kept ids and the window/sink tail, kept or not by their
+logical positions - so the lists hold cache rows and the read gathers them directly; K/V
+may then be one pool [1, slots, Hkv, D] shared by every batch row.
 
 Per-kv-head selection (the benchmark geometry) extends the shapes: index queries
 [R, G, D] against tables with a leading group axis [G, rows, ...] (one table per
@@ -179,6 +188,37 @@ def _queries(index_queries: torch.Tensor) -> torch.Tensor:
     return index_queries.contiguous()
 
 
+def _slot_args(slot_table: torch.Tensor | None, slot_rows: torch.Tensor | None, R: int, device):
+    """A paged cache's slot map for one call: (``const lsa_slot_map*`` or None, the tensors
+    it points at, kept alive by the caller until the launch). ``slot_table`` [n_rows, width]
+    (or [width]) maps logical positions to cache rows; ``slot_rows`` [R] names each query
+    row's table row (default: row 0 for a one-row table, row r for a table of R rows)."""
+    if slot_table is None:
+        if slot_rows is not None:
+            raise ValueError("slot_rows without a slot_table")
+        return None, ()
+    _on_device("the slot map", slot_table)
+    table = slot_table.to(device=device, dtype=torch.int32)
+    if table.dim() == 1:
+        table = table[None]
+    if table.dim() != 2 or table.shape[0] < 1 or table.shape[1] < 1:
+        raise ValueError(f"slot_table must be [n_rows, width] with both >= 1, got {tuple(slot_table.shape)}")
+    if table.stride(1) != 1:
+        table = table.contiguous()
+    if slot_rows is None:
+        if table.shape[0] == 1:
+            rows = torch.zeros(R, dtype=torch.int32, device=device)
+        elif table.shape[0] == R:
+            rows = torch.arange(R, dtype=torch.int32, device=device)
+        else:
+            raise ValueError(f"slot_rows is needed: {table.shape[0]} slot-table rows for {R} query rows")
+    else:
+        rows = slot_rows.to(device=device, dtype=torch.int32).reshape(-1).contiguous()
+        if rows.numel() != R:
+            raise ValueError(f"slot_rows holds {rows.numel()} rows for {R} query rows")
+    return _abi.slot_map(table, rows), (table, rows)
+
+
 # ----------------------------------------------------------------------------- selection
 
 
@@ -252,7 +292,7 @@ def _mask_for(scores: torch.Tensor, config: PortConfig, listed: torch.Tensor) ->
 
 
 def _expand(picks: torch.Tensor, picks_are_keys: bool, layout: _Layout, members: torch.Tensor,
-            positions: torch.Tensor, window: int, sink: int, top_k: int):
+            positions: torch.Tensor, window: int, sink: int, top_k: int, slot_table=None, slot_rows=None):
     device = picks.device
     picks = picks.contiguous()
     members = members.to(device=device, dtype=torch.int32).contiguous()
@@ -260,9 +300,11 @@ def _expand(picks: torch.Tensor, picks_are_keys: bool, layout: _Layout, members:
     width = top_k + window + sink
     lists = torch.empty(layout.out_shape(width), dtype=torch.int32, device=device)
     lengths = torch.empty(layout.out_shape(), dtype=torch.int32, device=device)
+    slots, _keep = _slot_args(slot_table, slot_rows, layout.R, device)
     _abi.call("lsa_expand", picks.data_ptr(), 1 if picks_are_keys else 0, layout.R, layout.G, P,
               members.data_ptr(), members.shape[-2], members.shape[-1], layout.row_tables, layout.group_tables,
-              positions.data_ptr(), window, sink, top_k, lists.data_ptr(), lengths.data_ptr(), _abi.stream(device))
+              positions.data_ptr(), slots, window, sink, top_k, lists.data_ptr(), lengths.data_ptr(),
+              _abi.stream(device))
     return lists, lengths
 
 
@@ -273,9 +315,12 @@ def flat_select_reference(
     config: PortConfig,
     top_k: int | None = None,
     score_dtype: str = "bf16",
+    slot_table: torch.Tensor | None = None,
+    slot_rows: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """The unfused select chain (reference pipeline.py:248-271): scores, the whole-path
-    listing, best-first keys, unpack, rank-order expansion - one HIP kernel each."""
+    listing, best-first keys, unpack, rank-order expansion - one HIP kernel each.
+    ``slot_table`` / ``slot_rows``: a paged cache's slot map (see the module notes)."""
     top_k = config.top_k if top_k is None else top_k
     scores, counts = _production_scores(index_queries, positions, buckets, config, score_dtype)
     layout = _Layout(index_queries, buckets.centroids)
@@ -283,7 +328,8 @@ def flat_select_reference(
     keys, listed = keys_mod.listed(flat_scores, counts.reshape(-1))
     picked = keys_mod.unpack_ids(best_first_keys(keys, config.top_p, counts=_mask_for(flat_scores, config, listed)))
     pos = _positions32(positions, scores.device)
-    return _expand(picked, False, layout, buckets.members, pos, config.window_size, config.sink_size, top_k)
+    return _expand(picked, False, layout, buckets.members, pos, config.window_size, config.sink_size, top_k,
+                   slot_table, slot_rows)
 
 
 def _select_splits(R: int, G: int, rows: int, top_p: int) -> int:
@@ -344,7 +390,7 @@ _RANK_MAX_SLOTS = 1 << 16
 _REP_MAX_UNITS = int(os.environ.get("LSA_DECODE_REP_UNITS", "0"))
 
 
-def _fused_select(index_queries, positions, buckets, config, top_k, score_dtype):
+def _fused_select(index_queries, positions, buckets, config, top_k, score_dtype, slot_table=None, slot_rows=None):
     device = _on_device("flat_select", index_queries, buckets.centroids, buckets.members)
     if positions.shape[0] != index_queries.shape[0]:
         raise ValueError(
@@ -363,10 +409,11 @@ def _fused_select(index_queries, positions, buckets, config, top_k, score_dtype)
     nbytes = _abi.size("lsa_select_flat_scratch_bytes", layout.R, layout.G, config.top_p, layout.rows, splits)
     ws = _abi.Workspace.get(device, "select", nbytes)
     counters = _abi.Counters.get(device, layout.R * layout.G) if nbytes else None
+    slots, _keep = _slot_args(slot_table, slot_rows, layout.R, device)
     _abi.call("lsa_select_flat", q.data_ptr(), _abi.dtype_code(q.dtype), layout.R, layout.G, layout.D,
               table.data_ptr(), members.data_ptr(), _abi.ptr(ends),
               _abi.TABLE_SPANS if (buckets.spans and ends is not None) else 0, layout.rows, members.shape[-1],
-              layout.row_tables, layout.group_tables, mode, pos.data_ptr(), config.cluster_block_size,
+              layout.row_tables, layout.group_tables, mode, pos.data_ptr(), slots, config.cluster_block_size,
               config.block_bucket_count, config.top_p, config.window_size, config.sink_size, top_k, splits,
               _abi.ptr(counters), _abi.ptr(ws), nbytes, lists.data_ptr(), lengths.data_ptr(), _abi.stream(device))
     return lists, lengths
@@ -379,6 +426,8 @@ def flat_select(
     config: PortConfig,
     top_k: int | None = None,
     score_dtype: str = "bf16",
+    slot_table: torch.Tensor | None = None,
+    slot_rows: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Select each query's keys - the production composition, implementation-switched.
 
@@ -387,7 +436,8 @@ def flat_select(
     kernel from the index queries to the read lists (canonical score, packed-key top-k,
     rank-order expansion); ``fused_unpack`` keeps the listing and best-first top-k and
     expands from the keys. All three produce byte-identical lists and lengths; unknown
-    values fail loudly.
+    values fail loudly. ``slot_table`` / ``slot_rows`` (a paged cache) make the lists hold
+    cache rows: every listed id goes through the slot table (see the module notes).
     """
     impl = os.environ.get("LSA_SELECT_IMPL", "reference")
     if impl not in ("reference", "fused", "fused_unpack"):
@@ -395,10 +445,11 @@ def flat_select(
             f"LSA_SELECT_IMPL must be reference|fused|fused_unpack, got {impl!r}"
         )
     if impl == "reference":
-        return flat_select_reference(index_queries, positions, buckets, config, top_k, score_dtype)
+        return flat_select_reference(index_queries, positions, buckets, config, top_k, score_dtype, slot_table,
+                                     slot_rows)
     top_k = config.top_k if top_k is None else top_k
     if impl == "fused":
-        return _fused_select(index_queries, positions, buckets, config, top_k, score_dtype)
+        return _fused_select(index_queries, positions, buckets, config, top_k, score_dtype, slot_table, slot_rows)
     if impl == "fused_unpack":
         scores, counts = _production_scores(index_queries, positions, buckets, config, score_dtype)
         layout = _Layout(index_queries, buckets.centroids)
@@ -406,7 +457,8 @@ def flat_select(
         keys, listed = keys_mod.listed(flat_scores, counts.reshape(-1))
         ordered = best_first_keys(keys, config.top_p, counts=_mask_for(flat_scores, config, listed))
         pos = _positions32(positions, scores.device)
-        return _expand(ordered, True, layout, buckets.members, pos, config.window_size, config.sink_size, top_k)
+        return _expand(ordered, True, layout, buckets.members, pos, config.window_size, config.sink_size, top_k,
+                       slot_table, slot_rows)
     raise AssertionError(f"unreachable impl {impl!r}")
 
 
@@ -418,14 +470,17 @@ def tree_select(
     config: PortConfig,
     top_k: int | None = None,
     score_dtype: str = "fp32",
+    slot_table: torch.Tensor | None = None,
+    slot_rows: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Select each query's keys by a beam down the node levels (reference pipeline.py:319-337).
 
-    See ``_tree.tree_select_batched``.
+    See ``_tree.tree_select_batched``; ``slot_table`` / ``slot_rows`` as ``flat_select``.
     """
     from lsa_rocm_lab.port._tree import tree_select_batched
 
-    return tree_select_batched(index_queries, positions, buckets, hierarchy, config, top_k, score_dtype)
+    return tree_select_batched(index_queries, positions, buckets, hierarchy, config, top_k, score_dtype,
+                               slot_table, slot_rows)
 
 
 # ----------------------------------------------------------------------------- reading
@@ -478,6 +533,8 @@ def flat_decode(
     splits: int | None = None,
     readers: int | None = None,
     status: torch.Tensor | None = None,
+    slot_table: torch.Tensor | None = None,
+    slot_rows: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """One decode step - index queries, flat select, sparse read - in one HIP launch.
 
@@ -493,7 +550,10 @@ def flat_decode(
     1 when a reader gives up waiting for its unit's selection; by default the library's
     pinned word, checked at the start of every call without a device sync: if an earlier
     launch gave up, the arrival counters are zeroed again and ``LsaError`` is raised
-    (``check_decode`` makes the same check after a sync).
+    (``check_decode`` makes the same check after a sync); a caller that passes its own
+    ``status`` checks it and, when it is set, calls ``reset_decode`` before the next launch.
+    ``slot_table`` / ``slot_rows`` (a paged cache; rows default to the batch row): the
+    lists hold cache rows and K/V may be one pool [1, slots, Hkv, D] for every batch row.
     """
     from lsa_rocm_lab.port.read_kernel_tiled import _kv_layout
 
@@ -504,12 +564,14 @@ def flat_decode(
         raise ValueError(f"q/k/v dtypes differ: {q.dtype} {k.dtype} {v.dtype}")
     B, _, Hq, D = q.shape
     Tk, Hkv = k.shape[1], k.shape[2]
-    if k.dim() != 4 or k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
-        raise ValueError(f"k/v must be [B={B}, Tk, Hkv, D={D}], got {tuple(k.shape)} / {tuple(v.shape)}")
+    if k.dim() != 4 or k.shape != v.shape or k.shape[0] not in (B, 1) or k.shape[3] != D:
+        raise ValueError(f"k/v must be [B={B} or 1, Tk, Hkv, D={D}], got {tuple(k.shape)} / {tuple(v.shape)}")
     if Hq % Hkv:
         raise ValueError(f"{Hq} query heads do not group onto {Hkv} kv-heads")
     q = q.contiguous()
     k, v, sb, st, sh = _kv_layout(k, v)
+    if k.shape[0] != B:  # one pool read by every batch row
+        sb = 0
     layout = _Layout(torch.empty((B, Hkv, D), device="meta"), buckets.centroids)
     table, mode = _score_table(buckets, score_dtype)
     members = buckets.members.to(device=device, dtype=torch.int32).contiguous()
@@ -538,9 +600,10 @@ def flat_decode(
             _decode_gave_up(device, status)
     ws = _abi.Workspace.get(device, "decode", nbytes)
     counters = _abi.Counters.get(device, max(n_counters, 1))
+    slots, _keep = _slot_args(slot_table, slot_rows, B, device)
     _abi.call("lsa_decode_flat", q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, Tk, Hq, Hkv, D, sb, st, sh,
               table.data_ptr(), members.data_ptr(), _abi.ptr(ends), flags, rows, cap, layout.row_tables,
-              layout.group_tables, mode, pos.data_ptr(), config.cluster_block_size, config.block_bucket_count,
+              layout.group_tables, mode, pos.data_ptr(), slots, config.cluster_block_size, config.block_bucket_count,
               config.top_p, config.window_size, config.sink_size, top_k, float(scale), splits, readers,
               counters.data_ptr(), counters.numel(), _abi.ptr(ws), nbytes, lists.data_ptr(), lengths.data_ptr(),
               out.data_ptr(), _abi.ptr(status), _abi.stream(device))
@@ -559,11 +622,13 @@ def tree_decode(
     top_k: int | None = None,
     score_dtype: str = "bf16",
     readers: int | None = None,
+    slot_table: torch.Tensor | None = None,
+    slot_rows: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """One decode step over a one-level node tree - index queries, tree select, sparse
     read - in one HIP launch (the reference's decode step, port/bench.py:147-153, with
-    ``tree_select``, pipeline.py:319-337, in place of ``flat_select``). Shapes as
-    ``flat_decode``; the lists and lengths are byte-identical to
+    ``tree_select``, pipeline.py:319-337, in place of ``flat_select``). Shapes and the slot
+    map as ``flat_decode``; the lists and lengths are byte-identical to
     ``tree_select(index_queries(q, Hkv)[:, 0], positions, buckets, hierarchy, config,
     score_dtype=score_dtype)``'s. Deeper hierarchies take ``tree_select`` + ``lsa_read``."""
     from lsa_rocm_lab.port.read_kernel_tiled import _kv_layout
@@ -580,12 +645,14 @@ def tree_decode(
         raise ValueError(f"q/k/v dtypes differ: {q.dtype} {k.dtype} {v.dtype}")
     B, _, Hq, D = q.shape
     Tk, Hkv = k.shape[1], k.shape[2]
-    if k.dim() != 4 or k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
-        raise ValueError(f"k/v must be [B={B}, Tk, Hkv, D={D}], got {tuple(k.shape)} / {tuple(v.shape)}")
+    if k.dim() != 4 or k.shape != v.shape or k.shape[0] not in (B, 1) or k.shape[3] != D:
+        raise ValueError(f"k/v must be [B={B} or 1, Tk, Hkv, D={D}], got {tuple(k.shape)} / {tuple(v.shape)}")
     if Hq % Hkv:
         raise ValueError(f"{Hq} query heads do not group onto {Hkv} kv-heads")
     q = q.contiguous()
     k, v, sb, st, sh = _kv_layout(k, v)
+    if k.shape[0] != B:  # one pool read by every batch row
+        sb = 0
     layout = _Layout(torch.empty((B, Hkv, D), device="meta"), buckets.centroids)
     node_layout = _Layout(torch.empty((B, Hkv, D), device="meta"), level.centroids)
     if (node_layout.row_tables, node_layout.group_tables) != (layout.row_tables, layout.group_tables):
@@ -620,10 +687,11 @@ def tree_decode(
         _decode_gave_up(device, status)
     ws = _abi.Workspace.get(device, "decode", nbytes)
     counters = _abi.Counters.get(device, max(n_counters, 1))
+    slots, _keep = _slot_args(slot_table, slot_rows, B, device)
     _abi.call("lsa_decode_tree", q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, Tk, Hq, Hkv, D, sb, st, sh,
               ncent.data_ptr(), children.data_ptr(), children.shape[-2], children.shape[-1],
               config.node_cluster_block_size, config.beam_width, table.data_ptr(), members.data_ptr(),
-              _abi.ptr(ends), flags, rows, cap, layout.row_tables, layout.group_tables, mode, pos.data_ptr(),
+              _abi.ptr(ends), flags, rows, cap, layout.row_tables, layout.group_tables, mode, pos.data_ptr(), slots,
               config.cluster_block_size, config.block_bucket_count, config.top_p, config.window_size,
               config.sink_size, top_k, float(scale), readers, counters.data_ptr(), counters.numel(), _abi.ptr(ws),
               nbytes, lists.data_ptr(), lengths.data_ptr(), out.data_ptr(), _abi.ptr(status), _abi.stream(device))
@@ -654,16 +722,34 @@ def check_decode(device: torch.device | int | None = None) -> None:
         _decode_gave_up(device, status)
 
 
-def lsa_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale, chunk_size: int = 64):
+def reset_decode(device: torch.device | int | None = None) -> None:
+    """Zeroes the fused decode's arrival counters and hand-off words on a device (outside
+    graph capture, with no launch in flight). Needed after a launch that gave up waiting
+    and reported it through a caller's own ``status`` word: such a launch may leave a late
+    record or published keys in the shared counters, which the next launch would read."""
+    device = torch.device("cuda", _abi.device_index(device))
+    if torch.cuda.is_current_stream_capturing():
+        raise _abi.LsaError(-6, "reset_decode: the counters cannot be reset under graph capture")
+    torch.cuda.synchronize(device)
+    _abi.Counters.reset(device)
+    torch.cuda.synchronize(device)
+
+
+def lsa_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale, chunk_size: int = 64,
+                     slot_table: torch.Tensor | None = None, slot_rows: torch.Tensor | None = None):
     """Chunked prefill read: every query row of a ``chunk_size`` chunk reads the chunk's
     shared per-kv-head list plus the chunk's own causal block.
 
     q [B, T, Hq, D] (query row t at cache position t), k/v [B, Tk, Hkv, D], chunk_lists
-    [B, C, Hkv, W] / chunk_lengths [B, C, Hkv] (or without B for B == 1).
+    [B, C, Hkv, W] / chunk_lengths [B, C, Hkv] (or without B for B == 1). A paged cache:
+    the lists hold cache rows (a select given the slot map made them), ``slot_table`` maps
+    the causal block's positions (``slot_rows`` [B], default row b for batch row b) and K/V
+    may be one pool [1, slots, Hkv, D].
     """
     from lsa_rocm_lab.port.read_kernel_tiled import sparse_read_chunked
 
-    return sparse_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale, chunk_size)
+    return sparse_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale, chunk_size, slot_table=slot_table,
+                               slot_rows=slot_rows)
 
 
 # ----------------------------------------------------------------------------- index build
@@ -718,11 +804,15 @@ def segment_starts(keys: torch.Tensor, target: int, pool: int = 16, max_size: in
     of ``pool`` positions, then the adjacent pair with the smallest Ward cost
     n_a n_b / (n_a + n_b) |mu_a - mu_b|^2 merges (ties to the leftmost pair, merges past
     ``max_size`` positions skipped) until ``target`` segments remain. Returns the segment
-    start positions [B, Hkv, target + 1] int64 (last = T). Raises ValueError when a table
-    cannot reach ``target`` under ``max_size``."""
+    start positions [B, Hkv, target + 1] int64 (last = T).
+
+    No host sync: a table that cannot reach ``target`` under ``max_size`` gets the even cut
+    (valid positions) and sets the device's pinned build status word, so the next build
+    call raises ValueError (``check_build`` syncs and raises at once)."""
     device = _on_device("segment_starts", keys)
     if keys.dim() != 4:
         raise ValueError(f"keys must be [B, T, Hkv, D], got {tuple(keys.shape)}")
+    _build_failed(device)
     if keys.stride(-1) != 1 or keys.data_ptr() % 16:
         keys = keys.contiguous()
     B, T, Hkv, D = keys.shape
@@ -733,11 +823,27 @@ def segment_starts(keys: torch.Tensor, target: int, pool: int = 16, max_size: in
     status = torch.empty(tables, dtype=torch.int32, device=device)
     _abi.call("lsa_ward_segments", keys.data_ptr(), _abi.dtype_code(keys.dtype), B, T, Hkv, D, keys.stride(0),
               keys.stride(1), keys.stride(2), pool, target, max_size, scratch.data_ptr(), scratch.numel(),
-              starts.data_ptr(), status.data_ptr(), _abi.stream(device))
-    bad = int(status.max().item())
-    if bad:
-        raise ValueError(f"segment_starts: a table cannot reach {target} segments with max_size {max_size}")
+              starts.data_ptr(), status.data_ptr(), _abi.StatusWord.get(device, "build").data_ptr(),
+              _abi.stream(device))
     return starts.view(B, Hkv, target + 1).long()
+
+
+def _build_failed(device: torch.device) -> None:
+    """Raises (and clears the word) if an earlier bucket-table build on the device could not
+    reach its segment count; reads the pinned status word, no device sync."""
+    word = _abi.StatusWord.get(device, "build")
+    if int(word[0]) != 0:
+        word.zero_()
+        raise ValueError("segment_starts: an earlier build could not reach its segment count under max_size "
+                         "(that table holds the even cut instead)")
+
+
+def check_build(device: torch.device | int | None = None) -> None:
+    """Synchronizes the device and raises ValueError if a bucket-table build on it could not
+    reach its segment count since the last check."""
+    device = torch.device("cuda", _abi.device_index(device))
+    torch.cuda.synchronize(device)
+    _build_failed(device)
 
 
 def segment_buckets(keys: torch.Tensor, target: int, pool: int = 16, max_size: int = 256, cap: int | None = None,

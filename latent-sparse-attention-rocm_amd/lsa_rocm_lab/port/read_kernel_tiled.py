@@ -55,8 +55,12 @@ def _sparse_read(q, k, v, read_ids, lengths, scale, empty_nan: bool, splits: int
     assert Hq % Hkv == 0, "query heads must group evenly onto KV heads"
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError(f"q/k/v dtypes differ: {q.dtype} {k.dtype} {v.dtype}")
+    if k.shape[0] not in (B, 1) or k.shape != v.shape:
+        raise ValueError(f"k/v {tuple(k.shape)} / {tuple(v.shape)} must hold {B} batch rows (or one shared pool)")
     q = q.contiguous()
     k, v, sb, st, sh = _kv_layout(k, v)
+    if k.shape[0] != B:  # one pool (a paged cache) read by every batch row
+        sb = 0
     rows = B * Tq
     width = read_ids.shape[-1]
     per_head = Hkv > 1 and lengths.numel() == rows * Hkv and lengths.numel() != rows
@@ -107,26 +111,35 @@ def sparse_read_auto(q, k, v, read_ids, lengths, scale=None):
     return _sparse_read(q, k, v, read_ids, lengths, scale, empty_nan=False)
 
 
-def sparse_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale=None, chunk_size: int = 64, path: str | None = None):
+def sparse_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale=None, chunk_size: int = 64, path: str | None = None,
+                        slot_table=None, slot_rows=None):
     """Chunked-prefill read: query row t reads chunk ``t // chunk_size``'s per-kv-head list
     and the chunk's causal block [chunk start, t]. chunk_lists [B, C, Hkv, W] (or
     [C, Hkv, W] for B == 1), chunk_lengths [B, C, Hkv] (or [C, Hkv]).
 
     ``path`` (default ``LSA_PREFILL_READ`` or ``auto``): ``auto`` runs the MFMA tile kernel
     where it applies (bf16/fp16, D 64/128, power-of-two chunk 16..256) and the gather kernel
-    elsewhere; ``gather`` / ``mfma`` force one (``mfma`` raises where it does not apply)."""
+    elsewhere; ``gather`` / ``mfma`` force one (``mfma`` raises where it does not apply).
+    ``slot_table`` / ``slot_rows`` (a paged cache): the causal block's positions go through
+    the slot table (rows default to the batch row); K/V may be one pool [1, slots, Hkv, D]."""
+    from lsa_rocm_lab.port.pipeline import _slot_args
+
     assert q.is_cuda and k.is_cuda and v.is_cuda, "the sparse read is a GPU kernel"
     B, T, Hq, D = q.shape
     Tk, Hkv = k.shape[1], k.shape[2]
     assert Hq % Hkv == 0, "query heads must group evenly onto KV heads"
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError(f"q/k/v dtypes differ: {q.dtype} {k.dtype} {v.dtype}")
+    if k.shape[0] not in (B, 1) or k.shape != v.shape:
+        raise ValueError(f"k/v {tuple(k.shape)} / {tuple(v.shape)} must hold {B} batch rows (or one shared pool)")
     C = -(-T // chunk_size)
     width = chunk_lists.shape[-1]
     ids = chunk_lists.to(torch.int32).reshape(B * C * Hkv, width).contiguous()
     lens = chunk_lengths.to(device=q.device, dtype=torch.int32).reshape(B * C * Hkv).contiguous()
     q = q.contiguous()
     k, v, sb, st, sh = _kv_layout(k, v)
+    if k.shape[0] != B:  # one pool (a paged cache) read by every batch row
+        sb = 0
     out = torch.empty_like(q)
     if B * T == 0:
         return out
@@ -134,7 +147,8 @@ def sparse_read_chunked(q, k, v, chunk_lists, chunk_lengths, scale=None, chunk_s
     codes = {"auto": _abi.CHUNKED_AUTO, "gather": _abi.CHUNKED_GATHER, "mfma": _abi.CHUNKED_MFMA}
     if path not in codes:
         raise ValueError(f"chunked read path must be auto|gather|mfma, got {path!r}")
+    slots, _keep = _slot_args(slot_table, slot_rows, B, q.device)
     _abi.call("lsa_read_chunked", q.data_ptr(), k.data_ptr(), v.data_ptr(), _abi.dtype_code(q.dtype), B, T, Tk, Hq,
-              Hkv, D, sb, st, sh, ids.data_ptr(), lens.data_ptr(), width, chunk_size,
+              Hkv, D, sb, st, sh, ids.data_ptr(), lens.data_ptr(), width, chunk_size, slots,
               float(D ** -0.5 if scale is None else scale), codes[path], out.data_ptr(), _abi.stream(q.device))
     return out

@@ -64,7 +64,10 @@ def select_topk_scores(scores: torch.Tensor, lengths: torch.Tensor, top_p: int) 
     return out[:, :keep].contiguous() if sampled and keep != k2 else out
 
 
-def _expand(picks, picks_are_keys, bucket_members, positions, window_size, sink_size, top_k):
+def _expand(picks, picks_are_keys, bucket_members, positions, window_size, sink_size, top_k, slot_table=None,
+            slot_rows=None):
+    from lsa_rocm_lab.port.pipeline import _slot_args
+
     device = picks.device
     picks = picks.contiguous()
     rows = picks.shape[0]
@@ -75,9 +78,10 @@ def _expand(picks, picks_are_keys, bucket_members, positions, window_size, sink_
     lengths = torch.empty(rows, device=device, dtype=torch.int32)
     if rows == 0:
         return out, lengths
+    slots, _keep = _slot_args(slot_table, slot_rows, rows, device)
     _abi.call("lsa_expand", picks.data_ptr(), 1 if picks_are_keys else 0, rows, 1, picks.shape[1],
-              members.data_ptr(), members.shape[0], members.shape[1], 0, 0, pos.data_ptr(), window_size, sink_size,
-              top_k, out.data_ptr(), lengths.data_ptr(), _abi.stream(device))
+              members.data_ptr(), members.shape[0], members.shape[1], 0, 0, pos.data_ptr(), slots, window_size,
+              sink_size, top_k, out.data_ptr(), lengths.data_ptr(), _abi.stream(device))
     return out, lengths
 
 
@@ -88,6 +92,8 @@ def expand_in_order_from_keys(
     window_size: int,
     sink_size: int,
     top_k: int,
+    slot_table: torch.Tensor | None = None,
+    slot_rows: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Read lists from ordered packed keys (reference select_fused.py:217-280).
 
@@ -98,6 +104,9 @@ def expand_in_order_from_keys(
         window_size: Recent positions read whole.
         sink_size: First positions read whole.
         top_k: Bucket members read at most.
+        slot_table: A paged cache's slot table [n_rows, width] int32 (the kernel's
+            ``MAP_SLOTS`` path, :147-205): every listed id is stored as its cache row.
+        slot_rows: Each row's slot-table row [R] int32.
 
     Returns:
         Read lists [R, top_k + window_size + sink_size] int32, -1 padded, and lengths [R].
@@ -113,7 +122,8 @@ def expand_in_order_from_keys(
             f"bucket_cap {bucket_cap} yields a non-power-of-two walk tile {tile * bucket_cap} "
             "- use a power-of-two bucket_cap (production: 16)"
         )
-    return _expand(ordered_keys, True, bucket_members, positions, window_size, sink_size, top_k)
+    return _expand(ordered_keys, True, bucket_members, positions, window_size, sink_size, top_k, slot_table,
+                   slot_rows)
 
 
 def expand_in_order(

@@ -225,6 +225,36 @@ def node_tree(buckets: Buckets, node_size: int = 16) -> Hierarchy:
     return Hierarchy(levels=[NodeLevel(n32, children, None, n16)])
 
 
+@dataclass
+class PagedCache:
+    """A cache moved into one pool of fixed-size pages, in shuffled page order."""
+
+    k: torch.Tensor           # [1, pool_rows, Hkv, D]: every batch row's pages
+    v: torch.Tensor
+    slot_table: torch.Tensor  # [B, T] int32: (batch row, position) -> pool row
+
+
+def paged(k: torch.Tensor, v: torch.Tensor, page: int = 16, seed: int = 0, spare_pages: int = 0) -> PagedCache:
+    """A paged copy of a cache k/v [B, T, Hkv, D]: every batch row's positions cut into
+    pages of ``page`` tokens, all rows' pages (plus ``spare_pages`` unused ones) placed in a
+    seeded random order in one pool, and the slot table mapping each (row, position) to
+    its pool row - the layout a serving engine's page allocator leaves behind (``page=1``:
+    every token on its own, the worst case for locality)."""
+    B, T, Hkv, D = k.shape
+    per_row = -(-T // page)
+    n_pages = B * per_row + spare_pages
+    g = torch.Generator().manual_seed(seed)
+    where = torch.randperm(n_pages, generator=g)[: B * per_row].view(B, per_row)  # page j of row b
+    slots = (where[:, :, None] * page + torch.arange(page)).reshape(B, per_row * page)[:, :T]
+    slots = slots.to(device=k.device, dtype=torch.int32).contiguous()
+    pool_k = torch.zeros(1, n_pages * page, Hkv, D, dtype=k.dtype, device=k.device)
+    pool_v = torch.zeros_like(pool_k)
+    flat = slots.reshape(-1).long()
+    pool_k[0, flat] = k.reshape(B * T, Hkv, D)
+    pool_v[0, flat] = v.reshape(B * T, Hkv, D)
+    return PagedCache(pool_k, pool_v, slots)
+
+
 # ----------------------------------------------------------------------------- configs
 
 DECODE_2K = PortConfig(cluster_block_size=64, bucket_size=64, bucket_cap=64, top_p=7, top_k=384,

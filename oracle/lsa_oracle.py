@@ -38,6 +38,9 @@ Pinning (what each function is checked against in tests/test_oracle.py):
   ward_segments_keys             brute force (every adjacent cost recomputed from the
                                  segments each step, no links), two-cluster closed form,
                                  invariants (contiguous cover, target count, max_size)
+  map_slots                      the identity table is the identity; a permutation's inverse
+                                 recovers the logical lists; the read over a row-shuffled
+                                 pool with mapped lists equals the unpaged read
   window/sink tail order         PARITY UNPINNED (upstream _append_window_and_sink is not
                                  available); the tail SET is pinned by causality and the
                                  read output is order-invariant.
@@ -200,6 +203,33 @@ def expand_in_order(picks: np.ndarray, members: np.ndarray, positions: np.ndarra
         table = members if members.ndim == 2 else members[r]
         lists[r], lengths[r] = expand_row(picks[r], table, int(positions[r]), window, sink, top_k)
     return lists, lengths
+
+
+def map_slots(lists: np.ndarray, lengths: np.ndarray, slot_table: np.ndarray,
+              slot_rows: np.ndarray) -> np.ndarray:
+    """A paged cache's read lists (reference select_fused.py:176-178, :197-199, :205, the
+    ``MAP_SLOTS`` path of the expansion): every listed id - the kept ids and the
+    window/sink tail, chosen on logical positions first - becomes
+    ``slot_table[slot_rows[r], id]``; the -1 padding stays. An id at or past the table's
+    width (or a table row outside the table) maps to -1 here, where the reference's masked
+    load has no bound. lists [R, ..., W] with lengths [R, ...]; slot_table [n_rows, width],
+    slot_rows [R]."""
+    lists = np.asarray(lists)
+    lengths = np.asarray(lengths)
+    table = np.asarray(slot_table).reshape(-1, np.asarray(slot_table).shape[-1])
+    out = np.full_like(lists, -1)
+    width = lists.shape[-1]
+    for r in range(lists.shape[0]):
+        k = int(slot_rows[r])
+        row = table[k] if 0 <= k < table.shape[0] else np.zeros(0, dtype=table.dtype)
+        lr, nr = lists[r].reshape(-1, width), lengths[r].reshape(-1)
+        o = out[r].reshape(-1, width)
+        for g in range(lr.shape[0]):
+            n = int(nr[g])
+            ids = lr[g, :n].astype(np.int64)
+            ok = (ids >= 0) & (ids < row.size)
+            o[g, :n] = np.where(ok, row[np.where(ok, ids, 0)] if row.size else -1, -1)
+    return out
 
 
 def visible_counts(positions: np.ndarray, rows: int, cluster_block_size: int, block_buckets: int,

@@ -29,7 +29,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_version_and_error_string():
     lib = _abi.load()
-    assert lib.lsa_abi_version() == 2
+    assert lib.lsa_abi_version() == 3
     assert isinstance(lib.lsa_last_error(), bytes)
 
 
@@ -38,8 +38,8 @@ def test_null_pointers_rejected_before_launch():
         _abi.call("lsa_read", None, None, None, 1, 1, 1, 8, 8, 2, 64, 1024, 128, 64, None, None, 4, 0, 0.1, 0, 1, None,
                   None, 0, None, None)
     with pytest.raises(ValueError, match="NULL"):
-        _abi.call("lsa_select_flat", None, 1, 1, 8, 128, None, None, None, 0, 512, 256, 0, 1, 0, None, 64, 1, 32, 0, 0,
-                  8192, 8, None, None, 0, None, None, None)
+        _abi.call("lsa_select_flat", None, 1, 1, 8, 128, None, None, None, 0, 512, 256, 0, 1, 0, None, None, 64, 1, 32,
+                  0, 0, 8192, 8, None, None, 0, None, None, None)
 
 
 @pytest.mark.parametrize("dim", [8, 100, 512])
@@ -71,8 +71,8 @@ def test_workspace_required_for_split_reads():
 def test_select_limits_rejected():
     # 8192 columns in one split exceed the LDS key budget
     with pytest.raises(ValueError, match="exceed"):
-        _abi.call("lsa_select_flat", 16, 1, 1, 1, 128, 16, 16, None, 0, 8192, 16, 0, 0, 0, 16, 512, 64, 32, 0, 0, 64, 1,
-                  None, None, 0, 16, 16, None)
+        _abi.call("lsa_select_flat", 16, 1, 1, 1, 128, 16, 16, None, 0, 8192, 16, 0, 0, 0, 16, None, 512, 64, 32, 0, 0,
+                  64, 1, None, None, 0, 16, 16, None)
 
 
 def _beam_args(levels=3, n_nodes=(1024, 256, 64), **kw):
@@ -83,7 +83,7 @@ def _beam_args(levels=3, n_nodes=(1024, 256, 64), **kw):
     args = dict(q=16, q_dtype=_abi.LSA_F32, R=1, G=1, D=128, n_levels=levels, cents=ctypes.addressof(ptrs),
                 kids=ctypes.addressof(ptrs), n_nodes=ctypes.addressof(counts), node_size=4, node_block=64,
                 top_level=3, centroids=16, members=16, ends=None, flags=0, rows=4096, cap=16, row_tables=0,
-                group_tables=0, mode=_abi.SCORE_F32, pos=16, cbs=512, bb=64, beam=64, top_p=1024, window=512,
+                group_tables=0, mode=_abi.SCORE_F32, pos=16, slots=None, cbs=512, bb=64, beam=64, top_p=1024, window=512,
                 sink=4, top_k=4096, lists=16, lengths=16, stream=None)
     args.update(kw)
     return [ptrs, counts], list(args.values())
@@ -118,7 +118,8 @@ def _decode_args(**kw):
     pointers; kw overrides by name."""
     args = dict(q=16, k=16, v=16, dtype=_abi.LSA_BF16, R=1, Tk=32768, Hq=32, Hkv=8, D=128, sb=0, st=1024, sh=128,
                 cent=16, members=16, ends=None, flags=0, rows=512, cap=256, row_tables=0, group_tables=1,
-                mode=_abi.SCORE_BF16, pos=16, cbs=64, bb=1, top_p=32, window=0, sink=0, top_k=8192, scale=0.088,
+                mode=_abi.SCORE_BF16, pos=16, slots=None, cbs=64, bb=1, top_p=32, window=0, sink=0, top_k=8192,
+                scale=0.088,
                 splits=16, readers=0, counters=16, n_counters=1 << 20, scratch=16, scratch_bytes=1 << 30, lists=16,
                 lengths=16, out=16, status=None, stream=None)
     args.update(kw)
@@ -190,7 +191,7 @@ def test_chunked_read_paths():
     assert lib.lsa_read_chunked_mfma_ok(_abi.LSA_F32, 128, 64) == 0
     assert lib.lsa_read_chunked_mfma_ok(_abi.LSA_BF16, 256, 64) == 0
     assert lib.lsa_read_chunked_mfma_ok(_abi.LSA_BF16, 128, 48) == 0
-    base = [16, 16, 16, _abi.LSA_F32, 1, 128, 128, 8, 2, 64, 0, 128, 64, 16, 16, 8, 64, 0.125]
+    base = [16, 16, 16, _abi.LSA_F32, 1, 128, 128, 8, 2, 64, 0, 128, 64, 16, 16, 8, 64, None, 0.125]
     with pytest.raises(ValueError, match="MFMA path"):
         _abi.call("lsa_read_chunked", *base, _abi.CHUNKED_MFMA, 16, None)
     with pytest.raises(ValueError, match="path"):
@@ -207,10 +208,12 @@ def test_segment_build_arguments_rejected_before_launch():
         a = dict(B=1, T=32768, H=8, D=128, pool=16, target=512, max_size=256, scratch_bytes=1 << 30)
         a.update(kw)
         _abi.call("lsa_ward_segments", p, _abi.LSA_BF16, a["B"], a["T"], a["H"], a["D"], a["T"] * a["H"] * a["D"],
-                  a["H"] * a["D"], a["D"], a["pool"], a["target"], a["max_size"], p, a["scratch_bytes"], p, p, None)
+                  a["H"] * a["D"], a["D"], a["pool"], a["target"], a["max_size"], p, a["scratch_bytes"], p, p, None,
+                  None)
 
     with pytest.raises(ValueError, match="NULL"):
-        _abi.call("lsa_ward_segments", None, _abi.LSA_BF16, 1, 64, 1, 64, 0, 64, 0, 16, 2, 64, p, 1 << 20, p, p, None)
+        _abi.call("lsa_ward_segments", None, _abi.LSA_BF16, 1, 64, 1, 64, 0, 64, 0, 16, 2, 64, p, 1 << 20, p, p, None,
+                  None)
     with pytest.raises(ValueError, match="pools exceed"):
         call(pool=4)  # 8192 pools
     with pytest.raises(ValueError, match="target"):
@@ -220,7 +223,31 @@ def test_segment_build_arguments_rejected_before_launch():
     with pytest.raises(ValueError, match="scratch"):
         call(scratch_bytes=1024)
     with pytest.raises(ValueError, match="dtype"):
-        _abi.call("lsa_ward_segments", p, 9, 1, 64, 1, 64, 0, 64, 0, 16, 2, 64, p, 1 << 20, p, p, None)
+        _abi.call("lsa_ward_segments", p, 9, 1, 64, 1, 64, 0, 64, 0, 16, 2, 64, p, 1 << 20, p, p, None, None)
+
+
+def _slots(table=16, rows=16, stride=32768, width=32768, n_rows=1):
+    return ctypes.pointer(_abi.SlotMap(table, rows, stride, width, n_rows))
+
+
+def test_slot_maps_rejected_before_launch():
+    """A paged cache's slot map (lsa_slot_map) is checked on the host by every entry that
+    takes one: a NULL table or rows, no rows, a width below 1 or a stride below the width."""
+    for bad, what in ((_slots(table=None), "NULL"), (_slots(rows=None), "NULL"), (_slots(n_rows=0), "n_rows"),
+                      (_slots(width=0), "width"), (_slots(stride=100, width=200), "stride")):
+        with pytest.raises(ValueError, match=what):
+            _abi.call("lsa_decode_flat", *_decode_args(slots=bad))
+        with pytest.raises(ValueError, match=what):
+            _abi.call("lsa_expand", 16, 0, 1, 1, 32, 16, 512, 16, 0, 0, 16, bad, 0, 0, 64, 16, 16, None)
+        with pytest.raises(ValueError, match=what):
+            _abi.call("lsa_select_flat", 16, 1, 1, 1, 128, 16, 16, None, 0, 512, 16, 0, 0, 0, 16, bad, 512, 64, 32,
+                      0, 0, 64, 1, None, None, 0, 16, 16, None)
+        keep, args = _beam_args(slots=bad)
+        with pytest.raises(ValueError, match=what):
+            _abi.call("lsa_select_beam", *args)
+        with pytest.raises(ValueError, match=what):
+            _abi.call("lsa_read_chunked", 16, 16, 16, _abi.LSA_BF16, 1, 128, 128, 8, 2, 64, 0, 128, 64, 16, 16, 8, 64,
+                      bad, 0.125, _abi.CHUNKED_AUTO, 16, None)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -5,7 +5,8 @@ Segment starts must equal the oracle's bit for bit (the merge order depends on e
 costs). Cases: fp32 / bf16 / fp16 keys, head dims 32 / 64 / 128, pool sizes 4 / 8 / 16, a
 shorter last pool, several (batch, kv-head) tables with strided cache views, the 32k
 table of the benchmark geometry, ties (identical keys merge leftmost first), a target no
-merge can reach under max_size (ValueError), and the tables feeding the fused decode
+merge can reach under max_size (reported without a sync: check_build raises ValueError), and
+the tables feeding the fused decode
 (lists equal the oracle's flat select over the same tables). The block-structured build
 (the reference's closed cluster blocks, 64 buckets of at most 16 keys a 512-key block)
 matches the oracle per block and drives the flat select; a cache extended block by block
@@ -72,8 +73,9 @@ def test_segment_starts_32k_table():
 def test_ties_merge_leftmost_and_unreachable_target_raises():
     keys = torch.ones(1, 64, 1, 64, dtype=torch.float32, device=DEV)
     assert pipeline.segment_starts(keys, 3, 8, 64).cpu().tolist() == [[[0, 48, 56, 64]]]
-    with pytest.raises(ValueError, match="cannot reach"):
-        pipeline.segment_starts(keys, 3, 8, 8)
+    pipeline.segment_starts(keys, 3, 8, 8)
+    with pytest.raises(ValueError, match="could not reach"):
+        pipeline.check_build()
 
 
 def test_built_tables_drive_the_fused_decode():

@@ -250,6 +250,59 @@ def test_chunked_read_is_shared_list_plus_causal_block():
     assert np.allclose(got[:, row], want[:, 0])
 
 
+def _paged_case():
+    """Logical lists of a small flat select, a row-shuffled pool and its slot table."""
+    T, Hkv, D = 96, 2, 16
+    k = RNG.standard_normal((1, T, Hkv, D)).astype(np.float32)
+    v = RNG.standard_normal((1, T, Hkv, D)).astype(np.float32)
+    q = RNG.standard_normal((1, 2, 4, D)).astype(np.float32)
+    cents = RNG.standard_normal((12, D)).astype(np.float32)
+    members = np.arange(96, dtype=np.int32).reshape(12, 8)
+    lists, lengths = oracle.flat_select(RNG.standard_normal((2, D)).astype(np.float32), np.array([95, 60]), cents,
+                                        members, cluster_block_size=8, block_buckets=1, top_p=4, top_k=16,
+                                        window=8, sink=2, mode="fp32")
+    perm = RNG.permutation(T).astype(np.int32)  # logical t lives in pool row perm[t] (rows >= T unused)
+    pool_k = np.zeros((1, T + 20, Hkv, D), np.float32)
+    pool_v = np.zeros_like(pool_k)
+    pool_k[0, perm], pool_v[0, perm] = k[0], v[0]
+    return q, k, v, lists, lengths, perm, pool_k, pool_v
+
+
+def test_map_slots_identity_inverse_and_bounds():
+    q, k, v, lists, lengths, perm, pool_k, pool_v = _paged_case()
+    ident = np.arange(96, dtype=np.int32)[None]
+    assert np.array_equal(oracle.map_slots(lists, lengths, ident, np.zeros(2)), lists)
+    mapped = oracle.map_slots(lists, lengths, perm[None], np.zeros(2))
+    inv = np.full(perm.max() + 1, -1)
+    inv[perm] = np.arange(perm.size)
+    for r in range(2):
+        n = int(lengths[r])
+        assert np.array_equal(inv[mapped[r, :n]], lists[r, :n])  # the permutation's inverse recovers them
+        assert (mapped[r, n:] == -1).all()  # padding stays -1
+    # two table rows: query row r reads its own row
+    two = np.stack([perm, perm[::-1]])
+    m2 = oracle.map_slots(lists, lengths, two, np.array([1, 0]))
+    assert np.array_equal(m2[1, : lengths[1]], perm[lists[1, : lengths[1]]])
+    assert np.array_equal(m2[0, : lengths[0]], perm[::-1][lists[0, : lengths[0]]])
+    # ids at or past the width, and a row outside the table, map to -1
+    short = perm[None, :50]
+    ms = oracle.map_slots(lists, lengths, short, np.zeros(2))
+    n0 = int(lengths[0])
+    assert np.array_equal(ms[0, :n0], np.where(lists[0, :n0] < 50, perm[np.minimum(lists[0, :n0], 49)], -1))
+    assert (oracle.map_slots(lists, lengths, perm[None], np.array([3, -1]))[:, :n0] == -1).all()
+
+
+def test_read_over_a_shuffled_pool_equals_the_unpaged_read():
+    q, k, v, lists, lengths, perm, pool_k, pool_v = _paged_case()
+    mapped = oracle.map_slots(lists, lengths, perm[None], np.zeros(2))
+    want = oracle.sparse_read(q, k, v, lists[None], lengths[None])
+    got = oracle.sparse_read(q, pool_k, pool_v, mapped[None], lengths[None])
+    assert np.array_equal(got, want)
+    # the transposed map (the inverse permutation) reads other rows: its read must differ
+    wrong = oracle.map_slots(lists, lengths, np.argsort(perm).astype(np.int32)[None], np.zeros(2))
+    assert not np.allclose(oracle.sparse_read(q, pool_k, pool_v, wrong[None], lengths[None]), want, atol=1e-3)
+
+
 # ----------------------------------------------------------------------------- selection end to end
 
 
