@@ -59,6 +59,23 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+class select_impl:
+    """Sets LSA_SELECT_IMPL for a block and restores the caller's value after it."""
+
+    def __init__(self, impl: str):
+        self.impl, self.prev = impl, None
+
+    def __enter__(self):
+        self.prev = os.environ.get("LSA_SELECT_IMPL")
+        os.environ["LSA_SELECT_IMPL"] = self.impl
+
+    def __exit__(self, *exc):
+        if self.prev is None:
+            os.environ.pop("LSA_SELECT_IMPL", None)
+        else:
+            os.environ["LSA_SELECT_IMPL"] = self.prev
+
+
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -73,6 +90,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--tree-steps", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-build", action="store_true", help="skip the bucket-table build leg")
+    ap.add_argument("--no-paged", action="store_true", help="skip the paged-cache decode leg")
+    ap.add_argument("--no-refcfg-prefill", action="store_true",
+                    help="skip the reference-knob prefill leg (32768 per-row selections)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run 3 plain device copies of this many MiB (calibrates HBM byte counters)")
     return ap.parse_args()
@@ -98,7 +118,7 @@ def copy_cache(c: DecodeCache):
     b = c.buckets
     nb = Buckets(b.centroids.clone(), b.members.clone(), b.sizes.clone(),
                  centroids_f32=None if b.centroids_f32 is None else b.centroids_f32.clone(),
-                 ends=None if b.ends is None else b.ends.clone(), spans=b.spans)
+                 ends=None if b.ends is None else b.ends.clone(), spans=b.spans, block_visible=b.block_visible)
     return DecodeCache(c.q.clone(), c.k.clone(), c.v.clone(), nb, c.pos.clone())
 
 
@@ -331,8 +351,8 @@ def batched_flat_leg(args, torch, np):
     us = graph_launch_us(step, NQ, max(1, args.tree_steps // NQ), torch)
     gbps = gathered / (us * 1e-6) / 1e9
     idx = pipeline.index_queries(qs[0], HKV)[:, 0]
-    os.environ["LSA_SELECT_IMPL"] = "fused"
-    l2, n2 = pipeline.flat_select(idx, pos, buckets, config)
+    with select_impl("fused"):
+        l2, n2 = pipeline.flat_select(idx, pos, buckets, config)
     same = bool(torch.equal(l2, res[0][0]) and torch.equal(n2, res[0][1]))
     log(f"batched flat decode B={B}: {us:.1f} us/step, {gbps:.0f} GB/s on {gathered / 1e6:.1f} MB gathered")
     del data
@@ -491,7 +511,6 @@ def refcfg_decode_leg(args, torch, np, dense_us):
     tree = pipeline.build_hierarchy_gpu(idx_k, buckets, config)
     pos = torch.arange(T - NQ, T, device="cuda", dtype=torch.int32)
     qs = [q[:, T - NQ + i:T - NQ + i + 1].contiguous() for i in range(NQ)]
-    os.environ["LSA_SELECT_IMPL"] = "fused"
     sel = {"flat": lambda i: pipeline.flat_select(idx_q[i:i + 1], pos[i:i + 1], buckets, config),
            "tree": lambda i: pipeline.tree_select(idx_q[i:i + 1], pos[i:i + 1], buckets, tree, config)}
     out = {}
@@ -546,6 +565,116 @@ def refcfg_decode_leg(args, torch, np, dense_us):
     return {"workload": "refcfg_decode_32k", "batch": 1, "context": T, "buckets": buckets.rows,
             "nodes": [lv.centroids.shape[0] for lv in tree.levels], "knobs": "reference PortConfig defaults",
             "timing": "hip graphs of back-to-back steps over 4 query tokens, HIP events", **out}
+
+
+def refcfg_prefill_leg(args, torch, np, dense_ms):
+    """The reference's own prefill arm at its default knobs (port/bench.py:113-154 with
+    phase="prefill": every query row selects its own keys, then the per-row read; PortConfig
+    defaults, pipeline.py:32-54: 512-key blocks of 64 buckets of at most 16 keys, top_p 1024
+    of up to 4096 visible buckets, top_k 4096, window 512, sink 4, one index-space table
+    shared by every head) on its benchmark geometry at 32k with Hq 32 / Hkv 8, D 128 bf16.
+    A step is the fused select of all 32768 rows (lists [32768, 4612]) and the split-K
+    read of every row's list for every head (the lists are shared by the heads). Timed by
+    HIP events around whole steps (median of --prefill-steps) and each stage alone; the
+    dense comparator is causal flash SDPA on the same tensors. Lists of 16 sampled rows
+    bit-exact against the oracle, two rows' read within the bf16 bar."""
+    import oracle
+    from lsa_rocm_lab import workloads
+    from lsa_rocm_lab.port import pipeline
+    from lsa_rocm_lab.port.pipeline import PortConfig
+    from lsa_rocm_lab.port.read_kernel_tiled import sparse_read_auto
+
+    cfg = PortConfig()
+    T = T_CTX
+    ws = workloads.index_space(T)
+    pos = torch.arange(T, device="cuda", dtype=torch.int32)
+    scale = D ** -0.5
+
+    def select():
+        return pipeline.flat_select(ws.idx_q, pos, ws.buckets, cfg)
+
+    def step():
+        lists, lengths = select()
+        return sparse_read_auto(ws.q, ws.k, ws.v, lists[None], lengths[None], scale), lists, lengths
+
+    out, lists, lengths = step()
+    torch.cuda.synchronize()
+    n = max(1, args.prefill_steps)
+    step_ms = statistics.median(event_launch_times(lambda i: step(), n, torch))
+    sel_ms = statistics.median(event_launch_times(lambda i: select(), n, torch))
+    read_ms = statistics.median(event_launch_times(
+        lambda i: sparse_read_auto(ws.q, ws.k, ws.v, lists[None], lengths[None], scale), n, torch))
+    keys = float(lengths.to(torch.float64).sum().item())
+    gathered = keys * HKV * D * 2 * 2  # K and V rows of every kv-head, bf16
+    flops = 4.0 * D * keys * HQ
+    rows = [0, 511, 512, 1024, 4096, 8191, 12345, 16384, 20000, 24576, 28000, 30000, 32255, 32256, 32700, 32767]
+    want_l, want_n = oracle.flat_select(ws.idx_q[rows].cpu().numpy(), np.array(rows),
+                                        ws.buckets.centroids.float().cpu().numpy(), ws.buckets.members.cpu().numpy(),
+                                        cluster_block_size=cfg.cluster_block_size,
+                                        block_buckets=cfg.block_bucket_count, top_p=cfg.top_p, top_k=cfg.top_k,
+                                        window=cfg.window_size, sink=cfg.sink_size, mode="bf16")
+    exact = bool(np.array_equal(lists[rows].cpu().numpy(), want_l)
+                 and np.array_equal(lengths[rows].cpu().numpy(), want_n))
+    two = [4096, 32767]
+    want = oracle.sparse_read(ws.q[:, two].float().cpu().numpy(), ws.k.float().cpu().numpy(),
+                              ws.v.float().cpu().numpy(), lists[two].cpu().numpy()[None],
+                              lengths[two].cpu().numpy()[None], scale)
+    err = np.abs(out[:, two].float().cpu().numpy() - want)
+    res = {"workload": "refcfg_prefill_32k", "batch": 1, "context": T, "heads_q": HQ, "heads_kv": HKV, "head_dim": D,
+           "knobs": "reference PortConfig defaults", "buckets": ws.buckets.rows, "list_width": int(lists.shape[1]),
+           "ms_per_step": round(step_ms, 3), "tok_per_s": round(T / (step_ms * 1e-3), 1),
+           "select_ms": round(sel_ms, 3), "read_ms": round(read_ms, 3),
+           "keys_per_row": round(keys / T, 1), "read_gathered_bytes": gathered,
+           "read_gbps": round(gathered / (read_ms * 1e-3) / 1e9, 1),
+           "read_tflops": round(flops / (read_ms * 1e-3) / 1e12, 2),
+           "dense_sdpa_ms": None if dense_ms is None else round(dense_ms, 3),
+           "speedup_vs_dense": None if dense_ms is None else round(dense_ms / step_ms, 3),
+           "reference_gfx1151_ms": 347.086,
+           "timing": f"HIP events around whole steps, median of {n}",
+           "parity": {"lists_bit_exact_sampled": exact, "rows_checked": len(rows), "read_max_abs": float(err.max()),
+                      "read_mean_abs": float(err.mean())}}
+    log(f"refcfg prefill {res}")
+    del ws
+    return res
+
+
+def paged_decode_leg(args, torch, np, caches, R, config, lists0, lengths0, out0):
+    """The headline decode over a paged cache: every rotation copy's K/V moved into one pool
+    of 16-token pages in shuffled order (and of single tokens: page 1), the slot table
+    handed to the same fused kernel (the expansion maps every listed id once; the gather
+    reads pool rows). A/B against the unpaged step in the same process, each a HIP graph of
+    back-to-back steps over the rotation; lists checked against the unpaged lists mapped
+    through the table, outputs equal to the unpaged step's."""
+    from lsa_rocm_lab import workloads
+    from lsa_rocm_lab.port import pipeline
+
+    reps = max(1, args.kernel_launches // R)
+    base_us = graph_launch_us(lambda i: decode_step(caches[i % R], config), R, reps, torch)
+    res = {"workload": "flat_decode_32k_paged", "unpaged_us_per_step": round(base_us, 3)}
+    t = lists0[0].cpu().numpy()
+    for page in (16, 1):
+        pools = [workloads.paged(c.k, c.v, page=page, seed=page) for c in caches]
+
+        def step(i, pools=pools):
+            c, pc = caches[i % R], pools[i % R]
+            return pipeline.flat_decode(c.q, pc.k, pc.v, c.pos, c.buckets, config, scale=D ** -0.5,
+                                        slot_table=pc.slot_table)
+
+        out1, l1, n1 = step(0)
+        torch.cuda.synchronize()
+        table = pools[0].slot_table[0].cpu().numpy()
+        n = lengths0[0].cpu().numpy()
+        want = np.full_like(t, -1)
+        for g in range(t.shape[0]):
+            want[g, : n[g]] = table[t[g, : n[g]]]
+        same = bool(np.array_equal(l1[0].cpu().numpy(), want) and torch.equal(n1, lengths0)
+                    and torch.equal(out1, out0))
+        us = graph_launch_us(step, R, reps, torch)
+        res[f"page{page}"] = {"us_per_step": round(us, 3), "vs_unpaged": round(us / base_us, 4),
+                              "lists_are_mapped_unpaged_lists_and_outputs_equal": same}
+        log(f"paged decode page {page}: {us:.2f} us/step against {base_us:.2f} unpaged; exact {same}")
+        del pools
+    return res
 
 
 # ----------------------------------------------------------------------------- config 1 and the CPU
@@ -739,9 +868,7 @@ def main() -> int:
     import numpy as np
     import torch
 
-    from lsa_rocm_lab import _abi, workloads
-    from lsa_rocm_lab.port import pipeline
-    from lsa_rocm_lab.port.read_kernel_tiled import sparse_read_auto
+    from lsa_rocm_lab import _abi
 
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
@@ -749,7 +876,17 @@ def main() -> int:
     _abi.load()  # fails loudly without the HIP library
     torch.cuda.set_device(0)
     dev = "cuda"
-    os.environ["LSA_SELECT_IMPL"] = "fused"
+    # every select in this run is the fused HIP kernel; the caller's setting is restored after
+    with select_impl("fused"):
+        return run(args, np, torch, dev)
+
+
+def run(args, np, torch, dev) -> int:
+    """Every leg of the benchmark, in one process; prints the JSON line."""
+    from lsa_rocm_lab import workloads
+    from lsa_rocm_lab.port import pipeline
+    from lsa_rocm_lab.port.read_kernel_tiled import sparse_read_auto
+
     config = workloads.FLAT_32K
 
     # ---- workload (seeded CPU draw, identical on every machine)
@@ -831,6 +968,9 @@ def main() -> int:
     log(f"fused decode kernel {fused_us:.2f} us per launch: {achieved:.0f} GB/s on gathered bytes; "
         f"unfused step {unfused_us:.2f} us (select {sel_us:.2f} + read {read_us:.2f} + index queries); "
         f"unfused lists identical: {unfused_same}")
+
+    # ---- the same decode over a paged cache (slot table), A/B against the unpaged step
+    paged = None if args.no_paged else paged_decode_leg(args, torch, np, caches, R, config, lists0, lengths0, out0)
 
     # ---- dense comparators on the same rotation
     dense = dense_leg(caches, R, us_step, torch)
@@ -915,6 +1055,11 @@ def main() -> int:
     if not args.no_tree:
         refcfg = refcfg_decode_leg(args, torch, np, dense.get("us_per_step") if dense else None)
 
+    # ---- the reference's prefill arm at its default knobs (per-row selection, per-row read)
+    refcfg_p = None
+    if not args.no_refcfg_prefill:
+        refcfg_p = refcfg_prefill_leg(args, torch, np, prefill.get("dense_sdpa_ms") if prefill else None)
+
     # ---- the bucket-table build (the index build before the path)
     build = None
     if not args.no_build:
@@ -992,6 +1137,8 @@ def main() -> int:
         "kernel_timing": "per launch, HIP graph of back-to-back launches over the rotation, HIP events",
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("decode_flat_kernel"),
+                     "traffic_source": "not measured in this run: the rocprofv3 FETCH_SIZE + WRITE_SIZE figure "
+                                       "of this kernel committed in profiles/decode_flat32k_pmc.md",
                      "kernel": "decode_flat_kernel<bf16,bf16,128,4>", "bytes_per_launch": gathered,
                      "all_bytes_per_launch": total_bytes},
         "dense": dense,
@@ -1003,6 +1150,8 @@ def main() -> int:
         "batched_flat_decode": batched,
         "tree_decode": tree,
         "refcfg_decode": refcfg,
+        "refcfg_prefill": refcfg_p,
+        "paged_decode": paged,
         "bucket_build": build,
         "cpu_baseline": cpu,
         "parity": parity,

@@ -281,6 +281,11 @@ int lsa_read_chunked_mfma_ok(int dtype, int32_t D, int32_t chunk);
  * reading the member rows (the same lists). Requires ends.
  * Limits: top_p (capped at rows) <= 64; head dim {32,64,128,256}; group {1,2,4,8}. */
 #define LSA_TABLE_SPANS 1
+/* Table flag (every select and decode entry): visibility by the closed-block rule (pos //
+ * cluster_block_size * block_buckets), as for tables without ends, while the ends serve the
+ * span expansion only. Positional block tables (reference pipeline.py:378-403) are spans,
+ * but a block is visible only once closed (pipeline.py:184-186), not when its span ends. */
+#define LSA_TABLE_BLOCK_VISIBLE 2
 int64_t lsa_decode_flat_counters(int64_t R, int32_t Hkv, int32_t rows, int32_t top_p);
 /* 1 when lsa_decode_flat's replicated form (select_splits 0) serves this shape. */
 int lsa_decode_flat_rep_ok(int dtype, int32_t D, int32_t group, int32_t rows, int32_t top_p, int score_mode,

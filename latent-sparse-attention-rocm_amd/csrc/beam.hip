@@ -42,6 +42,7 @@ struct BeamArgs {
   int cluster_block, block_buckets;
   int top_p, window, sink, top_k;
   int spans;   // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0), top_p <= 64
+  const int32_t* vends;  // the ends that decide visibility (nullptr: the closed-block rule)
   int screen;  // bf16 tables of a head dim screen_topk serves
   int cand_pow2, beam_pow2, top_pow2, carry_cap;
   SlotMap slots;  // a paged cache's slot table (table == nullptr: none)
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_beam_kernel(const QT* q, boo
   float qs[SPAN];
   load_query_slice<QT, SPAN>(q + i * D, threadIdx.x & 15, bf16_mode, qs);
   const int visible =
-      max(0, a.ends ? visible_count_block(position, a.rows, a.ends + t * a.rows, vis_lds)
+      max(0, a.vends ? visible_count_block(position, a.rows, a.vends + t * a.rows, vis_lds)
                     : visible_count(position, a.rows, a.cluster_block, a.block_buckets, nullptr));
 
   // the row's growth
@@ -219,8 +220,10 @@ extern "C" int lsa_select_beam(const void* queries, int q_dtype, int64_t R, int3
   LSA_REQUIRE(beam_width >= 1 && top_p >= 1 && window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE,
               "lsa_select_beam: beam_width, top_p >= 1; window, sink, top_k >= 0");
   LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "lsa_select_beam: cluster_block_size must be >= 1");
-  LSA_REQUIRE((table_flags & ~LSA_TABLE_SPANS) == 0, LSA_ERR_SHAPE, "lsa_select_beam: unknown table flags %d",
-              table_flags);
+  LSA_REQUIRE((table_flags & ~(LSA_TABLE_SPANS | LSA_TABLE_BLOCK_VISIBLE)) == 0, LSA_ERR_SHAPE,
+              "lsa_select_beam: unknown table flags %d", table_flags);
+  LSA_REQUIRE(!(table_flags & LSA_TABLE_BLOCK_VISIBLE) || cluster_block_size >= 1, LSA_ERR_SHAPE,
+              "lsa_select_beam: cluster_block_size must be >= 1");
   LSA_REQUIRE(!(table_flags & LSA_TABLE_SPANS) || ends, LSA_ERR_SHAPE,
               "lsa_select_beam: LSA_TABLE_SPANS needs the span ends");
   const int levels = n_levels < top_level ? n_levels : top_level;
@@ -256,6 +259,7 @@ extern "C" int lsa_select_beam(const void* queries, int q_dtype, int64_t R, int3
   }
   a.n_levels = levels; a.node_size = node_size; a.node_block = node_block; a.beam = beam_width;
   a.centroids = centroids; a.members = members; a.ends = ends; a.rows = rows; a.cap = cap;
+  a.vends = (table_flags & LSA_TABLE_BLOCK_VISIBLE) ? nullptr : ends;
   a.row_tables = row_tables; a.group_tables = group_tables; a.positions = positions;
   a.cluster_block = cluster_block_size; a.block_buckets = block_buckets;
   a.top_p = top_p; a.window = window; a.sink = sink; a.top_k = top_k;

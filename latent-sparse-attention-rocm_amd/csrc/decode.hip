@@ -119,6 +119,7 @@ size_t rep_lds_d(int D, int gq, int span) {
 // Why the replicated select cannot serve a shape (nullptr: it can).
 const char* rep_unfit(int dtype, int D, int gq, int rows, int top_p, int score_mode, int table_flags) {
   if (!(table_flags & LSA_TABLE_SPANS)) return "it needs span tables (LSA_TABLE_SPANS)";
+  if (table_flags & LSA_TABLE_BLOCK_VISIBLE) return "it takes visibility from the span ends";
   if (score_mode != LSA_SCORE_BF16) return "it scores bf16 centroids only";
   if (D > 128) return "head dim above 128";
   if (rows > kRepMaxRows) return "more buckets than it holds in LDS";
@@ -258,8 +259,10 @@ int decode_launch(const char* who, const void* q, const void* k, const void* v, 
   LSA_REQUIRE(top_p >= 1 && window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE,
               "%s: top_p >= 1, window/sink/top_k >= 0", who);
   LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "%s: cluster_block_size must be >= 1", who);
-  LSA_REQUIRE((table_flags & ~LSA_TABLE_SPANS) == 0, LSA_ERR_SHAPE, "%s: unknown table flags %d", who,
-              table_flags);
+  LSA_REQUIRE((table_flags & ~(LSA_TABLE_SPANS | LSA_TABLE_BLOCK_VISIBLE)) == 0, LSA_ERR_SHAPE,
+              "%s: unknown table flags %d", who, table_flags);
+  LSA_REQUIRE(!(table_flags & LSA_TABLE_BLOCK_VISIBLE) || cluster_block_size >= 1, LSA_ERR_SHAPE,
+              "%s: cluster_block_size must be >= 1", who);
   LSA_REQUIRE(!(table_flags & LSA_TABLE_SPANS) || ends, LSA_ERR_SHAPE,
               "%s: LSA_TABLE_SPANS needs the span ends", who);
   const int K = top_p < rows ? top_p : rows;
@@ -342,6 +345,7 @@ int decode_launch(const char* who, const void* q, const void* k, const void* v, 
   a.R = R; a.G = Hkv; a.Hq = Hq;
   a.Tk = Tk; a.kv_sb = kv_batch_stride; a.kv_st = kv_token_stride; a.kv_sh = kv_head_stride;
   a.centroids = centroids; a.members = members; a.ends = ends; a.rows = rows; a.cap = cap;
+  a.vends = (table_flags & LSA_TABLE_BLOCK_VISIBLE) ? nullptr : ends;
   a.vec_rows = (cap % 4 == 0 && ((uintptr_t)members % 16) == 0) ? 1 : 0;
   a.spans = (table_flags & LSA_TABLE_SPANS) ? 1 : 0;
   a.row_tables = row_tables; a.group_tables = group_tables; a.positions = positions;

@@ -48,6 +48,7 @@ struct DecodeArgs {
   int rows, cap;
   int vec_rows;        // cap % 4 == 0 and the member table 16-byte aligned
   int spans;           // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0)
+  const int32_t* vends;  // the ends that decide visibility (nullptr: the closed-block rule)
   int64_t row_tables, group_tables;
   const int32_t* positions;
   int cluster_block, block_buckets;
@@ -288,10 +289,11 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
   const int64_t t = r * a.row_tables + g * a.group_tables;
   const CT* cent = (const CT*)a.centroids + t * a.rows * (int64_t)D;
   const int32_t* ends = a.ends ? a.ends + t * a.rows : nullptr;
+  const int32_t* vends = a.vends ? a.vends + t * a.rows : nullptr;
   const int c0 = s * a.cs;
   const int c1 = min(c0 + a.cs, a.rows);
   const int n_local = c1 > c0 ? c1 - c0 : 0;
-  const int vis = ends ? 0 : visible_closed(position, a.rows, a.cluster_block, a.block_buckets);
+  const int vis = vends ? 0 : visible_closed(position, a.rows, a.cluster_block, a.block_buckets);
   const int64_t lim = position + 1;
   DECODE_MARK(0);
 
@@ -307,7 +309,7 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
       // span ends are nondecreasing: the visible rows are a prefix, counted once (a span-end
       // load per screened row would sit on the screen's critical path)
       __shared__ int vis_lds[2 * LSA_WAVES];
-      const int nvis = ends ? visible_count_block(position, a.rows, ends, vis_lds) : vis;
+      const int nvis = vends ? visible_count_block(position, a.rows, vends, vis_lds) : vis;
       screen_topk<D, 4>(
           qs, cent, a.rows, [](int j) { return j; }, [&](int j) { return j < nvis; }, a.K, a.kp, sbest, scr);
       for (int j = tid; j < a.K; j += LSA_BLOCK) {
@@ -337,7 +339,7 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
       col[k] = j < n_local ? c0 + j : -1;
       const int cc = col[k] >= 0 ? col[k] : 0;  // row 0: a split may hold no column (c0 >= rows)
       craw[k].load(cent + (int64_t)cc * D + p * SPAN);
-      e[k] = ends ? ends[cc] : 0;
+      e[k] = vends ? vends[cc] : 0;
     }
 #pragma unroll
     for (int j = 0; j < SPAN; ++j) {
@@ -353,14 +355,14 @@ __device__ __forceinline__ void select_role(const DecodeArgs& a, char* smem, int
 #pragma unroll
       for (int x = 0; x < SPAN; ++x) acc = fma((double)qs[x], (double)craw[k].at(x), acc);
       const float sc = score_tree16(acc);
-      const bool keep = col[k] >= 0 && (ends ? (int64_t)e[k] <= lim : col[k] < vis);
+      const bool keep = col[k] >= 0 && (vends ? (int64_t)e[k] <= lim : col[k] < vis);
       if (p == 0 && col[k] >= 0) keys[col[k]] = keep ? key_to_u(pack_key(sc, col[k])) : 0;
     }
   } else {
     group_mean_slice<T, SPAN, GQ>(qrow, tid & 15, BF16_MODE, qs);
     score_keys<CT, SPAN>(
         qs, cent, D, n_local, [&](int j) { return c0 + j; },
-        [&](int j) { return ends ? (int64_t)ends[c0 + j] <= lim : c0 + j < vis; }, keys + c0);
+        [&](int j) { return vends ? (int64_t)vends[c0 + j] <= lim : c0 + j < vis; }, keys + c0);
   }
   if (!picked) {
     DECODE_MARK(1);
@@ -544,8 +546,8 @@ __device__ __forceinline__ void tree_role(const DecodeArgs& a, char* smem, int64
   for (int x = tid; x < (a.rows + 31) / 32; x += LSA_BLOCK) seen[x] = 0;
   __syncthreads();
   const int visible =
-      max(0, ends ? vis_lds[0] + vis_lds[1] + vis_lds[2] + vis_lds[3]
-                  : visible_count(position, a.rows, a.cluster_block, a.block_buckets, nullptr));
+      max(0, a.vends ? vis_lds[0] + vis_lds[1] + vis_lds[2] + vis_lds[3]
+                     : visible_count(position, a.rows, a.cluster_block, a.block_buckets, nullptr));
   const int covered = min(visible / a.node_block * a.node_block, n_nodes * ns);
   const int made = covered / ns;
   const int n_fresh = max(0, visible - covered);
@@ -643,6 +645,26 @@ constexpr int kRepChunkTiles = 8;
 // `map` turns a logical position into its cache row (a paged cache's slot table row of the
 // unit's query row, loaded by the caller before its wait; the identity without one): the
 // list and the gather hold mapped ids, while which ids are kept was decided on positions.
+// A paged cache: reader `role` of the unit's NR readers touches its share of the 128-byte
+// lines of the slot table row's entries [0, min(width, position + 1)) - one load a thread,
+// at most LSA_BLOCK lines a reader - so the lines sit in the L2 of the XCD the unit runs on
+// (every workgroup of a unit does) when the expansion maps its ids. Issued before the
+// reader's wait; the caller consumes the value after it (keep_live), so nothing waits on it.
+__device__ __forceinline__ int32_t touch_slot_lines(const SlotRow& map, int64_t position, int role, int NR) {
+  if (map.row == nullptr) return 0;
+  const int64_t lim = (int64_t)map.width < position + 1 ? (int64_t)map.width : position + 1;
+  if (lim <= 0) return 0;
+  const int64_t lines = (lim + 31) / 32;
+  const int64_t per = (lines + NR - 1) / NR;
+  const int64_t l = (int64_t)role * per + threadIdx.x;
+  const int64_t e = l * 32 < lim ? l * 32 : lim - 1;  // in bounds whatever the lane
+  const int32_t x = map.row[e];
+  return threadIdx.x < per ? x : 0;
+}
+
+// Makes the compiler keep (and wait for) a value here without using it.
+__device__ __forceinline__ void keep_live(int32_t x) { asm volatile("" ::"v"(x)); }
+
 template <typename T, int D, int GQ>
 __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh, int32_t* ids, int64_t i, int role,
                                            const QueryRegs<T, D, GQ>& qr, int64_t position, int clear,
@@ -865,6 +887,7 @@ __device__ __forceinline__ void rank_reader(const DecodeArgs& a, char* smem, int
     const int32_t* ends = a.ends + t * rows;
     for (int m = tid; m < rows; m += LSA_BLOCK) ends_l[m] = ends[m];
   }
+  const int32_t touched = touch_slot_lines(map, position, role, a.NR);
 
   // wave 0 polls the published keys (every slot is nonzero once its split has written it)
   // and ranks them in its registers (wave_topk_hist); keys that defeat the histogram cut go
@@ -881,6 +904,7 @@ __device__ __forceinline__ void rank_reader(const DecodeArgs& a, char* smem, int
   }
   __syncthreads();
   DECODE_MARK(1);
+  keep_live(touched);
   if (sh.bad) {  // no keys: this reader writes nothing but still arrives (see reader_role)
     if (arrive_last(&a.rd_count[i], a.NR, &sh.rd.flag)) {
       for (int x = tid; x < rows; x += LSA_BLOCK) coherent_store_u64(pub + x, 0);
@@ -954,6 +978,7 @@ __device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int
   QueryRegs<T, D, GQ> qr;
   qr.load(qrow, a.scale_log2);
   const SlotRow map = slot_row_of(a.slots, r);
+  const int32_t touched = touch_slot_lines(map, position, role, a.NR);
 
   // wait for the unit's record; wave 0 polls its copy and decodes it
   if (w == 0) {
@@ -987,6 +1012,7 @@ __device__ __forceinline__ void reader_role(const DecodeArgs& a, char* smem, int
   }
   __syncthreads();
   DECODE_MARK(1);
+  keep_live(touched);
   if (sh.bad) {
     // no record: this reader writes nothing but still arrives, so the unit's counter
     // resets; *status tells the caller the unit's outputs are invalid

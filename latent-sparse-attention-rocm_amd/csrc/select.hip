@@ -149,6 +149,7 @@ struct FlatArgs {
   int stage;          // 1: the list row is assembled in LDS after keys and picks
   int screen;         // one split, bf16 tables that fit screen_topk: matrix-core screen + exact re-score
   int spans;          // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0)
+  const int32_t* vends;  // the ends that decide visibility (nullptr: the closed-block rule)
   uint64_t* ws_keys;  // [R*G, rows] every column's key (S > 1)
   int* ws_count;      // [R*G] arrival counters (S > 1)
   SlotMap slots;      // a paged cache's slot table (table == nullptr: none)
@@ -204,10 +205,11 @@ __global__ __launch_bounds__(LSA_BLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)
   const int64_t t = r * a.row_tables + g * a.group_tables;
   const CT* cent = (const CT*)a.centroids + t * a.rows * (int64_t)D;
   const int32_t* ends = a.ends ? a.ends + t * a.rows : nullptr;
+  const int32_t* vends = a.vends ? a.vends + t * a.rows : nullptr;
   const int c0 = s * a.cs;
   const int c1 = min(c0 + a.cs, a.rows);
   const int n_local = c1 > c0 ? c1 - c0 : 0;
-  const int vis = ends ? 0 : visible_closed(position, a.rows, a.cluster_block, a.block_buckets);
+  const int vis = vends ? 0 : visible_closed(position, a.rows, a.cluster_block, a.block_buckets);
   const int64_t lim = position + 1;
 
   float qs[SPAN];
@@ -219,7 +221,7 @@ __global__ __launch_bounds__(LSA_BLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)
       uint64_t* sbest = (uint64_t*)((char*)smem + sizeof(ScreenLds));
       // span ends are nondecreasing: the visible rows are a prefix, counted once
       __shared__ int vis_lds[2 * LSA_WAVES];
-      const int nvis = ends ? visible_count_block(position, a.rows, ends, vis_lds) : vis;
+      const int nvis = vends ? visible_count_block(position, a.rows, vends, vis_lds) : vis;
       screen_topk<D, 2>(
           qs, cent, a.rows, [](int j) { return j; }, [&](int j) { return j < nvis; }, a.K, a.kp, sbest, scr);
       for (int j = threadIdx.x; j < a.K; j += LSA_BLOCK) pk[j] = key_column(u_to_key(sbest[j]));
@@ -230,7 +232,7 @@ __global__ __launch_bounds__(LSA_BLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)
   }
   score_keys<CT, SPAN>(
       qs, cent, D, n_local, [&](int j) { return c0 + j; },
-      [&](int j) { return ends ? (int64_t)ends[c0 + j] <= lim : c0 + j < vis; }, keys + c0);
+      [&](int j) { return vends ? (int64_t)vends[c0 + j] <= lim : c0 + j < vis; }, keys + c0);
 
   if (a.S > 1) {
     __syncthreads();
@@ -279,6 +281,7 @@ struct TreeArgs {
   int nodes_pow2, beam_pow2, cand_cap, cand_pow2, top_pow2;
   int window, sink, top_k;
   int spans;  // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0)
+  const int32_t* vends;  // the ends that decide visibility (nullptr: the closed-block rule)
   int screen1, screen0;  // bf16 tables that fit screen_topk: node / bucket level on the matrix cores
   SlotMap slots;         // a paged cache's slot table (table == nullptr: none)
   int32_t* lists;
@@ -308,8 +311,8 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
   // count): nodes are made from whole blocks of node_block visible buckets, so the first
   // `covered` buckets lie under the made nodes [0, made) and [covered, visible) are fresh
   __shared__ int vis_lds[2 * LSA_WAVES];
-  const int visible = max(0, a.ends ? visible_count_block(position, a.rows, a.ends + t * a.rows, vis_lds)
-                                    : visible_count(position, a.rows, a.cluster_block, a.block_buckets, nullptr));
+  const int visible = max(0, a.vends ? visible_count_block(position, a.rows, a.vends + t * a.rows, vis_lds)
+                                     : visible_count(position, a.rows, a.cluster_block, a.block_buckets, nullptr));
   const int covered = min(visible / a.node_block * a.node_block, a.n_nodes * a.node_size);
   const int made = covered / a.node_size;
 
@@ -674,8 +677,10 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
   LSA_REQUIRE(top_p >= 1 && window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE,
               "lsa_select_flat: top_p >= 1, window/sink/top_k >= 0");
   LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "lsa_select_flat: cluster_block_size must be >= 1");
-  LSA_REQUIRE((table_flags & ~LSA_TABLE_SPANS) == 0, LSA_ERR_SHAPE, "lsa_select_flat: unknown table flags %d",
-              table_flags);
+  LSA_REQUIRE((table_flags & ~(LSA_TABLE_SPANS | LSA_TABLE_BLOCK_VISIBLE)) == 0, LSA_ERR_SHAPE,
+              "lsa_select_flat: unknown table flags %d", table_flags);
+  LSA_REQUIRE(ends || cluster_block_size >= 1 || !(table_flags & LSA_TABLE_BLOCK_VISIBLE), LSA_ERR_SHAPE,
+              "lsa_select_flat: cluster_block_size must be >= 1");
   LSA_REQUIRE(!(table_flags & LSA_TABLE_SPANS) || ends, LSA_ERR_SHAPE,
               "lsa_select_flat: LSA_TABLE_SPANS needs the span ends");
   LSA_REQUIRE(splits >= 1 && splits <= 256 && splits <= rows, LSA_ERR_SHAPE,
@@ -692,6 +697,7 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
   FlatArgs a;
   a.R = R; a.G = G; a.rows = rows; a.cap = cap; a.row_tables = row_tables; a.group_tables = group_tables;
   a.centroids = centroids; a.members = members; a.ends = ends; a.positions = positions;
+  a.vends = (table_flags & LSA_TABLE_BLOCK_VISIBLE) ? nullptr : ends;
   a.cluster_block = cluster_block_size; a.block_buckets = block_buckets;
   a.K = K; a.kp = kp; a.window = window; a.sink = sink; a.top_k = top_k;
   a.S = splits; a.cs = cs;
@@ -744,8 +750,10 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
               "lsa_select_tree: n_nodes, node_size, node_block, beam_width, top_p >= 1");
   LSA_REQUIRE(window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE, "lsa_select_tree: window/sink/top_k >= 0");
   LSA_REQUIRE(ends || cluster_block_size >= 1, LSA_ERR_SHAPE, "lsa_select_tree: cluster_block_size must be >= 1");
-  LSA_REQUIRE((table_flags & ~LSA_TABLE_SPANS) == 0, LSA_ERR_SHAPE, "lsa_select_tree: unknown table flags %d",
-              table_flags);
+  LSA_REQUIRE((table_flags & ~(LSA_TABLE_SPANS | LSA_TABLE_BLOCK_VISIBLE)) == 0, LSA_ERR_SHAPE,
+              "lsa_select_tree: unknown table flags %d", table_flags);
+  LSA_REQUIRE(!(table_flags & LSA_TABLE_BLOCK_VISIBLE) || cluster_block_size >= 1, LSA_ERR_SHAPE,
+              "lsa_select_tree: cluster_block_size must be >= 1");
   LSA_REQUIRE(!(table_flags & LSA_TABLE_SPANS) || ends, LSA_ERR_SHAPE,
               "lsa_select_tree: LSA_TABLE_SPANS needs the span ends");
   const int beam = beam_width < n_nodes ? beam_width : n_nodes;
@@ -760,6 +768,7 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
   TreeArgs a;
   a.R = R; a.G = G; a.node_centroids = node_centroids; a.children = children; a.n_nodes = n_nodes;
   a.node_size = node_size; a.centroids = centroids; a.members = members; a.ends = ends; a.rows = rows; a.cap = cap;
+  a.vends = (table_flags & LSA_TABLE_BLOCK_VISIBLE) ? nullptr : ends;
   a.row_tables = row_tables; a.group_tables = group_tables; a.positions = positions;
   a.cluster_block = cluster_block_size; a.block_buckets = block_buckets; a.node_block = node_block;
   a.beam = beam_width; a.top_p = top_p;

@@ -22,6 +22,7 @@ LSA_F32, LSA_BF16, LSA_F16 = 0, 1, 2
 CHUNKED_AUTO, CHUNKED_GATHER, CHUNKED_MFMA = 0, 1, 2
 SCORE_BF16, SCORE_F32 = 0, 1
 TABLE_SPANS = 1  # LSA_TABLE_SPANS: every bucket row holds exactly its span of `ends`
+TABLE_BLOCK_VISIBLE = 2  # LSA_TABLE_BLOCK_VISIBLE: visibility by closed blocks, ends for spans only
 BEAM_MAX_LEVELS = 4  # LSA_BEAM_MAX_LEVELS: node levels lsa_select_beam walks
 CENTROID_MEAN, CENTROID_NORMALIZED, CENTROID_SUM = 0, 1, 2
 

@@ -31,6 +31,7 @@ from lsa_rocm_lab.port.pipeline import (
     _positions32,
     _queries,
     _slot_args,
+    _table_flags,
 )
 
 
@@ -89,7 +90,7 @@ def tree_select_batched(
     q = _queries(index_queries)
     pos = _positions32(positions, device)
     ends = _ends(buckets)
-    flags = _abi.TABLE_SPANS if (buckets.spans and ends is not None) else 0
+    flags = _table_flags(buckets, ends)
     width = top_k + config.window_size + config.sink_size
     lists = torch.empty(layout.out_shape(width), dtype=torch.int32, device=device)
     lengths = torch.empty(layout.out_shape(), dtype=torch.int32, device=device)

@@ -93,6 +93,10 @@ class Buckets:
     # reserved for blocks that have not closed yet (members -1, size 0, zero centroids,
     # span end INT32_MAX, so no query sees them); None: every row is built
     built_rows: int | None = None
+    # True when the ends serve the span expansion only and a bucket is visible once its
+    # cluster block has closed (the reference's rule for tables without ends): positional
+    # block tables, whose spans end before their block closes
+    block_visible: bool = False
 
     @property
     def rows(self) -> int:
@@ -182,10 +186,38 @@ def _ends(buckets: Buckets) -> torch.Tensor | None:
     return None if buckets.ends is None else buckets.ends.to(torch.int32).contiguous()
 
 
+def _table_flags(buckets: Buckets, ends: torch.Tensor | None) -> int:
+    """The C ABI's table flags of a bucket table: span expansion, block visibility."""
+    if ends is None:
+        return 0
+    return (_abi.TABLE_SPANS if buckets.spans else 0) | (_abi.TABLE_BLOCK_VISIBLE if buckets.block_visible else 0)
+
+
+def visible_ends(buckets: Buckets) -> torch.Tensor | None:
+    """The span ends that decide which buckets a position sees, or None when the
+    closed-block rule decides (tables without ends, and block-visible tables)."""
+    return None if buckets.block_visible else buckets.ends
+
+
 def _queries(index_queries: torch.Tensor) -> torch.Tensor:
     if index_queries.dtype not in (torch.float32, torch.bfloat16, torch.float16):
         index_queries = index_queries.float()
     return index_queries.contiguous()
+
+
+_ROW_INDEX: dict[tuple, torch.Tensor] = {}
+
+
+def _row_index(device, R: int, shared: bool) -> torch.Tensor:
+    """The default slot rows of R query rows - all 0 (one table row) or 0..R-1 - made once
+    per device and size and never written, so a call (or a captured graph) adds no fill."""
+    key = (_abi.device_index(device), R, shared)
+    t = _ROW_INDEX.get(key)
+    if t is None:
+        t = (torch.zeros(R, dtype=torch.int32, device=device) if shared
+             else torch.arange(R, dtype=torch.int32, device=device))
+        _ROW_INDEX[key] = t
+    return t
 
 
 def _slot_args(slot_table: torch.Tensor | None, slot_rows: torch.Tensor | None, R: int, device):
@@ -207,9 +239,9 @@ def _slot_args(slot_table: torch.Tensor | None, slot_rows: torch.Tensor | None, 
         table = table.contiguous()
     if slot_rows is None:
         if table.shape[0] == 1:
-            rows = torch.zeros(R, dtype=torch.int32, device=device)
+            rows = _row_index(device, R, shared=True)
         elif table.shape[0] == R:
-            rows = torch.arange(R, dtype=torch.int32, device=device)
+            rows = _row_index(device, R, shared=False)
         else:
             raise ValueError(f"slot_rows is needed: {table.shape[0]} slot-table rows for {R} query rows")
     else:
@@ -236,7 +268,7 @@ def visible_counts(positions: torch.Tensor, buckets: Buckets, config: PortConfig
     G = groups or (buckets.centroids.shape[-3] if lead >= 1 else 1)
     row_tables, group_tables = (0, 0) if lead == 0 else ((0, 1) if lead == 1 else (G, 1))
     counts = torch.empty(R * G, dtype=torch.int32, device=device)
-    ends = _ends(buckets)
+    ends = None if buckets.block_visible else _ends(buckets)
     _abi.call("lsa_visible_counts", pos.data_ptr(), R, G, buckets.rows, config.cluster_block_size,
               config.block_bucket_count, _abi.ptr(ends), row_tables, group_tables, counts.data_ptr(),
               _abi.stream(device))
@@ -412,7 +444,7 @@ def _fused_select(index_queries, positions, buckets, config, top_k, score_dtype,
     slots, _keep = _slot_args(slot_table, slot_rows, layout.R, device)
     _abi.call("lsa_select_flat", q.data_ptr(), _abi.dtype_code(q.dtype), layout.R, layout.G, layout.D,
               table.data_ptr(), members.data_ptr(), _abi.ptr(ends),
-              _abi.TABLE_SPANS if (buckets.spans and ends is not None) else 0, layout.rows, members.shape[-1],
+              _table_flags(buckets, ends), layout.rows, members.shape[-1],
               layout.row_tables, layout.group_tables, mode, pos.data_ptr(), slots, config.cluster_block_size,
               config.block_bucket_count, config.top_p, config.window_size, config.sink_size, top_k, splits,
               _abi.ptr(counters), _abi.ptr(ws), nbytes, lists.data_ptr(), lengths.data_ptr(), _abi.stream(device))
@@ -576,7 +608,7 @@ def flat_decode(
     table, mode = _score_table(buckets, score_dtype)
     members = buckets.members.to(device=device, dtype=torch.int32).contiguous()
     ends = _ends(buckets)
-    flags = _abi.TABLE_SPANS if (buckets.spans and ends is not None) else 0
+    flags = _table_flags(buckets, ends)
     pos = _positions32(positions, device)
     if pos.numel() != B:
         raise ValueError(f"a position a batch row: {B} rows, {pos.numel()} positions")
@@ -666,7 +698,7 @@ def tree_decode(
     children = level.children.to(device=device, dtype=torch.int32).contiguous()
     members = buckets.members.to(device=device, dtype=torch.int32).contiguous()
     ends = _ends(buckets)
-    flags = _abi.TABLE_SPANS if (buckets.spans and ends is not None) else 0
+    flags = _table_flags(buckets, ends)
     pos = _positions32(positions, device)
     if pos.numel() != B:
         raise ValueError(f"a position a batch row: {B} rows, {pos.numel()} positions")
@@ -960,7 +992,11 @@ def position_buckets(index_keys: torch.Tensor, config: PortConfig, centroid: str
     """Positional block-sparse buckets - runs of ``bucket_size`` consecutive keys (reference
     pipeline.py:378-403). index_keys [T, d] gives one table; [B, T, Hkv, D] one table per
     kv-head ([Hkv, rows, ...] for B == 1, else [B, Hkv, rows, ...]). ``centroid`` is the
-    reference's normalized sum or the bucket-mean key."""
+    reference's normalized sum or the bucket-mean key. Every row is a run of consecutive
+    ids, so the tables carry span ends (the decode then expands picks from them, with no
+    member-row loads); a bucket is still visible only once its block has closed
+    (``block_visible``, the reference's rule for these tables, pipeline.py:184-186), and
+    only when the span ends cover the rows exactly (``bucket_cap >= bucket_size``)."""
     device = _on_device("position_buckets", index_keys)
     block, size, cap = config.cluster_block_size, config.bucket_size, config.bucket_cap
     T = index_keys.shape[0] if index_keys.dim() == 2 else index_keys.shape[1]
@@ -974,7 +1010,11 @@ def position_buckets(index_keys: torch.Tensor, config: PortConfig, centroid: str
         members = members.expand(*lead, rows, cap).contiguous()
     sizes = (members >= 0).sum(-1, dtype=torch.int32)
     c32, c16 = bucket_centroids(index_keys, members, centroid)
-    return Buckets(c16, members, sizes, centroids_f32=c32, centroid=centroid)
+    ends = None
+    if cap >= size:  # row j is exactly the ids j * size .. (j + 1) * size - 1
+        ends = (torch.arange(1, rows + 1, device=device, dtype=torch.int32) * size).expand(sizes.shape).contiguous()
+    return Buckets(c16, members, sizes, centroids_f32=c32, centroid=centroid, ends=ends, spans=ends is not None,
+                   block_visible=ends is not None)
 
 
 def build_hierarchy_gpu(index_keys: torch.Tensor, buckets: Buckets, config: PortConfig) -> Hierarchy:
@@ -1056,7 +1096,8 @@ def reserve_buckets(buckets: Buckets, capacity: int) -> Buckets:
     return Buckets(grown(buckets.centroids, 0), grown(buckets.members, -1), grown(buckets.sizes, 0),
                    centroids_f32=None if buckets.centroids_f32 is None else grown(buckets.centroids_f32, 0),
                    ends=None if buckets.ends is None else grown(buckets.ends, UNBUILT_END),
-                   spans=buckets.spans, centroid=buckets.centroid, built_rows=built)
+                   spans=buckets.spans, centroid=buckets.centroid, built_rows=built,
+                   block_visible=buckets.block_visible)
 
 
 def grow_buckets_(buckets: Buckets, keys: torch.Tensor, config: PortConfig, **build_kw) -> Buckets:

@@ -12,7 +12,8 @@ stores the member lists in CSR form, every row of every table in order:
   ends           int32 [*lead, rows], optional    exclusive span ends
 
 n_rows is the product of the table shape (*lead, rows). The metadata holds the format tag
-("lsa-bucket-tables/1"), the member row width (bucket_cap) and the span flag. Loading
+("lsa-bucket-tables/1"), the member row width (bucket_cap), the span flag and the block
+visibility flag (positional tables: visible once their block closes). Loading
 checks every invariant the select kernels rely on (offsets start at 0 and never decrease,
 no row wider than bucket_cap, member ids >= 0, shapes agree, ends nondecreasing along each
 table's rows, span tables hold exactly their span) and raises ValueError otherwise;
@@ -40,7 +41,7 @@ def save_buckets(path: str | os.PathLike, buckets: Buckets) -> None:
         buckets = Buckets(buckets.centroids[..., :b, :], buckets.members[..., :b, :], buckets.sizes[..., :b],
                           centroids_f32=None if buckets.centroids_f32 is None else buckets.centroids_f32[..., :b, :],
                           ends=None if buckets.ends is None else buckets.ends[..., :b], spans=buckets.spans,
-                          centroid=buckets.centroid)
+                          centroid=buckets.centroid, block_visible=buckets.block_visible)
     members = buckets.members.detach().to("cpu", torch.int32)
     sizes = buckets.sizes.detach().to("cpu", torch.int64)
     if members.dim() < 2 or tuple(sizes.shape) != tuple(members.shape[:-1]):
@@ -64,7 +65,8 @@ def save_buckets(path: str | os.PathLike, buckets: Buckets) -> None:
         tensors["centroids_f32"] = buckets.centroids_f32.detach().to("cpu", torch.float32).contiguous()
     if buckets.ends is not None:
         tensors["ends"] = buckets.ends.detach().to("cpu", torch.int32).contiguous()
-    meta = {"format": FORMAT, "bucket_cap": str(cap), "spans": "1" if buckets.spans else "0"}
+    meta = {"format": FORMAT, "bucket_cap": str(cap), "spans": "1" if buckets.spans else "0",
+            "block_visible": "1" if buckets.block_visible else "0"}
     save_file(tensors, os.fspath(path), metadata=meta)
 
 
@@ -82,6 +84,7 @@ def load_buckets(path: str | os.PathLike, device: str | torch.device = "cpu") ->
     try:
         cap = int(meta["bucket_cap"])
         spans = meta["spans"] == "1"
+        block_visible = meta.get("block_visible", "0") == "1"
     except (KeyError, ValueError) as e:
         raise ValueError(f"load_buckets: bad metadata {meta}") from e
     offsets, ids, cent = t["offsets"], t["member_ids"], t["centroids"]
@@ -137,4 +140,5 @@ def load_buckets(path: str | os.PathLike, device: str | torch.device = "cpu") ->
         centroids_f32=t["centroids_f32"].to(dev) if "centroids_f32" in t else None,
         ends=ends.to(dev) if ends is not None else None,
         spans=spans,
+        block_visible=block_visible and ends is not None,
     )

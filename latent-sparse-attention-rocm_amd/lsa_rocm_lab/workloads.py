@@ -226,6 +226,36 @@ def node_tree(buckets: Buckets, node_size: int = 16) -> Hierarchy:
 
 
 @dataclass
+class IndexSpace:
+    """The reference's own benchmark inputs: q/k/v and one index-space table shared by
+    every head (reference port/bench.py:75-81, :113-153)."""
+
+    q: torch.Tensor      # [1, T, Hq, D]
+    k: torch.Tensor      # [1, T, Hkv, D]
+    v: torch.Tensor
+    idx_q: torch.Tensor  # [T, D] fp32: the query heads' mean per position
+    idx_k: torch.Tensor  # [T, D] fp32: the key heads' mean per position
+    buckets: Buckets     # the closed blocks' bucket table over idx_k (one table)
+
+
+def index_space(T: int = 32768, Hq: int = 32, Hkv: int = 8, D: int = 128, seed: int = 20261105,
+                config: PortConfig | None = None, dtype=torch.bfloat16, device: str = "cuda") -> IndexSpace:
+    """The reference's benchmark geometry at its default knobs: q/k/v ~ 0.2 N(0, 1) (drawn q,
+    k, v on a seeded generator on ``device``), one index space shared by every head - here
+    the mean over the query (key) heads, a stand-in for upstream's ``regroup`` - and its
+    bucket table built block by block on the GPU (``build_buckets``: 512-key blocks of 64
+    buckets of at most 16 keys, normalized-sum centroids)."""
+    from lsa_rocm_lab.port.pipeline import build_buckets, index_queries
+
+    config = PortConfig() if config is None else config
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q, k, v = ((torch.randn(1, T, h, D, device=device, generator=gen) * 0.2).to(dtype) for h in (Hq, Hkv, Hkv))
+    idx_k = index_queries(k, 1)[0, :, 0].contiguous()
+    idx_q = index_queries(q, 1)[0, :, 0].contiguous()
+    return IndexSpace(q, k, v, idx_q, idx_k, build_buckets(idx_k, config))
+
+
+@dataclass
 class PagedCache:
     """A cache moved into one pool of fixed-size pages, in shuffled page order."""
 

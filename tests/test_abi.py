@@ -179,7 +179,7 @@ def test_decode_arguments_rejected_before_launch():
     with pytest.raises(_abi.LsaError, match="WORKSPACE"):
         _abi.call("lsa_decode_flat", *_decode_args(scratch_bytes=1024))
     with pytest.raises(ValueError, match="table flags"):
-        _abi.call("lsa_decode_flat", *_decode_args(flags=2))
+        _abi.call("lsa_decode_flat", *_decode_args(flags=4))
     with pytest.raises(ValueError, match="span ends"):  # span tables need their ends
         _abi.call("lsa_decode_flat", *_decode_args(flags=_abi.TABLE_SPANS))
 

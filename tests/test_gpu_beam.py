@@ -43,7 +43,8 @@ def _check(lists, lengths, idx, positions, buckets, hierarchy, config, score_dty
     """Every (row, group) of the GPU's lists against the oracle walk. tables: None (one
     shared table) or the kv-head count (one table per kv-head)."""
     bc = buckets.centroids_f32 if score_dtype == "fp32" else buckets.centroids.float()
-    ends = None if buckets.ends is None else _np(buckets.ends)
+    ve = pipeline.visible_ends(buckets)
+    ends = None if ve is None else _np(ve)
     groups = 1 if tables is None else tables
     for g in range(groups):
         t = None if tables is None else g

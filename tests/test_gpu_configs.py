@@ -53,7 +53,8 @@ def oracle_select(idx, buckets, config, T, score_dtype="bf16"):
     lists, lengths = [], []
     for g in range(Hkv):
         cent = (buckets.centroids_f32 if score_dtype == "fp32" else buckets.centroids.float())[g].cpu().numpy()
-        ends = None if buckets.ends is None else buckets.ends[g].cpu().numpy()
+        ve = pipeline.visible_ends(buckets)
+        ends = None if ve is None else ve[g].cpu().numpy()
         l, n = oracle.flat_select(_np(idx[:, g]), np.array([T - 1]), cent, buckets.members[g].cpu().numpy(),
                                   cluster_block_size=config.cluster_block_size,
                                   block_buckets=config.block_bucket_count, top_p=config.top_p, top_k=config.top_k,
@@ -296,3 +297,42 @@ def test_tree_decode_configured_geometry():
         want = oracle.sparse_read(_np(data.q[b:b + 1]), _np(data.k[b:b + 1]), _np(data.v[b:b + 1]),
                                   lists_np[b:b + 1, None], lengths_np[b:b + 1, None], D ** -0.5)
         check_read(out[b:b + 1], want)
+
+
+def test_refcfg_prefill_32k_per_row_selection():
+    """The reference's prefill arm at its own knobs (port/bench.py:113-154 with
+    phase="prefill"; PortConfig() defaults: 512-key blocks of 64 buckets (cap 16), top_p
+    1024 of up to 4096 visible buckets, top_k 4096, window 512, sink 4, one index-space
+    table): all 32768 query rows select their own lists (4612 slots) in one fused select
+    launch, then the per-row read. 64 sampled rows - block edges (the visible count steps
+    at every 512th position), the first rows (nothing visible), the window's reach past
+    the sinks, random rows - are bit-exact against the oracle; the read of 8 of them is
+    within the bf16 bar of the fp64 oracle."""
+    from lsa_rocm_lab.port.pipeline import PortConfig
+    from lsa_rocm_lab.port.read_kernel_tiled import sparse_read_auto
+
+    cfg = PortConfig()
+    T, D = 32768, 128
+    print("case refcfg prefill 32k", flush=True)
+    ws = workloads.index_space(T)
+    pos = torch.arange(T, device=DEV, dtype=torch.int32)
+    lists, lengths = fused(ws.idx_q, pos, ws.buckets, cfg)
+    assert lists.shape == (T, cfg.top_k + cfg.window_size + cfg.sink_size)
+    out = sparse_read_auto(ws.q, ws.k, ws.v, lists[None], lengths[None], D ** -0.5)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(7)
+    edges = [0, 1, 3, 4, 5, 511, 512, 513, 515, 516, 1023, 1024, 1535, 4095, 4096, 8191, 8192, 16383, 16384,
+             20479, 24575, 24576, 32255, 32256, 32766, 32767]
+    rows = sorted(set(edges) | set(rng.integers(0, T, 64 - len(edges)).tolist()))
+    assert len(rows) >= 64
+    want_l, want_n = oracle.flat_select(_np(ws.idx_q[rows]), np.array(rows), _np(ws.buckets.centroids.float()),
+                                        _np(ws.buckets.members), cluster_block_size=cfg.cluster_block_size,
+                                        block_buckets=cfg.block_bucket_count, top_p=cfg.top_p, top_k=cfg.top_k,
+                                        window=cfg.window_size, sink=cfg.sink_size, mode="bf16")
+    assert np.array_equal(_np(lengths[rows]), want_n)
+    assert np.array_equal(_np(lists[rows]), want_l)
+    assert int(lengths.max()) <= cfg.top_k + cfg.window_size + cfg.sink_size
+    some = [0, 512, 1024, 8192, 20000, 32256, 32600, 32767]
+    want = oracle.sparse_read(_np(ws.q[:, some]), _np(ws.k), _np(ws.v), _np(lists[some])[None],
+                              _np(lengths[some])[None], D ** -0.5)
+    check_read(out[:, some], want)

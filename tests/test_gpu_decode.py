@@ -45,7 +45,8 @@ def oracle_decode(q, k, v, positions, buckets, config, score_dtype, top_k=None):
         lb, nb = [], []
         for g in range(Hkv):
             sel = (b, g) if per_row else (g,)
-            ends = None if buckets.ends is None else _np(buckets.ends[sel])
+            ve = pipeline.visible_ends(buckets)
+            ends = None if ve is None else _np(ve[sel])
             l, n = oracle.flat_select(idx[b, g][None], np.array([int(positions[b])]), _np(cents[sel]),
                                       _np(buckets.members[sel]), cluster_block_size=config.cluster_block_size,
                                       block_buckets=config.block_bucket_count, top_p=config.top_p, top_k=top_k,

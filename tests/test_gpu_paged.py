@@ -50,7 +50,8 @@ def _oracle_lists(idx, pos, buckets, config, score_dtype="bf16"):
         lb, nb = [], []
         for g in range(Hkv):
             sel = (b, g) if buckets.members.dim() == 4 else (g,)
-            ends = None if buckets.ends is None else _np(buckets.ends[sel])
+            ve = pipeline.visible_ends(buckets)
+            ends = None if ve is None else _np(ve[sel])
             l, n = oracle.flat_select(_np(idx[b, g])[None], np.array([int(pos[b])]), _np(cents[sel]),
                                       _np(buckets.members[sel]), cluster_block_size=config.cluster_block_size,
                                       block_buckets=config.block_bucket_count, top_p=config.top_p,

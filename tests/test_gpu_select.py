@@ -224,7 +224,8 @@ def _index_space(T, d, seed):
 def _oracle_flat(idx_q, positions, buckets, config, score_dtype, top_k=None):
     top_k = config.top_k if top_k is None else top_k
     cent = (buckets.centroids_f32 if score_dtype == "fp32" else buckets.centroids.float()).cpu().numpy()
-    ends = None if buckets.ends is None else buckets.ends.cpu().numpy()
+    ve = pipeline.visible_ends(buckets)
+    ends = None if ve is None else ve.cpu().numpy()
     return oracle.flat_select(_np(idx_q.float()), _np(positions), cent, _np(buckets.members),
                               cluster_block_size=config.cluster_block_size,
                               block_buckets=config.block_bucket_count, top_p=config.top_p, top_k=top_k,

@@ -38,6 +38,7 @@ def same(a, b):
         x, y = getattr(a, f), getattr(b, f)
         assert (x is None and y is None) or (x.dtype == y.dtype and torch.equal(x, y)), f
     assert a.spans == b.spans
+    assert a.block_visible == b.block_visible
 
 
 @pytest.mark.parametrize("lead,rows,cap,dim", [((), 37, 16, 64), ((8,), 64, 256, 128), ((2, 3), 5, 4, 32)])
@@ -62,6 +63,21 @@ def test_span_tables_round_trip(tmp_path):
     got = tables.load_buckets(tmp_path / "s.safetensors")
     same(b, got)
     assert got.spans
+
+
+def test_block_visible_flag_round_trips(tmp_path):
+    """Positional tables: span ends with visibility by closed blocks; the flag survives a
+    save and load, and a file written before the flag existed reads as span visibility."""
+    import dataclasses
+
+    b = dataclasses.replace(span_table(2, [8] * 12, 8, 32), block_visible=True)
+    tables.save_buckets(tmp_path / "p.safetensors", b)
+    got = tables.load_buckets(tmp_path / "p.safetensors")
+    same(b, got)
+    assert got.block_visible and got.spans
+    plain = span_table(2, [8] * 12, 8, 32)
+    tables.save_buckets(tmp_path / "q.safetensors", plain)
+    assert not tables.load_buckets(tmp_path / "q.safetensors").block_visible
 
 
 def test_save_rejects_holes_and_bad_ids(tmp_path):
