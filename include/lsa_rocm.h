@@ -114,9 +114,9 @@ int lsa_expand(const void* picks, int picks_are_keys, int64_t R, int32_t G, int3
  * top-k lists the last one to arrive merges (splits == 1: counters and scratch unused).
  * counters: R * G int32 that read zero at launch; every launch leaves them zero again.
  * scratch: lsa_select_flat_scratch_bytes(), no initialisation. table_flags: 0 or
- * LSA_TABLE_SPANS (span tables: with at most 64 picks the expansion takes each pick's kept
- * ids from the span ends, with no member-row loads; the lists are the ones the member rows
- * give). Out as lsa_expand. */
+ * LSA_TABLE_SPANS (span tables: with at most 4096 picks the expansion takes each pick's
+ * kept ids from the span ends, with no member-row loads; the lists are the ones the member
+ * rows give), optionally with LSA_TABLE_BLOCK_VISIBLE. Out as lsa_expand. */
 size_t lsa_select_flat_scratch_bytes(int64_t R, int32_t G, int32_t top_p, int32_t N, int32_t splits);
 int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int32_t G, int32_t D, const void* centroids,
                     const int32_t* members, const int32_t* ends, int32_t table_flags, int32_t rows, int32_t cap,

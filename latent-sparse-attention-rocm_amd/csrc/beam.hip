@@ -56,6 +56,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_beam_kernel(const QT* q, boo
   extern __shared__ uint64_t smem[];
   __shared__ RadixState st;
   __shared__ TopkScratch tks;
+  __shared__ BinScratch bins;
   __shared__ ScreenLds scr;
   __shared__ uint32_t seen[kBeamSeenBits / 32];
   __shared__ int scan[LSA_WAVES];
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_beam_kernel(const QT* q, boo
     if (!done) {
       score_keys<CT, SPAN>(qs, ncent, D, a.cand_pow2, [&](int j) { return cand[j]; }, keys);
       __syncthreads();
-      block_topk_sorted(keys, a.cand_pow2, K, a.beam_pow2, best, &tks, &st);
+      block_topk_any(keys, a.cand_pow2, K, a.beam_pow2, best, &tks, &st, &bins);
     }
     // the kept nodes' children (rows of the level below) are carried
     const int32_t* kids = a.children[lv - 1] + t * (int64_t)nn * a.node_size;
@@ -167,17 +168,23 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_beam_kernel(const QT* q, boo
   if (!done0) {
     score_keys<CT, SPAN>(qs, bcent, D, a.cand_pow2, [&](int j) { return cand[j]; }, keys);
     __syncthreads();
-    block_topk_sorted(keys, a.cand_pow2, K0, a.top_pow2, best, &tks, &st);
+    block_topk_any(keys, a.cand_pow2, K0, a.top_pow2, best, &tks, &st, &bins);
   }
   for (int j = threadIdx.x; j < a.top_p; j += LSA_BLOCK) cand[j] = j < K0 ? key_column(u_to_key(best[j])) : -1;
   __syncthreads();
   const int width = a.top_k + a.window + a.sink;
   const SlotRow map = slot_row_of(a.slots, r);
   int len;
-  if (a.spans) {  // span tables: kept ids from the picks' span ends, no member rows
+  if (a.spans && a.top_p <= LSA_WAVE) {  // span tables: kept ids from the picks' span ends, no member rows
     __shared__ int span_lds[2 * LSA_WAVE + 1];
     len = expand_spans(cand, a.top_p, a.ends + t * a.rows, a.rows, position, a.window, a.sink, a.top_k,
                        a.lists + i * width, width, span_lds, map);
+  } else if (a.spans) {
+    len = a.top_p <= 4 * LSA_BLOCK
+              ? expand_spans_wide<4>(cand, a.top_p, a.ends + t * a.rows, a.rows, position, a.window, a.sink,
+                                     a.top_k, a.lists + i * width, width, nullptr, scan, map)
+              : expand_spans_wide<16>(cand, a.top_p, a.ends + t * a.rows, a.rows, position, a.window, a.sink,
+                                      a.top_k, a.lists + i * width, width, nullptr, scan, map);
   } else {
     const int32_t* tab = a.members + t * (int64_t)a.rows * a.cap;
     len = expand_walk(cand, a.top_p, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k, a.lists + i * width,
@@ -263,7 +270,7 @@ extern "C" int lsa_select_beam(const void* queries, int q_dtype, int64_t R, int3
   a.row_tables = row_tables; a.group_tables = group_tables; a.positions = positions;
   a.cluster_block = cluster_block_size; a.block_buckets = block_buckets;
   a.top_p = top_p; a.window = window; a.sink = sink; a.top_k = top_k;
-  a.spans = (table_flags & LSA_TABLE_SPANS) && top_p <= LSA_WAVE ? 1 : 0;  // else the member rows
+  a.spans = (table_flags & LSA_TABLE_SPANS) && top_p <= 16 * LSA_BLOCK ? 1 : 0;  // else the member rows
   a.screen = score_mode == LSA_SCORE_BF16 && (D == 32 || D == 64 || D == 128) ? 1 : 0;
   a.cand_pow2 = next_pow2((int)most);
   a.beam_pow2 = next_pow2(beam_width < a.cand_pow2 ? beam_width : a.cand_pow2);

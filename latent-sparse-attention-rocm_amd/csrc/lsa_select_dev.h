@@ -193,6 +193,8 @@ __device__ __forceinline__ void score_slice_keys(const float* qs, const CT* cent
 }
 
 // Shared state of the histogram top-k (one per workgroup, in LDS).
+constexpr int kTopBins = 512;  // bins of block_topk_bins (large K)
+
 struct TopkScratch {
   int hist[256];
   int off[256];   // first candidate slot of each bin (bins from the top down)
@@ -201,6 +203,14 @@ struct TopkScratch {
   float wmin[LSA_WAVES], wmax[LSA_WAVES];
   int wcnt[LSA_WAVES], wbad[LSA_WAVES];
   int cut, ok;
+};
+
+// State of block_topk_bins (large K), in LDS: keys a bin holds (counted down again as the
+// candidates are placed) and the keys in the bins above it (bins in descending order).
+struct BinScratch {
+  int bcnt[kTopBins], boff[kTopBins];
+  int wsum[LSA_WAVES], wocc[LSA_WAVES];
+  int bcut, bnc, btot;
 };
 
 // The score a u-ordered key was packed from (inverse of ordered_bits).
@@ -378,6 +388,119 @@ __device__ __forceinline__ bool wave_topk_hist(const uint64_t* x, int K, int kp,
   return true;
 }
 
+// The K best of keys[0..n) (u-ordered, in LDS; n <= KPT * LSA_BLOCK), sorted descending
+// into out[0..kp) (u == 0 past them), for any K: the block's keys are taken into registers
+// (KPT a thread), binned linearly by score over [min, max] into kTopBins bins (a monotone
+// map: a higher bin never holds a lower key), the bins' descending offsets found by one
+// block scan, and the bin holding the K-th key named; every key in it or above (at most K
+// plus that bin's) is placed at its bin's offset in keys[] (whose values the registers now
+// hold), and its rank is that offset plus the larger keys of its own bin. Six barriers, no
+// sort. Returns false (every thread; keys[] untouched) when a score is not finite or a
+// bin holds more than 64 keys (ties, a degenerate spread): the caller takes the radix
+// select. `out` must not overlap `keys`. Every thread calls it.
+template <int KPT>
+__device__ __forceinline__ bool block_topk_bins(uint64_t* keys, int n, int K, int kp, uint64_t* out,
+                                                TopkScratch* sc, BinScratch* bs) {
+  constexpr int NB = kTopBins, BPT = kTopBins / LSA_BLOCK;  // bins a thread owns in the scan
+  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
+  uint64_t x[KPT];
+  float mn = INFINITY, mx = -INFINITY;
+  int cnt = 0, bad = 0;
+#pragma unroll
+  for (int m = 0; m < KPT; ++m) {
+    const int j = m * LSA_BLOCK + tid;
+    x[m] = j < n ? keys[j] : 0;
+    const float sc_ = key_score(x[m]);
+    const bool live = x[m] != 0;
+    bad |= (live && sc_ - sc_ != 0.0f) ? 1 : 0;  // NaN or infinite
+    mn = live ? fminf(mn, sc_) : mn;
+    mx = live ? fmaxf(mx, sc_) : mx;
+    cnt += live ? 1 : 0;
+  }
+  for (int b = tid; b < NB; b += LSA_BLOCK) bs->bcnt[b] = 0;
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  cnt = wave_sum(cnt);
+  bad = wave_or(bad);
+  if (lane == 0) { sc->wmin[w] = mn; sc->wmax[w] = mx; sc->wcnt[w] = cnt; sc->wbad[w] = bad; }
+  __syncthreads();
+  mn = fminf(fminf(sc->wmin[0], sc->wmin[1]), fminf(sc->wmin[2], sc->wmin[3]));
+  mx = fmaxf(fmaxf(sc->wmax[0], sc->wmax[1]), fmaxf(sc->wmax[2], sc->wmax[3]));
+  cnt = sc->wcnt[0] + sc->wcnt[1] + sc->wcnt[2] + sc->wcnt[3];
+  bad = sc->wbad[0] | sc->wbad[1] | sc->wbad[2] | sc->wbad[3];
+  if (bad) return false;  // uniform: every thread sees the same totals
+  const int kc = cnt < K ? cnt : K;
+  const float scale = mx > mn ? (float)NB / (mx - mn) : 0.0f;
+  auto bin_of = [&](uint64_t k) {
+    const int b = (int)((key_score(k) - mn) * scale);
+    return b < 0 ? 0 : (b > NB - 1 ? NB - 1 : b);
+  };
+  int bin[KPT];
+#pragma unroll
+  for (int m = 0; m < KPT; ++m) {
+    bin[m] = bin_of(x[m]);
+    if (x[m] != 0) atomicAdd(&bs->bcnt[bin[m]], 1);
+  }
+  __syncthreads();
+  // thread t owns bins NB-1-BPT*t .. NB-BPT*(t+1), from the top: descending exclusive
+  // offsets by one block scan; the most crowded bin bounds the in-bin ranking below
+  int c[BPT], mine = 0, occ = 0;
+#pragma unroll
+  for (int e = 0; e < BPT; ++e) {
+    c[e] = bs->bcnt[NB - 1 - BPT * tid - e];
+    mine += c[e];
+    occ = c[e] > occ ? c[e] : occ;
+  }
+  const int inc = wave_inclusive_sum(mine);
+  const int wocc = wave_reduce_bits(occ, 0, [](int a, int b) { return a > b ? a : b; });
+  if (lane == LSA_WAVE - 1) bs->wsum[w] = inc;
+  if (lane == 0) bs->wocc[w] = wocc;
+  __syncthreads();
+  int before = 0;
+#pragma unroll
+  for (int v = 0; v < LSA_WAVES; ++v) before += v < w ? bs->wsum[v] : 0;
+  int o = before + inc - mine;
+#pragma unroll
+  for (int e = 0; e < BPT; ++e) {
+    const int b = NB - 1 - BPT * tid - e;
+    bs->boff[b] = o;
+    if (kc > 0 && o < kc && kc <= o + c[e]) {  // the bin of the kc-th key: one thread
+      bs->bcut = b;
+      bs->bnc = o + c[e];
+    }
+    o += c[e];
+  }
+  if (tid == 0) bs->btot = cnt;
+  const int maxocc = max(max(bs->wocc[0], bs->wocc[1]), max(bs->wocc[2], bs->wocc[3]));
+  if (kc == 0) {  // nothing live: EMPTY throughout
+    for (int m = tid; m < kp; m += LSA_BLOCK) out[m] = 0;
+    __syncthreads();
+    return true;
+  }
+  if (maxocc > LSA_WAVE) return false;  // uniform
+  __syncthreads();
+  const int cut = bs->bcut, nc = bs->bnc;
+  // the candidates at their bins' offsets, in keys[] (every key is in a register now)
+#pragma unroll
+  for (int m = 0; m < KPT; ++m) {
+    if (x[m] != 0 && bin[m] >= cut) keys[bs->boff[bin[m]] + atomicSub(&bs->bcnt[bin[m]], 1) - 1] = x[m];
+  }
+  __syncthreads();
+  // ranks: a candidate's bin offset plus the larger keys of its own bin (the bin below
+  // starts where this one ends)
+  for (int s = tid; s < nc; s += LSA_BLOCK) {
+    const uint64_t y = keys[s];
+    const int b = bin_of(y);
+    const int lo = bs->boff[b], hi = b > 0 ? bs->boff[b - 1] : bs->btot;
+    int rank = lo;
+    for (int m = lo; m < hi; ++m) rank += keys[m] > y ? 1 : 0;  // live keys are distinct
+    if (rank < K) out[rank] = y;
+  }
+  for (int m = kc + tid; m < kp; m += LSA_BLOCK) out[m] = 0;  // EMPTY past the live keys
+  __syncthreads();
+  return true;
+}
+
 // The K best of keys[0..n) (u-ordered, in LDS), sorted descending into out[0..kp) with
 // u == 0 past K (kp = next_pow2(K)). K <= 64 takes the histogram cut when it leaves at
 // most 64 candidates; otherwise a radix select + bitonic sort. 1 <= K <= n. Every thread
@@ -391,6 +514,19 @@ __device__ __forceinline__ void block_topk_sorted(const uint64_t* keys, int n, i
   for (int j = K + threadIdx.x; j < kp; j += LSA_BLOCK) out[j] = 0;
   __syncthreads();
   bitonic_sort_desc(out, kp);
+}
+
+// block_topk_sorted for selects whose K may exceed 64: a larger K over at most 8192 keys
+// takes the binned ranking (block_topk_bins, which reuses keys[] as its candidate buffer,
+// so the keys are gone afterwards), falling back to the radix select + bitonic sort.
+__device__ __forceinline__ void block_topk_any(uint64_t* keys, int n, int K, int kp, uint64_t* out, TopkScratch* sc,
+                                               RadixState* st, BinScratch* bs) {
+  if (K > LSA_WAVE && n <= 32 * LSA_BLOCK) {
+    const bool done = n <= 16 * LSA_BLOCK ? block_topk_bins<16>(keys, n, K, kp, out, sc, bs)
+                                          : block_topk_bins<32>(keys, n, K, kp, out, sc, bs);
+    if (done) return;
+  }
+  block_topk_sorted(keys, n, K, kp, out, sc, st);
 }
 
 // Closed-form visible count without span ends (reference pipeline.py:184-186).
@@ -447,6 +583,90 @@ __device__ __forceinline__ int expand_spans(const int32_t* picks, int n_picks, c
   const int64_t n_win = position + 1 - window_start > 0 ? position + 1 - window_start : 0;
   const int64_t n_sink = sink < window_start ? sink : window_start;
   for (int x = kept + tid; x < width; x += LSA_BLOCK) out[x] = map(tail_id(x - kept, window_start, n_win, n_sink));
+  return kept + (int)n_win + (int)n_sink;
+}
+
+// Writes a list row staged in LDS (`stage`: its first `filled` kept ids, already mapped)
+// to `out` in coalesced 16-byte stores: the kept ids, then the tail (window, sinks; mapped
+// here), then -1 to `width` (width % 4 == 0, out 16-byte aligned). Every thread calls it
+// after the barrier that completes `stage`.
+__device__ __forceinline__ void store_staged_row(const int32_t* stage, int filled, int64_t window_start, int64_t n_win,
+                                                 int64_t n_sink, int32_t* out, int width, SlotRow map) {
+  const int length = filled + (int)n_win + (int)n_sink;
+  for (int c = threadIdx.x; c < width / 4; c += LSA_BLOCK) {
+    const int s0 = 4 * c;
+    int4 v;
+    if (s0 + 4 <= filled) {
+      v = ((const int4*)stage)[c];
+    } else if (s0 >= length) {
+      v = make_int4(-1, -1, -1, -1);
+    } else {
+      int e[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int slot = s0 + k;
+        e[k] = slot < filled ? stage[slot] : map(tail_id(slot - filled, window_start, n_win, n_sink));
+      }
+      v = make_int4(e[0], e[1], e[2], e[3]);
+    }
+    ((int4*)out)[c] = v;
+  }
+}
+
+// Rank-order expansion of span tables for any number of picks (expand_spans serves at most
+// 64): thread t takes picks [PPT t, PPT (t + 1)), their kept ranges [max(begin, sink),
+// min(end, window start)) from the span ends (both ends of every pick in flight at once),
+// one block prefix sum places them, every kept id up to top_k goes to its slot of the LDS
+// row `stage` (width + 4 ints; 16-byte aligned) mapped, and the row leaves in coalesced
+// stores (store_staged_row). Without `stage` (or when width % 4 != 0) the ids are stored
+// directly. n_picks <= PPT * LSA_BLOCK; picks in LDS (bucket rows, -1 none). The same list
+// as expand_walk. Every thread calls it; returns the length.
+template <int PPT>
+__device__ __forceinline__ int expand_spans_wide(const int32_t* picks, int n_picks, const int32_t* ends, int rows,
+                                                 int64_t position, int window, int sink, int top_k, int32_t* out,
+                                                 int width, int32_t* stage, int* scan, SlotRow map) {
+  const int tid = threadIdx.x;
+  const int64_t ws = position + 1 - window;
+  const int64_t window_start = ws > 0 ? ws : 0;
+  int32_t eb[PPT], ee[PPT];
+  bool ok[PPT];
+#pragma unroll
+  for (int p = 0; p < PPT; ++p) {  // every pick's two span ends in flight together
+    const int j = tid * PPT + p;
+    const int b = j < n_picks ? picks[j] : -1;
+    ok[p] = b >= 0 && b < rows;
+    eb[p] = ends[ok[p] && b > 0 ? b - 1 : 0];
+    ee[p] = ends[ok[p] ? b : 0];
+  }
+  int lo[PPT], cnt[PPT], mine = 0;
+#pragma unroll
+  for (int p = 0; p < PPT; ++p) {
+    const int b = tid * PPT + p < n_picks ? picks[tid * PPT + p] : -1;
+    const int64_t begin = b > 0 ? eb[p] : 0;
+    const int64_t l = begin > sink ? begin : sink, h = (int64_t)ee[p] < window_start ? ee[p] : window_start;
+    lo[p] = (int)l;
+    cnt[p] = ok[p] && h > l ? (int)(h - l) : 0;
+    mine += cnt[p];
+  }
+  int total;
+  int at = block_exclusive_sum(mine, scan, &total);
+  const int kept = total < top_k ? total : top_k;
+  const bool staged = stage != nullptr && width % 4 == 0;
+  int32_t* dst = staged ? stage : out;
+#pragma unroll
+  for (int p = 0; p < PPT; ++p) {
+    const int e = cnt[p] < kept - at ? cnt[p] : (kept - at > 0 ? kept - at : 0);
+    for (int x = 0; x < e; ++x) dst[at + x] = map(lo[p] + x);
+    at += cnt[p];
+  }
+  const int64_t n_win = position + 1 - window_start > 0 ? position + 1 - window_start : 0;
+  const int64_t n_sink = sink < window_start ? sink : window_start;
+  if (staged) {
+    __syncthreads();
+    store_staged_row(stage, kept, window_start, n_win, n_sink, out, width, map);
+  } else {
+    for (int x = kept + tid; x < width; x += LSA_BLOCK) out[x] = map(tail_id(x - kept, window_start, n_win, n_sink));
+  }
   return kept + (int)n_win + (int)n_sink;
 }
 

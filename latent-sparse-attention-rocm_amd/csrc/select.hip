@@ -147,6 +147,7 @@ struct FlatArgs {
   int window, sink, top_k;
   int S, cs;          // splits and columns per split
   int stage;          // 1: the list row is assembled in LDS after keys and picks
+  int wide_stage;     // span tables with K > 64: the row is staged in the (dead) keys region after the picks
   int screen;         // one split, bf16 tables that fit screen_topk: matrix-core screen + exact re-score
   int spans;          // bucket row j holds exactly ids ends[j - 1] .. ends[j] - 1 (ends[-1] = 0)
   const int32_t* vends;  // the ends that decide visibility (nullptr: the closed-block rule)
@@ -166,10 +167,17 @@ __device__ __forceinline__ void expand_row(const FlatArgs& a, const int32_t* pk,
   const int width = a.top_k + a.window + a.sink;
   const SlotRow map = slot_row_of(a.slots, i / a.G);
   int len;
-  if (a.spans) {  // span tables: kept ids from the picks' span ends, no member rows
+  if (a.spans && a.K <= LSA_WAVE) {  // span tables: kept ids from the picks' span ends, no member rows
     __shared__ int span_lds[2 * LSA_WAVE + 1];
     len = expand_spans(pk, a.K, ends, a.rows, position, a.window, a.sink, a.top_k, a.lists + i * width, width,
                        span_lds, map);
+  } else if (a.spans) {  // more picks: one per-thread run of picks each, one block scan
+    int32_t* stage = a.wide_stage ? (int32_t*)((char*)smem + ((4 * (size_t)a.K + 15) & ~(size_t)15)) : nullptr;
+    len = a.K <= 4 * LSA_BLOCK
+              ? expand_spans_wide<4>(pk, a.K, ends, a.rows, position, a.window, a.sink, a.top_k, a.lists + i * width,
+                                     width, stage, scan, map)
+              : expand_spans_wide<16>(pk, a.K, ends, a.rows, position, a.window, a.sink, a.top_k,
+                                      a.lists + i * width, width, stage, scan, map);
   } else {
     const int32_t* tab = a.members + t * a.rows * (int64_t)a.cap;
     int32_t* stage = a.stage ? (int32_t*)(smem + ((a.rows + a.kp + 1) & ~1)) : nullptr;  // 16-byte aligned
@@ -194,6 +202,7 @@ __global__ __launch_bounds__(LSA_BLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)
   extern __shared__ uint64_t smem[];
   __shared__ RadixState st;
   __shared__ TopkScratch tks;
+  __shared__ BinScratch bins;
   __shared__ int scan[LSA_WAVES];
   __shared__ int flag;
   uint64_t* keys = smem;            // [rows]
@@ -239,22 +248,22 @@ __global__ __launch_bounds__(LSA_BLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)
     uint64_t* mine = a.ws_keys + i * (int64_t)a.rows;
     for (int j = threadIdx.x; j < n_local; j += LSA_BLOCK) coherent_store_u64(mine + c0 + j, keys[c0 + j]);
     if (!arrive_last(&a.ws_count[i], a.S, &flag)) return;
-    for (int jb = 0; jb < a.rows; jb += 4 * LSA_BLOCK) {  // four coherent loads in flight per thread
-      uint64_t v[4];
+    for (int jb = 0; jb < a.rows; jb += 16 * LSA_BLOCK) {  // 16 coherent loads in flight per thread
+      uint64_t v[16];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 16; ++u) {
         const int j = jb + u * LSA_BLOCK + threadIdx.x;
         v[u] = coherent_load_u64(mine + (j < a.rows ? j : 0));
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 16; ++u) {
         const int j = jb + u * LSA_BLOCK + threadIdx.x;
         if (j < a.rows) keys[j] = v[u];
       }
     }
   }
   __syncthreads();
-  block_topk_sorted(keys, a.rows, a.K, a.kp, best, &tks, &st);
+  block_topk_any(keys, a.rows, a.K, a.kp, best, &tks, &st, &bins);
   for (int j = threadIdx.x; j < a.K; j += LSA_BLOCK) pk[j] = key_column(u_to_key(best[j]));
   __syncthreads();
   expand_row(a, pk, t, ends, position, i, scan);
@@ -294,6 +303,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
   extern __shared__ uint64_t smem[];
   __shared__ RadixState st;
   __shared__ TopkScratch tks;
+  __shared__ BinScratch bins;
   __shared__ int scan[LSA_WAVES];
   __shared__ ScreenLds scr;
   uint64_t* keys = smem;                    // [max(nodes_pow2, cand_pow2)]
@@ -331,7 +341,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
   if (!done1) {
     score_slice_keys<CT, SPAN>(qs, ncent, D, 0, a.n_nodes, made, keys);
     __syncthreads();
-    block_topk_sorted(keys, a.n_nodes, beam, a.beam_pow2, best, &tks, &st);
+    block_topk_any(keys, a.n_nodes, beam, a.beam_pow2, best, &tks, &st, &bins);
   }
 
   // level 0 candidates: the kept nodes' children (only visible buckets), then the fresh
@@ -387,17 +397,23 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_tree_kernel(const QT* q, boo
   if (!done0) {
     score_keys<CT, SPAN>(qs, bcent, D, a.cand_pow2, [&](int j) { return cand[j]; }, keys);
     __syncthreads();
-    block_topk_sorted(keys, a.cand_pow2, k, a.top_pow2, best, &tks, &st);
+    block_topk_any(keys, a.cand_pow2, k, a.top_pow2, best, &tks, &st, &bins);
   }
   for (int j = threadIdx.x; j < a.top_p; j += LSA_BLOCK) cand[j] = j < k ? key_column(u_to_key(best[j])) : -1;
   __syncthreads();
   const int width = a.top_k + a.window + a.sink;
   const SlotRow map = slot_row_of(a.slots, r);
   int len;
-  if (a.spans) {  // span tables: kept ids from the picks' span ends, no member rows
+  if (a.spans && a.top_p <= LSA_WAVE) {  // span tables: kept ids from the picks' span ends, no member rows
     __shared__ int span_lds[2 * LSA_WAVE + 1];
     len = expand_spans(cand, a.top_p, a.ends + t * a.rows, a.rows, position, a.window, a.sink, a.top_k,
                        a.lists + i * width, width, span_lds, map);
+  } else if (a.spans) {
+    len = a.top_p <= 4 * LSA_BLOCK
+              ? expand_spans_wide<4>(cand, a.top_p, a.ends + t * a.rows, a.rows, position, a.window, a.sink,
+                                     a.top_k, a.lists + i * width, width, nullptr, scan, map)
+              : expand_spans_wide<16>(cand, a.top_p, a.ends + t * a.rows, a.rows, position, a.window, a.sink,
+                                      a.top_k, a.lists + i * width, width, nullptr, scan, map);
   } else {
     const int32_t* tab = a.members + t * (int64_t)a.rows * a.cap;
     len = expand_walk(cand, a.top_p, tab, a.rows, a.cap, position, a.window, a.sink, a.top_k, a.lists + i * width,
@@ -705,12 +721,16 @@ extern "C" int lsa_select_flat(const void* queries, int q_dtype, int64_t R, int3
   a.ws_keys = need ? (uint64_t*)scratch : nullptr;
   a.slots = sm;
   a.lists = lists; a.lengths = lengths;
-  a.spans = (table_flags & LSA_TABLE_SPANS) && K <= LSA_WAVE ? 1 : 0;  // more picks: the member rows
+  a.spans = (table_flags & LSA_TABLE_SPANS) && K <= 16 * LSA_BLOCK ? 1 : 0;  // more picks: the member rows
   // the list row is staged in LDS when it fits beside the keys (coalesced row stores)
   const int width = top_k + window + sink;
   const size_t base_lds = sizeof(uint64_t) * (((size_t)rows + kp + 1) & ~(size_t)1);
   const size_t stage_lds = sizeof(int32_t) * ((size_t)width + 4);
   a.stage = (!a.spans && width % 4 == 0 && ((uintptr_t)lists % 16) == 0 && base_lds + stage_lds <= kMaxDynLds) ? 1 : 0;
+  // span tables with more than 64 picks stage the row in the keys region, dead after the top-K
+  a.wide_stage = (a.spans && K > LSA_WAVE && width % 4 == 0 && ((uintptr_t)lists % 16) == 0 &&
+                  ((4 * (size_t)K + 15) & ~(size_t)15) + stage_lds <= sizeof(uint64_t) * (size_t)rows)
+                     ? 1 : 0;
   a.screen = splits == 1 && score_mode == LSA_SCORE_BF16 && screen_pays(D, rows, K) ? 1 : 0;
   size_t shmem = base_lds + (a.stage ? stage_lds : 0);
   const size_t screen_lds = sizeof(ScreenLds) + sizeof(uint64_t) * (size_t)kp;
@@ -775,7 +795,7 @@ extern "C" int lsa_select_tree(const void* queries, int q_dtype, int64_t R, int3
   a.nodes_pow2 = next_pow2(n_nodes); a.beam_pow2 = next_pow2(beam); a.cand_cap = (int)cand_cap;
   a.cand_pow2 = next_pow2((int)(cand_cap > 0 ? cand_cap : 1)); a.top_pow2 = next_pow2(top_p);
   a.window = window; a.sink = sink; a.top_k = top_k; a.lists = lists; a.lengths = lengths; a.slots = sm;
-  a.spans = (table_flags & LSA_TABLE_SPANS) && top_p <= LSA_WAVE ? 1 : 0;  // else the member rows
+  a.spans = (table_flags & LSA_TABLE_SPANS) && top_p <= 16 * LSA_BLOCK ? 1 : 0;  // else the member rows
   a.screen1 = score_mode == LSA_SCORE_BF16 && screen_pays(D, n_nodes, beam) ? 1 : 0;
   a.screen0 = score_mode == LSA_SCORE_BF16 && screen_pays(D, a.cand_pow2, top_p < a.cand_pow2 ? top_p : a.cand_pow2)
                   ? 1 : 0;

@@ -912,10 +912,11 @@ def build_buckets(keys: torch.Tensor, config: PortConfig, pool: int | None = Non
 
     keys [T, d] (one index-space table) or [B, T, Hkv, D] (per-kv-head tables: [Hkv, rows,
     ...] for B == 1, else [B, Hkv, rows, ...]). Blocks ``first_block`` .. T // block - 1 are
-    built (``extend_buckets`` appends newly closed blocks). ``spans``: also set the span
-    ends (span tables: the decode expands picks from the ends, and a bucket is visible once
-    its span has ended); without them the reference's rule applies - a query sees the
-    buckets of the closed blocks before its own."""
+    built (``extend_buckets`` appends newly closed blocks). The tables always carry their
+    span ends, so the selects and the decode expand picks from them with no member-row
+    loads. Visibility: by default the reference's rule - a query sees the buckets of the
+    closed blocks before its own (``block_visible``); ``spans=True`` makes a bucket visible
+    once its span has ended instead."""
     device = _on_device("build_buckets", keys)
     block, bpb, cap = config.cluster_block_size, config.block_bucket_count, config.bucket_cap
     pool = config.pool_size if pool is None else pool
@@ -954,8 +955,8 @@ def build_buckets(keys: torch.Tensor, config: PortConfig, pool: int | None = Non
         members, sizes, end = members[0], sizes[0], end[0]
     members = members.contiguous()
     c32, c16 = bucket_centroids(keys if flat else k4, members, centroid)
-    return Buckets(c16, members, sizes.contiguous(), centroids_f32=c32, ends=end.contiguous() if spans else None,
-                   spans=spans, centroid=centroid)
+    return Buckets(c16, members, sizes.contiguous(), centroids_f32=c32, ends=end.contiguous(), spans=True,
+                   centroid=centroid, block_visible=not spans)
 
 
 def extend_buckets(buckets: Buckets, keys: torch.Tensor, config: PortConfig, **build_kw) -> Buckets:
@@ -978,14 +979,14 @@ def extend_buckets(buckets: Buckets, keys: torch.Tensor, config: PortConfig, **b
     has_ends = buckets.ends is not None
     if buckets.spans and not has_ends:
         raise ValueError("extend_buckets: span tables need their ends")
-    new = build_buckets(keys, config, first_block=have, spans=has_ends, centroid=kind, **build_kw)
+    new = build_buckets(keys, config, first_block=have, spans=not buckets.block_visible, centroid=kind, **build_kw)
     return Buckets(torch.cat([buckets.centroids, new.centroids], dim=-2),
                    torch.cat([buckets.members, new.members], dim=-2),
                    torch.cat([buckets.sizes, new.sizes], dim=-1),
                    centroids_f32=(None if buckets.centroids_f32 is None
                                   else torch.cat([buckets.centroids_f32, new.centroids_f32], dim=-2)),
                    ends=torch.cat([buckets.ends, new.ends], dim=-1) if has_ends else None,
-                   spans=buckets.spans, centroid=kind)
+                   spans=buckets.spans, centroid=kind, block_visible=buckets.block_visible)
 
 
 def position_buckets(index_keys: torch.Tensor, config: PortConfig, centroid: str = "normalized") -> Buckets:
@@ -1070,17 +1071,19 @@ def reserve_buckets(buckets: Buckets, capacity: int) -> Buckets:
     """Capacity tables for in-place growth (the decode cache's incremental index,
     reference pipeline.py:184-186 visibility as blocks close; docs/PORT_NOTES.md:12-14):
     every table of ``buckets`` copied into tables of ``capacity`` rows, allocated once. The
-    rows past the built ones are reserved: members -1, size 0, zero centroids and, for
-    tables with span ends, the end ``UNBUILT_END``, so no position sees them. Every select
-    and decode entry takes the capacity tables as they are (``rows`` = capacity);
+    rows past the built ones are reserved: members -1, size 0, zero centroids and span ends
+    that keep them out of every list - ``UNBUILT_END`` where the ends decide visibility, an
+    empty span at the last built end where the closed-block rule does. Every select and
+    decode entry takes the capacity tables as they are (``rows`` = capacity);
     ``grow_buckets_`` writes newly closed blocks into the reserved rows without moving any
     tensor, so pointers captured in a HIP graph stay valid.
 
-    Visibility: with span ends a reserved row is never visible. Without them the
-    reference's block rule ``pos // cluster_block_size * block_bucket_count`` applies,
-    which reaches a reserved row only for a position past the blocks built, so a caller
-    grows the tables before it queries a position in a newly closed block (as a decode
-    step does: the block closes, the index grows, then the step selects)."""
+    Visibility: where the ends decide, a reserved row is never visible. Under the
+    reference's block rule ``pos // cluster_block_size * block_bucket_count`` a reserved row
+    is reached only for a position past the blocks built, so a caller grows the tables
+    before it queries a position in a newly closed block (as a decode step does: the block
+    closes, the index grows, then the step selects); a reserved row reached anyway holds
+    nothing."""
     built = buckets.rows if buckets.built_rows is None else buckets.built_rows
     if capacity < built:
         raise ValueError(f"reserve_buckets: capacity {capacity} < the {built} rows built")
@@ -1093,9 +1096,15 @@ def reserve_buckets(buckets: Buckets, capacity: int) -> Buckets:
         out.narrow(axis, 0, built).copy_(t.narrow(axis, 0, built))
         return out
 
+    ends = None
+    if buckets.ends is not None:
+        ends = grown(buckets.ends, UNBUILT_END)
+        if buckets.block_visible and built > 0:  # reserved rows: empty spans at the last built end
+            ends.narrow(len(lead), built, capacity - built).copy_(
+                buckets.ends.narrow(len(lead), built - 1, 1).expand(*lead, capacity - built))
     return Buckets(grown(buckets.centroids, 0), grown(buckets.members, -1), grown(buckets.sizes, 0),
                    centroids_f32=None if buckets.centroids_f32 is None else grown(buckets.centroids_f32, 0),
-                   ends=None if buckets.ends is None else grown(buckets.ends, UNBUILT_END),
+                   ends=ends,
                    spans=buckets.spans, centroid=buckets.centroid, built_rows=built,
                    block_visible=buckets.block_visible)
 
@@ -1120,7 +1129,7 @@ def grow_buckets_(buckets: Buckets, keys: torch.Tensor, config: PortConfig, **bu
         raise ValueError(f"grow_buckets_: {buckets.built_rows + new_rows} rows exceed the capacity {buckets.rows}")
     kind = buckets.centroid or build_kw.pop("centroid", "normalized")
     build_kw.pop("centroid", None)
-    new = build_buckets(keys, config, first_block=have, spans=buckets.ends is not None, centroid=kind, **build_kw)
+    new = build_buckets(keys, config, first_block=have, spans=not buckets.block_visible, centroid=kind, **build_kw)
     lo, hi = buckets.built_rows, buckets.built_rows + new_rows
     buckets.centroids[..., lo:hi, :].copy_(new.centroids)
     buckets.members[..., lo:hi, :].copy_(new.members)
@@ -1129,5 +1138,7 @@ def grow_buckets_(buckets: Buckets, keys: torch.Tensor, config: PortConfig, **bu
         buckets.centroids_f32[..., lo:hi, :].copy_(new.centroids_f32)
     if buckets.ends is not None:
         buckets.ends[..., lo:hi].copy_(new.ends)
+        if buckets.block_visible and hi < buckets.rows:  # reserved rows: empty spans at the new last end
+            buckets.ends[..., hi:].copy_(buckets.ends[..., hi - 1:hi].expand_as(buckets.ends[..., hi:]))
     buckets.built_rows = hi
     return buckets

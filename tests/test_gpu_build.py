@@ -124,7 +124,8 @@ def test_build_buckets_reference_blocks_and_select():
     keys = clustered_keys(1, T, 1, d, torch.float32, seed=31)[0, :, 0]
     buckets = pipeline.build_buckets(keys.to(DEV), config)
     want_members, _ = oracle_block_tables(keys.numpy(), config, config.pool_size, config.bucket_cap)
-    assert buckets.ends is None and not buckets.spans
+    # the closed-block rule decides visibility; the span ends serve the expansion
+    assert buckets.block_visible and buckets.spans and buckets.ends is not None
     assert np.array_equal(buckets.members.cpu().numpy(), want_members)
     cent = oracle.bucket_centroids(keys.numpy(), want_members, "normalized")
     assert np.abs(buckets.centroids_f32.cpu().numpy() - cent).max() <= 1e-6
@@ -151,7 +152,7 @@ def test_extend_buckets_equals_a_full_build():
         for f in ("centroids", "members", "sizes", "centroids_f32", "ends"):
             a, b = getattr(grown, f), getattr(full, f)
             assert (a is None and b is None) or torch.equal(a, b), f
-        assert grown.spans == spans
+        assert grown.spans and grown.block_visible == (not spans)
     members, end = oracle_block_tables(keys[0, :, 1].float().cpu().numpy(), config, 8, 32)
     assert np.array_equal(full.members[1].cpu().numpy(), members)
     assert np.array_equal(full.ends[1].cpu().numpy(), end)
@@ -169,7 +170,7 @@ def test_extend_buckets_keeps_centroid_kind_and_optional_fields():
         full = pipeline.build_buckets(keys, config, spans=spans, centroid="mean")
         part = pipeline.build_buckets(keys[:, :3 * 256 + 10], config, spans=spans, centroid="mean")
         grown = pipeline.extend_buckets(part, keys, config)
-        assert grown.centroid == "mean" and grown.spans == spans and (grown.ends is None) == (not spans)
+        assert grown.centroid == "mean" and grown.spans and grown.block_visible == (not spans)
         for f in ("centroids", "members", "sizes", "centroids_f32", "ends"):
             a, b = getattr(grown, f), getattr(full, f)
             assert (a is None and b is None) or torch.equal(a, b), (spans, f)
@@ -214,6 +215,8 @@ def test_grow_buckets_in_place_equals_a_full_build(tmp_path):
         assert bool((grown.centroids[:, 80:] == 0).all()) and bool((grown.centroids_f32[:, 80:] == 0).all())
         if spans:
             assert bool((grown.ends[:, 80:] == pipeline.UNBUILT_END).all())
+        else:  # empty spans at the last built end
+            assert bool((grown.ends[:, 80:] == grown.ends[:, 79:80]).all())
         idx = pipeline.index_queries(keys[:, -5:], 2)[0]  # five query rows [5, 2, 64]
         pos = torch.tensor([T_full - 1, 1300, 1100, 600, 250], dtype=torch.int32, device=DEV)
         for impl in ("fused", "reference"):
