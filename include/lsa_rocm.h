@@ -323,6 +323,34 @@ int lsa_decode_tree(const void* q, const void* k, const void* v, int dtype, int6
                     void* scratch, size_t scratch_bytes, int32_t* lists, int32_t* lengths, void* out,
                     int32_t* status, void* stream);
 
+/* Fused decode step over the reference's own layout - one index-space selection a query row
+ * shared by every kv-head (reference port/bench.py:147-153 `step` = pipeline.py:248-316
+ * flat_select on the index space, then read_kernel_tiled.py:92-156 over [B, Tq, W] lists
+ * shared by the heads) - at its own knobs (PortConfig, pipeline.py:32-54: up to 4096
+ * buckets, top_p 1024, top_k 4096). index_queries [R, D] fp32 (one a row: the reference's
+ * make_index_space output); one span table a row (row_tables 1) or for every row (0):
+ * centroids [tables, rows, D] (bf16 or fp32 per score_mode) and span ends [tables, rows]
+ * (LSA_TABLE_SPANS required, LSA_TABLE_BLOCK_VISIBLE optional). q [R, Hq, D], k/v as
+ * lsa_decode_flat's (bf16 or fp16, head dim 64 or 128). Writes lists [R, top_k + window +
+ * sink] and lengths [R] (identical to lsa_select_flat's on the same queries and table) and
+ * out [R, Hq, D] (the read of those lists). select_splits: select workgroups a row (0 = one
+ * a 64 buckets, at most 256); readers: reader workgroups a (row, kv-head) (0 = default, at
+ * most 64). counters: lsa_decode_shared_counters() int32 words (8-byte aligned), zero before
+ * the first launch; every launch leaves them zero. scratch: lsa_decode_shared_scratch_bytes().
+ * status as lsa_decode_flat's. Limits: at most 4096 buckets and 1024 picks a row, the
+ * reader LDS within 64 KiB. */
+int64_t lsa_decode_shared_counters(int64_t R, int32_t Hkv, int32_t rows);
+size_t lsa_decode_shared_scratch_bytes(int dtype, int64_t R, int32_t Hq, int32_t Hkv, int32_t D, int32_t rows,
+                                       int32_t top_p, int32_t window, int32_t sink, int32_t top_k, int32_t readers);
+int lsa_decode_shared(const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk, int32_t Hq,
+                      int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride, int64_t kv_head_stride,
+                      const float* index_queries, const void* centroids, const int32_t* ends, int32_t table_flags,
+                      int32_t rows, int64_t row_tables, int score_mode, const int32_t* positions,
+                      const lsa_slot_map* slots, int32_t cluster_block_size, int32_t block_buckets, int32_t top_p,
+                      int32_t window, int32_t sink, int32_t top_k, float scale, int32_t select_splits,
+                      int32_t readers, int32_t* counters, int64_t n_counters, void* scratch, size_t scratch_bytes,
+                      int32_t* lists, int32_t* lengths, void* out, int32_t* status, void* stream);
+
 /* lsa_decode_flat without caller buffers, for callers that cannot allocate (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart
  * in the reference. The counters and scratch live in a 16 MiB file-scope device array per

@@ -388,28 +388,25 @@ __device__ __forceinline__ bool wave_topk_hist(const uint64_t* x, int K, int kp,
   return true;
 }
 
-// The K best of keys[0..n) (u-ordered, in LDS; n <= KPT * LSA_BLOCK), sorted descending
-// into out[0..kp) (u == 0 past them), for any K: the block's keys are taken into registers
-// (KPT a thread), binned linearly by score over [min, max] into kTopBins bins (a monotone
-// map: a higher bin never holds a lower key), the bins' descending offsets found by one
-// block scan, and the bin holding the K-th key named; every key in it or above (at most K
-// plus that bin's) is placed at its bin's offset in keys[] (whose values the registers now
-// hold), and its rank is that offset plus the larger keys of its own bin. Six barriers, no
-// sort. Returns false (every thread; keys[] untouched) when a score is not finite or a
-// bin holds more than 64 keys (ties, a degenerate spread): the caller takes the radix
-// select. `out` must not overlap `keys`. Every thread calls it.
+// The K best of the block's keys held in registers (x[m] is key m * LSA_BLOCK + tid,
+// u-ordered, 0 = EMPTY), sorted descending into out[0..kp) (u == 0 past them), for any K:
+// the keys are binned linearly by score over [min, max] into kTopBins bins (a monotone map:
+// a higher bin never holds a lower key), the bins' descending offsets found by one block
+// scan, and the bin holding the K-th key named; every key in it or above (at most K + 63)
+// is placed at its bin's offset in cand[], and its rank is that offset plus the larger keys
+// of its own bin. Six barriers, no sort. Returns false (every thread) when a score is not
+// finite or a bin holds more than 64 keys (ties, a degenerate spread): the caller falls
+// back to a radix select. `out` and `cand` (capacity K + 64) must not overlap. Every
+// thread calls it.
 template <int KPT>
-__device__ __forceinline__ bool block_topk_bins(uint64_t* keys, int n, int K, int kp, uint64_t* out,
-                                                TopkScratch* sc, BinScratch* bs) {
+__device__ __forceinline__ bool topk_bins_regs(const uint64_t (&x)[KPT], int K, int kp, uint64_t* out,
+                                               uint64_t* cand, TopkScratch* sc, BinScratch* bs) {
   constexpr int NB = kTopBins, BPT = kTopBins / LSA_BLOCK;  // bins a thread owns in the scan
   const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
-  uint64_t x[KPT];
   float mn = INFINITY, mx = -INFINITY;
   int cnt = 0, bad = 0;
 #pragma unroll
   for (int m = 0; m < KPT; ++m) {
-    const int j = m * LSA_BLOCK + tid;
-    x[m] = j < n ? keys[j] : 0;
     const float sc_ = key_score(x[m]);
     const bool live = x[m] != 0;
     bad |= (live && sc_ - sc_ != 0.0f) ? 1 : 0;  // NaN or infinite
@@ -480,25 +477,106 @@ __device__ __forceinline__ bool block_topk_bins(uint64_t* keys, int n, int K, in
   if (maxocc > LSA_WAVE) return false;  // uniform
   __syncthreads();
   const int cut = bs->bcut, nc = bs->bnc;
-  // the candidates at their bins' offsets, in keys[] (every key is in a register now)
+  // the candidates at their bins' offsets, in cand[]
 #pragma unroll
   for (int m = 0; m < KPT; ++m) {
-    if (x[m] != 0 && bin[m] >= cut) keys[bs->boff[bin[m]] + atomicSub(&bs->bcnt[bin[m]], 1) - 1] = x[m];
+    if (x[m] != 0 && bin[m] >= cut) cand[bs->boff[bin[m]] + atomicSub(&bs->bcnt[bin[m]], 1) - 1] = x[m];
   }
   __syncthreads();
   // ranks: a candidate's bin offset plus the larger keys of its own bin (the bin below
-  // starts where this one ends)
+  // starts where this one ends); the bin is read 8 keys at a time, all 8 loads in flight
+  // (indexes clamped into the candidates, the ones past the bin masked)
   for (int s = tid; s < nc; s += LSA_BLOCK) {
-    const uint64_t y = keys[s];
+    const uint64_t y = cand[s];
     const int b = bin_of(y);
     const int lo = bs->boff[b], hi = b > 0 ? bs->boff[b - 1] : bs->btot;
     int rank = lo;
-    for (int m = lo; m < hi; ++m) rank += keys[m] > y ? 1 : 0;  // live keys are distinct
+    for (int m0 = lo; m0 < hi; m0 += 8) {
+      uint64_t c[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) c[u] = cand[min(m0 + u, nc - 1)];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) rank += (m0 + u < hi && c[u] > y) ? 1 : 0;  // live keys are distinct
+    }
     if (rank < K) out[rank] = y;
   }
   for (int m = kc + tid; m < kp; m += LSA_BLOCK) out[m] = 0;  // EMPTY past the live keys
   __syncthreads();
   return true;
+}
+
+
+// The K best of keys[0..n) (u-ordered, in LDS; n <= KPT * LSA_BLOCK) by topk_bins_regs,
+// taking the keys into registers and using keys[] as the candidate buffer (its values are
+// gone afterwards). Returns false as topk_bins_regs does (keys[] then untouched).
+template <int KPT>
+__device__ __forceinline__ bool block_topk_bins(uint64_t* keys, int n, int K, int kp, uint64_t* out,
+                                                TopkScratch* sc, BinScratch* bs) {
+  uint64_t x[KPT];
+#pragma unroll
+  for (int m = 0; m < KPT; ++m) {
+    const int j = m * LSA_BLOCK + threadIdx.x;
+    x[m] = j < n ? keys[j] : 0;
+  }
+  return topk_bins_regs<KPT>(x, K, kp, out, keys, sc, bs);
+}
+
+// The K best of the block's keys held in registers (as topk_bins_regs), sorted descending
+// into out[0..kp) by a radix select over the registers (8 passes of 8 bits at most) and a
+// bitonic sort of out: the path for any keys, ties and non-finite scores included. 1 <= K.
+// Every thread calls it.
+template <int KPT>
+__device__ __forceinline__ void topk_radix_regs(const uint64_t (&x)[KPT], int K, int kp, uint64_t* out,
+                                                RadixState* st) {
+  const int tid = threadIdx.x;
+  if (tid == 0) { st->prefix = 0; st->mask = 0; st->need = K; st->done = 0; }
+  for (int pass = 0; pass < 8; ++pass) {
+    const int shift = 56 - 8 * pass;
+    st->hist[tid] = 0;  // LSA_BLOCK == 256 bins
+    __syncthreads();
+    const uint64_t prefix = st->prefix, mask = st->mask;
+#pragma unroll
+    for (int m = 0; m < KPT; ++m)
+      if ((x[m] & mask) == prefix) atomicAdd(&st->hist[(x[m] >> shift) & 255], 1);
+    __syncthreads();
+    if (tid < LSA_WAVE) {
+      const int c0 = st->hist[255 - 4 * tid], c1 = st->hist[254 - 4 * tid];
+      const int c2 = st->hist[253 - 4 * tid], c3 = st->hist[252 - 4 * tid];
+      const int mine = c0 + c1 + c2 + c3;
+      const int inc = wave_inclusive_sum(mine);
+      int above = inc - mine;
+      const int need = st->need;
+      if (above < need && need <= inc) {
+        int d = 255 - 4 * tid, c = c0;
+        if (above + c0 < need) { above += c0; d -= 1; c = c1;
+          if (above + c1 < need) { above += c1; d -= 1; c = c2;
+            if (above + c2 < need) { above += c2; d -= 1; c = c3; } } }
+        const int rest = need - above;
+        st->prefix = prefix | ((uint64_t)d << shift);
+        st->mask = mask | (0xFFull << shift);
+        st->need = rest;
+        st->done = (c == rest) ? 1 : 0;
+      }
+    }
+    __syncthreads();
+    if (st->done) break;
+  }
+  if (tid == 0) st->slot = 0;
+  __syncthreads();
+  const uint64_t prefix = st->prefix;
+  const int done = st->done;
+#pragma unroll
+  for (int m = 0; m < KPT; ++m) {
+    const bool take = done ? (x[m] >= prefix) : (x[m] > prefix);
+    if (take) out[atomicAdd(&st->slot, 1)] = x[m];
+  }
+  __syncthreads();
+  if (!done) {
+    for (int i = st->slot + tid; i < K; i += LSA_BLOCK) out[i] = prefix;
+  }
+  for (int j = K + tid; j < kp; j += LSA_BLOCK) out[j] = 0;
+  __syncthreads();
+  bitonic_sort_desc(out, kp);
 }
 
 // The K best of keys[0..n) (u-ordered, in LDS), sorted descending into out[0..kp) with

@@ -642,6 +642,101 @@ def flat_decode(
     return out, lists, lengths
 
 
+def flat_decode_shared(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    index_queries: torch.Tensor,
+    positions: torch.Tensor,
+    buckets: Buckets,
+    config: PortConfig,
+    scale: float | None = None,
+    top_k: int | None = None,
+    score_dtype: str = "bf16",
+    splits: int | None = None,
+    readers: int | None = None,
+    slot_table: torch.Tensor | None = None,
+    slot_rows: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """One decode step over the reference's own layout in one HIP launch: one index-space
+    selection a batch row, shared by every head (the reference's decode step, port/bench.py:
+    147-153: ``flat_select`` on the index queries, then ``lsa_read`` over lists shared by
+    the heads), at any of its knobs up to 4096 buckets and 1024 picks (its defaults:
+    top_p 1024, top_k 4096, window 512, sink 4).
+
+    q [B, 1, Hq, D] (bf16 / fp16, D 64 or 128), k/v [B or 1, Tk, Hkv, D], index_queries
+    [B, d] fp32 (``make_index_space``'s queries for the decoded token), one span table for
+    every row ([rows, ...]) or one a row ([B, rows, ...]). Returns ``(out [B, 1, Hq, D],
+    lists [B, W], lengths [B])``; lists and lengths are byte-identical to
+    ``flat_select(index_queries, positions, buckets, config)``'s (any LSA_SELECT_IMPL) and
+    out is the read of those lists. ``splits`` / ``readers``: select workgroups a row and
+    reader workgroups a (row, kv-head) (default: the library's). Slot map as ``flat_decode``."""
+    from lsa_rocm_lab.port.read_kernel_tiled import _kv_layout
+
+    device = _on_device("flat_decode_shared", q, k, v, index_queries, buckets.centroids)
+    if q.dim() != 4 or q.shape[1] != 1:
+        raise ValueError(f"flat_decode_shared takes one query token per batch row: q [B, 1, Hq, D], got "
+                         f"{tuple(q.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"q/k/v dtypes differ: {q.dtype} {k.dtype} {v.dtype}")
+    B, _, Hq, D = q.shape
+    Tk, Hkv = k.shape[1], k.shape[2]
+    if k.dim() != 4 or k.shape != v.shape or k.shape[0] not in (B, 1) or k.shape[3] != D:
+        raise ValueError(f"k/v must be [B={B} or 1, Tk, Hkv, D={D}], got {tuple(k.shape)} / {tuple(v.shape)}")
+    if Hq % Hkv:
+        raise ValueError(f"{Hq} query heads do not group onto {Hkv} kv-heads")
+    if buckets.ends is None or not buckets.spans:
+        raise ValueError("flat_decode_shared expands picks from span ends: the tables need ends and spans")
+    idx = index_queries.reshape(B, -1).to(device=device, dtype=torch.float32).contiguous()
+    cent = buckets.centroids
+    if cent.dim() == 2:
+        row_tables = 0
+    elif cent.dim() == 3 and cent.shape[0] == B:
+        row_tables = 1
+    else:
+        raise ValueError(f"one bucket table for every row [rows, d] or one a row [B, rows, d], got "
+                         f"{tuple(cent.shape)}")
+    if idx.shape[1] != cent.shape[-1] or idx.shape[1] != D:
+        raise ValueError(f"index queries of dim {idx.shape[1]} for centroids of dim {cent.shape[-1]}: both must be "
+                         f"the head dim {D}")
+    q = q.contiguous()
+    k, v, sb, st, sh = _kv_layout(k, v)
+    if k.shape[0] != B:  # one pool read by every batch row
+        sb = 0
+    table, mode = _score_table(buckets, score_dtype)
+    ends = _ends(buckets)
+    flags = _table_flags(buckets, ends)
+    pos = _positions32(positions, device)
+    if pos.numel() != B:
+        raise ValueError(f"a position a batch row: {B} rows, {pos.numel()} positions")
+    top_k = config.top_k if top_k is None else top_k
+    scale = D ** -0.5 if scale is None else scale
+    rows = buckets.rows
+    width = top_k + config.window_size + config.sink_size
+    lists = torch.empty(B, width, dtype=torch.int32, device=device)
+    lengths = torch.empty(B, dtype=torch.int32, device=device)
+    out = torch.empty_like(q)
+    dt = _abi.dtype_code(q.dtype)
+    readers = int(os.environ.get("LSA_DECODE_READERS", "0")) if readers is None else readers
+    splits = int(os.environ.get("LSA_SELECT_SPLITS", "0")) if splits is None else splits
+    n_counters = _abi.size("lsa_decode_shared_counters", B, Hkv, rows)
+    nbytes = _abi.size("lsa_decode_shared_scratch_bytes", dt, B, Hq, Hkv, D, rows, config.top_p, config.window_size,
+                       config.sink_size, top_k, readers)
+    status = _abi.StatusWord.get(device)
+    if int(status[0]) != 0:
+        _decode_gave_up(device, status)
+    ws = _abi.Workspace.get(device, "decode_shared", nbytes)
+    counters = _abi.Counters.get(device, max(n_counters, 1))
+    slots, _keep = _slot_args(slot_table, slot_rows, B, device)
+    _abi.call("lsa_decode_shared", q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, Tk, Hq, Hkv, D, sb, st, sh,
+              idx.data_ptr(), table.data_ptr(), ends.data_ptr(), flags, rows, row_tables, mode, pos.data_ptr(),
+              slots, config.cluster_block_size, config.block_bucket_count, config.top_p, config.window_size,
+              config.sink_size, top_k, float(scale), splits, readers, counters.data_ptr(), counters.numel(),
+              _abi.ptr(ws), nbytes, lists.data_ptr(), lengths.data_ptr(), out.data_ptr(), _abi.ptr(status),
+              _abi.stream(device))
+    return out, lists, lengths
+
+
 def tree_decode(
     q: torch.Tensor,
     k: torch.Tensor,
