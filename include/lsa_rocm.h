@@ -351,6 +351,35 @@ int lsa_decode_shared(const void* q, const void* k, const void* v, int dtype, in
                       int32_t readers, int32_t* counters, int64_t n_counters, void* scratch, size_t scratch_bytes,
                       int32_t* lists, int32_t* lengths, void* out, int32_t* status, void* stream);
 
+/* lsa_decode_shared with the tree arm's selection: one multi-level beam walk a query row over
+ * the index-space hierarchy, shared by every kv-head (reference port/bench.py:147-153 `step`
+ * with tree_select = pipeline.py:319-337 over the index space, then read_kernel_tiled.py:
+ * 92-156 over [B, Tq, W] lists), at its own knobs (PortConfig: node size 4, node blocks of
+ * 64, 3 levels, beam 64, top_p 1024). Levels, children, growth and candidate rules as
+ * lsa_select_beam (n_levels, node_centroids, children, n_nodes, node_size, node_block,
+ * top_level, beam_width); one table a row (row_tables 1) or for every row (0), span ends
+ * required (LSA_TABLE_SPANS, optionally LSA_TABLE_BLOCK_VISIBLE); the other arguments as
+ * lsa_decode_shared. Lists and lengths are identical to lsa_select_beam's on the same
+ * queries and tables; out is the read of those lists. counters:
+ * lsa_decode_tree_shared_counters() int32 words (8-byte aligned), zero before the first
+ * launch, left zero; scratch: lsa_decode_shared_scratch_bytes(). Limits: rows and
+ * n_nodes[l] <= 8192, at most 4096 candidates a level, min(top_p, candidates) <= 1024
+ * picks, the reader LDS within 64 KiB. */
+int64_t lsa_decode_tree_shared_counters(int64_t R, int32_t Hkv, int32_t n_levels, const int32_t* n_nodes,
+                                        int32_t rows);
+int lsa_decode_tree_shared(const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk, int32_t Hq,
+                           int32_t Hkv, int32_t D, int64_t kv_batch_stride, int64_t kv_token_stride,
+                           int64_t kv_head_stride, const float* index_queries, int32_t n_levels,
+                           const void* const* node_centroids, const int32_t* const* children,
+                           const int32_t* n_nodes, int32_t node_size, int32_t node_block, int32_t top_level,
+                           const void* centroids, const int32_t* ends, int32_t table_flags, int32_t rows,
+                           int64_t row_tables, int score_mode, const int32_t* positions,
+                           const lsa_slot_map* slots, int32_t cluster_block_size, int32_t block_buckets,
+                           int32_t beam_width, int32_t top_p, int32_t window, int32_t sink, int32_t top_k,
+                           float scale, int32_t select_splits, int32_t readers, int32_t* counters,
+                           int64_t n_counters, void* scratch, size_t scratch_bytes, int32_t* lists,
+                           int32_t* lengths, void* out, int32_t* status, void* stream);
+
 /* lsa_decode_flat without caller buffers, for callers that cannot allocate (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart
  * in the reference. The counters and scratch live in a 16 MiB file-scope device array per

@@ -22,7 +22,8 @@ CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "lsa_rocm_lab" / "_lib" / "liblsa_rocm.so"
 SOURCES = ["lsa_abi.cpp", "select.hip", "beam.hip", "read.hip", "read_prefill.hip", "decode.hip", "decode_bf16.hip",
-           "decode_f16.hip", "decode_f32.hip", "decode_noalloc.hip", "decode_shared.hip", "build.hip"]
+           "decode_f16.hip", "decode_f32.hip", "decode_noalloc.hip", "decode_shared.hip", "decode_tree_shared.hip",
+           "build.hip"]
 ARCH = os.environ.get("LSA_OFFLOAD_ARCH", "gfx950")
 
 

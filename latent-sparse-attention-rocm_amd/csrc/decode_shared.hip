@@ -1,399 +1,11 @@
-// Fused decode step with one selection a query row shared by every kv-head, for gfx950:
-// the reference's own layout (one index-space table and one index query a position, the
-// lists shared by every head: pipeline.py:248-316 flat_select over the index space, then
-// read_kernel_tiled.py:92-156 with [B, Tq, W] lists; port/bench.py:147-153 `step`) at its
-// own knobs (PortConfig, pipeline.py:32-54: up to 4096 buckets, top_p 1024, top_k 4096).
-//
-// The 1-D grid holds S select workgroups a row, then NR readers for every (row, kv-head)
-// unit (unit fastest).
-//
-// Select workgroup (row r, split s): scores columns [s*cs, (s+1)*cs) of row r's bucket
-// table with the row's fp32 index query (the canonical score; visibility by span ends or by
-// closed blocks) and publishes each column's key + 1 (nonzero once written) with device-
-// scope stores. It never waits.
-//
-// Reader (unit (r, g), role): loads its kv-head's query rows, the table's span ends into
-// LDS and (a paged cache) warms the slot-table row in its XCD's L2; then every wave polls
-// its share of the row's published keys (16 a lane, all in flight each round) until all
-// are written (bounded: past the spin limit it sets *status, arrives and exits). The keys
-// stay in registers: the block ranks them (topk_bins_regs; a register radix select when a
-// score is not finite or a bin is crowded), takes each pick's kept range [max(begin, sink),
-// min(end, window start)) from the span ends, places them by one block scan (clipped at
-// top_k) and reads its contiguous run of the list's tiles: ids expanded (and mapped through
-// the slot table), written to the shared list by kv-head 0's readers, gathered with the
-// pipelined tile loop. Partials are combined by the unit's last reader; the last unit of a
-// row to finish clears the row's published keys, so every launch finds them zero.
-//
-// Readers wait only on select workgroups, which hold lower ids and never wait: dispatched
-// in id order, the select workgroups are resident (or done) before any reader holds a slot.
-#include "lsa_abi_common.h"
-#include "decode_dev.h"
+// Entry points of the fused decode with one flat selection a row shared by every kv-head
+// (reference pipeline.py:248-316 flat_select over the index space, then
+// read_kernel_tiled.py:92-156; port/bench.py:147-153 `step`). The kernel is in
+// decode_shared_impl.h.
+#include "decode_shared_impl.h"
 
 using namespace lsa;
-using namespace lsa::decode;
-
-namespace {
-
-constexpr int kShMaxRows = 16 * LSA_BLOCK;  // buckets a table: 16 keys a reader thread holds
-constexpr int kShMaxPicks = 4 * LSA_BLOCK;  // picks: 4 a thread in the placement scan
-constexpr int kShMaxReaders = 64;           // readers a unit (split partials of the combine)
-constexpr size_t kShMaxLds = 64 * 1024;
-
-struct SharedArgs {
-  const void* q;
-  const void* k;
-  const void* v;
-  void* out;
-  int64_t R;
-  int G, Hq;
-  int64_t Tk, kv_sb, kv_st, kv_sh;
-  const float* idx_q;       // [R, D] fp32 index queries
-  const void* centroids;    // [tables, rows, D], the scoring type
-  const int32_t* ends;      // [tables, rows] span ends
-  const int32_t* vends;     // the ends that decide visibility (nullptr: the closed-block rule)
-  int rows;
-  int64_t row_tables;       // table of row r: r * row_tables
-  const int32_t* positions;
-  int cluster_block, block_buckets;
-  int K, kp, window, sink, top_k, W;
-  int S, cs;                // select workgroups a row, columns each
-  int span, NR;             // slots a read tile, readers a unit
-  float scale_log2;
-  int spin_limit;
-  int skip_publish;         // test hook: the select workgroups never publish (readers give up)
-  uint64_t* pub;            // [R][rows] published keys + 1 (0: not yet written)
-  int* rd_count;            // [R * G] reader arrivals
-  int* done;                // [R] units of a row finished
-  float* ws_part;           // [R * G][NR][GQ * (D + 2)]
-  int32_t* lists;           // [R][W]
-  int32_t* lengths;         // [R]
-  int32_t* status;
-  SlotMap slots;
-};
-
-// Reader LDS: a header, the picks (first kept id and first list slot of each), then a
-// region the selection phase (span ends, sorted keys, candidates, top-K state) and the
-// read phase (ids of a chunk, the read's merge state) take in turn.
-struct ShHdr {
-  int filled, bad, last;
-  int wbad[LSA_WAVES];
-  int scan[LSA_WAVES];
-};
-constexpr size_t a16(size_t x) { return (x + 15) & ~(size_t)15; }
-__host__ __device__ inline size_t sh_picks_at() { return a16(sizeof(ShHdr)); }
-__host__ __device__ inline size_t sh_region_at(int kp) { return sh_picks_at() + a16(sizeof(int32_t) * (2 * (size_t)kp + 1)); }
-// selection phase, within the region
-__host__ __device__ inline size_t sh_best_at(int rows) { return a16(sizeof(int32_t) * (size_t)rows); }
-__host__ __device__ inline size_t sh_cand_at(int rows, int kp) { return sh_best_at(rows) + sizeof(uint64_t) * (size_t)kp; }
-__host__ __device__ inline size_t sh_topk_at(int rows, int kp) {
-  return a16(sh_cand_at(rows, kp) + sizeof(uint64_t) * ((size_t)kp + LSA_WAVE));
-}
-__host__ __device__ inline size_t sh_sel_bytes(int rows, int kp) {
-  return sh_topk_at(rows, kp) + a16(sizeof(TopkScratch)) + a16(sizeof(BinScratch)) + a16(sizeof(RadixState));
-}
-// read phase, within the region: ids of a chunk, then the merge state
-constexpr int kShChunkTiles = 32;
-template <int D, int GQ>
-__host__ __device__ inline size_t sh_rd_at(int span) { return a16(sizeof(int32_t) * (size_t)kShChunkTiles * span); }
-template <int D, int GQ>
-__host__ __device__ inline size_t sh_read_bytes(int span) {
-  return sh_rd_at<D, GQ>(span) + sizeof(ReadLds<D, GQ, kShMaxReaders>);
-}
-template <int D, int GQ>
-__host__ __device__ inline size_t sh_lds(int rows, int kp, int span) {
-  const size_t sel = sh_sel_bytes(rows, kp), rd = sh_read_bytes<D, GQ>(span);
-  return sh_region_at(kp) + (sel > rd ? sel : rd);
-}
-
-template <typename CT, int D>
-__device__ __forceinline__ void shared_select(const SharedArgs& a, char* smem, int64_t r, int s) {
-  constexpr int SPAN = D / 16;
-  uint64_t* keys = (uint64_t*)smem;  // [cs]
-  const int tid = threadIdx.x;
-  const int64_t position = a.positions[r];
-  const int64_t t = r * a.row_tables;
-  const CT* cent = (const CT*)a.centroids + t * a.rows * (int64_t)D;
-  const int32_t* vends = a.vends ? a.vends + t * a.rows : nullptr;
-  const int c0 = s * a.cs;
-  const int c1 = min(c0 + a.cs, a.rows);
-  const int n_local = c1 > c0 ? c1 - c0 : 0;
-  const int vis = vends ? 0 : visible_closed(position, a.rows, a.cluster_block, a.block_buckets);
-  const int64_t lim = position + 1;
-  float qs[SPAN];
-  load_query_slice<float, SPAN>(a.idx_q + r * D, tid & 15, __is_same(CT, bf16_t), qs);
-  score_keys<CT, SPAN>(
-      qs, cent, D, n_local, [&](int j) { return c0 + j; },
-      [&](int j) { return vends ? (int64_t)vends[c0 + j] <= lim : c0 + j < vis; }, keys);
-  __syncthreads();
-  DECODE_MARK(1);
-  if (a.skip_publish) return;
-  uint64_t* mine = a.pub + r * (int64_t)a.rows;
-  for (int j = tid; j < n_local; j += LSA_BLOCK) coherent_store_u64(mine + c0 + j, keys[j] + 1);
-  DECODE_MARK(6);
-}
-
-// The unit's last reader: the row's keys are cleared once every kv-head's unit is done.
-__device__ __forceinline__ void shared_unit_done(const SharedArgs& a, ShHdr& hd, int64_t r) {
-  if (threadIdx.x == 0) {
-    const int before = __hip_atomic_fetch_add(&a.done[r], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    hd.last = before == a.G - 1;
-    if (hd.last) __hip_atomic_store(&a.done[r], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (hd.last) {
-    uint64_t* pub = a.pub + r * (int64_t)a.rows;
-    for (int x = threadIdx.x; x < a.rows; x += LSA_BLOCK) coherent_store_u64(pub + x, 0);
-  }
-}
-
-template <typename T, int D, int GQ>
-__device__ __forceinline__ void shared_reader(const SharedArgs& a, char* smem, int64_t i, int role) {
-  using S = ReadShape<T, D, GQ>;
-  constexpr int VEC = S::VEC, LPT = S::LPT, KPT = kShMaxRows / LSA_BLOCK;
-  constexpr int PSTRIDE = GQ * (D + 2);
-  ShHdr& hd = *(ShHdr*)smem;
-  int32_t* first = (int32_t*)(smem + sh_picks_at());  // [kp]: a pick's first kept id
-  int32_t* start = first + a.kp;                        // [kp + 1]: its first list slot
-  char* region = smem + sh_region_at(a.kp);
-  int32_t* ends_l = (int32_t*)region;                                      // selection: [rows]
-  uint64_t* best = (uint64_t*)(region + sh_best_at(a.rows));               // [kp]
-  uint64_t* cand = (uint64_t*)(region + sh_cand_at(a.rows, a.kp));         // [kp + 64]
-  TopkScratch* tks = (TopkScratch*)(region + sh_topk_at(a.rows, a.kp));
-  BinScratch* bins = (BinScratch*)((char*)tks + a16(sizeof(TopkScratch)));
-  RadixState* rst = (RadixState*)((char*)bins + a16(sizeof(BinScratch)));
-  int32_t* ids = (int32_t*)region;                                          // read: [chunk * span]
-  ReadLds<D, GQ, kShMaxReaders>& rd = *(ReadLds<D, GQ, kShMaxReaders>*)(region + sh_rd_at<D, GQ>(a.span));
-  const int tid = threadIdx.x, lane = tid & (LSA_WAVE - 1), w = tid / LSA_WAVE;
-  const int K = a.K, rows = a.rows;
-  const int64_t r = (uint32_t)i / (uint32_t)a.G;
-  const int g = (int)((uint32_t)i % (uint32_t)a.G);
-  const int64_t position = a.positions[r];
-  const int64_t wstart = window_start_of(position, a.window);
-  const int64_t n_win = position + 1 - wstart > 0 ? position + 1 - wstart : 0;
-  const int64_t n_sink = a.sink < wstart ? a.sink : wstart;
-  const int64_t t = r * a.row_tables;
-
-  // the query rows, the slot table row and the span ends go out before the wait
-  const T* qrow = (const T*)a.q + (r * a.Hq + (int64_t)g * GQ) * D;
-  QueryRegs<T, D, GQ> qr;
-  qr.load(qrow, a.scale_log2);
-  const SlotRow map = slot_row_of(a.slots, r);
-  const int32_t* ends = a.ends + t * rows;
-  for (int m = tid; m < rows; m += LSA_BLOCK) ends_l[m] = ends[m];
-  const int32_t touched = touch_slot_lines(map, position, role, a.NR);
-
-  // every wave polls its share of the row's keys (key m * 256 + tid in x[m]) until all of
-  // them are written, every load of a round in flight together
-  const uint64_t* pub = a.pub + r * (int64_t)rows;
-  uint64_t x[KPT];
-  int bad = 0;
-  for (int it = 0;; ++it) {
-    bool ok = true;
-#pragma unroll
-    for (int m = 0; m < KPT; ++m) {
-      const int j = m * LSA_BLOCK + tid;
-      x[m] = coherent_load_u64(pub + (j < rows ? j : 0));
-      ok &= j >= rows || x[m] != 0;
-    }
-    if (__all(ok)) break;
-    if (it >= a.spin_limit) {
-      bad = 1;
-      break;
-    }
-    __builtin_amdgcn_s_sleep(2);
-  }
-  DECODE_MARK(1);
-#pragma unroll
-  for (int m = 0; m < KPT; ++m) x[m] = m * LSA_BLOCK + tid < rows ? x[m] - 1 : 0;  // EMPTY past the table
-  if (lane == 0) hd.wbad[w] = bad;
-  __syncthreads();
-  keep_live(touched);
-  if (hd.wbad[0] | hd.wbad[1] | hd.wbad[2] | hd.wbad[3]) {
-    // no keys: this reader writes nothing but still arrives, so the counters reset; *status
-    // tells the caller the launch's outputs are invalid
-    if (tid == 0 && a.status) __hip_atomic_store(a.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    if (arrive_last(&a.rd_count[i], a.NR, &rd.flag)) shared_unit_done(a, hd, r);
-    return;
-  }
-
-  // the K best keys, sorted (the select's top-K on the same keys)
-  if (!topk_bins_regs<KPT>(x, K, a.kp, best, cand, tks, bins)) topk_radix_regs<KPT>(x, K, a.kp, best, rst);
-  DECODE_MARK(7);
-
-  // each pick's kept range from the span ends, placed by one block scan, clipped at top_k
-  constexpr int PPT = kShMaxPicks / LSA_BLOCK;
-  int lo[PPT], cnt[PPT], mine = 0;
-#pragma unroll
-  for (int p = 0; p < PPT; ++p) {
-    const int j = PPT * tid + p;
-    const int32_t b = j < K ? key_column(u_to_key(best[j])) : -1;
-    const bool okb = b >= 0 && b < rows;
-    const int64_t begin = okb && b > 0 ? ends_l[b - 1] : 0, end_b = okb ? ends_l[b] : 0;
-    const int64_t l = begin > a.sink ? begin : a.sink, h = end_b < wstart ? end_b : wstart;
-    lo[p] = (int)l;
-    cnt[p] = okb && h > l ? (int)(h - l) : 0;
-    mine += cnt[p];
-  }
-  int total;
-  int at = block_exclusive_sum(mine, hd.scan, &total);
-  const int filled = total < a.top_k ? total : a.top_k;
-#pragma unroll
-  for (int p = 0; p < PPT; ++p) {
-    const int j = PPT * tid + p;
-    if (j < K) {
-      first[j] = lo[p];
-      start[j] = at < filled ? at : filled;
-    }
-    at += cnt[p];
-  }
-  if (tid == 0) {
-    start[K] = filled;
-    hd.filled = filled;
-    if (g == 0 && role == 0) a.lengths[r] = filled + (int)(n_win + n_sink);
-  }
-  __syncthreads();  // picks placed; the selection phase's LDS is free from here
-  DECODE_MARK(8);
-
-  // the read: reader `role` takes a contiguous run of the list's tiles
-  const int length = filled + (int)(n_win + n_sink);
-  const int span = a.span, NR = a.NR;
-  const int TT = (length + span - 1) / span;
-  const int q_t = TT / NR, rem = TT % NR;
-  const int t_lo = role * q_t + (role < rem ? role : rem);
-  const int t_hi = t_lo + q_t + (role < rem ? 1 : 0);
-  const int lo_s = t_lo * span, hi_s = min(length, t_hi * span);
-  const int n_part = TT < NR ? TT : NR;
-  int32_t* lrow = a.lists + r * (int64_t)a.W;
-  const bool writer = g == 0;  // the shared list is written once, by kv-head 0's readers
-  const int lp = lane % LPT;
-  const T* kb = (const T*)a.k + r * a.kv_sb + g * a.kv_sh + lp * VEC;
-  const T* vb = (const T*)a.v + r * a.kv_sb + g * a.kv_sh + lp * VEC;
-  auto pick_of = [&](int s_) {  // the last pick whose first slot is <= s_
-    int a_ = 0, b_ = K;
-    while (b_ - a_ > 1) {
-      const int m_ = (a_ + b_) >> 1;
-      if (start[m_] <= s_) a_ = m_; else b_ = m_;
-    }
-    return a_;
-  };
-  AttnState<T, D, GQ> st;
-  st.clear();
-  bool fresh = true;
-  for (int c_lo = lo_s; c_lo < hi_s; c_lo += kShChunkTiles * span) {
-    const int c_hi = min(hi_s, c_lo + kShChunkTiles * span);
-    const int n = c_hi - c_lo;
-    for (int k = tid; k < n; k += LSA_BLOCK) {
-      const int s_ = c_lo + k;
-      int32_t id;
-      if (s_ < filled) {
-        const int j = pick_of(s_);
-        id = first[j] + (s_ - start[j]);
-      } else {
-        id = tail_id(s_ - filled, wstart, n_win, n_sink);
-      }
-      id = map(id);
-      ids[k] = id;
-      if (writer) lrow[s_] = id;
-    }
-    __syncthreads();
-    attend_tiles<T, D, GQ, true>(
-        qr, kb, vb, a.kv_st, a.Tk, 0, n,
-        [&](int jj) {
-          const int32_t v_ = ids[jj < n ? jj : 0];
-          return jj < n ? v_ : -1;
-        },
-        a.scale_log2, fresh, st);
-    fresh = false;
-    __syncthreads();  // ids are rewritten by the next chunk
-  }
-
-  DECODE_MARK(3);
-  T* outp = (T*)a.out + (r * a.Hq + (int64_t)g * GQ) * D;
-  float* parts = a.ws_part + i * (int64_t)NR * PSTRIDE;
-  if (role < n_part) {
-    finish_span<T, D, GQ>(rd, st, n_part == 1, outp, n_part > 1 ? parts + (int64_t)role * PSTRIDE : nullptr, 0);
-  }
-  if (writer) {  // the list's padding [length, W), shared out over the readers
-    const int per = (a.W - length + NR - 1) / NR;
-    const int p0 = length + role * per;
-    const int p1 = min(p0 + per, a.W);
-    for (int k = p0 + tid; k < p1; k += LSA_BLOCK) lrow[k] = -1;
-  }
-  DECODE_MARK(11);
-  if (!arrive_last(&a.rd_count[i], NR, &rd.flag)) return;
-  if (n_part > 1) {
-    combine_partials<T, D, GQ>(rd, parts, n_part, outp, 0);
-  } else if (n_part == 0) {  // nothing to read: zeros
-    for (int k = tid; k < GQ * D; k += LSA_BLOCK) store_out<T>(outp + k, 0.0f);
-  }
-  DECODE_MARK(13);
-  shared_unit_done(a, hd, r);
-}
-
-template <typename T, typename CT, int D, int GQ>
-__global__ __launch_bounds__(LSA_BLOCK) void decode_shared_kernel(SharedArgs a) {
-  extern __shared__ __align__(16) char smem[];
-  const uint32_t nsel = (uint32_t)a.R * (uint32_t)a.S;  // the grid is < 2^31 workgroups (checked on the host)
-  const uint32_t id = blockIdx.x;
-  DECODE_TRACE_BEGIN();
-  if (id < nsel) {
-    shared_select<CT, D>(a, smem, id % (uint32_t)a.R, (int)(id / (uint32_t)a.R));
-  } else {
-    const uint32_t units = (uint32_t)a.R * (uint32_t)a.G;
-    const uint32_t rid = id - nsel;  // readers: unit fastest, then role (low roles have work)
-    shared_reader<T, D, GQ>(a, smem, rid % units, (int)(rid / units));
-  }
-  DECODE_TRACE_END();
-}
-
-// ------------------------------------------------------------------ host
-
-template <typename T, typename CT, int D>
-void launch_sh_gq(const SharedArgs& a, int gq, dim3 grid, size_t shmem, hipStream_t s) {
-  switch (gq) {
-    case 1: decode_shared_kernel<T, CT, D, 1><<<grid, LSA_BLOCK, shmem, s>>>(a); break;
-    case 2: decode_shared_kernel<T, CT, D, 2><<<grid, LSA_BLOCK, shmem, s>>>(a); break;
-    case 4: decode_shared_kernel<T, CT, D, 4><<<grid, LSA_BLOCK, shmem, s>>>(a); break;
-    default: decode_shared_kernel<T, CT, D, 8><<<grid, LSA_BLOCK, shmem, s>>>(a); break;
-  }
-}
-
-template <typename T, typename CT>
-void launch_sh_d(const SharedArgs& a, int D, int gq, dim3 grid, size_t shmem, hipStream_t s) {
-  if (D == 64) launch_sh_gq<T, CT, 64>(a, gq, grid, shmem, s);
-  else launch_sh_gq<T, CT, 128>(a, gq, grid, shmem, s);
-}
-
-template <int D>
-size_t sh_lds_gq(int gq, int rows, int kp, int span) {
-  switch (gq) {
-    case 1: return sh_lds<D, 1>(rows, kp, span);
-    case 2: return sh_lds<D, 2>(rows, kp, span);
-    case 4: return sh_lds<D, 4>(rows, kp, span);
-    default: return sh_lds<D, 8>(rows, kp, span);
-  }
-}
-
-// Readers per unit by default: about 24 (the list's tiles spread over CUs) but enough for
-// ~512 workgroups in all when there are many units, never more tiles than a list holds.
-constexpr int kShDefaultReaders = 24;
-constexpr int kShSpread = 512;
-
-int sh_readers(int64_t units, int K, int span, int top_k, int window, int sink) {
-  const int64_t tiles = ((int64_t)top_k + window + sink + span - 1) / span;
-  int64_t nr = kShDefaultReaders;
-  const int64_t spread = (kShSpread + units - 1) / units;
-  if (spread < nr) nr = spread;
-  if (tiles < nr) nr = tiles;
-  if (nr < 1) nr = 1;
-  (void)K;
-  return (int)nr;
-}
-
-// Word offset of the published keys (after the reader arrivals and the rows' unit counts).
-int64_t sh_keys_at(int64_t R, int32_t G) { return (R * G + R + 63) / 64 * 64; }
-
-}  // namespace
+using namespace lsa::shared;
 
 extern "C" int64_t lsa_decode_shared_counters(int64_t R, int32_t Hkv, int32_t rows) {
   if (R <= 0 || Hkv <= 0 || rows <= 0 || rows > kShMaxRows) return 0;
@@ -403,14 +15,8 @@ extern "C" int64_t lsa_decode_shared_counters(int64_t R, int32_t Hkv, int32_t ro
 extern "C" size_t lsa_decode_shared_scratch_bytes(int dtype, int64_t R, int32_t Hq, int32_t Hkv, int32_t D,
                                                   int32_t rows, int32_t top_p, int32_t window, int32_t sink,
                                                   int32_t top_k, int32_t readers) {
-  if (R <= 0 || Hkv <= 0 || Hq < Hkv || Hq % Hkv || rows <= 0 || top_p <= 0) return 0;
-  const int gq = Hq / Hkv;
-  const int span = lsa_read_tile_tokens(dtype, D, gq);
-  if (span <= 0) return 0;
-  const int K = top_p < rows ? top_p : rows;
-  const int NR = readers > 0 ? readers : sh_readers(R * Hkv, K, span, top_k < 0 ? 0 : top_k, window < 0 ? 0 : window,
-                                                    sink < 0 ? 0 : sink);
-  return NR > 1 ? (size_t)(R * Hkv) * NR * (size_t)(gq * (D + 2)) * sizeof(float) : 0;
+  if (rows <= 0 || top_p <= 0) return 0;
+  return sh_scratch(dtype, R, Hq, Hkv, D, top_k, window, sink, readers);
 }
 
 extern "C" int lsa_decode_shared(const void* q, const void* k, const void* v, int dtype, int64_t R, int64_t Tk,
@@ -424,95 +30,17 @@ extern "C" int lsa_decode_shared(const void* q, const void* k, const void* v, in
                                  void* scratch, size_t scratch_bytes, int32_t* lists, int32_t* lengths, void* out,
                                  int32_t* status, void* stream) {
   const char* who = "lsa_decode_shared";
-  LSA_REQUIRE(q && k && v && index_queries && centroids && ends && positions && lists && lengths && out && counters,
-              LSA_ERR_NULL, "%s: NULL pointer", who);
-  SlotMap sm;
-  LSA_TRY(check_slots(who, slots, &sm));
-  LSA_REQUIRE(dtype == LSA_BF16 || dtype == LSA_F16, LSA_ERR_DTYPE, "%s: bf16 or fp16 K/V, got dtype %d", who,
-              dtype);
-  LSA_REQUIRE(D == 64 || D == 128, LSA_ERR_SHAPE, "%s: head dim %d not in {64, 128}", who, D);
-  LSA_REQUIRE(Hq >= 1 && Hkv >= 1 && Hq % Hkv == 0, LSA_ERR_SHAPE, "%s: Hq %d must group onto Hkv %d", who, Hq, Hkv);
-  const int gq = Hq / Hkv;
-  LSA_REQUIRE(gq == 1 || gq == 2 || gq == 4 || gq == 8, LSA_ERR_SHAPE, "%s: group size %d not in {1,2,4,8}", who,
-              gq);
-  LSA_REQUIRE(score_mode == LSA_SCORE_BF16 || score_mode == LSA_SCORE_F32, LSA_ERR_DTYPE, "%s: bad score mode", who);
-  LSA_REQUIRE(rows >= 1 && rows <= kShMaxRows && row_tables >= 0, LSA_ERR_SHAPE,
-              "%s: tables of 1..%d buckets, got %d", who, kShMaxRows, rows);
-  LSA_REQUIRE(R >= 0 && Tk >= 0 && Tk <= 0x7FFFFFFF, LSA_ERR_SHAPE, "%s: bad sizes", who);
-  LSA_REQUIRE(top_p >= 1 && window >= 0 && sink >= 0 && top_k >= 0, LSA_ERR_SHAPE,
-              "%s: top_p >= 1, window/sink/top_k >= 0", who);
-  LSA_REQUIRE((table_flags & ~(LSA_TABLE_SPANS | LSA_TABLE_BLOCK_VISIBLE)) == 0 && (table_flags & LSA_TABLE_SPANS),
-              LSA_ERR_SHAPE, "%s: span tables (LSA_TABLE_SPANS, optionally LSA_TABLE_BLOCK_VISIBLE), got flags %d",
-              who, table_flags);
-  LSA_REQUIRE(!(table_flags & LSA_TABLE_BLOCK_VISIBLE) || cluster_block_size >= 1, LSA_ERR_SHAPE,
-              "%s: cluster_block_size must be >= 1", who);
+  SharedArgs a;
+  LSA_TRY(sh_common(who, a, q, k, v, dtype, R, Tk, Hq, Hkv, D, kv_batch_stride, kv_token_stride, kv_head_stride,
+                    index_queries, centroids, ends, table_flags, rows, row_tables, score_mode, positions, slots,
+                    cluster_block_size, block_buckets, top_p, window, sink, top_k, scale, readers, counters, lists,
+                    lengths, out, status));
+  LSA_REQUIRE(rows <= kShMaxRows, LSA_ERR_SHAPE, "%s: tables of 1..%d buckets, got %d", who, kShMaxRows, rows);
   const int K = top_p < rows ? top_p : rows;
   LSA_REQUIRE(K <= kShMaxPicks, LSA_ERR_SHAPE, "%s: %d picks exceed %d", who, K, kShMaxPicks);
-  LSA_REQUIRE((int64_t)top_k + window + sink <= 0x7FFFFFFF, LSA_ERR_SHAPE, "%s: list too wide", who);
-  const uintptr_t mis = ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)centroids) & 15;
-  LSA_REQUIRE(mis == 0 && ((uintptr_t)index_queries & 15) == 0, LSA_ERR_ALIGN,
-              "%s: q/k/v/centroids/index queries must be 16-byte aligned", who);
-  LSA_REQUIRE(kv_batch_stride >= 0 && kv_token_stride >= D && kv_head_stride >= D, LSA_ERR_SHAPE,
-              "%s: K/V strides must leave rows of %d elements apart", who, D);
-  LSA_REQUIRE(((kv_batch_stride | kv_token_stride | kv_head_stride) * 2) % 16 == 0, LSA_ERR_ALIGN,
-              "%s: K/V strides must keep rows 16-byte aligned", who);
-  const int64_t units = R * Hkv;
-  if (units == 0) return LSA_OK;
-  const int span = lsa_read_tile_tokens(dtype, D, gq);
-  LSA_REQUIRE(span > 0, LSA_ERR_SHAPE, "%s: no read tile for D=%d group=%d", who, D, gq);
-  LSA_REQUIRE(readers >= 0 && readers <= kShMaxReaders, LSA_ERR_SHAPE, "%s: readers in [0, %d], got %d", who,
-              kShMaxReaders, readers);
-  const int NR = readers > 0 ? readers : sh_readers(units, K, span, top_k, window, sink);
-  const int S = select_splits > 0 ? select_splits : (rows + 63) / 64 < 256 ? (rows + 63) / 64 : 256;
-  LSA_REQUIRE(S >= 1 && S <= 256 && S <= rows, LSA_ERR_SHAPE, "%s: select splits in [1, min(256, rows)], got %d",
-              who, S);
-  const int kp = next_pow2(K);
-  const size_t shmem = D == 64 ? sh_lds_gq<64>(gq, rows, kp, span) : sh_lds_gq<128>(gq, rows, kp, span);
-  const int cs = (rows + S - 1) / S;
-  const size_t sel_lds = sizeof(uint64_t) * (size_t)cs;
-  const size_t lds = shmem > sel_lds ? shmem : sel_lds;
-  LSA_REQUIRE(lds <= kShMaxLds, LSA_ERR_SHAPE, "%s: %zu bytes of LDS exceed %zu (fewer buckets or picks)", who, lds,
-              kShMaxLds);
-  const int64_t grid = R * S + units * NR;
-  LSA_REQUIRE(grid <= 0x7FFFFFFF && units < (1ll << 31), LSA_ERR_SHAPE, "%s: too many workgroups", who);
-  const int64_t need_counters = lsa_decode_shared_counters(R, Hkv, rows);
-  LSA_REQUIRE(need_counters > 0 && n_counters >= need_counters, LSA_ERR_WORKSPACE, "%s: %lld counters < %lld", who,
-              (long long)n_counters, (long long)need_counters);
-  const size_t need = lsa_decode_shared_scratch_bytes(dtype, R, Hq, Hkv, D, rows, top_p, window, sink, top_k, NR);
-  LSA_REQUIRE(need == 0 || (scratch && scratch_bytes >= need), LSA_ERR_WORKSPACE, "%s: scratch %zu < %zu bytes", who,
-              scratch_bytes, need);
-  LSA_REQUIRE(((uintptr_t)scratch % 16) == 0 && ((uintptr_t)counters % 8) == 0, LSA_ERR_ALIGN,
-              "%s: scratch must be 16-byte and counters 8-byte aligned", who);
-
-  SharedArgs a;
-  a.q = q; a.k = k; a.v = v; a.out = out;
-  a.R = R; a.G = Hkv; a.Hq = Hq;
-  a.Tk = Tk; a.kv_sb = kv_batch_stride; a.kv_st = kv_token_stride; a.kv_sh = kv_head_stride;
-  a.idx_q = index_queries; a.centroids = centroids; a.ends = ends;
-  a.vends = (table_flags & LSA_TABLE_BLOCK_VISIBLE) ? nullptr : ends;
-  a.rows = rows; a.row_tables = row_tables; a.positions = positions;
-  a.cluster_block = cluster_block_size; a.block_buckets = block_buckets;
-  a.K = K; a.kp = kp; a.window = window; a.sink = sink; a.top_k = top_k; a.W = top_k + window + sink;
-  a.S = S; a.cs = cs; a.span = span; a.NR = NR;
-  a.scale_log2 = scale * kLog2e;
-  a.spin_limit = decode_debug().spin_limit > 0 ? decode_debug().spin_limit : 1 << 22;
-  a.skip_publish = decode_debug().skip_publish;
-  a.rd_count = counters;
-  a.done = counters + units;
-  a.pub = (uint64_t*)(counters + sh_keys_at(R, Hkv));
-  a.ws_part = need ? (float*)scratch : nullptr;
-  a.lists = lists; a.lengths = lengths; a.status = status;
-  a.slots = sm;
-  const dim3 g3((unsigned)grid);
-  hipStream_t s = (hipStream_t)stream;
-  const bool bf16_table = score_mode == LSA_SCORE_BF16;
-  if (dtype == LSA_BF16) {
-    if (bf16_table) launch_sh_d<bf16_t, bf16_t>(a, D, gq, g3, lds, s);
-    else launch_sh_d<bf16_t, float>(a, D, gq, g3, lds, s);
-  } else {
-    if (bf16_table) launch_sh_d<_Float16, bf16_t>(a, D, gq, g3, lds, s);
-    else launch_sh_d<_Float16, float>(a, D, gq, g3, lds, s);
-  }
-  LSA_LAUNCHED(who);
-  return LSA_OK;
+  a.K = K;
+  a.kp = next_pow2(K);
+  a.n_cols = rows;
+  return sh_finish<false>(who, a, dtype, D, score_mode, select_splits, readers, sh_sel_bytes(rows, a.kp), counters,
+                          n_counters, lsa_decode_shared_counters(R, Hkv, rows), scratch, scratch_bytes, stream);
 }

@@ -90,6 +90,11 @@ SIGNATURES = {
     "lsa_decode_shared": (_int, [_p, _p, _p, _int, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _p, _i32,
                                  _i32, _i64, _int, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p,
                                  _i64, _p, _sz, _p, _p, _p, _p, _p]),
+    "lsa_decode_tree_shared_counters": (_i64, [_i64, _i32, _i32, _p, _i32]),
+    "lsa_decode_tree_shared": (_int, [_p, _p, _p, _int, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _i32, _p,
+                                      _p, _p, _i32, _i32, _i32, _p, _p, _i32, _i32, _i64, _int, _p, _p, _i32, _i32,
+                                      _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p, _i64, _p, _sz, _p, _p, _p,
+                                      _p, _p]),
     "lsa_decode_flat_noalloc": (_int, [_p, _p, _p, _int, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _p,
                                        _i32, _i32, _i32, _i64, _i64, _int, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                                        _f32, _i32, _i32, _i32, _p, _p, _p, _p, _p]),

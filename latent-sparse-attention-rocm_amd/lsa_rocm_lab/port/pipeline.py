@@ -38,6 +38,7 @@ buckets ending at or before ``position + 1``.
 
 from __future__ import annotations
 
+import ctypes
 import math
 import os
 from dataclasses import dataclass, field
@@ -734,6 +735,130 @@ def flat_decode_shared(
               config.sink_size, top_k, float(scale), splits, readers, counters.data_ptr(), counters.numel(),
               _abi.ptr(ws), nbytes, lists.data_ptr(), lengths.data_ptr(), out.data_ptr(), _abi.ptr(status),
               _abi.stream(device))
+    return out, lists, lengths
+
+
+def tree_decode_shared(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    index_queries: torch.Tensor,
+    positions: torch.Tensor,
+    buckets: Buckets,
+    hierarchy: Hierarchy,
+    config: PortConfig,
+    scale: float | None = None,
+    top_k: int | None = None,
+    score_dtype: str = "fp32",
+    splits: int | None = None,
+    readers: int | None = None,
+    slot_table: torch.Tensor | None = None,
+    slot_rows: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The tree arm of the reference's decode step in one HIP launch: one multi-level beam
+    selection a batch row over the index-space hierarchy, shared by every head (port/bench.py:
+    147-153 with ``tree_select``, pipeline.py:319-337, then ``lsa_read``), at any of its
+    knobs up to 8192 buckets / nodes a level and 1024 picks (its defaults: node size 4,
+    node blocks of 64, 3 levels, beam 64, top_p 1024, top_k 4096, window 512, sink 4).
+
+    Shapes as ``flat_decode_shared``; ``hierarchy`` as ``tree_select``'s (its levels' tables
+    one for every row or one a row, like the buckets'). Returns ``(out [B, 1, Hq, D], lists
+    [B, W], lengths [B])``; lists and lengths are byte-identical to ``tree_select(
+    index_queries, positions, buckets, hierarchy, config, score_dtype=score_dtype)``'s."""
+    from lsa_rocm_lab.port.read_kernel_tiled import _kv_layout
+
+    device = _on_device("tree_decode_shared", q, k, v, index_queries, buckets.centroids,
+                        *[level.centroids for level in hierarchy.levels])
+    if q.dim() != 4 or q.shape[1] != 1:
+        raise ValueError(f"tree_decode_shared takes one query token per batch row: q [B, 1, Hq, D], got "
+                         f"{tuple(q.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"q/k/v dtypes differ: {q.dtype} {k.dtype} {v.dtype}")
+    B, _, Hq, D = q.shape
+    Tk, Hkv = k.shape[1], k.shape[2]
+    if k.dim() != 4 or k.shape != v.shape or k.shape[0] not in (B, 1) or k.shape[3] != D:
+        raise ValueError(f"k/v must be [B={B} or 1, Tk, Hkv, D={D}], got {tuple(k.shape)} / {tuple(v.shape)}")
+    if Hq % Hkv:
+        raise ValueError(f"{Hq} query heads do not group onto {Hkv} kv-heads")
+    if buckets.ends is None or not buckets.spans:
+        raise ValueError("tree_decode_shared expands picks from span ends: the tables need ends and spans")
+    n_levels = len(hierarchy.levels)
+    if not 1 <= n_levels <= _abi.BEAM_MAX_LEVELS:
+        raise NotImplementedError(f"tree_decode_shared covers 1 to {_abi.BEAM_MAX_LEVELS} node levels, got {n_levels}")
+    if config.start_nodes is not None:
+        raise NotImplementedError("tree_decode_shared covers start_nodes=None (the top level down)")
+    idx = index_queries.reshape(B, -1).to(device=device, dtype=torch.float32).contiguous()
+    cent = buckets.centroids
+    if cent.dim() == 2:
+        row_tables = 0
+    elif cent.dim() == 3 and cent.shape[0] == B:
+        row_tables = 1
+    else:
+        raise ValueError(f"one bucket table for every row [rows, d] or one a row [B, rows, d], got "
+                         f"{tuple(cent.shape)}")
+    if idx.shape[1] != cent.shape[-1] or idx.shape[1] != D:
+        raise ValueError(f"index queries of dim {idx.shape[1]} for centroids of dim {cent.shape[-1]}: both must be "
+                         f"the head dim {D}")
+    for level in hierarchy.levels:
+        if level.centroids.dim() != cent.dim() or level.centroids.shape[:-2] != cent.shape[:-2]:
+            raise ValueError("node and bucket tables must share the same leading axes")
+    if score_dtype == "fp32":
+        if buckets.centroids_f32 is None:
+            raise ValueError("fp32 scoring needs buckets.centroids_f32")
+        ncents = [level.centroids.float() for level in hierarchy.levels]
+        bcent, mode = buckets.centroids_f32.float(), _abi.SCORE_F32
+    elif score_dtype == "bf16":
+        ncents = [level.centroids_bf16 if level.centroids_bf16 is not None else level.centroids.to(torch.bfloat16)
+                  for level in hierarchy.levels]
+        bcent, mode = buckets.centroids.to(torch.bfloat16), _abi.SCORE_BF16
+    else:
+        raise ValueError(f"score_dtype must be bf16|fp32, got {score_dtype!r}")
+    ncents = [c.contiguous() for c in ncents]
+    bcent = bcent.contiguous()
+    kids = [level.children.to(device=device, dtype=torch.int32).contiguous() for level in hierarchy.levels]
+    node_size = kids[0].shape[-1]
+    if any(kk.shape[-1] != node_size for kk in kids):
+        raise ValueError("every node level must hold node_bucket_size children a node")
+    q = q.contiguous()
+    k, v, sb, st, sh = _kv_layout(k, v)
+    if k.shape[0] != B:  # one pool read by every batch row
+        sb = 0
+    ends = _ends(buckets)
+    flags = _table_flags(buckets, ends)
+    pos = _positions32(positions, device)
+    if pos.numel() != B:
+        raise ValueError(f"a position a batch row: {B} rows, {pos.numel()} positions")
+    top_k = config.top_k if top_k is None else top_k
+    scale = D ** -0.5 if scale is None else scale
+    rows = buckets.rows
+    width = top_k + config.window_size + config.sink_size
+    lists = torch.empty(B, width, dtype=torch.int32, device=device)
+    lengths = torch.empty(B, dtype=torch.int32, device=device)
+    out = torch.empty_like(q)
+    dt = _abi.dtype_code(q.dtype)
+    readers = int(os.environ.get("LSA_DECODE_READERS", "0")) if readers is None else readers
+    splits = int(os.environ.get("LSA_SELECT_SPLITS", "0")) if splits is None else splits
+    cent_ptrs = (ctypes.c_void_p * n_levels)(*[c.data_ptr() for c in ncents])
+    kid_ptrs = (ctypes.c_void_p * n_levels)(*[kk.data_ptr() for kk in kids])
+    n_nodes = (ctypes.c_int32 * n_levels)(*[kk.shape[-2] for kk in kids])
+    levels = min(n_levels, config.top_level)
+    n_counters = _abi.size("lsa_decode_tree_shared_counters", B, Hkv, levels, ctypes.addressof(n_nodes), rows)
+    nbytes = _abi.size("lsa_decode_shared_scratch_bytes", dt, B, Hq, Hkv, D, rows, config.top_p, config.window_size,
+                       config.sink_size, top_k, readers)
+    status = _abi.StatusWord.get(device)
+    if int(status[0]) != 0:
+        _decode_gave_up(device, status)
+    ws = _abi.Workspace.get(device, "decode_shared", nbytes)
+    counters = _abi.Counters.get(device, max(n_counters, 1))
+    slots, _keep = _slot_args(slot_table, slot_rows, B, device)
+    _abi.call("lsa_decode_tree_shared", q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, Tk, Hq, Hkv, D, sb, st, sh,
+              idx.data_ptr(), n_levels, ctypes.addressof(cent_ptrs), ctypes.addressof(kid_ptrs),
+              ctypes.addressof(n_nodes), node_size, config.node_cluster_block_size, config.top_level,
+              bcent.data_ptr(), ends.data_ptr(), flags, rows, row_tables, mode, pos.data_ptr(), slots,
+              config.cluster_block_size, config.block_bucket_count, config.beam_width, config.top_p,
+              config.window_size, config.sink_size, top_k, float(scale), splits, readers, counters.data_ptr(),
+              counters.numel(), _abi.ptr(ws), nbytes, lists.data_ptr(), lengths.data_ptr(), out.data_ptr(),
+              _abi.ptr(status), _abi.stream(device))
     return out, lists, lengths
 
 
