@@ -61,6 +61,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_beam_kernel(const QT* q, boo
   __shared__ uint32_t seen[kBeamSeenBits / 32];
   __shared__ int scan[LSA_WAVES];
   __shared__ int vis_lds[2 * LSA_WAVES];
+  __shared__ int topk_ok;
   uint64_t* keys = smem;                                          // [cand_pow2]
   uint64_t* best = keys + a.cand_pow2;                            // [max(beam_pow2, top_pow2)]
   int32_t* cand = (int32_t*)(best + max(a.beam_pow2, a.top_pow2));  // [max(cand_pow2, top_p)]
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_beam_kernel(const QT* q, boo
     if (!done) {
       score_keys<CT, SPAN>(qs, ncent, D, a.cand_pow2, [&](int j) { return cand[j]; }, keys);
       __syncthreads();
-      block_topk_any(keys, a.cand_pow2, K, a.beam_pow2, best, &tks, &st, &bins);
+      block_topk_fast(keys, a.cand_pow2, K, a.beam_pow2, best, &tks, &st, &bins, &topk_ok);
     }
     // the kept nodes' children (rows of the level below) are carried
     const int32_t* kids = a.children[lv - 1] + t * (int64_t)nn * a.node_size;
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(LSA_BLOCK) void select_beam_kernel(const QT* q, boo
   if (!done0) {
     score_keys<CT, SPAN>(qs, bcent, D, a.cand_pow2, [&](int j) { return cand[j]; }, keys);
     __syncthreads();
-    block_topk_any(keys, a.cand_pow2, K0, a.top_pow2, best, &tks, &st, &bins);
+    block_topk_fast(keys, a.cand_pow2, K0, a.top_pow2, best, &tks, &st, &bins, &topk_ok);
   }
   for (int j = threadIdx.x; j < a.top_p; j += LSA_BLOCK) cand[j] = j < K0 ? key_column(u_to_key(best[j])) : -1;
   __syncthreads();

@@ -96,13 +96,14 @@ struct SharedArgs {
   int64_t col_base[LSA_BEAM_MAX_LEVELS + 1];  // first published column of each level, then of the buckets
   int node_size, node_block, beam;
   int cand_pow2, beam_pow2, carry_cap;
+  int cache_keys;           // the published keys' score halves are copied to LDS once
 };
 
 // Reader LDS: a header, the picks (first kept id and first list slot of each), then a
 // region the selection phase and the read phase (ids of a chunk, the read's merge state)
 // take in turn.
 struct ShHdr {
-  int filled, last;
+  int filled, last, ok;
   int wbad[LSA_WAVES];
   int scan[LSA_WAVES];
   int vis[2 * LSA_WAVES];
@@ -121,11 +122,12 @@ __host__ __device__ inline size_t sh_topk_at(int rows, int kp) {
 }
 __host__ __device__ inline size_t sh_sel_bytes(int rows, int kp) { return sh_topk_at(rows, kp) + sh_scratch_bytes(); }
 // tree selection phase, within the region: a level's keys, the sorted keys, candidates,
-// carried children, the dedup bitmap, top-K state
+// carried children, the dedup bitmap, top-K state, then (cache_cols > 0) the high halves
+// of the row's published keys
 struct TreeLds {
-  size_t keys, best, cand, carried, seen, topk, end;
+  size_t keys, best, cand, carried, seen, topk, cache, end;
 };
-__host__ __device__ inline TreeLds tree_lds(int cand_pow2, int best_slots, int carry_cap) {
+__host__ __device__ inline TreeLds tree_lds(int cand_pow2, int best_slots, int carry_cap, int64_t cache_cols) {
   TreeLds L;
   L.keys = 0;
   L.best = L.keys + sizeof(uint64_t) * (size_t)cand_pow2;
@@ -133,7 +135,8 @@ __host__ __device__ inline TreeLds tree_lds(int cand_pow2, int best_slots, int c
   L.carried = a16(L.cand + sizeof(int32_t) * (size_t)cand_pow2);
   L.seen = a16(L.carried + sizeof(int32_t) * (size_t)carry_cap);
   L.topk = a16(L.seen + sizeof(uint32_t) * (size_t)(kShSeenBits / 32));
-  L.end = L.topk + sh_scratch_bytes();
+  L.cache = a16(L.topk + sh_scratch_bytes());
+  L.end = L.cache + sizeof(uint32_t) * (size_t)cache_cols;
   return L;
 }
 // read phase, within the region: ids of a chunk, then the merge state
@@ -206,15 +209,6 @@ __device__ __forceinline__ bool block_gave_up(ShHdr& hd, int bad) {
   return (hd.wbad[0] | hd.wbad[1] | hd.wbad[2] | hd.wbad[3]) != 0;
 }
 
-// The K best of keys[0..n) (n <= kShMaxCand), sorted descending into out[0..kp): the
-// binned ranking for any K, the histogram / radix selects when it declines. keys[] are
-// gone afterwards.
-__device__ __forceinline__ void tree_topk(uint64_t* keys, int n, int K, int kp, uint64_t* out, TopkScratch* tks,
-                                          BinScratch* bins, RadixState* rst) {
-  if (block_topk_bins<kShMaxCand / LSA_BLOCK>(keys, n, K, kp, out, tks, bins)) return;
-  block_topk_sorted(keys, n, K, kp, out, tks, rst);
-}
-
 // One tree level's candidate list: the carried entries [0, n_carried), then the ids
 // first .. first + (n_cand - n_carried) - 1; ids outside [0, limit) and repeats (the first
 // entry to claim an id keeps it) become -1. n_ids: the ids the bitmap must clear.
@@ -272,13 +266,60 @@ __device__ __forceinline__ bool tree_gather(const SharedArgs& a, ShHdr& hd, cons
   return !block_gave_up(hd, bad);
 }
 
+// The row's published keys, polled until written (every load of a round in flight
+// together, 24 a thread a round), their high halves (the ordered score bits) kept in
+// cache[0..n_cols): a key is rebuilt from its column. False (every thread) when a wave gave
+// up at the spin limit.
+__device__ __forceinline__ bool tree_cache(const SharedArgs& a, ShHdr& hd, const uint64_t* pub, uint32_t* cache) {
+  constexpr int CPT = 24;
+  const int tid = threadIdx.x;
+  int bad = 0;
+  for (int64_t base = 0; base < a.n_cols && !bad; base += CPT * LSA_BLOCK) {
+    uint64_t x[CPT];
+    for (int it = 0;; ++it) {
+      bool ok = true;
+#pragma unroll
+      for (int m = 0; m < CPT; ++m) {
+        const int64_t j = base + m * LSA_BLOCK + tid;
+        x[m] = coherent_load_u64(pub + (j < a.n_cols ? j : 0));
+        ok &= j >= a.n_cols || x[m] != 0;
+      }
+      if (__all(ok)) break;
+      if (it >= a.spin_limit) {
+        bad = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+#pragma unroll
+    for (int m = 0; m < CPT; ++m) {
+      const int64_t j = base + m * LSA_BLOCK + tid;
+      if (j < a.n_cols) cache[j] = (uint32_t)((x[m] - 1) >> 32);
+    }
+  }
+  return !block_gave_up(hd, bad);
+}
+
+// Keys of a level's candidates cand[0..n) rebuilt from the cached score halves of its
+// columns (EMPTY for -1 entries): u = (score half << 32) | (0x7FFFFFFF - column).
+__device__ __forceinline__ void tree_gather_cached(const uint32_t* cache, const int32_t* cand, int n,
+                                                   uint64_t* keys) {
+  for (int j = threadIdx.x; j < n; j += LSA_BLOCK) {
+    const int32_t c = cand[j];
+    keys[j] = c >= 0 ? ((uint64_t)cache[c] << 32) | (uint64_t)(uint32_t)(0x7FFFFFFF - c) : 0;
+  }
+  __syncthreads();
+}
+
 // The multi-level beam walk of row r (reference _tree.py:318-373 _beam_pick_rows with the
 // growth of _tree.py:100-142 at page end V = the visible bucket count): best[0..kp) gets
 // the picked buckets' keys, sorted. False when a wait gave up.
 __device__ __forceinline__ bool tree_walk(const SharedArgs& a, ShHdr& hd, char* region, int64_t r, int64_t t,
                                           int64_t position, uint64_t* best) {
-  const TreeLds L = tree_lds(a.cand_pow2, a.kp > a.beam_pow2 ? a.kp : a.beam_pow2, a.carry_cap);
+  const TreeLds L =
+      tree_lds(a.cand_pow2, a.kp > a.beam_pow2 ? a.kp : a.beam_pow2, a.carry_cap, a.cache_keys ? a.n_cols : 0);
   uint64_t* keys = (uint64_t*)(region + L.keys);
+  uint32_t* cache = (uint32_t*)(region + L.cache);
   int32_t* cand = (int32_t*)(region + L.cand);
   int32_t* carried = (int32_t*)(region + L.carried);
   uint32_t* seen = (uint32_t*)(region + L.seen);
@@ -315,6 +356,7 @@ __device__ __forceinline__ bool tree_walk(const SharedArgs& a, ShHdr& hd, char* 
   }
 
   const uint64_t* pub = a.pub + r * a.n_cols;
+  if (a.cache_keys && !tree_cache(a, hd, pub, cache)) return false;
   const int ns = a.node_size;
   int n_carried = 0;
   for (int lv = start; lv >= 1; --lv) {  // the node levels, top-down
@@ -322,9 +364,10 @@ __device__ __forceinline__ bool tree_walk(const SharedArgs& a, ShHdr& hd, char* 
     const int first_open = lv == start ? 0 : closed[lv - 1];
     tree_candidates(cand, seen, nn, nn, carried, n_carried, first_open, n_carried + made[lv - 1] - first_open,
                     a.cand_pow2);
-    if (!tree_gather(a, hd, pub + a.col_base[lv - 1], cand, a.cand_pow2, keys)) return false;
+    if (a.cache_keys) tree_gather_cached(cache + a.col_base[lv - 1], cand, a.cand_pow2, keys);
+    else if (!tree_gather(a, hd, pub + a.col_base[lv - 1], cand, a.cand_pow2, keys)) return false;
     const int K = a.beam < a.cand_pow2 ? a.beam : a.cand_pow2;
-    tree_topk(keys, a.cand_pow2, K, a.beam_pow2, best, tks, bins, rst);
+    block_topk_fast(keys, a.cand_pow2, K, a.beam_pow2, best, tks, rst, bins, &hd.ok);
     const int32_t* kids = a.children[lv - 1] + t * (int64_t)nn * ns;
     n_carried = K * ns;  // <= carry_cap
     for (int j = threadIdx.x; j < n_carried; j += LSA_BLOCK) {
@@ -336,8 +379,9 @@ __device__ __forceinline__ bool tree_walk(const SharedArgs& a, ShHdr& hd, char* 
   // the buckets: the carried children below the visible count, then the fresh buckets
   const int n_fresh = visible - covered > 0 ? visible - covered : 0;
   tree_candidates(cand, seen, a.rows, visible, carried, n_carried, covered, n_carried + n_fresh, a.cand_pow2);
-  if (!tree_gather(a, hd, pub + a.col_base[a.n_levels], cand, a.cand_pow2, keys)) return false;
-  tree_topk(keys, a.cand_pow2, a.K, a.kp, best, tks, bins, rst);
+  if (a.cache_keys) tree_gather_cached(cache + a.col_base[a.n_levels], cand, a.cand_pow2, keys);
+  else if (!tree_gather(a, hd, pub + a.col_base[a.n_levels], cand, a.cand_pow2, keys)) return false;
+  block_topk_fast(keys, a.cand_pow2, a.K, a.kp, best, tks, rst, bins, &hd.ok);
   return true;
 }
 
@@ -411,7 +455,8 @@ __device__ __forceinline__ void shared_reader(const SharedArgs& a, char* smem, i
       if (!topk_bins_regs<KPT>(x, K, a.kp, best, cand, tks, bins)) topk_radix_regs<KPT>(x, K, a.kp, best, rst);
     }
   } else {
-    const TreeLds L = tree_lds(a.cand_pow2, a.kp > a.beam_pow2 ? a.kp : a.beam_pow2, a.carry_cap);
+    const TreeLds L =
+        tree_lds(a.cand_pow2, a.kp > a.beam_pow2 ? a.kp : a.beam_pow2, a.carry_cap, a.cache_keys ? a.n_cols : 0);
     best = (uint64_t*)(region + L.best);
     ends_at = ends;
     gave_up = !tree_walk(a, hd, region, r, t, position, best);
@@ -691,6 +736,7 @@ inline int sh_common(const char* who, SharedArgs& a, const void* q, const void* 
   a.lists = lists; a.lengths = lengths; a.status = status;
   a.slots = sm;
   a.n_levels = 0;
+  a.cache_keys = 0;
   return LSA_OK;
 }
 

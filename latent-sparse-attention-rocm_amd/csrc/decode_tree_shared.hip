@@ -73,7 +73,12 @@ extern "C" int lsa_decode_tree_shared(const void* q, const void* k, const void* 
   a.K = top_p < a.cand_pow2 ? top_p : a.cand_pow2;
   LSA_REQUIRE(a.K <= kShMaxPicks, LSA_ERR_SHAPE, "%s: %d picks exceed %d", who, a.K, kShMaxPicks);
   a.kp = next_pow2(a.K);
-  const TreeLds L = tree_lds(a.cand_pow2, a.kp > a.beam_pow2 ? a.kp : a.beam_pow2, a.carry_cap);
+  // the walk reads the published keys from LDS when their score halves fit beside it
+  const int best_slots = a.kp > a.beam_pow2 ? a.kp : a.beam_pow2;
+  const int span = lsa_read_tile_tokens(dtype, D, Hq / Hkv);
+  const size_t cached = sh_region_at(a.kp) + tree_lds(a.cand_pow2, best_slots, a.carry_cap, a.n_cols).end;
+  a.cache_keys = span > 0 && cached <= kShMaxLds ? 1 : 0;
+  const TreeLds L = tree_lds(a.cand_pow2, best_slots, a.carry_cap, a.cache_keys ? a.n_cols : 0);
   return sh_finish<true>(who, a, dtype, D, score_mode, select_splits, readers, L.end, counters, n_counters,
                          lsa_decode_tree_shared_counters(R, Hkv, levels, n_nodes, rows), scratch, scratch_bytes,
                          stream);

@@ -388,6 +388,133 @@ __device__ __forceinline__ bool wave_topk_hist(const uint64_t* x, int K, int kp,
   return true;
 }
 
+// Ranks of up to G placed candidates cand[s0 + q * stride] (q < G; those at or past nc
+// skipped): a candidate's rank is its bin's first slot lo_of(b) plus the larger keys among
+// the bin's slots [lo_of(b), hi_of(b)); out[rank] = key for ranks below K. Every load is
+// unconditional (indexes clamped into the candidates) and the counts branch-free, so the
+// G candidates' loads - their keys, their bins' bounds, 4 keys of each bin a round - are
+// in flight together. bin_of, lo_of and hi_of must be cheap and unconditional.
+template <int G, typename BinOf, typename LoOf, typename HiOf>
+__device__ __forceinline__ void rank_candidates(const uint64_t* cand, int nc, int s0, int stride, int K,
+                                                uint64_t* out, BinOf bin_of, LoOf lo_of, HiOf hi_of) {
+  uint64_t y[G];
+  int lo[G], hi[G], rk[G];
+#pragma unroll
+  for (int q = 0; q < G; ++q) {
+    const int s = s0 + q * stride;
+    y[q] = cand[s < nc ? s : nc - 1];
+  }
+  int len = 0;
+#pragma unroll
+  for (int q = 0; q < G; ++q) {
+    const bool on = s0 + q * stride < nc;
+    const int b = bin_of(y[q]);
+    const int l = lo_of(b), h = hi_of(b);
+    lo[q] = on ? l : 0;
+    hi[q] = on ? h : 0;
+    rk[q] = lo[q];
+    len = max(len, hi[q] - lo[q]);
+  }
+  for (int r0 = 0; r0 < len; r0 += 4) {
+#pragma unroll
+    for (int q = 0; q < G; ++q) {
+      uint64_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = cand[min(lo[q] + r0 + u, nc - 1)];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) rk[q] += (int)(lo[q] + r0 + u < hi[q]) & (int)(v[u] > y[q]);  // live keys are distinct
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < G; ++q) {
+    if (s0 + q * stride < nc && rk[q] < K) out[rk[q]] = y[q];
+  }
+}
+
+// The K best of the keys one wave holds in registers (x[m] is key m * LSA_WAVE + lane,
+// u-ordered, 0 = EMPTY), sorted descending into out[0..kp) (EMPTY past them), for any K:
+// the linear score bins of block_topk_hist (256 over [min, max]); every key in the bin of
+// the min(K, live)-th key or above is placed at its bin's offset in cand[] (capacity: the
+// live keys) and ranked by that offset plus the larger keys of its own bin, read 8 at a
+// time. No block barrier: the wave's LDS accesses run in program order and wave_barrier
+// keeps the compiler from moving them across the phases. Clears sc->hist and sc->fill
+// itself. Returns false (in every lane, before any store) when a score is not finite; the
+// caller then takes a block select. `out` and `cand` must not overlap.
+template <int KPL>
+__device__ __forceinline__ bool wave_topk_sort(const uint64_t (&x)[KPL], int K, int kp, uint64_t* out,
+                                               uint64_t* cand, TopkScratch* sc) {
+  const int lane = threadIdx.x & (LSA_WAVE - 1);
+  float mn = INFINITY, mx = -INFINITY;
+  int cnt = 0, bad = 0;
+#pragma unroll
+  for (int m = 0; m < KPL; ++m) {
+    const float s = key_score(x[m]);
+    const bool live = x[m] != 0;
+    bad |= (live && s - s != 0.0f) ? 1 : 0;  // NaN or infinite
+    mn = live ? fminf(mn, s) : mn;
+    mx = live ? fmaxf(mx, s) : mx;
+    cnt += live ? 1 : 0;
+  }
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  cnt = wave_sum(cnt);
+  if (wave_or(bad)) return false;
+  const int kc = cnt < K ? cnt : K;
+  for (int b = lane; b < 256; b += LSA_WAVE) {
+    sc->hist[b] = 0;
+    sc->fill[b] = 0;
+  }
+  const float scale = mx > mn ? 256.0f / (mx - mn) : 0.0f;
+  auto bin_of = [&](uint64_t k) {
+    const int b = (int)((key_score(k) - mn) * scale);
+    return b < 0 ? 0 : (b > 255 ? 255 : b);
+  };
+  __builtin_amdgcn_wave_barrier();
+  int bin[KPL];
+#pragma unroll
+  for (int m = 0; m < KPL; ++m) {
+    bin[m] = bin_of(x[m]);
+    if (x[m] != 0) atomicAdd(&sc->hist[bin[m]], 1);
+  }
+  __builtin_amdgcn_wave_barrier();
+  // lane l owns bins 255-4l .. 252-4l; exclusive offsets from the top bin down
+  const int c0 = sc->hist[255 - 4 * lane], c1 = sc->hist[254 - 4 * lane];
+  const int c2 = sc->hist[253 - 4 * lane], c3 = sc->hist[252 - 4 * lane];
+  const int mine = c0 + c1 + c2 + c3;
+  const int inc = wave_inclusive_sum(mine);
+  const int o0 = inc - mine, o1 = o0 + c0, o2 = o1 + c1, o3 = o2 + c2;
+  sc->off[255 - 4 * lane] = o0;
+  sc->off[254 - 4 * lane] = o1;
+  sc->off[253 - 4 * lane] = o2;
+  sc->off[252 - 4 * lane] = o3;
+  // the bin holding the kc-th key: it and the bins above are the candidates
+  const bool here = kc > 0 && o0 < kc && kc <= inc;
+  const int d = o1 >= kc ? 255 - 4 * lane : (o2 >= kc ? 254 - 4 * lane : (o3 >= kc ? 253 - 4 * lane : 252 - 4 * lane));
+  const uint64_t hm = __ballot(here);
+  const int cut = hm ? __builtin_amdgcn_readlane(d, __ffsll((long long)hm) - 1) : 256;
+  __builtin_amdgcn_wave_barrier();
+  // the candidates at their bins' offsets: every bin offset and slot claim in flight first
+  int off_m[KPL], pos[KPL];
+#pragma unroll
+  for (int m = 0; m < KPL; ++m) {
+    off_m[m] = sc->off[bin[m]];
+    pos[m] = x[m] != 0 && bin[m] >= cut ? atomicAdd(&sc->fill[bin[m]], 1) : 0;
+  }
+#pragma unroll
+  for (int m = 0; m < KPL; ++m) {
+    if (x[m] != 0 && bin[m] >= cut) cand[off_m[m] + pos[m]] = x[m];
+  }
+  __builtin_amdgcn_wave_barrier();
+  const int nc = cut < 256 ? sc->off[cut] + sc->hist[cut] : 0;
+  for (int g0 = 0; g0 < nc; g0 += 4 * LSA_WAVE) {
+    rank_candidates<4>(
+        cand, nc, g0 + lane, LSA_WAVE, K, out, bin_of, [&](int b) { return sc->off[b]; },
+        [&](int b) { return sc->off[b] + sc->hist[b]; });
+  }
+  for (int m = kc + lane; m < kp; m += LSA_WAVE) out[m] = 0;  // EMPTY past the live keys
+  return true;
+}
+
 // The K best of the block's keys held in registers (x[m] is key m * LSA_BLOCK + tid,
 // u-ordered, 0 = EMPTY), sorted descending into out[0..kp) (u == 0 past them), for any K:
 // the keys are binned linearly by score over [min, max] into kTopBins bins (a monotone map:
@@ -604,6 +731,31 @@ __device__ __forceinline__ void block_topk_any(uint64_t* keys, int n, int K, int
                                           : block_topk_bins<32>(keys, n, K, kp, out, sc, bs);
     if (done) return;
   }
+  block_topk_sorted(keys, n, K, kp, out, sc, st);
+}
+
+// The K best of keys[0..n) (u-ordered, in LDS), sorted descending into out[0..kp), for a
+// select whose levels hold few keys: up to 512 keys are ranked by wave 0 in registers
+// (wave_topk_sort, keys[] as its candidate buffer, no block barrier but the one after it);
+// up to 4096 by the binned ranking for any K; the histogram / radix selects when those
+// decline. keys[] are gone afterwards. flag: one int of LDS. Every thread calls it.
+__device__ __forceinline__ void block_topk_fast(uint64_t* keys, int n, int K, int kp, uint64_t* out, TopkScratch* sc,
+                                                RadixState* st, BinScratch* bs, int* flag) {
+  constexpr int KPL = 8;
+  if (n <= KPL * LSA_WAVE) {
+    if (threadIdx.x < LSA_WAVE) {
+      const int lane = threadIdx.x;
+      uint64_t x[KPL];
+#pragma unroll
+      for (int m = 0; m < KPL; ++m) x[m] = m * LSA_WAVE + lane < n ? keys[m * LSA_WAVE + lane] : 0;
+      __builtin_amdgcn_wave_barrier();
+      const bool ok = wave_topk_sort<KPL>(x, K, kp, out, keys, sc);
+      if (lane == 0) *flag = ok ? 1 : 0;
+    }
+    __syncthreads();
+    if (*flag) return;  // uniform
+  }
+  if (n <= 16 * LSA_BLOCK && block_topk_bins<16>(keys, n, K, kp, out, sc, bs)) return;
   block_topk_sorted(keys, n, K, kp, out, sc, st);
 }
 

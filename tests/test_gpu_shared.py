@@ -380,3 +380,27 @@ def test_tree_shared_decode_gives_up_and_recovers(space, tree):
     torch.cuda.synchronize()
     for a, b in zip(good, again):
         assert torch.equal(a, b)
+
+
+def test_tree_shared_decode_wide_table_gathers_from_l2():
+    """A 64k context at the reference knobs: 8192 buckets under levels of 2048/512/128 nodes
+    (10880 published keys a row, too many for the reader's LDS beside the walk), so each
+    level gathers its candidates' keys from the published ones in L2 instead of from the
+    LDS copy. Lists equal the beam select's, outputs within the bar of the oracle."""
+    cfg = PortConfig()
+    T = 65536
+    ws = workloads.index_space(T)
+    tree = pipeline.build_hierarchy_gpu(ws.idx_k, ws.buckets, cfg)
+    assert ws.buckets.rows == 8192 and sum(lv.centroids.shape[0] for lv in tree.levels) == 2688
+    positions = [T - 1, 40000]
+    pos = torch.tensor(positions, device=DEV, dtype=torch.int32)
+    print("case tree shared decode 64k (keys from L2)", flush=True)
+    q = ws.q[0, pos.long()][:, None].contiguous()
+    idx = ws.idx_q[pos.long()].contiguous()
+    out, lists, lengths = pipeline.tree_decode_shared(q, ws.k, ws.v, idx, pos, ws.buckets, tree, cfg)
+    want_l, want_n = pipeline.tree_select(idx, pos, ws.buckets, tree, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(lists, want_l) and torch.equal(lengths, want_n)
+    want = oracle.sparse_read(_np(q[:1]), _np(ws.k), _np(ws.v), _np(lists[:1])[None], _np(lengths[:1])[None],
+                              128 ** -0.5)
+    check_read(out[:1], want)
