@@ -811,18 +811,14 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
   DECODE_MARK(6);
 }
 
-// Wave 0 of a ranking reader: clears the top-K scratch's histogram, polls the unit's `rows`
-// published keys (KPL a lane, all loads in flight each round) until every one is nonzero
-// or the spin limit passes (*bad), then ranks them: wave_topk_hist into rk->best (*fast),
-// or, when the histogram cut does not serve, the keys go to LDS for block_topk_sorted.
+// Wave 0 of a ranking reader: polls the unit's `rows` published keys (KPL a lane, all
+// loads in flight each round) until every one is nonzero or the spin limit passes (*bad),
+// then ranks them: wave_topk_sort into rk->best (*fast, keys[] its candidate buffer), or,
+// when a score is not finite, the keys go to LDS for block_topk_sorted.
 template <int KPL>
 __device__ __forceinline__ void poll_and_rank(const DecodeArgs& a, const uint64_t* pub, int rows, uint64_t* keys,
                                               RankLds* rk, int* bad, int* fast) {
   const int lane = threadIdx.x & (LSA_WAVE - 1);
-  for (int b = lane; b < 256; b += LSA_WAVE) {
-    rk->tks.hist[b] = 0;
-    rk->tks.fill[b] = 0;
-  }
   uint64_t x[KPL];
   for (int it = 0;; ++it) {
     bool ok = true;
@@ -841,7 +837,7 @@ __device__ __forceinline__ void poll_and_rank(const DecodeArgs& a, const uint64_
   }
 #pragma unroll
   for (int m = 0; m < KPL; ++m) x[m] = m * LSA_WAVE + lane < rows ? x[m] - 1 : 0;  // EMPTY past the table
-  if (wave_topk_hist<KPL>(x, a.K, a.kp, rk->best, &rk->tks)) {
+  if (wave_topk_sort<KPL>(x, a.K, a.kp, rk->best, keys, &rk->tks)) {
     *fast = 1;
     return;
   }

@@ -506,10 +506,12 @@ __device__ __forceinline__ bool wave_topk_sort(const uint64_t (&x)[KPL], int K, 
   }
   __builtin_amdgcn_wave_barrier();
   const int nc = cut < 256 ? sc->off[cut] + sc->hist[cut] : 0;
-  for (int g0 = 0; g0 < nc; g0 += 4 * LSA_WAVE) {
-    rank_candidates<4>(
-        cand, nc, g0 + lane, LSA_WAVE, K, out, bin_of, [&](int b) { return sc->off[b]; },
-        [&](int b) { return sc->off[b] + sc->hist[b]; });
+  const auto lo_of = [&](int b) { return sc->off[b]; };
+  const auto hi_of = [&](int b) { return sc->off[b] + sc->hist[b]; };
+  if (nc <= LSA_WAVE) {  // uniform: one candidate a lane
+    if (nc > 0) rank_candidates<1>(cand, nc, lane, LSA_WAVE, K, out, bin_of, lo_of, hi_of);
+  } else {
+    for (int g0 = 0; g0 < nc; g0 += 4 * LSA_WAVE) rank_candidates<4>(cand, nc, g0 + lane, LSA_WAVE, K, out, bin_of, lo_of, hi_of);
   }
   for (int m = kc + lane; m < kp; m += LSA_WAVE) out[m] = 0;  // EMPTY past the live keys
   return true;
