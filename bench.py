@@ -493,10 +493,10 @@ def refcfg_decode_leg(args, torch, np, dense_us):
     mean over the key / query heads (a stand-in for upstream's regroup). Flat: the fused
     select (bf16 scores) + the split-K read; tree: the hierarchy of 1024/256/64 nodes, the
     multi-level beam (fp32 scores) + the same read. Each step rotates over the last 4 query
-    tokens (positions T-4 .. T-1); lists bit-exact against the numpy oracle on all 4, the
-    read within the bf16 bar on one. Each arm is also timed as one fused launch with the
-    selection shared by every kv-head (flat_decode_shared / tree_decode_shared): its lists
-    against the same oracle lists, its read against the fp64 read of them."""
+    tokens (positions T-4 .. T-1). Each arm's step is one fused launch with the selection
+    shared by every kv-head (flat_decode_shared / tree_decode_shared); the select kernel
+    followed by the read is timed beside it (two_launch). Lists of both bit-exact against
+    the numpy oracle on all 4 tokens, reads within the bf16 bar on one."""
     import oracle
     from lsa_rocm_lab.port import pipeline
     from lsa_rocm_lab.port.pipeline import PortConfig
@@ -557,13 +557,12 @@ def refcfg_decode_leg(args, torch, np, dense_us):
         want = oracle.sparse_read(qs[0].float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
                                   lists_np[None, :1], lengths_np[None, :1], D ** -0.5)
         err = np.abs(o0.float().cpu().numpy() - want)
-        out[name] = {"select_us": round(sel_us, 2), "read_us": round(read_us, 2), "us_per_step": round(step_us, 2),
-                     "tokens_read": round(toks, 1), "read_gbps": round(gathered / (read_us * 1e-6) / 1e9, 1),
-                     "speedup_vs_dense": None if dense_us is None else round(dense_us / step_us, 2),
-                     "lists_bit_exact": bool(np.array_equal(lists_np, want_l)
-                                             and np.array_equal(lengths_np, want_n)),
-                     "read_max_abs": float(err.max()), "read_mean_abs": float(err.mean())}
-        # the same arm as one fused launch (select workgroups + readers sharing the selection)
+        two = {"select_us": round(sel_us, 2), "read_us": round(read_us, 2), "us_per_step": round(step_us, 2),
+               "read_gbps": round(gathered / (read_us * 1e-6) / 1e9, 1),
+               "speedup_vs_dense": None if dense_us is None else round(dense_us / step_us, 2),
+               "lists_bit_exact": bool(np.array_equal(lists_np, want_l) and np.array_equal(lengths_np, want_n)),
+               "read_max_abs": float(err.max()), "read_mean_abs": float(err.mean())}
+        # the production step: one launch, select workgroups + readers sharing the selection
         if name == "flat":
             fused = lambda i: pipeline.flat_decode_shared(qs[i % NQ], k, v, idx_q[i % NQ:i % NQ + 1],
                                                           pos[i % NQ:i % NQ + 1], buckets, config)
@@ -576,17 +575,18 @@ def refcfg_decode_leg(args, torch, np, dense_us):
         f_lists = np.stack([r[1][0].cpu().numpy() for r in fres])
         f_lengths = np.array([int(r[2][0]) for r in fres])
         ferr = np.abs(fres[0][0].float().cpu().numpy() - want)
-        out[name]["fused_us_per_step"] = round(fused_us, 2)
-        out[name]["fused_speedup_vs_dense"] = None if dense_us is None else round(dense_us / fused_us, 2)
-        out[name]["fused_lists_bit_exact"] = bool(np.array_equal(f_lists, want_l) and np.array_equal(f_lengths, want_n))
-        out[name]["fused_read_max_abs"] = float(ferr.max())
-        out[name]["fused_read_mean_abs"] = float(ferr.mean())
+        out[name] = {"us_per_step": round(fused_us, 2), "tokens_read": round(toks, 1),
+                     "gbps": round(gathered / (fused_us * 1e-6) / 1e9, 1),
+                     "speedup_vs_dense": None if dense_us is None else round(dense_us / fused_us, 2),
+                     "lists_bit_exact": bool(np.array_equal(f_lists, want_l) and np.array_equal(f_lengths, want_n)),
+                     "read_max_abs": float(ferr.max()), "read_mean_abs": float(ferr.mean()),
+                     "two_launch": two}
         log(f"refcfg {name} decode {out[name]}")
     return {"workload": "refcfg_decode_32k", "batch": 1, "context": T, "buckets": buckets.rows,
             "nodes": [lv.centroids.shape[0] for lv in tree.levels], "knobs": "reference PortConfig defaults",
             "timing": "hip graphs of back-to-back steps over 4 query tokens, HIP events",
-            "fused": "one launch, the selection shared by every kv-head (lsa_decode_shared / "
-                     "lsa_decode_tree_shared)", **out}
+            "step": "one launch, the selection shared by every kv-head (lsa_decode_shared / "
+                    "lsa_decode_tree_shared); two_launch: the select kernel then the split-K read", **out}
 
 
 def refcfg_prefill_leg(args, torch, np, dense_ms):
