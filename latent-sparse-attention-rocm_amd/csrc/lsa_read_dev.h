@@ -309,25 +309,40 @@ __device__ __forceinline__ void attend_tiles_mfma(const QueryRegs<T, D, GQ>& q, 
     __builtin_amdgcn_wave_barrier();  // the reads before the next tile's writes
   };
 
-  MfmaTile<T, D, GQ> cur;
+  // the span is wave-uniform: scalar bounds make the tile loop's tests scalar branches
+  lo = __builtin_amdgcn_readfirstlane(lo);
+  hi = __builtin_amdgcn_readfirstlane(hi);
   if (PIPE && hi - lo > NT) {  // pipelined
-    int32_t id1 = id_of(lo + s0);
-    int32_t id2 = id_of(lo + NT + s0);
-    issue(id1, cur);
-    id1 = id2;
-    for (int base = lo; base < hi; base += NT) {
-      if (base + NT < hi) {  // uniform: a next tile
-        id2 = id_of(base + 2 * NT + s0);  // ids two tiles ahead, before the rows they do not feed
-        MfmaTile<T, D, GQ> nxt;
-        issue(id1, nxt);
-        compute(cur);
-        cur = nxt;
-        id1 = id2;
-      } else {
-        compute(cur);
-      }
+    // Two tile buffers that trade roles every tile (the loop body holds two tiles): the
+    // next tile's rows land in the other buffer while this one is computed. A copy from
+    // a "next" buffer into a "current" one would wait for the rows in flight, which
+    // leaves one tile's gather exposed every iteration.
+    MfmaTile<T, D, GQ> ta, tb;
+    // One exit, at the loop's head: a loop with exits in its middle is folded into one exit
+    // behind a flow block that re-enters the head with rows still in flight, and the head
+    // then waits for all of them.
+    const int n_tiles = (hi - lo + NT - 1) / NT;  // >= 2
+    int32_t id_a = id_of(lo + s0);
+    int32_t id_b = id_of(lo + NT + s0);
+    issue(id_a, ta);
+    int base = lo;
+    for (int t = 0; t + 2 < n_tiles; t += 2, base += 2 * NT) {  // ta holds tile t; t + 1, t + 2 exist
+      id_a = id_of(base + 2 * NT + s0);  // ids two tiles ahead, before the rows they do not feed
+      issue(id_b, tb);
+      compute(ta);
+      id_b = id_of(base + 3 * NT + s0);
+      issue(id_a, ta);
+      compute(tb);
+    }
+    if (base + NT < hi) {  // uniform: one more tile after ta's
+      issue(id_b, tb);
+      compute(ta);
+      compute(tb);
+    } else {
+      compute(ta);
     }
   } else {
+    MfmaTile<T, D, GQ> cur;
     int32_t id1 = id_of(lo + s0);
     for (int base = lo; base < hi; base += NT) {
       issue(id1, cur);
