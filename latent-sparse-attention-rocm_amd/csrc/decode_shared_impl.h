@@ -111,8 +111,9 @@ struct ShHdr {
 constexpr size_t a16(size_t x) { return (x + 15) & ~(size_t)15; }
 __host__ __device__ inline size_t sh_picks_at() { return a16(sizeof(ShHdr)); }
 __host__ __device__ inline size_t sh_region_at(int kp) { return sh_picks_at() + a16(sizeof(int32_t) * (2 * (size_t)kp + 1)); }
-__host__ __device__ inline size_t sh_scratch_bytes() {
-  return a16(sizeof(TopkScratch)) + a16(sizeof(BinScratch)) + a16(sizeof(RadixState));
+// top-K state: the flat reader bins its thousands of keys finer (BinScratchWide)
+__host__ __device__ inline size_t sh_scratch_bytes(bool wide) {
+  return a16(sizeof(TopkScratch)) + a16(wide ? sizeof(BinScratchWide) : sizeof(BinScratch)) + a16(sizeof(RadixState));
 }
 // flat selection phase, within the region: span ends, sorted keys, candidates, top-K state
 __host__ __device__ inline size_t sh_best_at(int rows) { return a16(sizeof(int32_t) * (size_t)rows); }
@@ -120,7 +121,7 @@ __host__ __device__ inline size_t sh_cand_at(int rows, int kp) { return sh_best_
 __host__ __device__ inline size_t sh_topk_at(int rows, int kp) {
   return a16(sh_cand_at(rows, kp) + sizeof(uint64_t) * ((size_t)kp + LSA_WAVE));
 }
-__host__ __device__ inline size_t sh_sel_bytes(int rows, int kp) { return sh_topk_at(rows, kp) + sh_scratch_bytes(); }
+__host__ __device__ inline size_t sh_sel_bytes(int rows, int kp) { return sh_topk_at(rows, kp) + sh_scratch_bytes(true); }
 // tree selection phase, within the region: a level's keys, the sorted keys, candidates,
 // carried children, the dedup bitmap, top-K state, then (cache_cols > 0) the high halves
 // of the row's published keys
@@ -135,7 +136,7 @@ __host__ __device__ inline TreeLds tree_lds(int cand_pow2, int best_slots, int c
   L.carried = a16(L.cand + sizeof(int32_t) * (size_t)cand_pow2);
   L.seen = a16(L.carried + sizeof(int32_t) * (size_t)carry_cap);
   L.topk = a16(L.seen + sizeof(uint32_t) * (size_t)(kShSeenBits / 32));
-  L.cache = a16(L.topk + sh_scratch_bytes());
+  L.cache = a16(L.topk + sh_scratch_bytes(false));
   L.end = L.cache + sizeof(uint32_t) * (size_t)cache_cols;
   return L;
 }
@@ -422,8 +423,8 @@ __device__ __forceinline__ void shared_reader(const SharedArgs& a, char* smem, i
     best = (uint64_t*)(region + sh_best_at(rows));                  // [kp]
     uint64_t* cand = (uint64_t*)(region + sh_cand_at(rows, a.kp));  // [kp + 64]
     TopkScratch* tks = (TopkScratch*)(region + sh_topk_at(rows, a.kp));
-    BinScratch* bins = (BinScratch*)((char*)tks + a16(sizeof(TopkScratch)));
-    RadixState* rst = (RadixState*)((char*)bins + a16(sizeof(BinScratch)));
+    BinScratchWide* bins = (BinScratchWide*)((char*)tks + a16(sizeof(TopkScratch)));
+    RadixState* rst = (RadixState*)((char*)bins + a16(sizeof(BinScratchWide)));
     for (int m = tid; m < rows; m += LSA_BLOCK) ends_l[m] = ends[m];
     ends_at = ends_l;
     // every wave polls its share of the row's keys (key m * 256 + tid in x[m]) until all of
@@ -452,7 +453,7 @@ __device__ __forceinline__ void shared_reader(const SharedArgs& a, char* smem, i
     gave_up = block_gave_up(hd, bad);
     if (!gave_up) {
       // the K best keys, sorted (the select's top-K on the same keys)
-      if (!topk_bins_regs<KPT>(x, K, a.kp, best, cand, tks, bins)) topk_radix_regs<KPT>(x, K, a.kp, best, rst);
+      if (!topk_bins_regs<KPT, kTopBinsWide>(x, K, a.kp, best, cand, tks, bins)) topk_radix_regs<KPT>(x, K, a.kp, best, rst);
     }
   } else {
     const TreeLds L =

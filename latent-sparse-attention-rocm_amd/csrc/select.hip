@@ -202,7 +202,7 @@ __global__ __launch_bounds__(LSA_BLOCK) __attribute__((amdgpu_waves_per_eu(4, 4)
   extern __shared__ uint64_t smem[];
   __shared__ RadixState st;
   __shared__ TopkScratch tks;
-  __shared__ BinScratch bins;
+  __shared__ BinScratchWide bins;
   __shared__ int scan[LSA_WAVES];
   __shared__ int flag;
   uint64_t* keys = smem;            // [rows]
