@@ -435,6 +435,105 @@ __device__ __forceinline__ void rank_candidates(const uint64_t* cand, int nc, in
   }
 }
 
+// The value lane ^ J holds (J a power of two below 64), 32 bits: DPP within a 16-lane row,
+// the gfx950 row swaps across rows.
+template <int J>
+__device__ __forceinline__ uint32_t wave_xor_lane(uint32_t v) {
+  if constexpr (J == 1) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
+  } else if constexpr (J == 2) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
+  } else if constexpr (J == 4) {
+    const int lane = threadIdx.x & (LSA_WAVE - 1);
+    const uint32_t up = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x104, 0xF, 0xF, false);  // row_shl:4
+    const uint32_t dn = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    return (lane & 4) ? dn : up;
+  } else if constexpr (J == 8) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else {
+    return __builtin_bit_cast(uint32_t, lane_xor(__builtin_bit_cast(float, v), J));
+  }
+}
+
+// Lanes that keep the smaller value at the step of distance J of a descending bitonic merge
+// of blocks of K lanes: those whose lane bits J and K differ.
+__host__ __device__ constexpr uint64_t bitonic_min_lanes(int K, int J) {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l)
+    if (((l & J) != 0) != ((l & K) != 0)) m |= 1ull << l;
+  return m;
+}
+
+// One compare-exchange step of the wave-wide bitonic sort (u64 values as high/low words): a
+// lane takes its partner's value when the partner's is larger and the lane keeps maxima, or
+// smaller and it keeps minima. One compare and a scalar XOR with a constant lane mask.
+template <int K, int J>
+__device__ __forceinline__ void wave_bitonic_step(uint32_t& vh, uint32_t& vl) {
+  const uint32_t ph = wave_xor_lane<J>(vh), pl = wave_xor_lane<J>(vl);
+  const uint64_t v = ((uint64_t)vh << 32) | vl, p = ((uint64_t)ph << 32) | pl;
+  constexpr uint64_t kMin = bitonic_min_lanes(K, J);
+  const bool take = __builtin_amdgcn_inverse_ballot_w64(__builtin_amdgcn_uicmpl(p, v, 34 /* unsigned > */) ^ kMin);
+  vh = take ? ph : vh;
+  vl = take ? pl : vl;
+}
+
+template <int K>
+__device__ __forceinline__ void wave_bitonic_merge(uint32_t& vh, uint32_t& vl) {
+  if constexpr (K >= 64) wave_bitonic_step<K, 32>(vh, vl);
+  if constexpr (K >= 32) wave_bitonic_step<K, 16>(vh, vl);
+  if constexpr (K >= 16) wave_bitonic_step<K, 8>(vh, vl);
+  if constexpr (K >= 8) wave_bitonic_step<K, 4>(vh, vl);
+  if constexpr (K >= 4) wave_bitonic_step<K, 2>(vh, vl);
+  wave_bitonic_step<K, 1>(vh, vl);
+}
+
+// The K (<= 32) best of the keys one wave holds in registers (x[m] is key m * LSA_WAVE +
+// lane, u-ordered, 0 = EMPTY), sorted descending into out[0..kp) (EMPTY past them), in
+// registers: the K-th largest top-16-bit prefix among the lanes' best keys, found bit by bit
+// with wave-wide counts, bounds the candidates from below (at least K keys lie at or above
+// it, since K lanes each hold one); the candidates are compacted by ballot into cand[0..64)
+// and sorted by a 64-lane bitonic sort (21 compare-exchange steps over DPP and row swaps),
+// after which lane r holds the r-th best. No LDS atomics, no bins, no score arithmetic:
+// the u64 order is the only one used, non-finite scores included. Returns false (every
+// lane, before touching out) when more than 64 keys reach the bound; the caller then ranks
+// another way. 1 <= K <= 32, kp <= 64.
+template <int KPL>
+__device__ __forceinline__ bool wave_topk_small(const uint64_t (&x)[KPL], int K, int kp, uint64_t* out,
+                                                uint64_t* cand) {
+  const int lane = threadIdx.x & (LSA_WAVE - 1);
+  uint32_t mh = (uint32_t)(x[0] >> 32);
+#pragma unroll
+  for (int m = 1; m < KPL; ++m) mh = max(mh, (uint32_t)(x[m] >> 32));
+  uint32_t t = 0;
+#pragma unroll
+  for (int b = 31; b >= 16; --b) {
+    const uint32_t c = t | (1u << b);
+    if (__popcll(__builtin_amdgcn_uicmp(mh, c, 35 /* unsigned >= */)) >= K) t = c;
+  }
+  const uint64_t t0 = t ? (uint64_t)t << 32 : 1;  // fewer than K lanes hold keys: every live key
+  int nc = 0;
+#pragma unroll
+  for (int m = 0; m < KPL; ++m) {
+    const uint64_t b = __builtin_amdgcn_uicmpl(x[m], t0, 35 /* unsigned >= */);
+    const int slot = nc + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0));
+    if (__builtin_amdgcn_inverse_ballot_w64(b) && slot < LSA_WAVE) cand[slot] = x[m];
+    nc += __popcll(b);
+  }
+  if (nc > LSA_WAVE) return false;  // uniform
+  __builtin_amdgcn_wave_barrier();
+  const uint64_t y = lane < nc ? cand[lane] : 0;
+  uint32_t vh = (uint32_t)(y >> 32), vl = (uint32_t)y;
+  wave_bitonic_merge<2>(vh, vl);
+  wave_bitonic_merge<4>(vh, vl);
+  wave_bitonic_merge<8>(vh, vl);
+  wave_bitonic_merge<16>(vh, vl);
+  wave_bitonic_merge<32>(vh, vl);
+  wave_bitonic_merge<64>(vh, vl);
+  const int kc = nc < K ? nc : K;
+  if (lane < kp) out[lane] = lane < kc ? (((uint64_t)vh << 32) | vl) : 0;
+  return true;
+}
+
 // The K best of the keys one wave holds in registers (x[m] is key m * LSA_WAVE + lane,
 // u-ordered, 0 = EMPTY), sorted descending into out[0..kp) (EMPTY past them), for any K:
 // the linear score bins of block_topk_hist (256 over [min, max]); every key in the bin of
