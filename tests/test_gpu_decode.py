@@ -247,6 +247,40 @@ def test_tied_scores_take_the_block_top_k():
         assert torch.equal(lists[0, g, :n].cpu(), torch.arange(n, dtype=torch.int32))
 
 
+@pytest.mark.parametrize("case", ["pos-inf", "neg-inf", "half-tied", "half-tied-32k", "top1", "top17", "early"])
+def test_rank_form_register_top_k_edges(case):
+    """The rank form's readers rank up to 32 picks in registers: the K-th best lane maximum's
+    16-bit score prefix bounds the candidates, a 64-lane bitonic sort ranks them, and more
+    than 64 candidates fall back to the binned ranking. Lists must still equal the oracle's
+    at the edges of that scheme: infinite scores (ranked by their packed keys like any
+    other), half the buckets tied (ties go to the lower bucket; the tied keys share every
+    prefix), one and 17 picks, and a position with fewer visible buckets than picks."""
+    T = 32768 if case.endswith("32k") else 8192
+    Hq, Hkv, D = 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=128, seed=21, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    config = workloads.FLAT_32K
+    pos = torch.tensor([T - 1], dtype=torch.int32)
+    cent = buckets.centroids.clone()
+    if case == "pos-inf":
+        cent[0, 5, 3] = float("inf")
+        cent[1, 9, 7] = float("inf")
+    elif case == "neg-inf":
+        cent[0, 5, 3] = float("-inf")
+        cent[1, 100, 7] = float("-inf")
+    elif case.startswith("half-tied"):
+        n = cent.shape[1]
+        cent[:, n // 2:] = cent[:, :1]  # the upper half all score like bucket 0
+    elif case == "top1":
+        config = dataclasses.replace(config, top_p=1)
+    elif case == "top17":
+        config = dataclasses.replace(config, top_p=17)
+    elif case == "early":
+        pos = torch.tensor([700], dtype=torch.int32)
+    odd = dataclasses.replace(buckets, centroids=cent, centroids_f32=cent.float())
+    check_decode(data.q[:, -1:], data.k, data.v, pos, odd, config, label=f"register top-k {case}")
+
+
 @pytest.mark.parametrize("form", ["rank-spans", "rank-members", "record"])
 def test_give_up_is_reported_and_the_next_launch_is_clean(form):
     """The host makes every reader's bounded wait give up (select workgroups skip
