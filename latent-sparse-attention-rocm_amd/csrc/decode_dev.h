@@ -632,8 +632,9 @@ __device__ __forceinline__ void tree_role(const DecodeArgs& a, char* smem, int64
 // the unit's list of L = filled + tail slots is cut into tiles of `span` slots, and reader
 // `role` takes a contiguous run of them (the first TT % NR readers one tile more), so only
 // the last tile of a list is partial. The run is expanded into `ids` (and the list) in
-// chunks of up to a.chunk tiles and read with the software-pipelined tile loop; then
-// the reader writes its share of the list padding, publishes its split partial and
+// chunks of up to a.chunk tiles and read with the software-pipelined tile loop (its share
+// of the list padding goes out first: it needs only the list's length, and stores issued
+// before the gathers stay off the tail); then the reader publishes its split partial and
 // arrives. The last reader of the unit combines the partials and leaves the unit's hand-off
 // words zero for the next launch (`clear`: 1 the record copies, 2 the published keys).
 // Tiles of an id chunk: a reader restarts its gather pipeline once a chunk, so the exchange
@@ -702,6 +703,13 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
     }
     return a_;
   };
+  // the list's padding [length, W) is shared out over the unit's readers
+  {
+    const int per = (a.W - length + NR - 1) / NR;
+    const int p0 = length + role * per;
+    const int p1 = min(p0 + per, a.W);
+    for (int k = p0 + tid; k < p1; k += LSA_BLOCK) lrow[k] = -1;
+  }
   AttnState<T, D, GQ> st;
   st.clear();
   bool fresh = true;
@@ -783,13 +791,6 @@ __device__ __forceinline__ void read_parts(const DecodeArgs& a, RdLds<D, GQ>& sh
   float* parts = a.ws_part + i * (int64_t)a.NR * PSTRIDE;
   if (role < n_part) {
     finish_span<T, D, GQ>(sh.rd, st, n_part == 1, outp, n_part > 1 ? parts + (int64_t)role * PSTRIDE : nullptr, 0);
-  }
-  // the list's padding [length, W) is shared out over the unit's readers
-  {
-    const int per = (a.W - length + NR - 1) / NR;
-    const int p0 = length + role * per;
-    const int p1 = min(p0 + per, a.W);
-    for (int k = p0 + tid; k < p1; k += LSA_BLOCK) lrow[k] = -1;
   }
   DECODE_MARK(4);
   if (!arrive_last(&a.rd_count[i], NR, &sh.rd.flag)) return;

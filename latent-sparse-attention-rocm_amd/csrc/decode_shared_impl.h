@@ -534,6 +534,12 @@ __device__ __forceinline__ void shared_reader(const SharedArgs& a, char* smem, i
     }
     return a_;
   };
+  if (writer) {  // the list's padding [length, W), shared out over the readers
+    const int per = (a.W - length + NR - 1) / NR;
+    const int p0 = length + role * per;
+    const int p1 = min(p0 + per, a.W);
+    for (int k = p0 + tid; k < p1; k += LSA_BLOCK) lrow[k] = -1;
+  }
   AttnState<T, D, GQ> st;
   st.clear();
   bool fresh = true;
@@ -570,12 +576,6 @@ __device__ __forceinline__ void shared_reader(const SharedArgs& a, char* smem, i
   float* parts = a.ws_part + i * (int64_t)NR * PSTRIDE;
   if (role < n_part) {
     finish_span<T, D, GQ>(rd, st, n_part == 1, outp, n_part > 1 ? parts + (int64_t)role * PSTRIDE : nullptr, 0);
-  }
-  if (writer) {  // the list's padding [length, W), shared out over the readers
-    const int per = (a.W - length + NR - 1) / NR;
-    const int p0 = length + role * per;
-    const int p1 = min(p0 + per, a.W);
-    for (int k = p0 + tid; k < p1; k += LSA_BLOCK) lrow[k] = -1;
   }
   DECODE_MARK(11);
   if (!arrive_last(&a.rd_count[i], NR, &rd.flag)) return;
