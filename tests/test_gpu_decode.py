@@ -61,12 +61,14 @@ def oracle_decode(q, k, v, positions, buckets, config, score_dtype, top_k=None):
     return lists, lengths, out
 
 
-def check_decode(q, k, v, positions, buckets, config, score_dtype="bf16", top_k=None, splits=None, label=""):
-    print(f"case {label} B={q.shape[0]} Hq={q.shape[2]} D={q.shape[3]} {q.dtype} {score_dtype} splits={splits}",
-          flush=True)
+def check_decode(q, k, v, positions, buckets, config, score_dtype="bf16", top_k=None, splits=None, label="",
+                 readers=None):
+    print(f"case {label} B={q.shape[0]} Hq={q.shape[2]} D={q.shape[3]} {q.dtype} {score_dtype} splits={splits} "
+          f"readers={readers}", flush=True)
     status = torch.zeros(1, dtype=torch.int32, device=DEV)
     out, lists, lengths = pipeline.flat_decode(q, k, v, positions.to(DEV), buckets, config, top_k=top_k,
-                                               score_dtype=score_dtype, splits=splits, status=status)
+                                               score_dtype=score_dtype, splits=splits, readers=readers,
+                                               status=status)
     want_l, want_n, want_o = oracle_decode(q, k, v, positions, buckets, config, score_dtype, top_k)
     assert int(status.item()) == 0
     assert np.array_equal(_np(lengths), want_n), label
@@ -106,6 +108,27 @@ def test_select_splits_past_the_table(form, splits):
     pos = torch.tensor([T - 1], dtype=torch.int32)
     check_decode(data.q[:, -1:], data.k, data.v, pos, buckets, workloads.FLAT_32K, splits=splits,
                  label=f"{form} splits={splits} rows=128")
+
+
+@pytest.mark.parametrize("form", ["rank", "record"])
+@pytest.mark.parametrize("readers", [1, 2, 5, 40, 256])
+def test_reader_counts_match_oracle(form, readers):
+    """Any reader count splits a unit's list the same way. The list here holds 44 tiles of
+    64 slots (32 buckets' keys below the window, then a 1024-key window and 4 sinks: 2782 and
+    2764 slots): one reader writes
+    the output itself (no partials); 2 and 5 leave a remainder of tiles; 40 publish more
+    partials than the combine's first batch of loads covers; 256 (the most the host accepts)
+    leave readers without a tile, which still write their share of the list's padding and
+    arrive. Both hand-off forms (the rank form: 8 select splits publish keys; the record: one
+    split). Lists bit-exact vs the oracle, output within the bf16 bar."""
+    T, Hq, Hkv, D = 8192, 8, 2, 128
+    data = workloads.clustered(T, Hq, Hkv, D, n_clusters=128, seed=6, device=DEV)
+    buckets = workloads.cluster_buckets(data, target=T // 64)
+    config = dataclasses.replace(workloads.FLAT_32K, window_size=1024, sink_size=4)
+    pos = torch.tensor([T - 1], dtype=torch.int32)
+    _, _, lengths = check_decode(data.q[:, -1:], data.k, data.v, pos, buckets, config,
+                                 splits=8 if form == "rank" else 1, readers=readers, label=f"{form} readers={readers}")
+    assert _np(lengths).min() > 40 * 64  # more tiles than 40 readers take one each
 
 
 @pytest.mark.parametrize("dtype,hq,hkv", [(torch.bfloat16, 8, 8), (torch.bfloat16, 8, 4), (torch.bfloat16, 16, 2),
