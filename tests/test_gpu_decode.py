@@ -6,7 +6,7 @@ those lists within the dtype's bar (max-abs / mean-abs vs fp64: fp32 1e-4 / 1e-5
 2e-2 / 2e-3). Cases: the clustered decode geometry up to 32k, positional buckets with
 window and sink tails, top_k cutting a bucket short, fewer visible buckets than picks,
 nothing visible (zeros), batch rows with their own tables and positions, every select
-split count, both hand-off forms (the rank form, span and member tables: every reader ranks the
+split count, reader counts from 1 to 256, both hand-off forms (the rank form, span and member tables: every reader ranks the
 splits' published keys; with one split, the select's record), both
 scoring dtypes, and repeated launches (the record or published keys, counters and
 partials are reused and must come back clean).
