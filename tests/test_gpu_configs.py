@@ -232,13 +232,16 @@ def test_tree_decode_ragged_positions_follow_growth():
                 assert (picks[picks >= 0] < visible).all()
 
 
+@pytest.mark.parametrize("readers", [None, 1, 7, 64])
 @pytest.mark.parametrize("spans", [True, False])
-def test_fused_tree_decode_equals_select_then_read(spans):
+def test_fused_tree_decode_equals_select_then_read(spans, readers):
     """The one-launch tree decode (lsa_decode_tree): lists and lengths byte-identical to
     tree_select on the group-mean index queries, at ragged positions (growth covers only
     whole node blocks, the rest are fresh; a row early enough to see no bucket reads its
     window and sinks alone), with span tables or member rows, in both
-    scoring types; the output within the bf16 bar of the fp64 read over those lists."""
+    scoring types, at the default reader count and at 1 (no partials), 7 and 64 (more
+    readers than some rows' lists have tiles); the output within the bf16 bar of the fp64
+    read over those lists."""
     import dataclasses
 
     B, T, Hq, Hkv, D = 3, 16384, 8, 2, 128
@@ -251,8 +254,9 @@ def test_fused_tree_decode_equals_select_then_read(spans):
     q = data.q[:, -1:].contiguous()
     idx = pipeline.index_queries(q, Hkv)[:, 0]
     for score_dtype in ("bf16", "fp32"):
+        print(f"case fused tree spans={spans} readers={readers} {score_dtype}", flush=True)
         out, lists, lengths = pipeline.tree_decode(q, data.k, data.v, pos, buckets, tree, config,
-                                                   score_dtype=score_dtype)
+                                                   score_dtype=score_dtype, readers=readers)
         want_l, want_n = pipeline.tree_select(idx, pos, buckets, tree, config, score_dtype=score_dtype)
         assert torch.equal(lists, want_l) and torch.equal(lengths, want_n), score_dtype
         want = oracle.sparse_read(_np(q.float()), _np(data.k.float()), _np(data.v.float()), _np(lists)[:, None],
