@@ -401,13 +401,6 @@ int lsa_decode_flat_noalloc(const void* q, const void* k, const void* v, int dty
                             int32_t reset_counters, int32_t* lists, int32_t* lengths, void* out, int32_t* status,
                             void* stream);
 
-/* Test hook (thread-local, this thread's later lsa_decode_flat calls): skip_publish != 0
- * makes the select workgroups skip publishing the record or their keys, and spin_limit > 0 replaces the
- * readers' poll limit, so a test can make the bounded wait give up with every workgroup
- * still exiting normally. lsa_debug_decode(0, 0) restores the defaults. No counterpart in
- * the reference (its decode has no cross-workgroup wait). */
-void lsa_debug_decode(int32_t skip_publish, int32_t spin_limit);
-
 #ifdef __cplusplus
 }
 #endif

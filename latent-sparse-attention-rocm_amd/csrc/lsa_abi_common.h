@@ -9,6 +9,7 @@
 #include <stdio.h>
 
 #include "lsa_rocm.h"
+#include "lsa_rocm_testing.h"
 
 namespace lsa {
 

@@ -1,5 +1,6 @@
-"""The C ABI without a GPU: the library loads, exports every symbol include/lsa_rocm.h
-declares, and its host-side validation rejects bad arguments before any HIP call."""
+"""The C ABI without a GPU: the library loads, exports every symbol the headers under
+include/ declare (the interface, lsa_rocm.h, and the test hooks, lsa_rocm_testing.h), and its
+host-side validation rejects bad arguments before any HIP call."""
 
 import ctypes
 import pathlib
@@ -9,11 +10,11 @@ import pytest
 
 from lsa_rocm_lab import _abi
 
-HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "lsa_rocm.h"
+HEADERS = sorted((pathlib.Path(__file__).resolve().parents[1] / "include").glob("*.h"))
 
 
 def declared() -> list[str]:
-    text = HEADER.read_text()
+    text = "".join(h.read_text() for h in HEADERS)
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(lsa_\w+)\(", text, flags=re.M)))
 
 
